@@ -1,0 +1,332 @@
+"""ctypes bindings for the CPU checkers.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()`` and by
+bench.py's cpu_baseline leg, never by the product package.
+
+* ``Oracle``    -- oracle/liboracle.so, the C restatement of the reference path.
+* ``Reference`` -- oracle/_ref/libsapphire_ref.so, the reference engine compiled from
+  its own sources by ``make -C oracle ref`` (present only where it was built).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libsapphire_ref.so")
+REF_DECODE_LIB = os.path.join(HERE, "_ref", "libref_decode.so")
+
+F32P = C.POINTER(C.c_float)
+
+
+def _p(a: np.ndarray, t=C.c_void_p):
+    return C.cast(a.ctypes.data, t) if a is not None else None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+
+
+class ModelStruct(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+        ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("max_ctx", C.c_int),
+        ("sliding_window", C.c_int), ("global_mask", C.c_ulonglong),
+        ("query_pre_attn_scalar", C.c_float), ("eps", C.c_float),
+        ("wdtype", C.c_int), ("lm_dtype", C.c_int),
+        ("wq", C.POINTER(C.c_void_p)), ("wk", C.POINTER(C.c_void_p)), ("wv", C.POINTER(C.c_void_p)),
+        ("wo", C.POINTER(C.c_void_p)), ("wgate", C.POINTER(C.c_void_p)), ("wup", C.POINTER(C.c_void_p)),
+        ("wdown", C.POINTER(C.c_void_p)),
+        ("norm_attn", C.POINTER(F32P)), ("norm_attn_post", C.POINTER(F32P)),
+        ("norm_ffn", C.POINTER(F32P)), ("norm_ffn_post", C.POINTER(F32P)),
+        ("q_norm", C.POINTER(F32P)), ("k_norm", C.POINTER(F32P)),
+        ("q_norm_len", C.c_int), ("k_norm_len", C.c_int),
+        ("embed_bf16", C.c_void_p), ("norm_final", F32P), ("lm_head", C.c_void_p),
+        ("k_cache", F32P), ("v_cache", F32P),
+        ("rope_cos_global", F32P), ("rope_sin_global", F32P),
+        ("rope_cos_local", F32P), ("rope_sin_local", F32P),
+        ("nthreads", C.c_int),
+    ]
+
+
+class Oracle:
+    def __init__(self, path: str = LIB):
+        if not os.path.exists(path):
+            build()
+        L = self.lib = C.CDLL(path)
+        vp, ip, i, f = C.c_void_p, C.c_void_p, C.c_int, C.c_float
+        L.oracle_q4_0_row.restype = f
+        L.oracle_q4_0_row.argtypes = [vp, vp, i, i]
+        L.oracle_q8_0_row.restype = f
+        L.oracle_q8_0_row.argtypes = [vp, vp, i, i]
+        L.oracle_gemv.restype = i
+        L.oracle_gemv.argtypes = [i, vp, i, i, vp, vp, i]
+        L.oracle_dequant.argtypes = [i, vp, i, vp]
+        L.oracle_q4_0_unpack_ints.argtypes = [vp, i, vp]
+        L.oracle_q8_0_unpack_ints.argtypes = [vp, i, vp]
+        for n in ("oracle_rmsnorm", "oracle_rmsnorm_delta"):
+            getattr(L, n).restype = i
+            getattr(L, n).argtypes = [vp, vp, vp, f, i]
+        L.oracle_rope_precompute_freqs.restype = i
+        L.oracle_rope_precompute_freqs.argtypes = [vp, vp, i, i, f]
+        L.oracle_rope_apply_fast.argtypes = [vp, i, i, vp, vp]
+        L.oracle_gelu.restype = f
+        L.oracle_gelu.argtypes = [f]
+        L.oracle_gelu_mul.argtypes = [vp, vp, i]
+        L.oracle_softmax.argtypes = [vp, i]
+        L.oracle_sample_greedy.restype = i
+        L.oracle_sample_greedy.argtypes = [vp, i]
+        L.oracle_vec_dot.restype = f
+        L.oracle_vec_dot.argtypes = [vp, vp, i]
+        L.oracle_decode_step.restype = i
+        L.oracle_decode_step.argtypes = [C.POINTER(ModelStruct), i, i, vp]
+
+    # -- numpy conveniences --------------------------------------------------
+    def gemv(self, dtype, blocks, x, nthreads=1):
+        m, nb = blocks.shape
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(m, np.float32)
+        rc = self.lib.oracle_gemv(dtype, _p(np.ascontiguousarray(blocks)), m, x.shape[0], _p(x), _p(y), nthreads)
+        assert rc == 0
+        return y
+
+    def row(self, dtype, blocks_row, x):
+        fn = self.lib.oracle_q4_0_row if dtype == 3 else self.lib.oracle_q8_0_row
+        return np.float32(fn(_p(np.ascontiguousarray(blocks_row)), _p(x), blocks_row.shape[0], 32))
+
+    def dequant(self, dtype, blocks):
+        flat = np.ascontiguousarray(blocks).reshape(-1)
+        out = np.empty(flat.shape[0] * 32, np.float32)
+        self.lib.oracle_dequant(dtype, _p(flat), flat.shape[0], _p(out))
+        return out
+
+    def unpack_ints(self, dtype, blocks):
+        flat = np.ascontiguousarray(blocks).reshape(-1)
+        out = np.empty(flat.shape[0] * 32, np.int8)
+        fn = self.lib.oracle_q4_0_unpack_ints if dtype == 3 else self.lib.oracle_q8_0_unpack_ints
+        fn(_p(flat), flat.shape[0], _p(out))
+        return out
+
+    def rmsnorm_delta(self, x, w, eps=1e-6):
+        out = np.empty_like(x)
+        assert self.lib.oracle_rmsnorm_delta(_p(out), _p(x), _p(w), eps, x.shape[0]) == 0
+        return out
+
+    def rmsnorm(self, x, w, eps=1e-6):
+        out = np.empty_like(x)
+        assert self.lib.oracle_rmsnorm(_p(out), _p(x), _p(w), eps, x.shape[0]) == 0
+        return out
+
+    def rope_tables(self, d_k, max_ctx, base):
+        c = np.empty(max_ctx * d_k, np.float32)
+        s = np.empty(max_ctx * d_k, np.float32)
+        assert self.lib.oracle_rope_precompute_freqs(_p(c), _p(s), d_k, max_ctx, base) == 0
+        return c, s
+
+    def rope_apply(self, x, pos, cos_t, sin_t):
+        x = x.copy()
+        self.lib.oracle_rope_apply_fast(_p(x), pos, x.shape[0], _p(cos_t), _p(sin_t))
+        return x
+
+    def gelu_mul(self, gate, up):
+        g = gate.copy()
+        self.lib.oracle_gelu_mul(_p(g), _p(up), g.shape[0])
+        return g
+
+    def softmax(self, x):
+        x = x.copy()
+        self.lib.oracle_softmax(_p(x), x.shape[0])
+        return x
+
+    def argmax(self, x):
+        return self.lib.oracle_sample_greedy(_p(x), x.shape[0])
+
+
+class Reference:
+    """The compiled reference engine (oracle/_ref), when it was built."""
+
+    @staticmethod
+    def available() -> bool:
+        return os.path.exists(REF_LIB)
+
+    def __init__(self, path: str = REF_LIB):
+        L = self.lib = C.CDLL(path)
+        vp, i, f = C.c_void_p, C.c_int, C.c_float
+        for n in ("quantized_gemv_q4_0_aligned", "quantized_gemv_q4_0_unaligned",
+                  "quantized_gemv_q8_0_aligned", "quantized_gemv_q8_0_unaligned"):
+            getattr(L, n).restype = f
+            getattr(L, n).argtypes = [vp, vp, i, i]
+        L.kernel_ctx_create.restype = vp
+        L.kernel_ctx_create.argtypes = [i, i]
+        L.kernel_ctx_init.restype = i
+        L.kernel_ctx_init.argtypes = [vp]
+        L.kernel_ctx_destroy.argtypes = [vp]
+        L.tensor_create_view.restype = vp
+        L.tensor_create_view.argtypes = [i, i, vp, vp]
+        L.tensor_release.argtypes = [vp]
+        L.kernel_gemv.restype = i
+        L.kernel_gemv.argtypes = [vp, vp, vp, vp]
+        for n in ("rmsnorm", "rmsnorm_delta"):
+            getattr(L, n).restype = i
+            getattr(L, n).argtypes = [vp, vp, vp, f, i]
+        L.rope_precompute_freqs.restype = i
+        L.rope_precompute_freqs.argtypes = [vp, vp, i, i, f]
+        L.rope_apply_fast.argtypes = [vp, i, i, vp, vp]
+        L.gelu.restype = f
+        L.gelu.argtypes = [f]
+        L.gelu_inplace.argtypes = [vp, i]
+        L.softmax.argtypes = [vp, i]
+        L.sample_greedy.restype = i
+        L.sample_greedy.argtypes = [vp, i]
+        L.vec_dot.restype = f
+        L.vec_dot.argtypes = [vp, vp, i]
+        # the reference logs through stderr; keep it quiet below WARN
+        try:
+            L.log_set_level.argtypes = [i]
+            L.log_set_level(40)
+        except AttributeError:
+            pass
+        self._ctx = {}
+
+    def ctx(self, nthreads: int):
+        if nthreads not in self._ctx:
+            c = self.lib.kernel_ctx_create(nthreads, 16)
+            assert c and self.lib.kernel_ctx_init(c) == 0
+            self._ctx[nthreads] = c
+        return self._ctx[nthreads]
+
+    def close(self):
+        for c in self._ctx.values():
+            self.lib.kernel_ctx_destroy(c)
+        self._ctx.clear()
+
+    def gemv(self, dtype, blocks, x, nthreads=1, y=None):
+        m, nb = blocks.shape
+        k = x.shape[0]
+        shape = (C.c_int * 2)(m, k)
+        t = self.lib.tensor_create_view(dtype, 2, shape, _p(blocks))
+        if y is None:
+            y = np.empty(m, np.float32)
+        rc = self.lib.kernel_gemv(self.ctx(nthreads), _p(y), t, _p(x))
+        self.lib.tensor_release(t)
+        assert rc == 0
+        return y
+
+    def row(self, dtype, blocks_row, x, aligned=False):
+        name = "quantized_gemv_q4_0_" if dtype == 3 else "quantized_gemv_q8_0_"
+        fn = getattr(self.lib, name + ("aligned" if aligned else "unaligned"))
+        return np.float32(fn(_p(np.ascontiguousarray(blocks_row)), _p(x), blocks_row.shape[0], 32))
+
+
+class RefCfg(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+        ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("max_ctx", C.c_int),
+        ("sliding_window", C.c_int), ("global_mask", C.c_ulonglong),
+        ("query_pre_attn_scalar", C.c_float), ("rope_theta", C.c_float), ("rope_local_base", C.c_float),
+        ("wdtype", C.c_int), ("lm_dtype", C.c_int),
+    ]
+
+
+class RefWeights(C.Structure):
+    _fields_ = [
+        ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
+        ("wgate", C.c_void_p), ("wup", C.c_void_p), ("wdown", C.c_void_p),
+        ("norm_attn", C.c_void_p), ("norm_attn_post", C.c_void_p), ("norm_ffn", C.c_void_p),
+        ("norm_ffn_post", C.c_void_p), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p),
+        ("q_norm_len", C.c_int), ("k_norm_len", C.c_int),
+        ("embed_bf16", C.c_void_p), ("norm_final", C.c_void_p), ("lm_head", C.c_void_p),
+    ]
+
+
+def ref_decode_available() -> bool:
+    return os.path.exists(REF_DECODE_LIB)
+
+
+# ---------------------------------------------------------------------------
+# Decode drivers over a sapphire_amd.model.SyntheticModel
+# ---------------------------------------------------------------------------
+_PROJ = ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+
+
+def oracle_decode(orc: "Oracle", model, k_cache, v_cache, token, pos, steps, nthreads=1, keep_logits=False):
+    """Greedy decode with the oracle. k_cache/v_cache are updated in place.
+    Returns (tokens[steps], logits[steps, vocab] or last logits)."""
+    cfg = model.cfg
+    L = cfg.n_layers
+    keep = []
+
+    def ptrs(arrs, t=C.c_void_p):
+        a = (t * L)(*[C.cast(x.ctypes.data, t) for x in arrs])
+        keep.append(arrs)
+        return a
+
+    ms = ModelStruct()
+    ms.n_layers, ms.hidden, ms.n_heads, ms.n_kv_heads = L, cfg.hidden, cfg.n_heads, cfg.n_kv_heads
+    ms.head_dim, ms.ffn, ms.vocab, ms.max_ctx = cfg.head_dim, cfg.ffn, cfg.vocab, cfg.max_ctx
+    ms.sliding_window, ms.global_mask = cfg.sliding_window, cfg.global_mask
+    ms.query_pre_attn_scalar, ms.eps = cfg.query_pre_attn_scalar, cfg.eps
+    ms.wdtype, ms.lm_dtype = cfg.wdtype, cfg.lm_dtype
+    for n in _PROJ:
+        setattr(ms, n, ptrs([np.ascontiguousarray(model.weights[n][l]) for l in range(L)]))
+    for n in ("norm_attn", "norm_attn_post", "norm_ffn", "norm_ffn_post", "q_norm", "k_norm"):
+        setattr(ms, n, ptrs([np.ascontiguousarray(model.norms[n][l]) for l in range(L)], F32P))
+    ms.q_norm_len = ms.k_norm_len = cfg.head_dim
+    ms.embed_bf16 = model.embed_bf16.ctypes.data
+    ms.norm_final = C.cast(model.norm_final.ctypes.data, F32P)
+    ms.lm_head = model.lm_head.ctypes.data
+    assert k_cache.flags.c_contiguous and v_cache.flags.c_contiguous
+    ms.k_cache = C.cast(k_cache.ctypes.data, F32P)
+    ms.v_cache = C.cast(v_cache.ctypes.data, F32P)
+    cg, sg = orc.rope_tables(cfg.head_dim, cfg.max_ctx, cfg.rope_theta)
+    cl, sl = orc.rope_tables(cfg.head_dim, cfg.max_ctx, cfg.rope_local_base)
+    keep.append((cg, sg, cl, sl))
+    ms.rope_cos_global, ms.rope_sin_global = C.cast(cg.ctypes.data, F32P), C.cast(sg.ctypes.data, F32P)
+    ms.rope_cos_local, ms.rope_sin_local = C.cast(cl.ctypes.data, F32P), C.cast(sl.ctypes.data, F32P)
+    ms.nthreads = nthreads
+    tokens = np.empty(steps, np.int32)
+    logits = np.empty((steps if keep_logits else 1, cfg.vocab), np.float32)
+    for s in range(steps):
+        out = logits[s if keep_logits else 0]
+        t = orc.lib.oracle_decode_step(C.byref(ms), int(token), int(pos + s), out.ctypes.data)
+        assert t >= 0
+        tokens[s] = token = t
+    return tokens, logits
+
+
+def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False):
+    """Greedy decode through the compiled reference engine (oracle/_ref)."""
+    cfg = model.cfg
+    lib = C.CDLL(REF_DECODE_LIB)
+    lib.ref_decode_run.restype = C.c_int
+    lib.ref_decode_run.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p,
+                                   C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    try:
+        C.CDLL(REF_LIB).log_set_level(40)
+    except AttributeError:
+        pass
+    rc = RefCfg(cfg.n_layers, cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn, cfg.vocab,
+                cfg.max_ctx, cfg.sliding_window, cfg.global_mask, cfg.query_pre_attn_scalar,
+                cfg.rope_theta, cfg.rope_local_base, cfg.wdtype, cfg.lm_dtype)
+    keep = {n: np.ascontiguousarray(model.weights[n]) for n in _PROJ}
+    keep.update({n: np.ascontiguousarray(model.norms[n]) for n in model.norms})
+    rw = RefWeights()
+    for n in _PROJ:
+        setattr(rw, n, keep[n].ctypes.data)
+    for n in ("norm_attn", "norm_attn_post", "norm_ffn", "norm_ffn_post", "q_norm", "k_norm"):
+        setattr(rw, n, keep[n].ctypes.data)
+    rw.q_norm_len = rw.k_norm_len = cfg.head_dim
+    rw.embed_bf16 = model.embed_bf16.ctypes.data
+    rw.norm_final = model.norm_final.ctypes.data
+    rw.lm_head = model.lm_head.ctypes.data
+    tokens = np.empty(steps, np.int32)
+    logits = np.empty((steps, cfg.vocab), np.float32) if keep_logits else None
+    r = lib.ref_decode_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data, int(token),
+                           int(pos), int(steps), tokens.ctypes.data,
+                           logits.ctypes.data if logits is not None else None)
+    assert r == 0
+    return tokens, logits
