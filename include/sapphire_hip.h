@@ -1,0 +1,100 @@
+/*
+ * sapphire_hip.h - device-pointer, stream-ordered API of libsapphire_hip.so.
+ *
+ * kernels.h keeps the reference's synchronous host-pointer contract. This header is the
+ * MI355X-native layer beneath it: every operation takes device pointers and a HIP stream
+ * (passed as void*; NULL = the null stream) and only enqueues work, so a host engine can
+ * keep activations, logits and the KV cache resident in HBM and capture a whole decode
+ * step in a hipGraph. All functions return 0 on success and -1 on bad arguments or a HIP
+ * error (message via sapphire_last_error()).
+ *
+ * None of these entry points exists in the reference; each names the reference routine
+ * whose semantics it implements.
+ */
+#ifndef SAPPHIRE_HIP_H
+#define SAPPHIRE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes are tensor_dtype_t's: F32 0, BF16 1, F16 2, Q4_0 3, Q8_0 4 */
+enum { SAPPHIRE_F32 = 0, SAPPHIRE_BF16 = 1, SAPPHIRE_F16 = 2, SAPPHIRE_Q4_0 = 3, SAPPHIRE_Q8_0 = 4 };
+
+/* Weight layouts in device memory for Q4_0/Q8_0.
+ *  AOS    : the reference block array, rows contiguous, row stride ceil(K/32)*B_blk
+ *           (B_blk 20 for Q4_0, 36 for Q8_0; include/kernels.h:29-38).
+ *  PACKED : the same quants and scales split in two planes, built by
+ *           sapphire_q_repack_dev: quants [M][nb][16|32] bytes (byte order of the
+ *           reference block), then, at offset sapphire_q_scales_offset(), fp32
+ *           scales [M][nb]. Values are bit-identical; only their placement differs. */
+enum { SAPPHIRE_LAYOUT_AOS = 0, SAPPHIRE_LAYOUT_PACKED = 1 };
+
+const char *sapphire_last_error(void);
+const char *sapphire_version(void);
+
+/* ---- device memory / streams / events (thin wrappers over the HIP runtime) ---- */
+int sapphire_device_count(void);
+int sapphire_set_device(int device);
+void *sapphire_malloc(size_t bytes);                 /* NULL on failure */
+int sapphire_free(void *dev_ptr);
+int sapphire_memcpy_h2d(void *dst_dev, const void *src_host, size_t bytes);
+int sapphire_memcpy_d2h(void *dst_host, const void *src_dev, size_t bytes);
+int sapphire_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes, void *stream);
+int sapphire_memset(void *dev_ptr, int value, size_t bytes);
+int sapphire_synchronize(void);
+void *sapphire_stream_create(void);                  /* default priority, non-blocking */
+int sapphire_stream_destroy(void *stream);
+int sapphire_stream_synchronize(void *stream);
+void *sapphire_event_create(void);
+int sapphire_event_destroy(void *event);
+int sapphire_event_record(void *event, void *stream);
+int sapphire_event_synchronize(void *event);
+float sapphire_event_elapsed_ms(void *start, void *stop);   /* < 0 on error */
+
+/* ---- quantized weights ---- */
+size_t sapphire_q_aos_bytes(int dtype, int M, int K);
+size_t sapphire_q_packed_bytes(int dtype, int M, int K);
+size_t sapphire_q_scales_offset(int dtype, int M, int K);
+/* AOS -> PACKED (both on device). */
+int sapphire_q_repack_dev(int dtype, const void *w_aos, int M, int K, void *w_packed, void *stream);
+/* Integer weight values (nib-8 or q) of every element, [M][nb*32] int8: the unpack
+ * of q4_0_avx.c:61-66 / q8_0_avx.c:45-56. */
+int sapphire_q_unpack_ints_dev(int dtype, int layout, const void *w, int M, int K, int8_t *out, void *stream);
+/* Dequantised weights fl(int * scale), [M][nb*32] f32: q4_0_avx.c:38-40, q8_0_avx.c:50-59. */
+int sapphire_q_dequant_dev(int dtype, int layout, const void *w, int M, int K, float *out, void *stream);
+
+/* y[M] = W[M,K] . x[K]  (kernel_gemv semantics, dispatch.c:101-156). K must be a
+ * multiple of 32 for Q4_0/Q8_0 (callers pad activations, as the reference's session
+ * scratch does; inference.c:377-394). */
+int sapphire_gemv_q_dev(int dtype, int layout, const void *w, int M, int K,
+                        const float *x, float *y, void *stream);
+/* y[M] = W[M,K] . x[K] for F32 or BF16 row-major W (f32_avx.c:44-83, bf16_avx.c:55-108). */
+int sapphire_gemv_f_dev(int dtype, const void *w, int M, int K, const float *x, float *y, void *stream);
+
+/* ---- LM-head epilogue ----
+ * probs = softmax(logits) (utils.c:18-59) written to probs (may equal logits) and the
+ * greedy token (utils.c:145-156: first index of the maximum) written to *argmax_dev.
+ * probs may be NULL to compute only the argmax. */
+int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *argmax_dev, void *stream);
+
+/* ---- primitives on device vectors ---- */
+/* out[b] = rmsnorm_delta(in[b]) for b < batch, rows of length dim (normalization.c:104-117). */
+int sapphire_rmsnorm_delta_dev(float *out, const float *in, const float *w, float eps, int dim, int batch, void *stream);
+int sapphire_rmsnorm_dev(float *out, const float *in, const float *w, float eps, int dim, int batch, void *stream);
+/* Half-split rotation of n_heads consecutive heads at position pos (rope.c:99-117). */
+int sapphire_rope_apply_dev(float *x, int n_heads, int head_dim, int pos,
+                            const float *cos_table, const float *sin_table, void *stream);
+/* gate[i] = gelu(gate[i]) * up[i] (transformer.c:150-157, activations.c:64-82). */
+int sapphire_gelu_mul_dev(float *gate, const float *up, int n, void *stream);
+/* Residual pattern n = rmsnorm_delta(h, w); resid += n; h = resid
+ * (attention.c:358-366, transformer.c:231-239). */
+int sapphire_norm_residual_dev(float *hidden, float *resid, const float *w, float eps, int dim, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SAPPHIRE_HIP_H */

@@ -1,0 +1,63 @@
+"""Builds sapphire_amd/libsapphire_hip.so with hipcc for gfx950.
+
+    python -m sapphire_amd.build            # compile (always recompiles)
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "libsapphire_hip.so")
+SOURCES = ["runtime.cpp", "tensor.cpp", "dispatch.cpp", "gemv.hip", "ops.hip", "decode.hip"]
+ARCH = os.environ.get("SAPPHIRE_OFFLOAD_ARCH", "gfx950")
+
+COMMON = [
+    "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    # contraction only where the source writes an explicit fmaf
+    "-ffp-contract=off",
+    # packed fp32 instructions are not used on this target
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-D__HIP_PLATFORM_AMD__",
+]
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("hipcc not found")
+
+
+def build(verbose: bool = False) -> str:
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix="sapphire_build_") as tmp:
+        objs = []
+        for src in SOURCES:
+            path = os.path.join(CSRC, src)
+            if not os.path.exists(path):
+                continue
+            obj = os.path.join(tmp, os.path.basename(src) + ".o")
+            cmd = [cc, f"--offload-arch={ARCH}", *COMMON, "-c", path, "-o", obj]
+            if src.endswith(".cpp"):
+                cmd.insert(1, "-x")
+                cmd.insert(2, "hip")
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            subprocess.run(cmd, check=True)
+            objs.append(obj)
+        tmp_out = OUT + ".tmp"
+        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_out, *objs, "-lpthread"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        os.replace(tmp_out, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

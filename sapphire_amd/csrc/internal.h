@@ -1,0 +1,59 @@
+// internal.h - shared declarations of libsapphire_hip.so (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+
+namespace sapphire {
+
+enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_Q4_0 = 3, DT_Q8_0 = 4 };
+enum : int { LAYOUT_AOS = 0, LAYOUT_PACKED = 1 };
+
+constexpr int kBlock = 32;                      // weights per quant block
+inline int quant_bytes(int dt) { return dt == DT_Q4_0 ? 16 : 32; }   // payload per block
+inline int block_bytes(int dt) { return dt == DT_Q4_0 ? 20 : 36; }   // AoS block size
+inline bool is_quant(int dt) { return dt == DT_Q4_0 || dt == DT_Q8_0; }
+
+// Error reporting: the last message is kept per thread and also written to stderr.
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+bool hip_ok(hipError_t e, const char *what);
+
+#define SPH_CHECK(expr)                                   \
+    do {                                                  \
+        if (!::sapphire::hip_ok((expr), #expr)) return -1; \
+    } while (0)
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- kernel launchers (device pointers, stream ordered); return 0 / -1 ----
+size_t q_aos_bytes(int dt, int M, int K);
+size_t q_scales_offset(int dt, int M, int K);
+size_t q_packed_bytes(int dt, int M, int K);
+int launch_repack(int dt, const void *aos, int M, int K, void *packed, hipStream_t s);
+int launch_unpack_ints(int dt, int layout, const void *w, int M, int K, int8_t *out, hipStream_t s);
+int launch_dequant(int dt, int layout, const void *w, int M, int K, float *out, hipStream_t s);
+int launch_gemv_q(int dt, int layout, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
+int launch_gemm_q(int dt, int layout, const void *w, int M, int K, const float *X, float *Y, int batch,
+                  hipStream_t s);
+int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
+
+int launch_rmsnorm(float *out, const float *in, const float *w, float eps, int dim, int batch, bool delta,
+                   hipStream_t s);
+int launch_rope(float *x, int n_heads, int head_dim, int pos, const float *cos_t, const float *sin_t,
+                hipStream_t s);
+int launch_gelu_mul(float *gate, const float *up, int n, hipStream_t s);
+int launch_softmax_argmax(const float *logits, int n, float *probs, int *argmax, float *scratch,
+                          hipStream_t s);
+size_t softmax_scratch_floats(int n);
+enum : int { UOP_GELU = 0, UOP_SILU = 1, UOP_RELU = 2, UOP_SCALE = 3, UOP_SOFTCAP = 4 };
+int launch_unary(float *x, int n, int op, float a, hipStream_t s);
+int launch_axpy(float *dst, const float *src, int n, float a, bool fused, hipStream_t s);
+int launch_geglu_split(float *out, const float *in, int n, hipStream_t s);
+int launch_bf16_to_f32(float *dst, const uint16_t *src, int n, hipStream_t s);
+int launch_dot_ref(const float *a, const float *b, int n, float *out, hipStream_t s);
+int launch_norm_residual(float *hidden, float *resid, const float *w, float eps, int dim, hipStream_t s);
+
+}  // namespace sapphire

@@ -1,0 +1,198 @@
+// runtime.cpp - error reporting, device-memory/stream/event wrappers and the
+// device-pointer entry points of sapphire_hip.h.
+#include <cstdarg>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/sapphire_hip.h"
+#include "internal.h"
+
+namespace sapphire {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "[sapphire-hip] %s\n", g_err);
+}
+
+bool hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+}  // namespace sapphire
+
+using namespace sapphire;
+
+namespace {
+
+bool valid_quant_args(int dtype, const void *w, int M, int K) {
+    if (!is_quant(dtype)) { set_error("dtype %d is not Q4_0/Q8_0", dtype); return false; }
+    if (!w || M <= 0 || K <= 0) { set_error("bad quantized matrix arguments (w=%p M=%d K=%d)", w, M, K); return false; }
+    if ((reinterpret_cast<uintptr_t>(w) & 3u) != 0) { set_error("weights must be 4-byte aligned"); return false; }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *sapphire_last_error(void) { return g_err; }
+const char *sapphire_version(void) { return "sapphire-hip 0.1 (gfx950)"; }
+
+int sapphire_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int sapphire_set_device(int device) { SPH_CHECK(hipSetDevice(device)); return 0; }
+
+void *sapphire_malloc(size_t bytes) {
+    void *p = nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc")) return nullptr;
+    return p;
+}
+
+int sapphire_free(void *p) { SPH_CHECK(hipFree(p)); return 0; }
+
+int sapphire_memcpy_h2d(void *dst, const void *src, size_t n) {
+    SPH_CHECK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+    return 0;
+}
+
+int sapphire_memcpy_d2h(void *dst, const void *src, size_t n) {
+    SPH_CHECK(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int sapphire_memcpy_d2d(void *dst, const void *src, size_t n, void *stream) {
+    SPH_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, as_stream(stream)));
+    return 0;
+}
+
+int sapphire_memset(void *p, int v, size_t n) { SPH_CHECK(hipMemset(p, v, n)); return 0; }
+int sapphire_synchronize(void) { SPH_CHECK(hipDeviceSynchronize()); return 0; }
+
+void *sapphire_stream_create(void) {
+    hipStream_t s = nullptr;
+    if (!hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return nullptr;
+    return s;
+}
+
+int sapphire_stream_destroy(void *s) { SPH_CHECK(hipStreamDestroy(as_stream(s))); return 0; }
+int sapphire_stream_synchronize(void *s) { SPH_CHECK(hipStreamSynchronize(as_stream(s))); return 0; }
+
+void *sapphire_event_create(void) {
+    hipEvent_t e = nullptr;
+    if (!hip_ok(hipEventCreate(&e), "hipEventCreate")) return nullptr;
+    return e;
+}
+
+int sapphire_event_destroy(void *e) { SPH_CHECK(hipEventDestroy(reinterpret_cast<hipEvent_t>(e))); return 0; }
+
+int sapphire_event_record(void *e, void *s) {
+    SPH_CHECK(hipEventRecord(reinterpret_cast<hipEvent_t>(e), as_stream(s)));
+    return 0;
+}
+
+int sapphire_event_synchronize(void *e) {
+    SPH_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(e)));
+    return 0;
+}
+
+float sapphire_event_elapsed_ms(void *a, void *b) {
+    float ms = -1.f;
+    if (!hip_ok(hipEventElapsedTime(&ms, reinterpret_cast<hipEvent_t>(a), reinterpret_cast<hipEvent_t>(b)),
+                "hipEventElapsedTime"))
+        return -1.f;
+    return ms;
+}
+
+size_t sapphire_q_aos_bytes(int dt, int M, int K) { return is_quant(dt) ? q_aos_bytes(dt, M, K) : 0; }
+size_t sapphire_q_packed_bytes(int dt, int M, int K) { return is_quant(dt) ? q_packed_bytes(dt, M, K) : 0; }
+size_t sapphire_q_scales_offset(int dt, int M, int K) { return is_quant(dt) ? q_scales_offset(dt, M, K) : 0; }
+
+int sapphire_q_repack_dev(int dt, const void *w_aos, int M, int K, void *w_packed, void *stream) {
+    if (!valid_quant_args(dt, w_aos, M, K) || !w_packed) return -1;
+    return launch_repack(dt, w_aos, M, K, w_packed, as_stream(stream));
+}
+
+int sapphire_q_unpack_ints_dev(int dt, int layout, const void *w, int M, int K, int8_t *out, void *stream) {
+    if (!valid_quant_args(dt, w, M, K) || !out) return -1;
+    return launch_unpack_ints(dt, layout, w, M, K, out, as_stream(stream));
+}
+
+int sapphire_q_dequant_dev(int dt, int layout, const void *w, int M, int K, float *out, void *stream) {
+    if (!valid_quant_args(dt, w, M, K) || !out) return -1;
+    return launch_dequant(dt, layout, w, M, K, out, as_stream(stream));
+}
+
+int sapphire_gemv_q_dev(int dt, int layout, const void *w, int M, int K, const float *x, float *y, void *stream) {
+    if (!valid_quant_args(dt, w, M, K) || !x || !y) return -1;
+    if (K % kBlock != 0) { set_error("K=%d is not a multiple of 32", K); return -1; }
+    if (layout != LAYOUT_AOS && layout != LAYOUT_PACKED) { set_error("bad layout %d", layout); return -1; }
+    return launch_gemv_q(dt, layout, w, M, K, x, y, as_stream(stream));
+}
+
+int sapphire_gemv_f_dev(int dt, const void *w, int M, int K, const float *x, float *y, void *stream) {
+    if ((dt != DT_F32 && dt != DT_BF16) || !w || !x || !y || M <= 0 || K <= 0) {
+        set_error("bad F32/BF16 GEMV arguments");
+        return -1;
+    }
+    return launch_gemv_f(dt, w, M, K, x, y, as_stream(stream));
+}
+
+int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *argmax, void *stream) {
+    if (!logits || n <= 0 || (!probs && !argmax)) { set_error("bad softmax arguments"); return -1; }
+    // The partials live in a small per-device buffer shared by all calls on one stream order.
+    static std::mutex mu;
+    static float *scratch[64] = {nullptr};
+    int dev = 0;
+    SPH_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) { set_error("device index %d out of range", dev); return -1; }
+    {
+        std::lock_guard<std::mutex> g(mu);
+        if (!scratch[dev]) {
+            void *p = nullptr;
+            SPH_CHECK(hipMalloc(&p, softmax_scratch_floats(n) * sizeof(float)));
+            scratch[dev] = static_cast<float *>(p);
+        }
+    }
+    return launch_softmax_argmax(logits, n, probs, argmax, scratch[dev], as_stream(stream));
+}
+
+int sapphire_rmsnorm_delta_dev(float *out, const float *in, const float *w, float eps, int dim, int batch, void *s) {
+    if (!out || !in || !w || dim <= 0 || batch <= 0 || eps < 0.f) { set_error("bad rmsnorm arguments"); return -1; }
+    return launch_rmsnorm(out, in, w, eps, dim, batch, true, as_stream(s));
+}
+
+int sapphire_rmsnorm_dev(float *out, const float *in, const float *w, float eps, int dim, int batch, void *s) {
+    if (!out || !in || !w || dim <= 0 || batch <= 0 || eps < 0.f) { set_error("bad rmsnorm arguments"); return -1; }
+    return launch_rmsnorm(out, in, w, eps, dim, batch, false, as_stream(s));
+}
+
+int sapphire_rope_apply_dev(float *x, int n_heads, int head_dim, int pos, const float *c, const float *sn, void *s) {
+    if (!x || !c || !sn || n_heads <= 0 || head_dim <= 0 || (head_dim & 1) || pos < 0) {
+        set_error("bad rope arguments");
+        return -1;
+    }
+    return launch_rope(x, n_heads, head_dim, pos, c, sn, as_stream(s));
+}
+
+int sapphire_gelu_mul_dev(float *gate, const float *up, int n, void *s) {
+    if (!gate || !up || n <= 0) { set_error("bad gelu_mul arguments"); return -1; }
+    return launch_gelu_mul(gate, up, n, as_stream(s));
+}
+
+int sapphire_norm_residual_dev(float *hidden, float *resid, const float *w, float eps, int dim, void *s) {
+    if (!hidden || !resid || !w || dim <= 0 || eps < 0.f) { set_error("bad norm_residual arguments"); return -1; }
+    return launch_norm_residual(hidden, resid, w, eps, dim, as_stream(s));
+}
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+// tensor_impl.h - private layout of tensor_t (not installed).
+#pragma once
+
+#include <mutex>
+
+#include "../../include/tensor.h"
+#include "internal.h"
+
+struct tensor_t {
+    void *data = nullptr;         // host data (owned unless is_external)
+    int ndim = 0;
+    int shape[8] = {0};
+    tensor_dtype_t dtype = DTYPE_F32;
+    memory_layout_t layout = LAYOUT_ROW_MAJOR;
+    size_t nbytes = 0;
+    int ref_count = 0;
+    int is_external = 0;
+    // device copy of the weights (created on first GPU use)
+    std::mutex dev_mu;
+    void *dev = nullptr;
+    size_t dev_bytes = 0;
+    int dev_layout = 0;           // sapphire::LAYOUT_AOS for F32/BF16, LAYOUT_PACKED for Q4_0/Q8_0
+    int dev_device = -1;
+};
+
+namespace sapphire {
+// Device copy of a 2-D weight tensor on the current device (uploaded on first use).
+const void *tensor_device_weights(const tensor_t *t, int *layout, hipStream_t s);
+void tensor_drop_device(tensor_t *t);
+}  // namespace sapphire

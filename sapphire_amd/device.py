@@ -1,0 +1,124 @@
+"""numpy-facing helpers over the device-pointer API (sapphire_hip.h)."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import load, synth
+
+
+def lib():
+    return load()
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        err = lib().sapphire_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {err}")
+
+
+class DeviceArray:
+    """Owning device buffer with shape/dtype bookkeeping for numpy round trips."""
+
+    def __init__(self, nbytes: int, shape=None, dtype=np.uint8):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().sapphire_malloc(max(self.nbytes, 1))
+        if not self.ptr:
+            raise MemoryError(lib().sapphire_last_error().decode())
+        self.shape = shape if shape is not None else (self.nbytes,)
+        self.dtype = np.dtype(dtype)
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.nbytes, a.shape, a.dtype)
+        check(lib().sapphire_memcpy_h2d(d.ptr, a.ctypes.data, a.nbytes), "h2d")
+        return d
+
+    @classmethod
+    def empty(cls, shape, dtype=np.float32) -> "DeviceArray":
+        shape = tuple(np.atleast_1d(shape))
+        return cls(int(np.prod(shape)) * np.dtype(dtype).itemsize, shape, dtype)
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib().sapphire_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), "d2h")
+        return out
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib().sapphire_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes), "h2d")
+
+    def zero(self) -> None:
+        check(lib().sapphire_memset(self.ptr, 0, self.nbytes), "memset")
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().sapphire_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class QMatrix:
+    """A Q4_0/Q8_0 weight matrix resident on the device, in AOS and/or PACKED layout."""
+
+    def __init__(self, dtype: int, blocks: np.ndarray, packed: bool = True, keep_aos: bool = False):
+        self.dtype = dtype
+        self.M, nb = blocks.shape
+        self.K = nb * 32
+        aos = DeviceArray.from_numpy(synth.as_bytes(blocks))
+        self.aos = aos if keep_aos or not packed else None
+        self.packed = None
+        if packed:
+            L = lib()
+            self.packed = DeviceArray(L.sapphire_q_packed_bytes(dtype, self.M, self.K))
+            check(L.sapphire_q_repack_dev(dtype, aos.ptr, self.M, self.K, self.packed.ptr, None), "repack")
+            check(L.sapphire_synchronize(), "sync")
+            if not keep_aos:
+                aos.free()
+
+    def ptr(self, layout: int) -> int:
+        return (self.packed if layout == 1 else self.aos).ptr
+
+    @property
+    def algorithmic_bytes(self) -> int:
+        """M*ceil(K/32)*B_blk + 4K + 4M: weights + activation + output."""
+        return self.M * (self.K // 32) * synth.BLOCK_BYTES[self.dtype] + 4 * self.K + 4 * self.M
+
+
+def gemv(qm: QMatrix, x: DeviceArray, y: DeviceArray, layout: int = 1, stream=None) -> None:
+    check(lib().sapphire_gemv_q_dev(qm.dtype, layout, qm.ptr(layout), qm.M, qm.K, x.ptr, y.ptr, stream), "gemv")
+
+
+class Timer:
+    """HIP-event timing on a given stream (None = null stream)."""
+
+    def __init__(self, stream=None):
+        L = lib()
+        self.stream = stream
+        self.a = L.sapphire_event_create()
+        self.b = L.sapphire_event_create()
+
+    def start(self):
+        check(lib().sapphire_event_record(self.a, self.stream), "event")
+
+    def stop(self) -> float:
+        L = lib()
+        check(L.sapphire_event_record(self.b, self.stream), "event")
+        check(L.sapphire_event_synchronize(self.b), "event sync")
+        return float(L.sapphire_event_elapsed_ms(self.a, self.b))
+
+    def __del__(self):
+        try:
+            L = lib()
+            L.sapphire_event_destroy(self.a)
+            L.sapphire_event_destroy(self.b)
+        except Exception:
+            pass
