@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decode hot path on one MI355X.
+
+Workload (the LM-head configuration, 262144 x 640): one step is
+  * Q8_0 GEMV 262144 x 640 (36-byte blocks) -> fp32 logits -> fused softmax + argmax
+  * Q4_0 GEMV 262144 x 640 (20-byte blocks) -> fp32 logits -> fused softmax + argmax
+on seeded synthetic weights (scale |N(0,0.01)|, uniform quants) and an N(0,1) hidden
+vector, all resident in HBM before timing. Two copies of the weights are rotated so
+that consecutive steps never find their weights in the 256 MB last-level cache.
+
+value = algorithmic bytes of a step (M*ceil(K/32)*B_blk + 4K + 4M per GEMV, plus 1 MiB
+read + 1 MiB written per softmax) / step time.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--decode-steps N]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+M_LM, K_LM = 262144, 640
+METRIC = "Q4_0/Q8_0 GEMV HBM GB/s (% of peak) + decode tok/s, Gemma-3-270M shape"
+
+
+def gemv_bytes(dtype: int, m: int, k: int) -> int:
+    from sapphire_amd import synth
+    return m * ((k + 31) // 32) * synth.BLOCK_BYTES[dtype] + 4 * k + 4 * m
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the Q8_0 LM-head GEMV, from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel)."""
+    path = os.path.join(ROOT, "profiles", "gemv_lm_head_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_q8_0_lm_head\s*[:=]\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(x, w8, w4, budget_s: float = 12.0):
+    """The reference's own pooled kernel_gemv (compiled from its sources into
+    oracle/_ref) on this host, or the oracle's restatement when that was not built."""
+    from oracle.oracle import Oracle, Reference
+    from sapphire_amd import synth
+    try:
+        ncpu = len(os.sched_getaffinity(0))
+    except AttributeError:
+        ncpu = os.cpu_count() or 1
+    threads = max(1, min(ncpu, int(os.environ.get("OMP_NUM_THREADS", ncpu)), 16))
+    if Reference.available():
+        ref, kind = Reference(), "reference"
+        run = lambda dt, w: ref.gemv(dt, w, x, nthreads=threads)   # noqa: E731
+    else:
+        orc, kind = Oracle(), "port"
+        run = lambda dt, w: orc.gemv(dt, w, x, nthreads=threads)   # noqa: E731
+    total_bytes, total_t, reps = 0, 0.0, 0
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s:
+        for dt, w in ((synth.Q8_0, w8), (synth.Q4_0, w4)):
+            t0 = time.perf_counter()
+            run(dt, w)
+            total_t += time.perf_counter() - t0
+            total_bytes += gemv_bytes(dt, M_LM, K_LM)
+        reps += 1
+    return {
+        "value": round(total_bytes / total_t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+        "sample": f"{reps} x (Q8_0 + Q4_0 GEMV 262144x640) with the pooled kernel_gemv, "
+                  f"{threads} threads, {total_t:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--decode-steps", type=int, default=64, help="greedy decode steps (0 skips decode)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the path has no multi-GPU mode in this build "
+              "(the one-GPU box runs --gpus 1).", file=sys.stderr)
+        return 2
+
+    from sapphire_amd import load, synth
+    from sapphire_amd.device import DeviceArray, QMatrix, Timer, check
+    L = load()
+    if L.sapphire_device_count() < 1:
+        print("no GPU visible", file=sys.stderr)
+        return 1
+
+    seed = 20260101
+    w8 = synth.quant_matrix(synth.Q8_0, M_LM, K_LM, seed, 1)
+    w4 = synth.quant_matrix(synth.Q4_0, M_LM, K_LM, seed, 2)
+    x = synth.normal_f32(K_LM, seed, 3)
+    n_sets = 2
+    q8 = [QMatrix(synth.Q8_0, w8) for _ in range(n_sets)]
+    q4 = [QMatrix(synth.Q4_0, w4) for _ in range(n_sets)]
+    dx = DeviceArray.from_numpy(x)
+    logits = DeviceArray.empty(M_LM)
+    probs = DeviceArray.empty(M_LM)
+    arg = DeviceArray.empty(1, np.int32)
+    stream = L.sapphire_stream_create()
+
+    def step(i, t8=None):
+        s = i % n_sets
+        if t8 is not None:
+            L.sapphire_event_record(t8[0], stream)
+        check(L.sapphire_gemv_q_dev(synth.Q8_0, 1, q8[s].ptr(1), M_LM, K_LM, dx.ptr, logits.ptr, stream))
+        if t8 is not None:
+            L.sapphire_event_record(t8[1], stream)
+        check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream))
+        check(L.sapphire_gemv_q_dev(synth.Q4_0, 1, q4[s].ptr(1), M_LM, K_LM, dx.ptr, logits.ptr, stream))
+        check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream))
+
+    for i in range(args.warmup):
+        step(i)
+    check(L.sapphire_stream_synchronize(stream))
+
+    # whole steps, back to back
+    t = Timer(stream)
+    t.start()
+    for i in range(args.steps):
+        step(i)
+    ms_total = t.stop()
+    ms_step = ms_total / args.steps
+
+    # dominant kernel (Q8_0 GEMV): per-launch HIP events on its stream
+    evs = [(L.sapphire_event_create(), L.sapphire_event_create()) for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(i, evs[i])
+    check(L.sapphire_stream_synchronize(stream))
+    q8_ms = float(np.mean([L.sapphire_event_elapsed_ms(a, b) for a, b in evs]))
+    for a, b in evs:
+        L.sapphire_event_destroy(a)
+        L.sapphire_event_destroy(b)
+
+    # each kernel alone, for the per-kernel table
+    def time_alone(fn, iters=20):
+        tt = Timer(stream)
+        tt.start()
+        for i in range(iters):
+            fn(i)
+        return tt.stop() / iters
+    q4_ms = time_alone(lambda i: check(L.sapphire_gemv_q_dev(
+        synth.Q4_0, 1, q4[i % n_sets].ptr(1), M_LM, K_LM, dx.ptr, logits.ptr, stream)))
+    sm_ms = time_alone(lambda i: check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream)))
+
+    b8, b4 = gemv_bytes(synth.Q8_0, M_LM, K_LM), gemv_bytes(synth.Q4_0, M_LM, K_LM)
+    b_sm = 2 * 4 * M_LM
+    step_bytes = b8 + b4 + 2 * b_sm
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    achieved = b8 / (q8_ms * 1e-3) / 1e9
+
+    decode = None
+    if args.decode_steps > 0:
+        try:
+            from sapphire_amd.engine import bench_decode
+            decode = bench_decode(args.decode_steps)
+        except ImportError:
+            decode = None
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q8_0/Q4_0 blocks, N(0,1) activations)",
+        "config": {
+            "workload": "lm_head 262144x640: Q8_0 GEMV + softmax/argmax, Q4_0 GEMV + softmax/argmax",
+            "weights_rotated": n_sets, "step_bytes": step_bytes,
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "gemv_q8_0 262144x640",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+        },
+        "kernels": {
+            "gemv_q8_0_lm_head": {"us": round(q8_ms * 1e3, 2), "GB/s": round(achieved, 1),
+                                  "frac_peak": round(achieved / HBM_PEAK_GBS, 4)},
+            "gemv_q4_0_lm_head": {"us": round(q4_ms * 1e3, 2), "GB/s": round(b4 / (q4_ms * 1e-3) / 1e9, 1),
+                                  "frac_peak": round(b4 / (q4_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "softmax_argmax_262144": {"us": round(sm_ms * 1e3, 2)},
+        },
+        "decode": decode,
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(x, w8, w4)
+    print(json.dumps(out), flush=True)
+    L.sapphire_stream_destroy(stream)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -31,8 +31,13 @@ __device__ float sum_sq_ref(const float *__restrict__ in, int dim) {
     return sum;
 }
 
+// Correctly rounded fp32 square root. The fp32 sqrt lowers to v_sqrt_f32 (about 1 ulp);
+// the fp64 one is Newton-refined with FMAs, and rounding its result to fp32 is exact-
+// rounding safe because 53 >= 2*24 + 2.
+__device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt((double)a); }
+
 __device__ __forceinline__ float rms_inv_of(float ss, int dim, float eps) {
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)dim), eps)));
+    return __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)dim), eps)));
 }
 
 // Eight lanes each run one sequential chain so the loads of the eight chains overlap.
