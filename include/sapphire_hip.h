@@ -17,6 +17,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "tensor.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -80,6 +82,13 @@ int sapphire_gemv_f_dev(int dtype, const void *w, int M, int K, const float *x, 
  * greedy token (utils.c:145-156: first index of the maximum) written to *argmax_dev.
  * probs may be NULL to compute only the argmax. */
 int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *argmax_dev, void *stream);
+
+/* ---- device copies of tensor_t weights ----
+ * The device-resident copy kernel_gemv keeps for a 2-D weight tensor (Q4_0/Q8_0 in the
+ * PACKED layout, F32/BF16 as is), created on first use; *layout receives its layout.
+ * NULL on error. sapphire_tensor_invalidate drops it (call after changing host data). */
+const void *sapphire_tensor_device_data(const tensor_t *t, int *layout, void *stream);
+int sapphire_tensor_invalidate(tensor_t *t);
 
 /* ---- primitives on device vectors ---- */
 /* out[b] = rmsnorm_delta(in[b]) for b < batch, rows of length dim (normalization.c:104-117). */

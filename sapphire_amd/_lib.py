@@ -25,7 +25,9 @@ def load_library(path: str):
         raise RuntimeError(
             f"{path} is missing: build it with `python -m sapphire_amd.build` "
             "(there is no CPU fallback for the HIP path)")
-    lib = C.CDLL(path, mode=C.RTLD_GLOBAL)
+    # RTLD_LOCAL: the library exports the reference's own C API names, so it must not
+    # interpose on another library of that API loaded into the same process.
+    lib = C.CDLL(path, mode=C.RTLD_LOCAL)
     P = lambda n, r, a: _proto(lib, n, r, a)  # noqa: E731
     # sapphire_hip.h
     P("sapphire_last_error", C.c_char_p, [])

@@ -128,3 +128,18 @@ def synthetic_model(cfg: DecodeConfig, seed: int) -> SyntheticModel:
 
 def start_token(cfg: DecodeConfig, seed: int) -> int:
     return int(synth.rng(seed, 999).integers(0, cfg.vocab))
+
+
+def model_digest(m: SyntheticModel, k_cache: np.ndarray = None, v_cache: np.ndarray = None) -> str:
+    """sha256 over every input array of a synthetic model (and optional KV caches), to
+    detect a change of the generator behind a seed."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in PROJ:
+        h.update(np.ascontiguousarray(m.weights[name]).tobytes())
+    for name in sorted(m.norms):
+        h.update(np.ascontiguousarray(m.norms[name]).tobytes())
+    for a in (m.embed_bf16, m.norm_final, m.lm_head, k_cache, v_cache):
+        if a is not None:
+            h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()

@@ -1,0 +1,227 @@
+"""Writes the golden fixtures of this directory from the compiled reference.
+
+The reference engine is compiled from its own C sources by ``make -C oracle ref``
+into oracle/_ref/libsapphire_ref.so (and oracle/_ref/libref_decode.so for the decode
+loop). This script calls it on fixed inputs and stores inputs and outputs (as fp32
+bit patterns) so that the oracle can be pinned where the reference tree is absent.
+
+    make -C oracle ref && python tests/golden/make_golden.py
+
+Fixtures:
+  known_answers.json  the reference's own known-answer cases: test_dispatch.c:6-29 and
+                      the sum(y) of bench_sapphire_end_to_end.c:76-110,166-173
+  gemv.npz            seeded Q4_0/Q8_0 pooled kernel_gemv at small shapes (dispatch.c:101)
+  primitives.npz      rmsnorm(_delta), rope tables + rotation, gelu, geglu, softcap,
+                      softmax, sample_greedy, vec_dot
+  decode_tiny.json    greedy decode of a 3-layer Gemma-3-shaped model (tokens + logits
+                      digests), generated from a recorded seed with a recorded input digest
+"""
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle.oracle import Reference, ref_decode  # noqa: E402
+from sapphire_amd import model as smodel  # noqa: E402
+from sapphire_amd import synth  # noqa: E402
+
+Q4, Q8 = synth.Q4_0, synth.Q8_0
+
+
+def f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def aligned32(a):
+    """Copy of a float32 vector at a 32-byte aligned address (the reference's aligned
+    row kernels use aligned AVX loads)."""
+    a = np.ascontiguousarray(a, np.float32)
+    buf = np.empty(a.size + 8, np.float32)
+    off = (-buf.ctypes.data % 32) // 4
+    out = buf[off:off + a.size]
+    out[:] = a
+    assert out.ctypes.data % 32 == 0
+    return out
+
+
+def p(a):
+    return C.c_void_p(a.ctypes.data)
+
+
+# --------------------------------------------------------------------------------------
+# Inputs of the reference's own known-answer cases
+# --------------------------------------------------------------------------------------
+def dispatch_row():
+    """test_dispatch.c:6-29: 4 Q4_0 blocks, scale 0.05(1+b), q[i] = ((i+1)&15)<<4 | i."""
+    W = np.zeros(4, synth.Q4_BLOCK)
+    for b in range(4):
+        W[b]["scale"] = np.float32(0.05) * np.float32(1.0 + b)
+        W[b]["q"] = [(((i + 1) & 0x0F) << 4) | (i & 0x0F) for i in range(16)]
+    x = (np.float32(0.001) * np.arange(1, 129, dtype=np.float32)).astype(np.float32)
+    return W, x
+
+
+def e2e_matrices(rows, bpr):
+    """bench_sapphire_end_to_end.c:76-95 (Q4_0) and :166-173 (Q8_0)."""
+    r = np.arange(rows)[:, None]
+    b = np.arange(bpr)[None, :]
+    sc = (np.float32(0.01) * (1.0 + ((r + b) & 7)).astype(np.float32)).astype(np.float32)
+    W4 = np.zeros((rows, bpr), synth.Q4_BLOCK)
+    W4["scale"] = sc
+    i = np.arange(16)[None, None, :]
+    lo = (i * 2 + 0 + r[..., None] + b[..., None]) & 0x0F
+    hi = (i * 2 + 1 + r[..., None] + b[..., None]) & 0x0F
+    W4["q"] = ((hi << 4) | lo).astype(np.uint8)
+    W8 = np.zeros((rows, bpr), synth.Q8_BLOCK)
+    W8["scale"] = sc
+    i = np.arange(32)[None, None, :]
+    W8["q"] = (((i + r[..., None] + b[..., None]) & 0x1F) - 16).astype(np.int8)
+    x = (np.float32(0.001) * np.arange(1, bpr * 32 + 1, dtype=np.float32)).astype(np.float32)
+    return W4, W8, x
+
+
+E2E_CONFIGS = [(64, 2), (128, 4), (256, 8), (1024, 16), (8192, 32)]
+GEMV_SHAPES = [(64, 256), (33, 96), (17, 640), (5, 2048), (3, 32), (9, 1152)]
+
+
+def main():
+    if not Reference.available():
+        sys.exit("oracle/_ref is not built: run `make -C oracle ref` first")
+    ref = Reference()
+    L = ref.lib
+    L.sapphire_geglu.restype = C.c_int
+    L.sapphire_geglu.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+    L.vec_softcap.argtypes = [C.c_void_p, C.c_int, C.c_float]
+
+    # ---- known answers ----
+    W, x = dispatch_row()
+    known = {
+        "dispatch_row": {
+            "source": "src/test/test_dispatch.c:6-29",
+            "unaligned_bits": int(ref.row(Q4, W, x).view(np.uint32)),
+            "aligned_bits": int(ref.row(Q4, W, aligned32(x), aligned=True).view(np.uint32)),
+            "printed": "-0.08400002",
+        },
+        "e2e_sums": [],
+    }
+    for rows, bpr in E2E_CONFIGS:
+        W4, W8, xe = e2e_matrices(rows, bpr)
+        y4 = ref.gemv(Q4, W4, xe, nthreads=4)
+        y8 = ref.gemv(Q8, W8, xe, nthreads=4)
+        known["e2e_sums"].append({
+            "rows": rows, "blocks_per_row": bpr,
+            "q4_sum": float(np.sum(y4.astype(np.float64))), "q8_sum": float(np.sum(y8.astype(np.float64))),
+            "q4_y_sha256": hashlib.sha256(y4.tobytes()).hexdigest(),
+            "q8_y_sha256": hashlib.sha256(y8.tobytes()).hexdigest(),
+        })
+    with open(os.path.join(HERE, "known_answers.json"), "w") as f:
+        json.dump(known, f, indent=1)
+
+    # ---- seeded GEMVs ----
+    g = {}
+    for dt in (Q4, Q8):
+        for (m, k) in GEMV_SHAPES:
+            Wm = synth.quant_matrix(dt, m, k, 1234, m * 31 + k)
+            xv = synth.normal_f32(k, 1234, 7 + k)
+            y1 = ref.gemv(dt, Wm, xv, nthreads=1)
+            y3 = ref.gemv(dt, Wm, xv, nthreads=3)
+            assert np.array_equal(y1.view(np.uint32), y3.view(np.uint32))
+            key = f"{synth.DTYPE_NAME[dt]}_{m}x{k}"
+            g[key + "_w"] = synth.as_bytes(Wm)
+            g[key + "_x"] = xv
+            g[key + "_y"] = y1
+    np.savez_compressed(os.path.join(HERE, "gemv.npz"), **g)
+
+    # ---- primitives ----
+    pr = {}
+    for dim in (640, 256, 1152, 7, 1001):
+        xv = f32(synth.normal_f32(dim, 55, dim) * 3)
+        wv = f32(synth.normal_f32(dim, 55, dim + 1, 1.0, 0.1))
+        for name in ("rmsnorm", "rmsnorm_delta"):
+            out = np.empty(dim, np.float32)
+            assert getattr(L, name)(p(out), p(xv), p(wv), C.c_float(1e-6), dim) == 0
+            pr[f"{name}_{dim}_out"] = out
+        pr[f"rms_{dim}_x"] = xv
+        pr[f"rms_{dim}_w"] = wv
+    rope_pos = np.array([0, 1, 7, 511, 1024, 2047], np.int32)
+    pr["rope_pos"] = rope_pos
+    for base in (10000.0, 1000000.0):
+        hd, ctx = 256, 2048
+        c = np.empty(ctx * hd, np.float32)
+        s = np.empty(ctx * hd, np.float32)
+        assert L.rope_precompute_freqs(p(c), p(s), hd, ctx, C.c_float(base)) == 0
+        tag = f"rope_{int(base)}"
+        pr[tag + "_cos_rows"] = c.reshape(ctx, hd)[rope_pos]
+        pr[tag + "_sin_rows"] = s.reshape(ctx, hd)[rope_pos]
+        pr[tag + "_cos_sha256"] = np.frombuffer(hashlib.sha256(c.tobytes()).digest(), np.uint8)
+        pr[tag + "_sin_sha256"] = np.frombuffer(hashlib.sha256(s.tobytes()).digest(), np.uint8)
+        xh = f32(synth.normal_f32((len(rope_pos), hd), 56, int(base) % 1000))
+        outs = []
+        for j, pos in enumerate(rope_pos):
+            v = xh[j].copy()
+            L.rope_apply_fast(p(v), int(pos), hd, p(c), p(s))
+            outs.append(v)
+        pr[tag + "_x"] = xh
+        pr[tag + "_out"] = np.stack(outs)
+    gx = f32(np.concatenate([np.linspace(-12, 12, 2001, dtype=np.float32), synth.normal_f32(999, 57, 1) * 3,
+                             np.array([0.0, -0.0, 1e-30, -1e-30, 30.0, -30.0], np.float32)]))
+    pr["gelu_x"] = gx
+    pr["gelu_out"] = f32([L.gelu(C.c_float(v)) for v in gx])
+    gi = gx.copy()
+    L.gelu_inplace(p(gi), gi.shape[0])
+    pr["gelu_inplace_out"] = gi
+    gin = f32(synth.normal_f32(2 * 777, 58, 1) * 2)
+    gout = np.empty(777, np.float32)
+    assert L.sapphire_geglu(p(gout), p(gin), gin.shape[0]) == 0
+    pr["geglu_in"], pr["geglu_out"] = gin, gout
+    sc = f32(np.array([-100, -31, -1, 0, 1, 29.9, 100, 3.5, -7.25], np.float32))
+    sco = sc.copy()
+    L.vec_softcap(p(sco), sco.shape[0], C.c_float(30.0))
+    pr["softcap_in"], pr["softcap_out"] = sc, sco
+    for n in (1, 5, 8, 13, 1000, 1087):
+        v = f32(synth.normal_f32(n, 59, n) * 4)
+        if n > 10:
+            v[n // 3] = v[n // 2] = v.max() + 1.0
+        o = v.copy()
+        L.softmax(p(o), n)
+        pr[f"softmax_{n}_in"], pr[f"softmax_{n}_out"] = v, o
+        pr[f"greedy_{n}"] = np.array([L.sample_greedy(p(v), n)], np.int32)
+    for n in (256, 255, 7, 640):
+        a = f32(synth.normal_f32(n, 60, n))
+        b = f32(synth.normal_f32(n, 61, n))
+        pr[f"dot_{n}_a"], pr[f"dot_{n}_b"] = a, b
+        pr[f"dot_{n}_out"] = np.array([L.vec_dot(p(a), p(b), n)], np.float32)
+    np.savez_compressed(os.path.join(HERE, "primitives.npz"), **pr)
+
+    # ---- tiny decode ----
+    cfg, seed, steps, n_prefill = smodel.TINY, 4242, 8, 40
+    mdl = smodel.synthetic_model(cfg, seed)
+    k, v = mdl.kv_prefill(n_prefill)
+    tok0 = smodel.start_token(cfg, seed)
+    digest = smodel.model_digest(mdl, k, v)
+    toks, logits = ref_decode(mdl, k, v, tok0, n_prefill, steps, keep_logits=True)
+    dec = {
+        "config": "TINY", "seed": seed, "steps": steps, "prefill": n_prefill, "start_token": tok0,
+        "input_sha256": digest,
+        "tokens": [int(t) for t in toks],
+        "logits_sha256": [hashlib.sha256(l.tobytes()).hexdigest() for l in logits],
+        "logits_first_bits": [int(b) for b in logits[0][:64].view(np.uint32)],
+        "logits_last_bits": [int(b) for b in logits[-1][:64].view(np.uint32)],
+    }
+    with open(os.path.join(HERE, "decode_tiny.json"), "w") as f:
+        json.dump(dec, f, indent=1)
+    ref.close()
+    print("golden fixtures written to", HERE)
+
+
+if __name__ == "__main__":
+    main()

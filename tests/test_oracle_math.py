@@ -1,0 +1,226 @@
+"""The oracle against what the mathematics fixes, independently of the reference build:
+closed forms, exact special cases, float64 brute force, invariants. Each check is chosen
+so that a plausible slip (wrong nibble order, dropped -8 offset, a missing scale, a sign
+or index error, a transposed operand) fails it."""
+import numpy as np
+import pytest
+
+from sapphire_amd import model as smodel
+from sapphire_amd import synth
+
+Q4, Q8 = synth.Q4_0, synth.Q8_0
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_q4_unpack_every_byte(oracle):
+    """Every byte value in every position: element 2j is the low nibble of byte j minus
+    8, element 2j+1 the high nibble minus 8 (bench_q4.c:26-32 scalar form)."""
+    W = np.zeros(16, synth.Q4_BLOCK)
+    allb = np.arange(256, dtype=np.uint8)
+    for b in range(16):
+        W[b]["q"] = allb[16 * b:16 * b + 16]
+        W[b]["scale"] = 1.0
+    ints = oracle.unpack_ints(Q4, W).reshape(16, 32)
+    for b in range(16):
+        for j in range(16):
+            byte = 16 * b + j
+            assert ints[b, 2 * j] == (byte & 15) - 8 and ints[b, 2 * j + 1] == (byte >> 4) - 8
+
+
+def test_q8_unpack_every_byte(oracle):
+    W = np.zeros(8, synth.Q8_BLOCK)
+    W["q"] = np.arange(256, dtype=np.uint8).view(np.int8).reshape(8, 32)
+    ints = oracle.unpack_ints(Q8, W)
+    assert np.array_equal(ints.astype(np.int32), np.arange(256, dtype=np.uint8).view(np.int8).astype(np.int32))
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8])
+def test_dequant_is_one_rounded_product(oracle, dtype):
+    W = synth.quant_matrix(dtype, 64, 256, 1, 1)
+    ints = synth.unpack_ints(dtype, W).reshape(64, 8, 32).astype(np.float64)
+    want = (ints * W["scale"][..., None].astype(np.float64)).astype(np.float32)   # fl(exact product)
+    assert np.array_equal(bits(oracle.dequant(dtype, W)), bits(want.reshape(-1)))
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8])
+@pytest.mark.parametrize("k", [32, 96, 640, 2048])
+def test_gemv_exact_case_matches_exact_arithmetic(oracle, dtype, k):
+    """Power-of-two scales and small-integer x: every product and partial sum is exact,
+    so the fp32 result must equal the exact integer dot product bit for bit."""
+    m = 50
+    W = synth.quant_matrix(dtype, m, k, 2, k)
+    g = synth.rng(2, k + 1)
+    W["scale"] = np.ldexp(1.0, -g.integers(0, 6, size=W["scale"].shape)).astype(np.float32)
+    x = g.integers(-3, 4, size=k).astype(np.float32)
+    ints = synth.unpack_ints(dtype, W).astype(np.float64).reshape(m, k // 32, 32)
+    exact = np.einsum("mbe,mb,be->m", ints, W["scale"].astype(np.float64), x.reshape(-1, 32).astype(np.float64))
+    assert np.array_equal(bits(oracle.gemv(dtype, W, x)), bits(exact.astype(np.float32)))
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8])
+def test_gemv_float64_brute_force(oracle, dtype):
+    m, k = 300, 640
+    W = synth.quant_matrix(dtype, m, k, 3, 1)
+    x = synth.normal_f32(k, 3, 2)
+    deq = synth.unpack_ints(dtype, W).astype(np.float64).reshape(m, -1, 32) * W["scale"][..., None]
+    want = deq.reshape(m, k) @ x.astype(np.float64)
+    got = oracle.gemv(dtype, W, x).astype(np.float64)
+    scale = np.abs(deq.reshape(m, k)) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-7)
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8])
+def test_gemv_invariants(oracle, dtype):
+    m, k = 97, 640
+    W = synth.quant_matrix(dtype, m, k, 4, 1)
+    x = synth.normal_f32(k, 4, 2)
+    y = oracle.gemv(dtype, W, x)
+    assert np.array_equal(bits(oracle.gemv(dtype, W, 4.0 * x)), bits(4.0 * y))            # power-of-2 linearity
+    W2 = W.copy()
+    W2["scale"] *= np.float32(0.5)
+    assert np.array_equal(bits(oracle.gemv(dtype, W2, x)), bits(0.5 * y))                  # scale linearity
+    perm = synth.rng(4, 3).permutation(m)
+    assert np.array_equal(bits(oracle.gemv(dtype, W[perm], x)), bits(y[perm]))              # row permutation
+    W3 = W.copy()
+    W3["scale"][5] = 0.0
+    assert np.all(oracle.gemv(dtype, W3, x)[5] == 0.0)                                      # zero scale
+
+
+@pytest.mark.parametrize("dim", [7, 256, 640, 1152])
+def test_rmsnorm_float64(oracle, dim):
+    x = synth.normal_f32(dim, 5, dim) * 3
+    w = synth.normal_f32(dim, 5, dim + 1, 1.0, 0.1)
+    x64 = x.astype(np.float64)
+    r = 1.0 / np.sqrt(np.mean(x64 * x64) + 1e-6)
+    assert np.allclose(oracle.rmsnorm_delta(x, w), x64 * r * (1.0 + w), rtol=2e-6, atol=0)
+    assert np.allclose(oracle.rmsnorm(x, w), x64 * r * w, rtol=2e-6, atol=0)
+
+
+def test_rope_properties(oracle):
+    hd = 256
+    for base in (1e4, 1e6):
+        c, s = oracle.rope_tables(hd, 2048, base)
+        x = synth.normal_f32(hd, 6, int(base) % 13)
+        assert np.array_equal(bits(oracle.rope_apply(x, 0, c, s)), bits(x))                  # pos 0: identity
+        for pos in (1, 100, 2047):
+            y = oracle.rope_apply(x, pos, c, s).astype(np.float64)
+            half = hd // 2
+            ang = pos * (1.0 / np.power(base, 2.0 * np.arange(half) / hd))
+            x0, x1 = x[:half].astype(np.float64), x[half:].astype(np.float64)
+            want = np.concatenate([x0 * np.cos(ang) - x1 * np.sin(ang), x1 * np.cos(ang) + x0 * np.sin(ang)])
+            # fp32 angles at pos up to 2047 carry ~pos*ulp error: loose absolute bound
+            assert np.allclose(y, want, atol=2e-3 * max(1, pos / 64), rtol=0)
+            n_in = x0 * x0 + x1 * x1
+            n_out = y[:half] ** 2 + y[half:] ** 2
+            assert np.allclose(n_in, n_out, rtol=1e-5, atol=1e-6)                             # pair norms kept
+
+
+def test_gelu_float64(oracle):
+    x = np.concatenate([np.linspace(-10, 10, 4001), synth.normal_f32(1000, 7, 1) * 3]).astype(np.float32)
+    x64 = x.astype(np.float64)
+    want = 0.5 * x64 * (1 + np.tanh(np.sqrt(2 / np.pi) * (x64 + 0.044715 * x64 ** 3)))
+    got = np.array([oracle.lib.oracle_gelu(float(v)) for v in x], np.float64)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+    up = synth.normal_f32(x.shape[0], 7, 2)
+    assert np.allclose(oracle.gelu_mul(x, up), want * up, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n", [1, 9, 1000, 262144])
+def test_softmax_and_argmax(oracle, n):
+    x = synth.normal_f32(n, 8, n) * 5
+    p = oracle.softmax(x).astype(np.float64)
+    e = np.exp(x.astype(np.float64) - x.max())
+    # utils.c:43-46 sums exp() left to right in fp32: terms below half an ulp of the running
+    # sum are dropped, so the normaliser is only accurate to about n * 2^-24 relative
+    assert np.allclose(p, e / e.sum(), rtol=1e-5 + n * 2.0 ** -24, atol=1e-9)
+    seq = np.cumsum(e.astype(np.float32), dtype=np.float32)[-1]       # the same left-to-right sum
+    assert abs(1.0 / p.max() * np.exp(0.0) - seq) <= 1e-5 * seq
+    assert abs(p.sum() - 1.0) < 1e-5 + n * 2.0 ** -24
+    assert oracle.argmax(x) == int(np.argmax(x))
+    if n > 3:
+        x[n - 1] = x[1] = x.max() + 2.0                       # tie: the lowest index wins
+        assert oracle.argmax(x) == 1
+
+
+def _np_decode_step(m, k_cache, v_cache, token, pos):
+    """An independent float64 restatement of one decode step (the composition of
+    inference.c:616-651, attention.c:311-375, transformer.c:96-283,393-408)."""
+    c = m.cfg
+    H, hd, nq = c.hidden, c.head_dim, c.n_heads
+    ints = {n: synth.unpack_ints(c.wdtype, m.weights[n]).astype(np.float64) for n in smodel.PROJ}
+
+    def proj(name, l, x):
+        w = m.weights[name][l]
+        deq = ints[name][l].reshape(w.shape[0], -1, 32) * w["scale"][..., None]
+        return deq.reshape(w.shape[0], -1) @ x
+
+    def norm(x, w):
+        return x / np.sqrt(np.mean(x * x) + 1e-6) * (1.0 + w)
+
+    def gelu(v):
+        return 0.5 * v * (1 + np.tanh(0.7978845608 * (v + 0.044715 * v ** 3)))
+
+    emb = (m.embed_bf16[token].astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    h = emb * np.sqrt(np.float32(H))
+    for l in range(c.n_layers):
+        glob = c.is_global(l)
+        base = c.rope_theta if glob else c.rope_local_base
+        half = hd // 2
+        ang = pos * (1.0 / np.power(base, 2.0 * np.arange(half) / hd))
+        cs, sn = np.cos(ang), np.sin(ang)
+
+        def rope(v):
+            a, b = v[:half].copy(), v[half:].copy()
+            return np.concatenate([a * cs - b * sn, b * cs + a * sn])
+        resid = h.copy()
+        xn = norm(h, m.norms["norm_attn"][l])
+        q = proj("wq", l, xn).reshape(nq, hd)
+        k = proj("wk", l, xn).reshape(c.n_kv_heads, hd)
+        v = proj("wv", l, xn).reshape(c.n_kv_heads, hd)
+        q = np.stack([rope(norm(q[i], m.norms["q_norm"][l])) for i in range(nq)])
+        k = np.stack([rope(norm(k[i], m.norms["k_norm"][l])) for i in range(c.n_kv_heads)])
+        k_cache[l, :, pos] = k
+        v_cache[l, :, pos] = v
+        seq = pos + 1
+        start = seq - c.sliding_window if (not glob and seq > c.sliding_window) else 0
+        out = np.zeros((nq, hd))
+        for i in range(nq):
+            kv = i // (nq // c.n_kv_heads)
+            sc = k_cache[l, kv, start:seq].astype(np.float64) @ q[i] / np.sqrt(c.query_pre_attn_scalar)
+            p = np.exp(sc - sc.max())
+            p /= p.sum()
+            out[i] = p @ v_cache[l, kv, start:seq].astype(np.float64)
+        h = proj("wo", l, out.reshape(-1))
+        resid = resid + norm(h, m.norms["norm_attn_post"][l])
+        xn = norm(resid, m.norms["norm_ffn"][l])
+        g = gelu(proj("wgate", l, xn)) * proj("wup", l, xn)
+        h = proj("wdown", l, g)
+        resid = resid + norm(h, m.norms["norm_ffn_post"][l])
+        h = resid
+    xn = norm(h, m.norm_final)
+    lm = m.lm_head
+    deq = synth.unpack_ints(c.lm_dtype, lm).astype(np.float64).reshape(lm.shape[0], -1, 32) * lm["scale"][..., None]
+    return deq.reshape(lm.shape[0], -1) @ xn
+
+
+def test_decode_step_float64(oracle):
+    """The oracle's decode composition against an independent float64 restatement: a
+    dropped norm, residual, window or RoPE term moves the logits far beyond rounding."""
+    from oracle.oracle import oracle_decode
+    cfg = smodel.TINY
+    m = smodel.synthetic_model(cfg, 31)
+    k, v = m.kv_prefill(40)
+    k64, v64 = k.astype(np.float64), v.astype(np.float64)
+    tok = smodel.start_token(cfg, 31)
+    toks, logits = oracle_decode(oracle, m, k, v, tok, 40, 3, keep_logits=True)
+    t = tok
+    for s in range(3):
+        want = _np_decode_step(m, k64, v64, t, 40 + s)
+        got = logits[s].astype(np.float64)
+        err = np.abs(got - want).max() / np.abs(want).max()
+        assert err < 2e-4, f"step {s}: relative error {err}"
+        t = int(np.argmax(want))
+        assert t == toks[s]

@@ -1,0 +1,121 @@
+"""The oracle against the reference engine compiled from its own sources (oracle/_ref),
+bit for bit, on seeded inputs at the workload shapes. Skipped where oracle/_ref was not
+built (it is built by `make -C oracle ref` wherever the reference tree exists)."""
+import numpy as np
+import pytest
+
+from oracle.oracle import Reference, oracle_decode, ref_decode, ref_decode_available
+from sapphire_amd import model as smodel
+from sapphire_amd import synth
+
+pytestmark = pytest.mark.skipif(not Reference.available(), reason="oracle/_ref not built")
+
+Q4, Q8 = synth.Q4_0, synth.Q8_0
+
+
+@pytest.fixture(scope="module")
+def ref():
+    r = Reference()
+    yield r
+    r.close()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def aligned32(a):
+    buf = np.empty(a.size + 8, np.float32)
+    off = (-buf.ctypes.data % 32) // 4
+    out = buf[off:off + a.size]
+    out[:] = a
+    return out
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("nb", [1, 2, 3, 20, 21, 32, 36, 64, 216])
+def test_row_kernels(oracle, ref, dtype, nb):
+    """Both row kernels, aligned and unaligned x, including odd block counts (the
+    Q4_0 odd-tail bank, q4_0_avx.c:118-120)."""
+    W = synth.quant_matrix(dtype, 8, nb * 32, 77, nb)
+    for r in range(8):
+        x = synth.normal_f32(nb * 32, 77, 1000 + r)
+        want = oracle.row(dtype, W[r], x)
+        assert bits(ref.row(dtype, W[r], x)) == bits(want)
+        assert bits(ref.row(dtype, W[r], aligned32(x), aligned=True)) == bits(want)
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("shape", [(2048, 640), (640, 2048), (1024, 640), (256, 640), (640, 1024),
+                                   (333, 1152), (96, 6912)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_pooled_gemv(oracle, ref, dtype, shape):
+    m, k = shape
+    W = synth.quant_matrix(dtype, m, k, 78, m + k)
+    x = synth.normal_f32(k, 78, k)
+    want = oracle.gemv(dtype, W, x, nthreads=4)
+    for nt in (1, 8):
+        assert np.array_equal(bits(ref.gemv(dtype, W, x, nthreads=nt)), bits(want))
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8], ids=["q4_0", "q8_0"])
+def test_lm_head_gemv(oracle, ref, dtype):
+    W = synth.quant_matrix(dtype, 262144, 640, 79, dtype)
+    x = synth.normal_f32(640, 79, 1)
+    assert np.array_equal(bits(ref.gemv(dtype, W, x, nthreads=8)), bits(oracle.gemv(dtype, W, x, nthreads=8)))
+
+
+def test_primitives_random(oracle, ref):
+    import ctypes as C
+    L = ref.lib
+    p = lambda a: C.c_void_p(a.ctypes.data)  # noqa: E731
+    for dim in (1, 8, 9, 255, 640, 6912):
+        x = synth.normal_f32(dim, 80, dim) * 10
+        w = synth.normal_f32(dim, 81, dim, 1.0, 0.1)
+        for name in ("rmsnorm", "rmsnorm_delta"):
+            out = np.empty(dim, np.float32)
+            assert getattr(L, name)(p(out), p(x), p(w), C.c_float(1e-6), dim) == 0
+            assert np.array_equal(bits(out), bits(getattr(oracle, name)(x, w)))
+        s = x.copy()
+        L.softmax(p(s), dim)
+        assert np.array_equal(bits(s), bits(oracle.softmax(x)))
+        assert L.sample_greedy(p(x), dim) == oracle.argmax(x)
+        y = synth.normal_f32(dim, 82, dim)
+        assert bits(np.float32(L.vec_dot(p(x), p(y), dim))) == bits(
+            np.float32(oracle.lib.oracle_vec_dot(x.ctypes.data, y.ctypes.data, dim)))
+    for base in (10000.0, 1000000.0):
+        hd, ctx = 64, 300
+        c = np.empty(ctx * hd, np.float32)
+        s = np.empty(ctx * hd, np.float32)
+        L.rope_precompute_freqs(p(c), p(s), hd, ctx, C.c_float(base))
+        oc, os_ = oracle.rope_tables(hd, ctx, base)
+        assert np.array_equal(bits(c), bits(oc)) and np.array_equal(bits(s), bits(os_))
+        for pos in (0, 3, 299):
+            xv = synth.normal_f32(hd, 83, pos)
+            r = xv.copy()
+            L.rope_apply_fast(p(r), pos, hd, p(c), p(s))
+            assert np.array_equal(bits(r), bits(oracle.rope_apply(xv, pos, oc, os_)))
+    g = synth.normal_f32(4096, 84, 1) * 4
+    assert np.array_equal(bits(np.array([L.gelu(float(v)) for v in g], np.float32)),
+                          bits(np.array([oracle.lib.oracle_gelu(float(v)) for v in g], np.float32)))
+
+
+MID = smodel.DecodeConfig(n_layers=6, hidden=256, n_heads=4, n_kv_heads=1, head_dim=128, ffn=512,
+                          vocab=8192, max_ctx=160, sliding_window=48, global_layers=(5,))
+
+
+@pytest.mark.skipif(not ref_decode_available(), reason="oracle/_ref decode harness not built")
+@pytest.mark.parametrize("cfg,seed,prefill,steps", [(smodel.TINY, 5, 30, 12), (MID, 6, 100, 10)],
+                         ids=["tiny", "mid"])
+def test_decode_matches_reference(oracle, cfg, seed, prefill, steps):
+    """Greedy decode through the reference's own session/layer functions against the
+    oracle's decode step: tokens, logits and the updated KV cache bit for bit. The
+    prefill crosses the sliding window so the local-layer window path is exercised."""
+    m = smodel.synthetic_model(cfg, seed)
+    k1, v1 = m.kv_prefill(prefill)
+    k2, v2 = k1.copy(), v1.copy()
+    tok = smodel.start_token(cfg, seed)
+    t_ref, l_ref = ref_decode(m, k1, v1, tok, prefill, steps, keep_logits=True)
+    t_orc, l_orc = oracle_decode(oracle, m, k2, v2, tok, prefill, steps, keep_logits=True)
+    assert list(t_ref) == list(t_orc)
+    assert np.array_equal(bits(l_ref), bits(l_orc))
+    assert np.array_equal(bits(k1), bits(k2)) and np.array_equal(bits(v1), bits(v2))
