@@ -104,8 +104,9 @@ def main() -> int:
     w4 = synth.quant_matrix(synth.Q4_0, M_LM, K_LM, seed, 2)
     x = synth.normal_f32(K_LM, seed, 3)
     n_sets = 2
-    q8 = [QMatrix(synth.Q8_0, w8) for _ in range(n_sets)]
-    q4 = [QMatrix(synth.Q4_0, w4) for _ in range(n_sets)]
+    LAY = 2   # TILED: the matrix-core layout kernel_gemv uses for matrices this long
+    q8 = [QMatrix(synth.Q8_0, w8, layout=LAY) for _ in range(n_sets)]
+    q4 = [QMatrix(synth.Q4_0, w4, layout=LAY) for _ in range(n_sets)]
     dx = DeviceArray.from_numpy(x)
     logits = DeviceArray.empty(M_LM)
     probs = DeviceArray.empty(M_LM)
@@ -116,11 +117,11 @@ def main() -> int:
         s = i % n_sets
         if t8 is not None:
             L.sapphire_event_record(t8[0], stream)
-        check(L.sapphire_gemv_q_dev(synth.Q8_0, 1, q8[s].ptr(1), M_LM, K_LM, dx.ptr, logits.ptr, stream))
+        check(L.sapphire_gemv_q_dev(synth.Q8_0, LAY, q8[s].ptr(), M_LM, K_LM, dx.ptr, logits.ptr, stream))
         if t8 is not None:
             L.sapphire_event_record(t8[1], stream)
         check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream))
-        check(L.sapphire_gemv_q_dev(synth.Q4_0, 1, q4[s].ptr(1), M_LM, K_LM, dx.ptr, logits.ptr, stream))
+        check(L.sapphire_gemv_q_dev(synth.Q4_0, LAY, q4[s].ptr(), M_LM, K_LM, dx.ptr, logits.ptr, stream))
         check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream))
 
     for i in range(args.warmup):
@@ -153,7 +154,7 @@ def main() -> int:
             fn(i)
         return tt.stop() / iters
     q4_ms = time_alone(lambda i: check(L.sapphire_gemv_q_dev(
-        synth.Q4_0, 1, q4[i % n_sets].ptr(1), M_LM, K_LM, dx.ptr, logits.ptr, stream)))
+        synth.Q4_0, LAY, q4[i % n_sets].ptr(), M_LM, K_LM, dx.ptr, logits.ptr, stream)))
     sm_ms = time_alone(lambda i: check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream)))
 
     b8, b4 = gemv_bytes(synth.Q8_0, M_LM, K_LM), gemv_bytes(synth.Q4_0, M_LM, K_LM)

@@ -32,8 +32,12 @@ enum { SAPPHIRE_F32 = 0, SAPPHIRE_BF16 = 1, SAPPHIRE_F16 = 2, SAPPHIRE_Q4_0 = 3,
  *  PACKED : the same quants and scales split in two planes, built by
  *           sapphire_q_repack_dev: quants [M][nb][16|32] bytes (byte order of the
  *           reference block), then, at offset sapphire_q_scales_offset(), fp32
- *           scales [M][nb]. Values are bit-identical; only their placement differs. */
-enum { SAPPHIRE_LAYOUT_AOS = 0, SAPPHIRE_LAYOUT_PACKED = 1 };
+ *           scales [M][nb]. Values are bit-identical; only their placement differs.
+ *  TILED  : the matrix-core layout of long matrices (K/128 in {5, 8, 9}): 16-row tiles,
+ *           4-block groups, each group's quants stored in the order the MFMA operand
+ *           registers of a wave take them (one contiguous KiB per load instruction),
+ *           then fp32 scales [tile][group][block][row]. Rows past M are zero. */
+enum { SAPPHIRE_LAYOUT_AOS = 0, SAPPHIRE_LAYOUT_PACKED = 1, SAPPHIRE_LAYOUT_TILED = 2 };
 
 const char *sapphire_last_error(void);
 const char *sapphire_version(void);
@@ -63,6 +67,10 @@ size_t sapphire_q_packed_bytes(int dtype, int M, int K);
 size_t sapphire_q_scales_offset(int dtype, int M, int K);
 /* AOS -> PACKED (both on device). */
 int sapphire_q_repack_dev(int dtype, const void *w_aos, int M, int K, void *w_packed, void *stream);
+/* Bytes of an M x K matrix in `layout` (0 if the layout cannot hold it), and the
+ * conversion of an on-device AOS array into PACKED or TILED. */
+size_t sapphire_q_layout_bytes(int dtype, int layout, int M, int K);
+int sapphire_q_convert_dev(int dtype, const void *w_aos, int M, int K, int layout, void *out, void *stream);
 /* Integer weight values (nib-8 or q) of every element, [M][nb*32] int8: the unpack
  * of q4_0_avx.c:61-66 / q8_0_avx.c:45-56. */
 int sapphire_q_unpack_ints_dev(int dtype, int layout, const void *w, int M, int K, int8_t *out, void *stream);

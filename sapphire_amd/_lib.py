@@ -53,6 +53,8 @@ def load_library(path: str):
     P("sapphire_q_packed_bytes", sz, [i32, i32, i32])
     P("sapphire_q_scales_offset", sz, [i32, i32, i32])
     P("sapphire_q_repack_dev", i32, [i32, vp, i32, i32, vp, vp])
+    P("sapphire_q_layout_bytes", sz, [i32, i32, i32, i32])
+    P("sapphire_q_convert_dev", i32, [i32, vp, i32, i32, i32, vp, vp])
     P("sapphire_q_unpack_ints_dev", i32, [i32, i32, vp, i32, i32, vp, vp])
     P("sapphire_q_dequant_dev", i32, [i32, i32, vp, i32, i32, vp, vp])
     P("sapphire_gemv_q_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp])

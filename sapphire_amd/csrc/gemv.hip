@@ -663,14 +663,17 @@ static int launch_unpack(int dt, int layout, const void *w, int M, int K, int8_t
 }
 
 int launch_unpack_ints(int dt, int layout, const void *w, int M, int K, int8_t *out, hipStream_t st) {
+    if (layout == LAYOUT_TILED) return launch_tiled_unpack(dt, w, M, K, out, nullptr, st);
     return launch_unpack(dt, layout, w, M, K, out, nullptr, st);
 }
 
 int launch_dequant(int dt, int layout, const void *w, int M, int K, float *out, hipStream_t st) {
+    if (layout == LAYOUT_TILED) return launch_tiled_unpack(dt, w, M, K, nullptr, out, st);
     return launch_unpack(dt, layout, w, M, K, nullptr, out, st);
 }
 
 int launch_gemv_q(int dt, int layout, const void *w, int M, int K, const float *x, float *y, hipStream_t st) {
+    if (layout == LAYOUT_TILED) return launch_gemv_tiled(dt, w, M, K, x, y, st);
     const int nb = K / kBlock;
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     const size_t so = q_scales_offset(dt, M, K);
@@ -683,6 +686,11 @@ int launch_gemv_q(int dt, int layout, const void *w, int M, int K, const float *
 
 int launch_gemm_q(int dt, int layout, const void *w, int M, int K, const float *X, float *Y, int batch,
                   hipStream_t st) {
+    if (layout == LAYOUT_TILED) {
+        for (int b = 0; b < batch; ++b)
+            if (launch_gemv_tiled(dt, w, M, K, X + (size_t)b * K, Y + (size_t)b * M, st) != 0) return -1;
+        return 0;
+    }
     const int nb = K / kBlock;
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     const size_t so = q_scales_offset(dt, M, K);

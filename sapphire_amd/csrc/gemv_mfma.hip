@@ -1,0 +1,326 @@
+// gemv_mfma.hip - Q8_0 / Q4_0 GEMV on the CDNA4 matrix cores, for long weight matrices
+// (the LM head: 262144 x 640 and 262144 x 1152).
+//
+// Semantics are those of the reference's kernel_gemv (dispatch.c:101-156 with the row
+// kernels q4_0_avx.c:102-148 / q8_0_avx.c:16-136): y[r] = sum_b scale[r][b] * sum_e
+// int(r, b, e) * x[32b + e], int = (nib - 8) for Q4_0 (element 2j = low nibble of byte j)
+// and the int8 quant for Q8_0.
+//
+// Why the matrix cores. A fp32 GEMV spends two VALU operations per weight (convert +
+// FMA); at 20 bytes per 32 Q4_0 weights that keeps the SIMDs as busy as HBM, and the two
+// phases do not overlap well. Here the integer weights go straight into
+// v_mfma_i32_16x16x32_i8, so the VALU work per block shrinks to applying its scale.
+//
+// x is turned into exact integers once per wave: per 32-element block, X = rint(x*2^sh)
+// with sh chosen so that the block's largest |x| maps below 2^30 (an absolute error
+// <= 2^-31 * max|x_block| per element, below the rounding of fp32 products), and X is
+// split into four signed 8-bit digits, X = sum_d D_d * 256^d. The B operand of the MFMA
+// holds the digits: column n = 4j + d (j = block of a 4-block group, d = digit), so one
+// MFMA per block of the group leaves in C[row][4j+d] the exact integer sum_e int*D_d over
+// block j. Each lane then applies scale[row][block] * 2^(8d - sh) to its four C values
+// with one FMA each, and the sixteen columns of a row are summed across the lanes of a
+// 16-lane row group with ds_swizzle.
+//
+// Weights live in the TILED layout (built by launch_convert), so every load instruction
+// of a wave reads one contiguous KiB:
+//   quants  [tile = 16 rows][group = 4 blocks][..][lane 64][16 B]
+//     Q8_0: two 1 KiB halves per (tile, group); lane l = 16m + i holds, for blocks 2h and
+//           2h+1 of the group, the 8 quants e = 8m..8m+7 of row i (the MFMA A operand).
+//     Q4_0: one 1 KiB slab; lane l holds, for blocks 0..3 of the group, the 4 bytes
+//           4m..4m+3 of row i's block (elements 8m..8m+7), expanded in registers.
+//   scales  [tile][group][block 4][row 16] fp32, after the quants at a 256-byte boundary.
+// Rows past M in the last tile are zero.
+#include <algorithm>
+
+#include "internal.h"
+
+namespace sapphire {
+
+namespace {
+
+constexpr int kWave = 64;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileRows = 16;
+constexpr int kGroupBlocks = 4;
+constexpr int kNT = 2;   // nontemporal: the weights are streamed once
+
+template <int DT> struct TL;
+template <> struct TL<DT_Q4_0> { static constexpr int BB = 20; };   // AoS block bytes
+template <> struct TL<DT_Q8_0> { static constexpr int BB = 36; };
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT));
+}
+
+// Sum over the 16 lanes of a row group (lanes 16m..16m+15), result in every lane.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (8 << 10)));
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (4 << 10)));
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (2 << 10)));
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (1 << 10)));
+    return v;
+}
+
+// The MFMA B operand of this lane for group g (8 signed digits) and the factor
+// 2^(8d - sh) of its column. Lane l supplies column n = l % 16 (block j = n / 4 of the
+// group, digit d = n % 4) for the k-slots of lane group m = l / 16: elements 8m..8m+7 of
+// block 4g + j, in the order the A operand holds them (natural for Q8_0; even then odd
+// elements for Q4_0, whose A bytes are the low nibbles, then the high nibbles).
+template <int DT>
+__device__ __forceinline__ void lane_digits(const float *__restrict__ x, int g, int lane, uint32_t &w0,
+                                            uint32_t &w1, float &p) {
+    const int n = lane & 15, m = lane >> 4;
+    const int j = n >> 2, d = n & 3;
+    const float4 *xp = reinterpret_cast<const float4 *>(x + (4 * g + j) * 32 + 8 * m);
+    const float4 va = xp[0], vb = xp[1];
+    float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+    int mexp = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mexp = max(mexp, (int)((__float_as_uint(v[i]) >> 23) & 0xFFu));
+    // the block's 32 elements are held by lanes n, n+16, n+32, n+48
+    mexp = max(mexp, __shfl_xor(mexp, 16, kWave));
+    mexp = max(mexp, __shfl_xor(mexp, 32, kWave));
+    const int sh = 156 - mexp;   // max |x_block| < 2^(mexp-126), so |X| < 2^30
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int src = DT == DT_Q8_0 ? i : (i < 4 ? 2 * i : 2 * (i - 4) + 1);
+        const int X = (int)rintf(ldexpf(v[src], sh));
+        const uint32_t U = ((uint32_t)X + 0x80808080u) ^ 0x80808080u;   // bytes = signed digits
+        b[i] = (U >> (8 * d)) & 0xFFu;
+    }
+    w0 = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    w1 = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    // Q4_0 A bytes carry 16 * (nib - 8); the 1/16 is folded in here (exact)
+    p = ldexpf(1.0f, 8 * d - sh - (DT == DT_Q4_0 ? 4 : 0));
+}
+
+// A operand of the MFMA for block jj of the group.
+template <int DT>
+__device__ __forceinline__ long a_operand(const u32x4 (&a)[2], int jj) {
+    if constexpr (DT == DT_Q8_0) {
+        const u32x4 h = a[jj >> 1];
+        const uint32_t lo = (jj & 1) ? h.z : h.x, hi = (jj & 1) ? h.w : h.y;
+        return (long)(((unsigned long)hi << 32) | lo);
+    } else {
+        const uint32_t q = a[0][jj] ^ 0x88888888u;   // nibble -> 4-bit two's complement of nib-8
+        const uint32_t even = (q << 4) & 0xF0F0F0F0u;   // int8 16*(nib-8) of elements 0,2,4,6
+        const uint32_t odd = q & 0xF0F0F0F0u;           // ... of elements 1,3,5,7
+        return (long)(((unsigned long)odd << 32) | even);
+    }
+}
+
+// One wave per 16-row tile at a time; waves walk the tiles with a grid stride.
+template <int DT, int NG>
+__global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq, uint32_t q_bytes,
+                                                 const uint8_t *__restrict__ wsc, uint32_t s_bytes,
+                                                 const float *__restrict__ x, float *__restrict__ y, int M,
+                                                 int ntiles) {
+    constexpr int NQ = DT == DT_Q8_0 ? 2 : 1;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int nwaves = gridDim.x * (blockDim.x / kWave);
+    const int n = lane & 15, m = lane >> 4;
+    const int jc = n >> 2;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(wq, q_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(wsc, s_bytes);
+
+    u32x4 a[NG][2];
+    u32x4 sv[NG];
+    auto issue = [&](int t) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const uint32_t gb = (uint32_t)(t * NG + g);
+#pragma unroll
+            for (int h = 0; h < NQ; ++h) a[g][h] = load16(rq, (gb * NQ + h) * 1024u + lane * 16u);
+            sv[g] = load16(rs, ((gb * 4u + jc) * 16u + 4u * m) * 4u);
+        }
+    };
+    int t = wave;
+    if (t < ntiles) issue(t);
+
+    uint32_t d0[NG], d1[NG];
+    float p[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) lane_digits<DT>(x, g, lane, d0[g], d1[g], p[g]);
+
+    for (; t < ntiles; t += nwaves) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            i32x4 C = {0, 0, 0, 0};
+            const long bop = (long)(((unsigned long)d1[g] << 32) | d0[g]);
+#pragma unroll
+            for (int jj = 0; jj < kGroupBlocks; ++jj)
+                C = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_operand<DT>(a[g], jj), jc == jj ? bop : 0L, C, 0, 0, 0);
+            const float s[4] = {__uint_as_float(sv[g].x), __uint_as_float(sv[g].y), __uint_as_float(sv[g].z),
+                                __uint_as_float(sv[g].w)};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf((float)C[r], s[r] * p[g], acc[r]);
+        }
+        const int tn = t + nwaves;
+        if (tn < ntiles) issue(tn);     // next tile in flight during the reduction
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = row16_sum(acc[r]);
+        if (n == 0) {
+            const int row0 = t * kTileRows + 4 * m;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (row0 + r < M) y[row0 + r] = acc[r];
+        }
+    }
+}
+
+// One thread per (row, block) of the AoS array: scatter into the TILED layout.
+template <int DT>
+__global__ void to_tiled_kernel(const uint8_t *__restrict__ aos, uint8_t *__restrict__ q, float *__restrict__ sc,
+                                int M, int nb) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)M * nb) return;
+    const int r = (int)(idx / nb), b = (int)(idx - (long)r * nb);
+    const int G = nb / kGroupBlocks;
+    const int t = r / kTileRows, i = r % kTileRows, g = b / kGroupBlocks, j = b % kGroupBlocks;
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(aos + (size_t)idx * TL<DT>::BB);
+    const size_t gb = (size_t)t * G + g;
+    sc[(gb * kGroupBlocks + j) * kTileRows + i] = __uint_as_float(src[0]);
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        if constexpr (DT == DT_Q8_0) {
+            uint32_t *dst = reinterpret_cast<uint32_t *>(q + (gb * 2 + (j >> 1)) * 1024 + (mm * 16 + i) * 16 +
+                                                         (j & 1) * 8);
+            dst[0] = src[1 + 2 * mm];
+            dst[1] = src[2 + 2 * mm];
+        } else {
+            uint32_t *dst = reinterpret_cast<uint32_t *>(q + gb * 1024 + (mm * 16 + i) * 16 + j * 4);
+            dst[0] = src[1 + mm];
+        }
+    }
+}
+
+// The reference block image (scale + quants) of block (r, b) read back from TILED.
+template <int DT>
+__global__ void tiled_unpack_kernel(const uint8_t *__restrict__ q, const float *__restrict__ sc, int M, int nb,
+                                    int8_t *__restrict__ ints, float *__restrict__ deq) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)M * nb) return;
+    const int r = (int)(idx / nb), b = (int)(idx - (long)r * nb);
+    const int G = nb / kGroupBlocks;
+    const int t = r / kTileRows, i = r % kTileRows, g = b / kGroupBlocks, j = b % kGroupBlocks;
+    const size_t gb = (size_t)t * G + g;
+    const float s = sc[(gb * kGroupBlocks + j) * kTileRows + i];
+    uint8_t qb[32];
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        if constexpr (DT == DT_Q8_0) {
+            const uint8_t *p = q + (gb * 2 + (j >> 1)) * 1024 + (mm * 16 + i) * 16 + (j & 1) * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qb[8 * mm + e] = p[e];
+        } else {
+            const uint8_t *p = q + gb * 1024 + (mm * 16 + i) * 16 + j * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qb[4 * mm + e] = p[e];
+        }
+    }
+    for (int e = 0; e < 32; ++e) {
+        int v;
+        if constexpr (DT == DT_Q4_0) v = (int)((e & 1) ? (qb[e >> 1] >> 4) : (qb[e >> 1] & 0xFu)) - 8;
+        else v = (int)(int8_t)qb[e];
+        if (ints) ints[(size_t)idx * 32 + e] = (int8_t)v;
+        if (deq) deq[(size_t)idx * 32 + e] = __fmul_rn((float)v, s);
+    }
+}
+
+int cus_of_current_device() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+template <int DT, int NG>
+int launch_mfma_typed(const uint8_t *w, int M, int K, const float *x, float *y, hipStream_t st) {
+    const int ntiles = (M + kTileRows - 1) / kTileRows;
+    const size_t so = q_tiled_scales_offset(DT, M, K);
+    const size_t sbytes = q_tiled_bytes(DT, M, K) - so;
+    const long waves = std::min<long>(ntiles, (long)cus_of_current_device() * 8);
+    const unsigned blocks = (unsigned)((waves + 3) / 4);
+    hipLaunchKernelGGL((gemv_mfma<DT, NG>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
+                       (uint32_t)sbytes, x, y, M, ntiles);
+    return hip_ok(hipGetLastError(), "gemv_mfma launch") ? 0 : -1;
+}
+
+}  // namespace
+
+bool tiled_supported(int dt, int M, int K) {
+    if (!is_quant(dt) || M <= 0 || K <= 0 || K % (kGroupBlocks * kBlock) != 0) return false;
+    const int ng = K / (kGroupBlocks * kBlock);
+    if (ng != 5 && ng != 8 && ng != 9) return false;
+    return q_tiled_bytes(dt, M, K) < (size_t(1) << 32) - 256;   // 32-bit buffer offsets
+}
+
+size_t q_tiled_scales_offset(int dt, int M, int K) {
+    const size_t tiles = (size_t)(M + kTileRows - 1) / kTileRows, groups = (size_t)K / (kGroupBlocks * kBlock);
+    const size_t qbytes = tiles * groups * (dt == DT_Q4_0 ? 1024 : 2048);
+    return (qbytes + 255) & ~size_t(255);
+}
+
+size_t q_tiled_bytes(int dt, int M, int K) {
+    const size_t tiles = (size_t)(M + kTileRows - 1) / kTileRows, groups = (size_t)K / (kGroupBlocks * kBlock);
+    return q_tiled_scales_offset(dt, M, K) + tiles * groups * kGroupBlocks * kTileRows * sizeof(float);
+}
+
+int launch_to_tiled(int dt, const void *aos, int M, int K, void *out, hipStream_t st) {
+    const int nb = K / kBlock;
+    uint8_t *q = static_cast<uint8_t *>(out);
+    float *sc = reinterpret_cast<float *>(q + q_tiled_scales_offset(dt, M, K));
+    if (!hip_ok(hipMemsetAsync(out, 0, q_tiled_bytes(dt, M, K), st), "tiled memset")) return -1;
+    const long n = (long)M * nb;
+    const dim3 g((unsigned)((n + 255) / 256)), b(256);
+    if (dt == DT_Q4_0)
+        hipLaunchKernelGGL(to_tiled_kernel<DT_Q4_0>, g, b, 0, st, static_cast<const uint8_t *>(aos), q, sc, M, nb);
+    else
+        hipLaunchKernelGGL(to_tiled_kernel<DT_Q8_0>, g, b, 0, st, static_cast<const uint8_t *>(aos), q, sc, M, nb);
+    return hip_ok(hipGetLastError(), "to_tiled launch") ? 0 : -1;
+}
+
+int launch_tiled_unpack(int dt, const void *w, int M, int K, int8_t *ints, float *deq, hipStream_t st) {
+    const int nb = K / kBlock;
+    const uint8_t *q = static_cast<const uint8_t *>(w);
+    const float *sc = reinterpret_cast<const float *>(q + q_tiled_scales_offset(dt, M, K));
+    const long n = (long)M * nb;
+    const dim3 g((unsigned)((n + 255) / 256)), b(256);
+    if (dt == DT_Q4_0)
+        hipLaunchKernelGGL(tiled_unpack_kernel<DT_Q4_0>, g, b, 0, st, q, sc, M, nb, ints, deq);
+    else
+        hipLaunchKernelGGL(tiled_unpack_kernel<DT_Q8_0>, g, b, 0, st, q, sc, M, nb, ints, deq);
+    return hip_ok(hipGetLastError(), "tiled unpack launch") ? 0 : -1;
+}
+
+int launch_gemv_tiled(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t st) {
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    const int ng = K / (kGroupBlocks * kBlock);
+    if (dt == DT_Q4_0) {
+        if (ng == 5) return launch_mfma_typed<DT_Q4_0, 5>(wb, M, K, x, y, st);
+        if (ng == 8) return launch_mfma_typed<DT_Q4_0, 8>(wb, M, K, x, y, st);
+        if (ng == 9) return launch_mfma_typed<DT_Q4_0, 9>(wb, M, K, x, y, st);
+    } else {
+        if (ng == 5) return launch_mfma_typed<DT_Q8_0, 5>(wb, M, K, x, y, st);
+        if (ng == 8) return launch_mfma_typed<DT_Q8_0, 8>(wb, M, K, x, y, st);
+        if (ng == 9) return launch_mfma_typed<DT_Q8_0, 9>(wb, M, K, x, y, st);
+    }
+    set_error("TILED GEMV: K=%d is not supported (K/128 must be 5, 8 or 9)", K);
+    return -1;
+}
+
+}  // namespace sapphire

@@ -10,9 +10,10 @@
 namespace sapphire {
 
 enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_Q4_0 = 3, DT_Q8_0 = 4 };
-enum : int { LAYOUT_AOS = 0, LAYOUT_PACKED = 1 };
+enum : int { LAYOUT_AOS = 0, LAYOUT_PACKED = 1, LAYOUT_TILED = 2 };
 
 constexpr int kBlock = 32;                      // weights per quant block
+constexpr int kTiledMinRows = 16384;            // weight matrices this long use the TILED layout
 inline int quant_bytes(int dt) { return dt == DT_Q4_0 ? 16 : 32; }   // payload per block
 inline int block_bytes(int dt) { return dt == DT_Q4_0 ? 20 : 36; }   // AoS block size
 inline bool is_quant(int dt) { return dt == DT_Q4_0 || dt == DT_Q8_0; }
@@ -38,6 +39,13 @@ int launch_dequant(int dt, int layout, const void *w, int M, int K, float *out, 
 int launch_gemv_q(int dt, int layout, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 int launch_gemm_q(int dt, int layout, const void *w, int M, int K, const float *X, float *Y, int batch,
                   hipStream_t s);
+// TILED layout + matrix-core GEMV (gemv_mfma.hip)
+bool tiled_supported(int dt, int M, int K);
+size_t q_tiled_scales_offset(int dt, int M, int K);
+size_t q_tiled_bytes(int dt, int M, int K);
+int launch_to_tiled(int dt, const void *aos, int M, int K, void *out, hipStream_t s);
+int launch_tiled_unpack(int dt, const void *w, int M, int K, int8_t *ints, float *deq, hipStream_t s);
+int launch_gemv_tiled(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 
 int launch_rmsnorm(float *out, const float *in, const float *w, float eps, int dim, int batch, bool delta,

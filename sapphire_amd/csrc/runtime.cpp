@@ -123,20 +123,49 @@ int sapphire_q_repack_dev(int dt, const void *w_aos, int M, int K, void *w_packe
     return launch_repack(dt, w_aos, M, K, w_packed, as_stream(stream));
 }
 
+size_t sapphire_q_layout_bytes(int dt, int layout, int M, int K) {
+    if (!is_quant(dt) || M <= 0 || K <= 0) return 0;
+    if (layout == LAYOUT_AOS) return q_aos_bytes(dt, M, K);
+    if (layout == LAYOUT_PACKED) return q_packed_bytes(dt, M, K);
+    if (layout == LAYOUT_TILED && tiled_supported(dt, M, K)) return q_tiled_bytes(dt, M, K);
+    return 0;
+}
+
+int sapphire_q_convert_dev(int dt, const void *w_aos, int M, int K, int layout, void *out, void *stream) {
+    if (!valid_quant_args(dt, w_aos, M, K) || !out) return -1;
+    if (layout == LAYOUT_PACKED) return launch_repack(dt, w_aos, M, K, out, as_stream(stream));
+    if (layout == LAYOUT_TILED) {
+        if (!tiled_supported(dt, M, K)) {
+            set_error("TILED layout needs K/128 in {5, 8, 9} (K=%d)", K);
+            return -1;
+        }
+        return launch_to_tiled(dt, w_aos, M, K, out, as_stream(stream));
+    }
+    set_error("bad target layout %d", layout);
+    return -1;
+}
+
+static bool valid_layout(int dt, int layout, int M, int K) {
+    if (layout == LAYOUT_AOS || layout == LAYOUT_PACKED) return true;
+    if (layout == LAYOUT_TILED && tiled_supported(dt, M, K)) return true;
+    set_error("layout %d is not valid for a %d x %d matrix", layout, M, K);
+    return false;
+}
+
 int sapphire_q_unpack_ints_dev(int dt, int layout, const void *w, int M, int K, int8_t *out, void *stream) {
-    if (!valid_quant_args(dt, w, M, K) || !out) return -1;
+    if (!valid_quant_args(dt, w, M, K) || !out || !valid_layout(dt, layout, M, K)) return -1;
     return launch_unpack_ints(dt, layout, w, M, K, out, as_stream(stream));
 }
 
 int sapphire_q_dequant_dev(int dt, int layout, const void *w, int M, int K, float *out, void *stream) {
-    if (!valid_quant_args(dt, w, M, K) || !out) return -1;
+    if (!valid_quant_args(dt, w, M, K) || !out || !valid_layout(dt, layout, M, K)) return -1;
     return launch_dequant(dt, layout, w, M, K, out, as_stream(stream));
 }
 
 int sapphire_gemv_q_dev(int dt, int layout, const void *w, int M, int K, const float *x, float *y, void *stream) {
     if (!valid_quant_args(dt, w, M, K) || !x || !y) return -1;
     if (K % kBlock != 0) { set_error("K=%d is not a multiple of 32", K); return -1; }
-    if (layout != LAYOUT_AOS && layout != LAYOUT_PACKED) { set_error("bad layout %d", layout); return -1; }
+    if (!valid_layout(dt, layout, M, K)) return -1;
     return launch_gemv_q(dt, layout, w, M, K, x, y, as_stream(stream));
 }
 

@@ -187,17 +187,21 @@ const void *tensor_device_weights(const tensor_t *tc, int *layout, hipStream_t s
     const int M = t->shape[0], K = t->shape[t->ndim - 1];
     void *dst = nullptr;
     if (is_quant(t->dtype)) {
-        const size_t aos = q_aos_bytes(t->dtype, M, K), packed = q_packed_bytes(t->dtype, M, K);
+        // Long matrices (the LM head) go to the matrix-core TILED layout, the rest to PACKED.
+        const int lay = (M >= kTiledMinRows && tiled_supported(t->dtype, M, K)) ? LAYOUT_TILED : LAYOUT_PACKED;
+        const size_t aos = q_aos_bytes(t->dtype, M, K);
+        const size_t bytes = lay == LAYOUT_TILED ? q_tiled_bytes(t->dtype, M, K) : q_packed_bytes(t->dtype, M, K);
         void *tmp = nullptr;
-        if (!hip_ok(hipMalloc(&dst, packed), "hipMalloc(weights)")) return nullptr;
+        if (!hip_ok(hipMalloc(&dst, bytes), "hipMalloc(weights)")) return nullptr;
         if (!hip_ok(hipMalloc(&tmp, aos), "hipMalloc(staging)")) { (void)hipFree(dst); return nullptr; }
         bool ok = hip_ok(hipMemcpyAsync(tmp, t->data, aos, hipMemcpyHostToDevice, s), "upload weights") &&
-                  launch_repack(t->dtype, tmp, M, K, dst, s) == 0 &&
+                  (lay == LAYOUT_TILED ? launch_to_tiled(t->dtype, tmp, M, K, dst, s)
+                                       : launch_repack(t->dtype, tmp, M, K, dst, s)) == 0 &&
                   hip_ok(hipStreamSynchronize(s), "repack sync");
         (void)hipFree(tmp);
         if (!ok) { (void)hipFree(dst); return nullptr; }
-        t->dev_layout = LAYOUT_PACKED;
-        t->dev_bytes = packed;
+        t->dev_layout = lay;
+        t->dev_bytes = bytes;
     } else {
         const size_t bytes = (size_t)M * (size_t)K * dtype_element_size(t->dtype);
         if (!hip_ok(hipMalloc(&dst, bytes), "hipMalloc(weights)")) return nullptr;

@@ -67,25 +67,41 @@ class DeviceArray:
 
 
 class QMatrix:
-    """A Q4_0/Q8_0 weight matrix resident on the device, in AOS and/or PACKED layout."""
+    """A Q4_0/Q8_0 weight matrix resident on the device in one layout (AOS, PACKED or
+    TILED; see sapphire_hip.h), optionally keeping the AOS copy too."""
 
-    def __init__(self, dtype: int, blocks: np.ndarray, packed: bool = True, keep_aos: bool = False):
+    def __init__(self, dtype: int, blocks: np.ndarray, packed: bool = True, keep_aos: bool = False,
+                 layout: int = None):
         self.dtype = dtype
         self.M, nb = blocks.shape
         self.K = nb * 32
+        if layout is None:
+            layout = 1 if packed else 0
+        self.layout = layout
         aos = DeviceArray.from_numpy(synth.as_bytes(blocks))
-        self.aos = aos if keep_aos or not packed else None
-        self.packed = None
-        if packed:
+        self.aos = aos if keep_aos or layout == 0 else None
+        self.conv = None
+        if layout != 0:
             L = lib()
-            self.packed = DeviceArray(L.sapphire_q_packed_bytes(dtype, self.M, self.K))
-            check(L.sapphire_q_repack_dev(dtype, aos.ptr, self.M, self.K, self.packed.ptr, None), "repack")
+            nbytes = L.sapphire_q_layout_bytes(dtype, layout, self.M, self.K)
+            if nbytes == 0:
+                raise ValueError(f"layout {layout} cannot hold a {self.M}x{self.K} matrix")
+            self.conv = DeviceArray(nbytes)
+            check(L.sapphire_q_convert_dev(dtype, aos.ptr, self.M, self.K, layout, self.conv.ptr, None), "convert")
             check(L.sapphire_synchronize(), "sync")
-            if not keep_aos:
+            if self.aos is None:
                 aos.free()
 
-    def ptr(self, layout: int) -> int:
-        return (self.packed if layout == 1 else self.aos).ptr
+    @property
+    def packed(self):
+        return self.conv if self.layout == 1 else None
+
+    def ptr(self, layout: int = None) -> int:
+        layout = self.layout if layout is None else layout
+        if layout == 0:
+            return self.aos.ptr
+        assert layout == self.layout, f"matrix is held in layout {self.layout}, not {layout}"
+        return self.conv.ptr
 
     @property
     def algorithmic_bytes(self) -> int:

@@ -29,7 +29,7 @@ SHAPES = [
 
 def _gemv(hip, dtype, blocks, x, layout):
     from sapphire_amd.device import DeviceArray, QMatrix, gemv
-    qm = QMatrix(dtype, blocks, packed=(layout == 1), keep_aos=(layout == 0))
+    qm = QMatrix(dtype, blocks, layout=layout)
     dx = DeviceArray.from_numpy(x)
     dy = DeviceArray.empty(qm.M)
     gemv(qm, dx, dy, layout)
@@ -50,21 +50,59 @@ def test_gemv_matches_oracle(hip, oracle, dtype, layout, shape):
     assert ok, f"max abs err {err}"
 
 
+TILED_SHAPES = [
+    (16, 640), (1000, 640), (4099, 1024), (333, 1152), (17, 1152), (65536, 640), (20000, 1152),
+]
+
+
 @pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
-def test_lm_head_full_shape(hip, oracle, dtype):
+@pytest.mark.parametrize("shape", TILED_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_tiled_matches_oracle(hip, oracle, dtype, shape):
+    """The matrix-core kernel on the TILED layout, ragged row counts included."""
+    m, k = shape
+    print(f"tiled gemv dtype={dtype} shape={shape}", flush=True)
+    W = synth.quant_matrix(dtype, m, k, seed=12, tensor_id=m * 5 + k)
+    x = synth.normal_f32(k, 12, 9 + k)
+    ref = oracle.gemv(dtype, W, x, nthreads=8)
+    got = _gemv(hip, dtype, W, x, 2)
+    ok, err = close(got, ref)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("layout", [1, 2], ids=["packed", "tiled"])
+def test_lm_head_full_shape(hip, oracle, dtype, layout):
     """262144 x 640, the LM-head shape, against the oracle on every row."""
-    print(f"lm head dtype={dtype}", flush=True)
+    print(f"lm head dtype={dtype} layout={layout}", flush=True)
     W = synth.quant_matrix(dtype, 262144, 640, seed=3, tensor_id=dtype)
     x = synth.normal_f32(640, 3, 77)
     ref = oracle.gemv(dtype, W, x, nthreads=8)
-    got = _gemv(hip, dtype, W, x, 1)
+    got = _gemv(hip, dtype, W, x, layout)
     ok, err = close(got, ref)
     assert ok, f"max abs err {err}"
     assert int(np.argmax(got)) == int(np.argmax(ref))
 
 
 @pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
-@pytest.mark.parametrize("layout", [0, 1], ids=["aos", "packed"])
+def test_gemv_tiled_x_extremes(hip, oracle, dtype):
+    """Blocks of x spanning many binades, all-zero blocks and denormals: the per-block
+    integer conversion of x must keep the tolerance."""
+    m, k = 2048, 640
+    W = synth.quant_matrix(dtype, m, k, seed=13, tensor_id=1)
+    x = synth.normal_f32(k, 13, 2)
+    x[0:32] = 0.0                                   # an all-zero block
+    x[32:64] *= np.float32(1e-30)                   # tiny block
+    x[64:96] = np.float32(1e-40)                    # denormals
+    x[96] = np.float32(3e4)                         # one huge element in a block
+    x[128:160] = np.ldexp(1.0, np.arange(-16, 16)).astype(np.float32)   # 32 binades
+    ref = oracle.gemv(dtype, W, x)
+    got = _gemv(hip, dtype, W, x, 2)
+    ok, err = close(got, ref)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["aos", "packed", "tiled"])
 def test_gemv_exact_special_case(hip, oracle, dtype, layout):
     """Scales 2^-e and small-integer x: every product and sum is exact in fp32, so any
     summation order gives the reference's bits."""
@@ -79,24 +117,25 @@ def test_gemv_exact_special_case(hip, oracle, dtype, layout):
 
 
 @pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
-@pytest.mark.parametrize("layout", [0, 1], ids=["aos", "packed"])
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["aos", "packed", "tiled"])
 def test_unpack_and_dequant_bit_exact(hip, oracle, dtype, layout):
-    """Every byte value in every quant position; ints and fl(int*scale) bit for bit."""
+    """Every byte value in every quant position; ints and fl(int*scale) bit for bit.
+    Rotation offsets b + 13r cover 0..255 for (rows, blocks) = (4, 256) and (52, 20)."""
     from sapphire_amd.device import DeviceArray, QMatrix, check
-    nb = 256
-    W = np.zeros((4, nb), dtype=synth.block_dtype(dtype))
+    rows, nb = (4, 256) if layout != 2 else (52, 20)
+    W = np.zeros((rows, nb), dtype=synth.block_dtype(dtype))
     vals = np.arange(256, dtype=np.uint8)
     qb = 16 if dtype == synth.Q4_0 else 32
-    for r in range(4):
+    for r in range(rows):
         for b in range(nb):
             W["q"][r, b] = np.roll(vals, b + 13 * r)[:qb].view(W["q"].dtype)
-    W["scale"] = synth.normal_f32((4, nb), 9, 9, 0.0, 0.01)
-    qm = QMatrix(dtype, W, packed=(layout == 1), keep_aos=(layout == 0))
+    W["scale"] = synth.normal_f32((rows, nb), 9, 9, 0.0, 0.01)
+    qm = QMatrix(dtype, W, layout=layout)
     L = hip
-    ints = DeviceArray.empty(4 * nb * 32, np.int8)
-    deq = DeviceArray.empty(4 * nb * 32, np.float32)
-    check(L.sapphire_q_unpack_ints_dev(dtype, layout, qm.ptr(layout), 4, nb * 32, ints.ptr, None))
-    check(L.sapphire_q_dequant_dev(dtype, layout, qm.ptr(layout), 4, nb * 32, deq.ptr, None))
+    ints = DeviceArray.empty(rows * nb * 32, np.int8)
+    deq = DeviceArray.empty(rows * nb * 32, np.float32)
+    check(L.sapphire_q_unpack_ints_dev(dtype, layout, qm.ptr(layout), rows, nb * 32, ints.ptr, None))
+    check(L.sapphire_q_dequant_dev(dtype, layout, qm.ptr(layout), rows, nb * 32, deq.ptr, None))
     got_i = ints.numpy()
     assert np.array_equal(got_i, oracle.unpack_ints(dtype, W))
     assert np.array_equal(got_i, synth.unpack_ints(dtype, W).reshape(-1))
