@@ -86,6 +86,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--decode-steps", type=int, default=64, help="greedy decode steps (0 skips decode)")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="only launch each LM-head kernel 10 times plus a 256 MiB device copy (the "
+                         "calibration kernel of the FETCH_SIZE/WRITE_SIZE counters), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the path has no multi-GPU mode in this build "
@@ -123,6 +126,18 @@ def main() -> int:
         check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream))
         check(L.sapphire_gemv_q_dev(synth.Q4_0, LAY, q4[s].ptr(), M_LM, K_LM, dx.ptr, logits.ptr, stream))
         check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream))
+
+    if args.profile_kernels:
+        copy_bytes = 256 << 20
+        src, dst = DeviceArray(copy_bytes), DeviceArray(copy_bytes)
+        check(L.sapphire_memset(src.ptr, 1, copy_bytes), "memset")
+        for i in range(10):
+            step(i)
+        for i in range(10):
+            check(L.sapphire_memcpy_d2d(dst.ptr, src.ptr, copy_bytes, stream), "copy")
+        check(L.sapphire_stream_synchronize(stream))
+        print(json.dumps({"profile_kernels": "done", "copy_bytes": copy_bytes}), flush=True)
+        return 0
 
     for i in range(args.warmup):
         step(i)

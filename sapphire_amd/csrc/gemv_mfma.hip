@@ -27,7 +27,8 @@
 //     Q8_0: two 1 KiB halves per (tile, group); lane l = 16m + i holds, for blocks 2h and
 //           2h+1 of the group, the 8 quants e = 8m..8m+7 of row i (the MFMA A operand).
 //     Q4_0: one 1 KiB slab; lane l holds, for blocks 0..3 of the group, the 4 bytes
-//           4m..4m+3 of row i's block (elements 8m..8m+7), expanded in registers.
+//           4m..4m+3 of row i's block (elements 8m..8m+7), each nibble stored as
+//           nib ^ 8 (the 4-bit two's complement of nib - 8), expanded in registers.
 //   scales  [tile][group][block 4][row 16] fp32, after the quants at a 256-byte boundary.
 // Rows past M in the last tile are zero.
 #include <algorithm>
@@ -109,70 +110,118 @@ __device__ __forceinline__ long a_operand(const u32x4 (&a)[2], int jj) {
         const uint32_t lo = (jj & 1) ? h.z : h.x, hi = (jj & 1) ? h.w : h.y;
         return (long)(((unsigned long)hi << 32) | lo);
     } else {
-        const uint32_t q = a[0][jj] ^ 0x88888888u;   // nibble -> 4-bit two's complement of nib-8
+        const uint32_t q = a[0][jj];                    // nibbles stored as nib ^ 8
         const uint32_t even = (q << 4) & 0xF0F0F0F0u;   // int8 16*(nib-8) of elements 0,2,4,6
         const uint32_t odd = q & 0xF0F0F0F0u;           // ... of elements 1,3,5,7
         return (long)(((unsigned long)odd << 32) | even);
     }
 }
 
-// One wave per 16-row tile at a time; waves walk the tiles with a grid stride.
+// Registers of one tile's loads: the A operands of every group and the lane's scales.
+template <int NG>
+struct TileRegs {
+    u32x4 a[NG][2];
+    u32x4 sv[NG];
+};
+
+template <int DT, int NG>
+__device__ __forceinline__ void tile_issue(TileRegs<NG> &R, __amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rs,
+                                           int t, int lane) {
+    constexpr int NQ = DT == DT_Q8_0 ? 2 : 1;
+    const int jc = (lane & 15) >> 2, m = lane >> 4;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const uint32_t gb = (uint32_t)(t * NG + g);
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) R.a[g][h] = load16(rq, (gb * NQ + h) * 1024u + lane * 16u);
+        R.sv[g] = load16(rs, ((gb * 4u + jc) * 16u + 4u * m) * 4u);
+    }
+}
+
+// Four MFMAs per group (one per block; the lane's B digits enter only the MFMA of the
+// block its column belongs to) and the scales applied to the C values: acc[r] = this
+// lane's column of rows 4m + r.
+template <int DT, int NG>
+__device__ __forceinline__ void tile_mfma(const TileRegs<NG> &R, const long (&bop)[NG], const float (&p)[NG],
+                                          int lane, float (&acc)[4]) {
+    const int jc = (lane & 15) >> 2;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        i32x4 C = {0, 0, 0, 0};
+#pragma unroll
+        for (int jj = 0; jj < kGroupBlocks; ++jj)
+            C = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_operand<DT>(R.a[g], jj), jc == jj ? bop[g] : 0L, C, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[r] = __builtin_fmaf((float)C[r], __uint_as_float(R.sv[g][r]) * p[g], acc[r]);
+    }
+}
+
+// The 16 columns of each row summed across the row group; lane 16m stores rows 4m..4m+3.
+__device__ __forceinline__ void tile_store(float (&acc)[4], float *__restrict__ y, int M, int t, int lane) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = row16_sum(acc[r]);
+    if ((lane & 15) == 0) {
+        const int row0 = t * kTileRows + 4 * (lane >> 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (row0 + r < M) y[row0 + r] = acc[r];
+    }
+}
+
+// Waves walk the 16-row tiles with a grid stride. Where two tiles' loads fit in registers
+// (DB) the next tile is loaded before the current one is consumed; otherwise its loads
+// are issued as soon as the current tile's MFMAs have read their operands. Each wave
+// builds its B digits once.
 template <int DT, int NG>
 __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq, uint32_t q_bytes,
                                                  const uint8_t *__restrict__ wsc, uint32_t s_bytes,
                                                  const float *__restrict__ x, float *__restrict__ y, int M,
                                                  int ntiles) {
     constexpr int NQ = DT == DT_Q8_0 ? 2 : 1;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-    const int nwaves = gridDim.x * (blockDim.x / kWave);
-    const int n = lane & 15, m = lane >> 4;
-    const int jc = n >> 2;
+    constexpr bool DB = NG * (NQ + 1) * 4 * 2 <= 128;   // VGPRs of two tiles' loads
+    const int lane = threadIdx.x & (kWave - 1), nw_blk = blockDim.x / kWave;
+    const int wave = blockIdx.x * nw_blk + threadIdx.x / kWave;
+    const int nwaves = gridDim.x * nw_blk;
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(wq, q_bytes);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(wsc, s_bytes);
 
-    u32x4 a[NG][2];
-    u32x4 sv[NG];
-    auto issue = [&](int t) {
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            const uint32_t gb = (uint32_t)(t * NG + g);
-#pragma unroll
-            for (int h = 0; h < NQ; ++h) a[g][h] = load16(rq, (gb * NQ + h) * 1024u + lane * 16u);
-            sv[g] = load16(rs, ((gb * 4u + jc) * 16u + 4u * m) * 4u);
-        }
-    };
+    TileRegs<NG> RA;
     int t = wave;
-    if (t < ntiles) issue(t);
+    if (t < ntiles) tile_issue<DT, NG>(RA, rq, rs, t, lane);
 
-    uint32_t d0[NG], d1[NG];
     float p[NG];
+    long bop[NG];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) lane_digits<DT>(x, g, lane, d0[g], d1[g], p[g]);
+    for (int g = 0; g < NG; ++g) {
+        uint32_t w0, w1;
+        lane_digits<DT>(x, g, lane, w0, w1, p[g]);
+        bop[g] = (long)(((unsigned long)w1 << 32) | w0);
+    }
 
-    for (; t < ntiles; t += nwaves) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            i32x4 C = {0, 0, 0, 0};
-            const long bop = (long)(((unsigned long)d1[g] << 32) | d0[g]);
-#pragma unroll
-            for (int jj = 0; jj < kGroupBlocks; ++jj)
-                C = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_operand<DT>(a[g], jj), jc == jj ? bop : 0L, C, 0, 0, 0);
-            const float s[4] = {__uint_as_float(sv[g].x), __uint_as_float(sv[g].y), __uint_as_float(sv[g].z),
-                                __uint_as_float(sv[g].w)};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf((float)C[r], s[r] * p[g], acc[r]);
+    float acc[4];
+    if constexpr (DB) {
+        TileRegs<NG> RB;
+        while (t < ntiles) {
+            if (t + nwaves < ntiles) tile_issue<DT, NG>(RB, rq, rs, t + nwaves, lane);
+            tile_mfma<DT, NG>(RA, bop, p, lane, acc);
+            tile_store(acc, y, M, t, lane);
+            t += nwaves;
+            if (t >= ntiles) break;
+            if (t + nwaves < ntiles) tile_issue<DT, NG>(RA, rq, rs, t + nwaves, lane);
+            tile_mfma<DT, NG>(RB, bop, p, lane, acc);
+            tile_store(acc, y, M, t, lane);
+            t += nwaves;
         }
-        const int tn = t + nwaves;
-        if (tn < ntiles) issue(tn);     // next tile in flight during the reduction
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = row16_sum(acc[r]);
-        if (n == 0) {
-            const int row0 = t * kTileRows + 4 * m;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (row0 + r < M) y[row0 + r] = acc[r];
+    } else {
+        while (t < ntiles) {
+            tile_mfma<DT, NG>(RA, bop, p, lane, acc);
+            const int tn = t + nwaves;
+            if (tn < ntiles) tile_issue<DT, NG>(RA, rq, rs, tn, lane);
+            tile_store(acc, y, M, t, lane);
+            t = tn;
         }
     }
 }
@@ -198,7 +247,7 @@ __global__ void to_tiled_kernel(const uint8_t *__restrict__ aos, uint8_t *__rest
             dst[1] = src[2 + 2 * mm];
         } else {
             uint32_t *dst = reinterpret_cast<uint32_t *>(q + gb * 1024 + (mm * 16 + i) * 16 + j * 4);
-            dst[0] = src[1 + mm];
+            dst[0] = src[1 + mm] ^ 0x88888888u;
         }
     }
 }
@@ -224,7 +273,7 @@ __global__ void tiled_unpack_kernel(const uint8_t *__restrict__ q, const float *
         } else {
             const uint8_t *p = q + gb * 1024 + (mm * 16 + i) * 16 + j * 4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) qb[4 * mm + e] = p[e];
+            for (int e = 0; e < 4; ++e) qb[4 * mm + e] = p[e] ^ 0x88u;
         }
     }
     for (int e = 0; e < 32; ++e) {
