@@ -91,6 +91,15 @@ int sapphire_gemv_f_dev(int dtype, const void *w, int M, int K, const float *x, 
  * probs may be NULL to compute only the argmax. */
 int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *argmax_dev, void *stream);
 
+/* The LM head with its epilogue fused: logits = W . x as sapphire_gemv_q_dev, then probs
+ * and the greedy token as sapphire_softmax_argmax_dev. On the TILED layout the GEMV's
+ * workgroups leave (max, sum exp, argmax) partials and one short kernel finishes the
+ * softmax, instead of two more passes over the logits. probs may be NULL (argmax only)
+ * or equal logits. The partials use a small per-device buffer: calls that overlap on one
+ * device must be ordered on one stream. */
+int sapphire_gemv_softmax_dev(int dtype, int layout, const void *w, int M, int K, const float *x, float *logits,
+                              float *probs, int *argmax_dev, void *stream);
+
 /* ---- device copies of tensor_t weights ----
  * The device-resident copy kernel_gemv keeps for a 2-D weight tensor (Q4_0/Q8_0 in the
  * PACKED layout, F32/BF16 as is), created on first use; *layout receives its layout.

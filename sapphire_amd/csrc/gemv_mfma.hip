@@ -19,7 +19,7 @@
 // MFMA per block of the group leaves in C[row][4j+d] the exact integer sum_e int*D_d over
 // block j. Each lane then applies scale[row][block] * 2^(8d - sh) to its four C values
 // with one FMA each, and the sixteen columns of a row are summed across the lanes of a
-// 16-lane row group with ds_swizzle.
+// 16-lane row group with a ds_swizzle reduce-scatter.
 //
 // Weights live in the TILED layout (built by launch_convert), so every load instruction
 // of a wave reads one contiguous KiB:
@@ -59,13 +59,26 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT));
 }
 
-// Sum over the 16 lanes of a row group (lanes 16m..16m+15), result in every lane.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (8 << 10)));
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (4 << 10)));
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (2 << 10)));
-    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (1 << 10)));
-    return v;
+template <int MASK>
+__device__ __forceinline__ float swz_xor(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (MASK << 10)));
+}
+
+// Reduce-scatter over the 16 lanes of a row group (lanes 16m..16m+15): lane n enters with
+// its column's contributions a[0..3] to rows 4m..4m+3 and leaves with the full row sum of
+// row 4m + ((n >> 2) & 3). Lane bit 3 picks the row pair kept at the first exchange, bit
+// 2 the row kept of that pair; bits 1 and 0 finish the sum.
+__device__ __forceinline__ float row16_scatter(const float (&a)[4], int n) {
+    const bool b3 = (n & 8) != 0, b2 = (n & 4) != 0;
+    float k0 = b3 ? a[2] : a[0], k1 = b3 ? a[3] : a[1];
+    const float s0 = b3 ? a[0] : a[2], s1 = b3 ? a[1] : a[3];
+    k0 += swz_xor<8>(s0);
+    k1 += swz_xor<8>(s1);
+    float k = b2 ? k1 : k0;
+    k += swz_xor<4>(b2 ? k0 : k1);
+    k += swz_xor<2>(k);
+    k += swz_xor<1>(k);
+    return k;
 }
 
 // The MFMA B operand of this lane for group g (8 signed digits) and the factor
@@ -159,27 +172,60 @@ __device__ __forceinline__ void tile_mfma(const TileRegs<NG> &R, const long (&bo
     }
 }
 
-// The 16 columns of each row summed across the row group; lane 16m stores rows 4m..4m+3.
-__device__ __forceinline__ void tile_store(float (&acc)[4], float *__restrict__ y, int M, int t, int lane) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = row16_sum(acc[r]);
-    if ((lane & 15) == 0) {
-        const int row0 = t * kTileRows + 4 * (lane >> 4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (row0 + r < M) y[row0 + r] = acc[r];
+// Running (max, sum of exp(v - max), first index of the max) of a stream of logits: the
+// softmax / greedy-argmax partial of the rows a lane stores (utils.c:18-59, 145-156).
+struct SoftPart {
+    float m, s;
+    int i;
+};
+
+__device__ __forceinline__ void soft_push(SoftPart &p, float v, int row) {
+    if (v > p.m) {                      // strict: an equal later value keeps the earlier index
+        p.s = (p.m == -INFINITY ? 0.f : p.s * expf(p.m - v)) + 1.f;
+        p.m = v;
+        p.i = row;
+    } else {
+        p.s += expf(v - p.m);
+    }
+}
+
+__device__ __forceinline__ SoftPart soft_merge(SoftPart a, SoftPart b) {
+    const float m = fmaxf(a.m, b.m);
+    SoftPart r;
+    r.m = m;
+    r.s = (a.m == -INFINITY ? 0.f : a.s * expf(a.m - m)) + (b.m == -INFINITY ? 0.f : b.s * expf(b.m - m));
+    r.i = (b.m > a.m || (b.m == a.m && b.i < a.i)) ? b.i : a.i;
+    return r;
+}
+
+__device__ __forceinline__ SoftPart soft_shfl_xor(SoftPart p, int mask) {
+    return SoftPart{__shfl_xor(p.m, mask, kWave), __shfl_xor(p.s, mask, kWave), __shfl_xor(p.i, mask, kWave)};
+}
+
+// The 16 columns of each row summed across the row group; lane 16m + 4r stores row
+// 4m + r and, with SM, folds it into its softmax partial.
+template <bool SM>
+__device__ __forceinline__ void tile_store(const float (&acc)[4], float *__restrict__ y, int M, int t, int lane,
+                                           SoftPart &sp) {
+    const int n = lane & 15;
+    const float v = row16_scatter(acc, n);
+    const int row = t * kTileRows + 4 * (lane >> 4) + ((n >> 2) & 3);
+    if ((n & 3) == 0 && row < M) {
+        y[row] = v;
+        if constexpr (SM) soft_push(sp, v, row);
     }
 }
 
 // Waves walk the 16-row tiles with a grid stride. Where two tiles' loads fit in registers
 // (DB) the next tile is loaded before the current one is consumed; otherwise its loads
 // are issued as soon as the current tile's MFMAs have read their operands. Each wave
-// builds its B digits once.
-template <int DT, int NG>
+// builds its B digits once. With SM every workgroup also leaves the softmax/argmax partial
+// of its rows in part[blockIdx.x] (folded by softmax_finish_parts).
+template <int DT, int NG, bool SM>
 __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq, uint32_t q_bytes,
                                                  const uint8_t *__restrict__ wsc, uint32_t s_bytes,
                                                  const float *__restrict__ x, float *__restrict__ y, int M,
-                                                 int ntiles) {
+                                                 int ntiles, SoftPart *__restrict__ part) {
     constexpr int NQ = DT == DT_Q8_0 ? 2 : 1;
     constexpr bool DB = NG * (NQ + 1) * 4 * 2 <= 128;   // VGPRs of two tiles' loads
     const int lane = threadIdx.x & (kWave - 1), nw_blk = blockDim.x / kWave;
@@ -202,17 +248,18 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
     }
 
     float acc[4];
+    SoftPart sp{-INFINITY, 0.f, 0x7fffffff};
     if constexpr (DB) {
         TileRegs<NG> RB;
         while (t < ntiles) {
             if (t + nwaves < ntiles) tile_issue<DT, NG>(RB, rq, rs, t + nwaves, lane);
             tile_mfma<DT, NG>(RA, bop, p, lane, acc);
-            tile_store(acc, y, M, t, lane);
+            tile_store<SM>(acc, y, M, t, lane, sp);
             t += nwaves;
             if (t >= ntiles) break;
             if (t + nwaves < ntiles) tile_issue<DT, NG>(RA, rq, rs, t + nwaves, lane);
             tile_mfma<DT, NG>(RB, bop, p, lane, acc);
-            tile_store(acc, y, M, t, lane);
+            tile_store<SM>(acc, y, M, t, lane, sp);
             t += nwaves;
         }
     } else {
@@ -220,8 +267,77 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
             tile_mfma<DT, NG>(RA, bop, p, lane, acc);
             const int tn = t + nwaves;
             if (tn < ntiles) tile_issue<DT, NG>(RA, rq, rs, tn, lane);
-            tile_store(acc, y, M, t, lane);
+            tile_store<SM>(acc, y, M, t, lane, sp);
             t = tn;
+        }
+    }
+    if constexpr (SM) {
+        // lanes 16m + 4r hold the wave's partials (the others are still empty)
+        sp = soft_merge(sp, soft_shfl_xor(sp, 4));
+        sp = soft_merge(sp, soft_shfl_xor(sp, 8));
+        sp = soft_merge(sp, soft_shfl_xor(sp, 16));
+        sp = soft_merge(sp, soft_shfl_xor(sp, 32));
+        __shared__ SoftPart wparts[4];
+        const int wid = threadIdx.x / kWave;
+        if (lane == 0) wparts[wid] = sp;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            SoftPart b = wparts[0];
+            for (int w = 1; w < nw_blk; ++w) b = soft_merge(b, wparts[w]);
+            part[blockIdx.x] = b;
+        }
+    }
+}
+
+// Every block folds the nparts partials (256 threads, then the block), block 0 writes the
+// greedy token, and each block turns its chunk of logits into probabilities:
+// probs[i] = exp(logits[i] - max) / sum (utils.c:43-58).
+__global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restrict__ logits, int n, int chunk,
+                                                            const SoftPart *__restrict__ part, int nparts,
+                                                            float *__restrict__ probs, int *__restrict__ argmax,
+                                                            int aligned) {
+    __shared__ SoftPart wp[4];
+    __shared__ SoftPart tot;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    SoftPart b{-INFINITY, 0.f, 0x7fffffff};
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) b = soft_merge(b, part[i]);
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) b = soft_merge(b, soft_shfl_xor(b, off));
+    if (lane == 0) wp[wid] = b;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        SoftPart t = wp[0];
+        for (int w = 1; w < (int)(blockDim.x / kWave); ++w) t = soft_merge(t, wp[w]);
+        tot = t;
+        if (blockIdx.x == 0 && argmax) *argmax = t.i;
+    }
+    __syncthreads();
+    if (!probs) return;
+    const float m = tot.m, inv = 1.0f / tot.s;
+    const int begin = blockIdx.x * chunk, end = min(n, begin + chunk);
+    if (!aligned) {
+        for (int i = begin + threadIdx.x; i < end; i += blockDim.x) probs[i] = expf(logits[i] - m) * inv;
+        return;
+    }
+    // eight 16-byte loads in flight per thread, then their exps and stores
+    constexpr int U = 8;
+    for (int i0 = begin + 4 * threadIdx.x; i0 < end; i0 += 4 * U * blockDim.x) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + 4 * u * blockDim.x;
+            v[u] = i + 3 < end ? *reinterpret_cast<const float4 *>(logits + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + 4 * u * blockDim.x;
+            if (i + 3 < end) {
+                const float4 r = make_float4(expf(v[u].x - m) * inv, expf(v[u].y - m) * inv, expf(v[u].z - m) * inv,
+                                             expf(v[u].w - m) * inv);
+                *reinterpret_cast<float4 *>(probs + i) = r;
+            } else {
+                for (int e = i; e < end && e < i + 4; ++e) probs[e] = expf(logits[e] - m) * inv;
+            }
         }
     }
 }
@@ -297,16 +413,37 @@ int cus_of_current_device() {
     return cus[dev];
 }
 
+unsigned tiled_blocks(int M) {
+    const int ntiles = (M + kTileRows - 1) / kTileRows;
+    const long waves = std::min<long>(ntiles, (long)cus_of_current_device() * 8);
+    return (unsigned)((waves + 3) / 4);
+}
+
 template <int DT, int NG>
-int launch_mfma_typed(const uint8_t *w, int M, int K, const float *x, float *y, hipStream_t st) {
+int launch_mfma_typed(const uint8_t *w, int M, int K, const float *x, float *y, SoftPart *part, hipStream_t st) {
     const int ntiles = (M + kTileRows - 1) / kTileRows;
     const size_t so = q_tiled_scales_offset(DT, M, K);
     const size_t sbytes = q_tiled_bytes(DT, M, K) - so;
-    const long waves = std::min<long>(ntiles, (long)cus_of_current_device() * 8);
-    const unsigned blocks = (unsigned)((waves + 3) / 4);
-    hipLaunchKernelGGL((gemv_mfma<DT, NG>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
-                       (uint32_t)sbytes, x, y, M, ntiles);
+    const unsigned blocks = tiled_blocks(M);
+    if (part)
+        hipLaunchKernelGGL((gemv_mfma<DT, NG, true>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
+                           (uint32_t)sbytes, x, y, M, ntiles, part);
+    else
+        hipLaunchKernelGGL((gemv_mfma<DT, NG, false>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
+                           (uint32_t)sbytes, x, y, M, ntiles, part);
     return hip_ok(hipGetLastError(), "gemv_mfma launch") ? 0 : -1;
+}
+
+int launch_tiled(int dt, const void *w, int M, int K, const float *x, float *y, SoftPart *part, hipStream_t st) {
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    const int ng = K / (kGroupBlocks * kBlock);
+#define SPH_TILED_CASE(DTV, NGV) \
+    if (dt == DTV && ng == NGV) return launch_mfma_typed<DTV, NGV>(wb, M, K, x, y, part, st);
+    SPH_TILED_CASE(DT_Q4_0, 5) SPH_TILED_CASE(DT_Q4_0, 8) SPH_TILED_CASE(DT_Q4_0, 9)
+    SPH_TILED_CASE(DT_Q8_0, 5) SPH_TILED_CASE(DT_Q8_0, 8) SPH_TILED_CASE(DT_Q8_0, 9)
+#undef SPH_TILED_CASE
+    set_error("TILED GEMV: K=%d is not supported (K/128 must be 5, 8 or 9)", K);
+    return -1;
 }
 
 }  // namespace
@@ -356,20 +493,24 @@ int launch_tiled_unpack(int dt, const void *w, int M, int K, int8_t *ints, float
     return hip_ok(hipGetLastError(), "tiled unpack launch") ? 0 : -1;
 }
 
+size_t tiled_softmax_scratch_bytes(int M) { return sizeof(SoftPart) * (size_t)tiled_blocks(M); }
+
+int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *x, float *logits, float *probs,
+                              int *argmax, void *scratch, hipStream_t st) {
+    SoftPart *part = static_cast<SoftPart *>(scratch);
+    if (launch_tiled(dt, w, M, K, x, logits, part, st) != 0) return -1;
+    // 8192 logits per block (one pass of eight float4 per thread); chunks are multiples of
+    // 4 floats so the float4 accesses stay aligned
+    const int blocks = probs ? std::max(1, (M + 8191) / 8192) : 1;
+    const int chunk = ((M + blocks - 1) / blocks + 3) & ~3;
+    const int aligned = ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(probs)) & 15u) == 0;
+    hipLaunchKernelGGL(softmax_finish_parts, dim3(blocks), dim3(256), 0, st, logits, M, chunk, part,
+                       (int)tiled_blocks(M), probs, argmax, aligned);
+    return hip_ok(hipGetLastError(), "softmax_finish_parts launch") ? 0 : -1;
+}
+
 int launch_gemv_tiled(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t st) {
-    const uint8_t *wb = static_cast<const uint8_t *>(w);
-    const int ng = K / (kGroupBlocks * kBlock);
-    if (dt == DT_Q4_0) {
-        if (ng == 5) return launch_mfma_typed<DT_Q4_0, 5>(wb, M, K, x, y, st);
-        if (ng == 8) return launch_mfma_typed<DT_Q4_0, 8>(wb, M, K, x, y, st);
-        if (ng == 9) return launch_mfma_typed<DT_Q4_0, 9>(wb, M, K, x, y, st);
-    } else {
-        if (ng == 5) return launch_mfma_typed<DT_Q8_0, 5>(wb, M, K, x, y, st);
-        if (ng == 8) return launch_mfma_typed<DT_Q8_0, 8>(wb, M, K, x, y, st);
-        if (ng == 9) return launch_mfma_typed<DT_Q8_0, 9>(wb, M, K, x, y, st);
-    }
-    set_error("TILED GEMV: K=%d is not supported (K/128 must be 5, 8 or 9)", K);
-    return -1;
+    return launch_tiled(dt, w, M, K, x, y, nullptr, st);
 }
 
 }  // namespace sapphire

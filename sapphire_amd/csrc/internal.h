@@ -46,6 +46,12 @@ size_t q_tiled_bytes(int dt, int M, int K);
 int launch_to_tiled(int dt, const void *aos, int M, int K, void *out, hipStream_t s);
 int launch_tiled_unpack(int dt, const void *w, int M, int K, int8_t *ints, float *deq, hipStream_t s);
 int launch_gemv_tiled(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
+// TILED GEMV with the softmax epilogue: logits, then probs (if not NULL) and the greedy
+// token (if not NULL). scratch: tiled_softmax_scratch_bytes(M) bytes of device memory for
+// the per-workgroup partials.
+size_t tiled_softmax_scratch_bytes(int M);
+int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *x, float *logits, float *probs,
+                              int *argmax, void *scratch, hipStream_t s);
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 
 int launch_rmsnorm(float *out, const float *in, const float *w, float eps, int dim, int batch, bool delta,

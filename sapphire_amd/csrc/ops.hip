@@ -7,6 +7,8 @@
 // the reference. RoPE applies the same two fused multiply-adds the reference build
 // produces (rope.c:113-115). GELU/softmax use the device expf/tanhf, which may differ
 // from glibc by an ulp; softmax sums in parallel rather than left to right.
+#include <algorithm>
+
 #include "internal.h"
 
 namespace sapphire {

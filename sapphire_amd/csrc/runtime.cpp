@@ -177,23 +177,60 @@ int sapphire_gemv_f_dev(int dt, const void *w, int M, int K, const float *x, flo
     return launch_gemv_f(dt, w, M, K, x, y, as_stream(stream));
 }
 
+}  // extern "C"
+
+namespace {
+
+// Per-device scratch for reduction partials (softmax/argmax), allocated and zeroed once
+// per device on first use and kept until the process ends. Calls that overlap on one
+// device share it. The fused GEMV epilogue owns the first half, the standalone softmax
+// the second.
+constexpr size_t kPartialBytes = 256 * 1024;
+constexpr size_t kFusedBytes = kPartialBytes / 2;
+
+void *partial_scratch() {
+    static std::mutex mu;
+    static void *scratch[64] = {nullptr};
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (dev < 0 || dev >= 64) { set_error("device index %d out of range", dev); return nullptr; }
+    std::lock_guard<std::mutex> g(mu);
+    if (!scratch[dev]) {
+        void *p = nullptr;
+        if (!hip_ok(hipMalloc(&p, kPartialBytes), "hipMalloc(partials)")) return nullptr;
+        if (!hip_ok(hipMemset(p, 0, kPartialBytes), "hipMemset(partials)")) { (void)hipFree(p); return nullptr; }
+        scratch[dev] = p;
+    }
+    return scratch[dev];
+}
+
+float *standalone_part(void *scratch) { return reinterpret_cast<float *>(static_cast<char *>(scratch) + kFusedBytes); }
+
+}  // namespace
+
+extern "C" {
+
 int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *argmax, void *stream) {
     if (!logits || n <= 0 || (!probs && !argmax)) { set_error("bad softmax arguments"); return -1; }
-    // The partials live in a small per-device buffer shared by all calls on one stream order.
-    static std::mutex mu;
-    static float *scratch[64] = {nullptr};
-    int dev = 0;
-    SPH_CHECK(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) { set_error("device index %d out of range", dev); return -1; }
-    {
-        std::lock_guard<std::mutex> g(mu);
-        if (!scratch[dev]) {
-            void *p = nullptr;
-            SPH_CHECK(hipMalloc(&p, softmax_scratch_floats(n) * sizeof(float)));
-            scratch[dev] = static_cast<float *>(p);
-        }
+    void *scratch = partial_scratch();
+    if (!scratch) return -1;
+    return launch_softmax_argmax(logits, n, probs, argmax, standalone_part(scratch), as_stream(stream));
+}
+
+int sapphire_gemv_softmax_dev(int dt, int layout, const void *w, int M, int K, const float *x, float *logits,
+                              float *probs, int *argmax, void *stream) {
+    if (!valid_quant_args(dt, w, M, K) || !x || !logits || (!probs && !argmax)) return -1;
+    if (K % kBlock != 0) { set_error("K=%d is not a multiple of 32", K); return -1; }
+    if (!valid_layout(dt, layout, M, K)) return -1;
+    void *scratch = partial_scratch();
+    if (!scratch) return -1;
+    hipStream_t s = as_stream(stream);
+    if (layout != LAYOUT_TILED) {
+        if (launch_gemv_q(dt, layout, w, M, K, x, logits, s) != 0) return -1;
+        return launch_softmax_argmax(logits, M, probs, argmax, standalone_part(scratch), s);
     }
-    return launch_softmax_argmax(logits, n, probs, argmax, scratch[dev], as_stream(stream));
+    if (tiled_softmax_scratch_bytes(M) > kFusedBytes) { set_error("too many GEMV workgroups for M=%d", M); return -1; }
+    return launch_gemv_tiled_softmax(dt, w, M, K, x, logits, probs, argmax, scratch, s);
 }
 
 int sapphire_rmsnorm_delta_dev(float *out, const float *in, const float *w, float eps, int dim, int batch, void *s) {

@@ -140,3 +140,46 @@ def test_unpack_and_dequant_bit_exact(hip, oracle, dtype, layout):
     assert np.array_equal(got_i, oracle.unpack_ints(dtype, W))
     assert np.array_equal(got_i, synth.unpack_ints(dtype, W).reshape(-1))
     assert np.array_equal(deq.numpy().view(np.uint32), oracle.dequant(dtype, W).view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("layout", [1, 2], ids=["packed", "tiled"])
+@pytest.mark.parametrize("shape", [(262144, 640), (20000, 1152), (1000, 640)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_softmax_fused(hip, oracle, dtype, layout, shape):
+    """LM head + softmax + greedy token in one call (the GEMV epilogue leaves the softmax
+    partials on the TILED layout): logits against the oracle GEMV, probabilities against
+    the oracle softmax of the same logits, argmax against the oracle's (a different index
+    is accepted only at a near-tie within the logit tolerance)."""
+    from sapphire_amd.device import DeviceArray, QMatrix, check
+    m, k = shape
+    print(f"gemv+softmax dtype={dtype} layout={layout} shape={shape}", flush=True)
+    W = synth.quant_matrix(dtype, m, k, seed=21, tensor_id=m + k + dtype)
+    x = synth.normal_f32(k, 21, 3)
+    qm = QMatrix(dtype, W, layout=layout)
+    dx = DeviceArray.from_numpy(x)
+    logits, probs = DeviceArray.empty(m), DeviceArray.empty(m)
+    arg = DeviceArray.empty(1, np.int32)
+    check(hip.sapphire_gemv_softmax_dev(dtype, layout, qm.ptr(), m, k, dx.ptr, logits.ptr, probs.ptr, arg.ptr, None))
+    got_l, got_p, got_a = logits.numpy(), probs.numpy(), int(arg.numpy()[0])
+    ref_l = oracle.gemv(dtype, W, x, nthreads=8)
+    ok, err = close(got_l, ref_l)
+    assert ok, f"logits: max abs err {err}"
+    ok, err = close(got_p, oracle.softmax(got_l), rel=1e-3, abs_=1e-9)
+    assert ok, f"probs: max abs err {err}"
+    assert got_a == oracle.argmax(got_l)
+    ra = oracle.argmax(ref_l)
+    if got_a != ra:
+        assert abs(float(ref_l[got_a]) - float(ref_l[ra])) <= 1e-4 + 1e-3 * abs(float(ref_l[ra])), "argmax differs"
+    # argmax only (probs not written), repeated: each call must see a clean reduction state
+    for rep in range(3):
+        arg.upload(np.array([-1], np.int32))
+        check(hip.sapphire_gemv_softmax_dev(dtype, layout, qm.ptr(), m, k, dx.ptr, logits.ptr, None, arg.ptr, None))
+        assert int(arg.numpy()[0]) == got_a, f"repeat {rep}"
+    # a different input vector on the same weights
+    x2 = synth.normal_f32(k, 22, 4)
+    dx2 = DeviceArray.from_numpy(x2)
+    check(hip.sapphire_gemv_softmax_dev(dtype, layout, qm.ptr(), m, k, dx2.ptr, logits.ptr, probs.ptr, arg.ptr, None))
+    l2 = logits.numpy()
+    assert int(arg.numpy()[0]) == oracle.argmax(l2)
+    ok, err = close(probs.numpy(), oracle.softmax(l2), rel=1e-3, abs_=1e-9)
+    assert ok, f"probs (second input): max abs err {err}"
