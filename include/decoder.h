@@ -1,0 +1,77 @@
+/*
+ * decoder.h - device-resident greedy decode of a Gemma-3-shaped model on one MI355X.
+ *
+ * The reference runs a decode step as inference_forward (src/inference/inference.c:612-651):
+ * sapphire_embed_lookup, then sapphire_transformer_layer for every layer (attention stage
+ * attention.c:311-375, FFN stage transformer.c:96-171, finalize transformer.c:211-283),
+ * then lm_head (transformer.c:393-408) and sample_greedy (utils.c:145-156), calling
+ * kernel_gemv and the vector primitives with host buffers. Those entry points take the
+ * reference's own inference_session_t, so a drop-in at that level would put a PCIe round
+ * trip behind every GEMV. This engine is the MI355X-native form of the same step: weights,
+ * activations, the KV cache and the sampled token stay in HBM, and one step is a captured
+ * HIP graph of fused kernels. The host engine keeps its model loader and session and hands
+ * the weights over once.
+ *
+ * Not a reference interface: the reference has no device engine. Semantics follow the
+ * functions cited above; weights are the reference's Q4_0 / Q8_0 block arrays
+ * (kernels.h:29-38), rows = outputs, exactly as the reference's tensor views hold them.
+ */
+#ifndef SAPPHIRE_HIP_DECODER_H
+#define SAPPHIRE_HIP_DECODER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
+    int sliding_window;             /* local layers' window; <= 0 -> 1024 (attention.c:113) */
+    unsigned long long global_mask; /* bit l set -> layer l is global; 0 -> (l+1) % 6 == 0 */
+    float query_pre_attn_scalar;    /* scores scaled by 1/sqrt(this); <= 0 -> head_dim (attention.c:129) */
+    float rope_theta;               /* RoPE base of global layers (inference.c:477-483) */
+    float rope_local_base;          /* RoPE base of local layers (inference.c:485-491) */
+    float eps;                      /* RMSNorm epsilon; the reference uses 1e-6 everywhere */
+    int wdtype;                     /* DTYPE_Q4_0 (3) or DTYPE_Q8_0 (4): the seven projections */
+    int lm_dtype;                   /* DTYPE_Q4_0 or DTYPE_Q8_0: the LM head */
+} sapphire_decoder_config_t;
+
+/* Host pointers, read once by sapphire_decoder_create. Projection arrays hold one pointer
+ * per layer to that layer's block array ([rows][ceil(K/32)] blocks): wq [H*hd x hidden],
+ * wk/wv [n_kv*hd x hidden], wo [hidden x H*hd], wgate/wup [ffn x hidden], wdown [hidden x ffn].
+ * Norm weights are fp32 and applied as (1 + w) (normalization.c:104-117); q_norm and k_norm
+ * are head_dim long and shared by every head (attention.c:228-269). */
+typedef struct {
+    const void *const *wq, *const *wk, *const *wv, *const *wo, *const *wgate, *const *wup, *const *wdown;
+    const float *const *norm_attn, *const *norm_attn_post, *const *norm_ffn, *const *norm_ffn_post;
+    const float *const *q_norm, *const *k_norm;
+    const uint16_t *embed_bf16;     /* [vocab][hidden] bf16, scaled by sqrt(hidden) on lookup */
+    const float *norm_final;        /* [hidden] */
+    const void *lm_head;            /* [vocab][hidden] blocks of lm_dtype */
+} sapphire_decoder_weights_t;
+
+typedef struct sapphire_decoder sapphire_decoder_t;
+
+/* Uploads the weights to the current device (NULL on error; sapphire_last_error()). */
+sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg,
+                                            const sapphire_decoder_weights_t *w);
+void sapphire_decoder_destroy(sapphire_decoder_t *dec);
+
+/* The KV caches as [n_layers][n_kv_heads][max_ctx][head_dim] fp32 (kv_cache.c:101-106). */
+int sapphire_decoder_set_kv(sapphire_decoder_t *dec, const float *k, const float *v);
+int sapphire_decoder_get_kv(sapphire_decoder_t *dec, float *k, float *v);
+
+/* Greedy decode: `steps` steps starting with `token` at position `pos`; step s feeds
+ * tokens_out[s-1] back (token for s = 0). tokens_out[steps] receives the argmax of every
+ * step (lowest index on ties). logits_out, if not NULL, receives [steps][vocab] logits
+ * (copied back after each step, which costs time). elapsed_ms, if not NULL, receives the
+ * device time of the steps (HIP events on the decoder's stream). 0 / -1. */
+int sapphire_decoder_generate(sapphire_decoder_t *dec, int token, int pos, int steps, int *tokens_out,
+                              float *logits_out, float *elapsed_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SAPPHIRE_HIP_DECODER_H */

@@ -1,0 +1,60 @@
+// decode_kernels.h - launchers of the fused decode-step kernels (decode.hip), used by the
+// device engine (decoder.cpp). Not installed.
+#pragma once
+
+#include "internal.h"
+
+namespace sapphire {
+
+// A Q4_0 / Q8_0 matrix in the PACKED layout: quants [M][K/32][16|32], scales [M][K/32].
+struct QMat {
+    const uint8_t *q = nullptr;
+    const float *s = nullptr;
+    int M = 0, K = 0;
+};
+
+// Input vector of a fused GEMV: h = resid_in (+ rmsnorm_delta(delta, w_delta) when delta is
+// set: the residual pattern of attention.c:358-366 / transformer.c:231-239); workgroup 0
+// writes h to resid_out when set; x = rmsnorm_delta(h, w_norm) when w_norm is set, else h.
+struct GemvIn {
+    const float *resid_in = nullptr;
+    const float *delta = nullptr;
+    const float *w_delta = nullptr;
+    float *resid_out = nullptr;
+    const float *w_norm = nullptr;
+    float eps = 1e-6f;
+};
+
+constexpr int kDecMaxK = 2048;       // longest GEMV input of the fused kernels
+constexpr int kAttnMaxQ = 2048;      // n_heads * head_dim
+constexpr int kAttnMaxKV = 512;      // n_kv_heads * head_dim
+constexpr int kAttnSplit = 32;       // workgroups over the positions of one attention
+
+// y = W . x(in)  (rows M of w, K = w.K)
+int dec_gemv(int dt, const QMat &w, const GemvIn &in, float *y, hipStream_t s);
+// g = gelu(Wg . x(in)) * (Wu . x(in))  (transformer.c:141-157)
+int dec_geglu(int dt, const QMat &wg, const QMat &wu, const GemvIn &in, float *g, hipStream_t s);
+// out = x(in) for K elements (one workgroup): the final norm before the LM head
+int dec_prologue_only(const GemvIn &in, int K, float *out, hipStream_t s);
+
+struct AttnArgs {
+    const float *qkv = nullptr;      // [nh*hd | nkv*hd | nkv*hd]: q, k, v projections
+    const float *qn = nullptr, *kn = nullptr;   // [hd] QK-norm gammas (attention.c:221-226)
+    const float *cos_t = nullptr, *sin_t = nullptr;   // [max_ctx][hd] RoPE tables of the layer
+    float *kc = nullptr, *vc = nullptr;          // this layer's caches [nkv][max_ctx][hd]
+    const int *d_pos = nullptr;      // position of the token (device)
+    float *part = nullptr;           // [kAttnSplit][nh][hd + 2] partial (o, max, sum)
+    int nh = 0, nkv = 0, hd = 0, max_ctx = 0;
+    int window = 0;                  // sliding window of a local layer, 0 for a global one
+    float scale = 1.f, eps = 1e-6f;
+};
+// QK-norm, RoPE, KV write and split attention partials, then their combination into
+// out[nh*hd] (attention.c:93-163, 271-309; kv_cache.c:252-278).
+int dec_attention(const AttnArgs &a, float *out, hipStream_t s);
+
+// resid[i] = bf16 row of *d_token * es (transformer.c:347-365)
+int dec_embed(const uint16_t *embed, int hidden, float es, const int *d_token, float *resid, hipStream_t s);
+// log[*d_step] = *d_token; ++*d_step; ++*d_pos
+int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, hipStream_t s);
+
+}  // namespace sapphire

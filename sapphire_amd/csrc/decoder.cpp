@@ -1,0 +1,431 @@
+// decoder.cpp - the device-resident decode engine of include/decoder.h.
+//
+// Weights are uploaded once: the seven projections as PACKED Q4_0/Q8_0 matrices (q, k and v
+// concatenated into one QKV matrix), the LM head as TILED (matrix-core GEMV) where its
+// width allows, else PACKED. One decode step is recorded once into a HIP graph and
+// replayed: embedding of the token in device memory, 18 x (QKV GEMV, attention, o-proj,
+// gate/up GEMV, down GEMV), final norm, LM head with its argmax epilogue writing the next
+// token, and a one-thread kernel that logs the token and advances the position. The host
+// only launches the graph; nothing crosses PCIe between steps.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "../../include/decoder.h"
+#include "decode_kernels.h"
+#include "internal.h"
+
+using namespace sapphire;
+
+namespace {
+
+struct Layer {
+    QMat qkv, o, gate, up, down;
+    const float *n_attn = nullptr, *n_attn_post = nullptr, *n_ffn = nullptr, *n_ffn_post = nullptr;
+    const float *qn = nullptr, *kn = nullptr;
+    bool global = false;
+};
+
+}  // namespace
+
+struct sapphire_decoder {
+    sapphire_decoder_config_t cfg{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void *> allocs;
+    std::vector<Layer> layers;
+    const uint16_t *embed = nullptr;
+    const float *norm_final = nullptr;
+    const void *lm = nullptr;
+    int lm_layout = LAYOUT_PACKED;
+    float *kc = nullptr, *vc = nullptr;
+    float *cos_g = nullptr, *sin_g = nullptr, *cos_l = nullptr, *sin_l = nullptr;
+    float *resid[2] = {nullptr, nullptr};
+    float *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr, *ffn_out = nullptr, *xfin = nullptr;
+    float *logits = nullptr, *attn_part = nullptr;
+    void *lm_scratch = nullptr;
+    int *state = nullptr;   // [0] token, [1] position, [2] step
+    int *log = nullptr;     // [max_ctx] tokens of the steps
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+bool dev_alloc(sapphire_decoder *d, void **p, size_t bytes, const char *what) {
+    *p = nullptr;
+    if (!hip_ok(hipMalloc(p, bytes ? bytes : 1), what)) return false;
+    d->allocs.push_back(*p);
+    return true;
+}
+
+template <class T>
+bool dev_alloc_t(sapphire_decoder *d, T **p, size_t count, const char *what) {
+    void *v = nullptr;
+    if (!dev_alloc(d, &v, count * sizeof(T), what)) return false;
+    *p = static_cast<T *>(v);
+    return true;
+}
+
+bool upload(sapphire_decoder *d, const void *host, size_t bytes, void **dst, const char *what) {
+    if (!host) {
+        set_error("decoder weights: %s is NULL", what);
+        return false;
+    }
+    return dev_alloc(d, dst, bytes, what) && hip_ok(hipMemcpy(*dst, host, bytes, hipMemcpyHostToDevice), what);
+}
+
+const float *upload_f32(sapphire_decoder *d, const float *host, size_t n, const char *what) {
+    void *p = nullptr;
+    return upload(d, host, n * sizeof(float), &p, what) ? static_cast<const float *>(p) : nullptr;
+}
+
+// Block arrays (AOS, rows concatenated in order) -> one PACKED matrix of sum(rows) x K.
+bool upload_packed(sapphire_decoder *d, int dt, std::initializer_list<std::pair<const void *, int>> parts, int K,
+                   QMat *out, const char *what) {
+    int M = 0;
+    for (const auto &p : parts) {
+        if (!p.first) {
+            set_error("decoder weights: %s is NULL", what);
+            return false;
+        }
+        M += p.second;
+    }
+    void *aos = nullptr;
+    if (!hip_ok(hipMalloc(&aos, q_aos_bytes(dt, M, K)), what)) return false;
+    size_t off = 0;
+    bool ok = true;
+    for (const auto &p : parts) {
+        const size_t b = q_aos_bytes(dt, p.second, K);
+        ok = ok && hip_ok(hipMemcpy(static_cast<char *>(aos) + off, p.first, b, hipMemcpyHostToDevice), what);
+        off += b;
+    }
+    void *packed = nullptr;
+    ok = ok && dev_alloc(d, &packed, q_packed_bytes(dt, M, K), what) &&
+         launch_repack(dt, aos, M, K, packed, d->stream) == 0 && hip_ok(hipStreamSynchronize(d->stream), what);
+    (void)hipFree(aos);
+    if (!ok) return false;
+    out->q = static_cast<const uint8_t *>(packed);
+    out->s = reinterpret_cast<const float *>(static_cast<const uint8_t *>(packed) + q_scales_offset(dt, M, K));
+    out->M = M;
+    out->K = K;
+    return true;
+}
+
+// rope_precompute_freqs (rope.c:41-63): half-split tables [max_ctx][hd] in fp32 with the
+// host libm, exactly as the reference computes them at session creation.
+void rope_tables(int hd, int max_ctx, float base, std::vector<float> &c, std::vector<float> &s) {
+    c.assign((size_t)max_ctx * hd, 0.f);
+    s.assign((size_t)max_ctx * hd, 0.f);
+    const int half = hd / 2;
+    for (int pos = 0; pos < max_ctx; ++pos)
+        for (int m = 0; m < half; ++m) {
+            const float freq = 1.0f / powf(base, 2.0f * (float)m / (float)hd);
+            const float angle = (float)pos * freq;
+            const float cv = cosf(angle), sv = sinf(angle);
+            c[(size_t)pos * hd + m] = c[(size_t)pos * hd + m + half] = cv;
+            s[(size_t)pos * hd + m] = s[(size_t)pos * hd + m + half] = sv;
+        }
+}
+
+bool layer_is_global(const sapphire_decoder_config_t &c, int l) {   // attention.c:104-111
+    if (c.global_mask) return ((c.global_mask >> (unsigned)l) & 1ULL) != 0ULL;
+    return ((l + 1) % 6) == 0;
+}
+
+// One decode step, enqueued on d->stream (recorded into the graph).
+int enqueue_step(sapphire_decoder *d) {
+    const auto &c = d->cfg;
+    hipStream_t s = d->stream;
+    const int H = c.hidden, hd = c.head_dim;
+    const float es = sqrtf((float)H);
+    const float scale = 1.0f / sqrtf(c.query_pre_attn_scalar > 0.f ? c.query_pre_attn_scalar : (float)hd);
+    const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
+    if (dec_embed(d->embed, H, es, d->state, d->resid[0], s) != 0) return -1;
+    int cur = 0;
+    const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer &L = d->layers[l];
+        // previous layer's finalize (transformer.c:231-239) + attention pre-norm (attention.c:316-325)
+        GemvIn a_in;
+        a_in.resid_in = d->resid[cur];
+        a_in.eps = c.eps;
+        a_in.w_norm = L.n_attn;
+        if (l > 0) {
+            a_in.delta = d->ffn_out;
+            a_in.w_delta = d->layers[l - 1].n_ffn_post;
+            a_in.resid_out = d->resid[1 - cur];
+            cur = 1 - cur;
+        }
+        if (dec_gemv(c.wdtype, L.qkv, a_in, d->qkv, s) != 0) return -1;
+        AttnArgs at;
+        at.qkv = d->qkv;
+        at.qn = L.qn;
+        at.kn = L.kn;
+        at.cos_t = L.global ? d->cos_g : d->cos_l;
+        at.sin_t = L.global ? d->sin_g : d->sin_l;
+        at.kc = d->kc + (size_t)l * layer_kv;
+        at.vc = d->vc + (size_t)l * layer_kv;
+        at.d_pos = d->state + 1;
+        at.part = d->attn_part;
+        at.nh = c.n_heads;
+        at.nkv = c.n_kv_heads;
+        at.hd = hd;
+        at.max_ctx = c.max_ctx;
+        at.window = L.global ? 0 : win;
+        at.scale = scale;
+        at.eps = c.eps;
+        if (dec_attention(at, d->attn, s) != 0) return -1;
+        GemvIn o_in;
+        o_in.resid_in = d->attn;
+        if (dec_gemv(c.wdtype, L.o, o_in, d->o, s) != 0) return -1;
+        // post-attention norm + residual (attention.c:356-366), FFN pre-norm (transformer.c:119-121)
+        GemvIn f_in;
+        f_in.resid_in = d->resid[cur];
+        f_in.delta = d->o;
+        f_in.w_delta = L.n_attn_post;
+        f_in.resid_out = d->resid[1 - cur];
+        f_in.w_norm = L.n_ffn;
+        f_in.eps = c.eps;
+        cur = 1 - cur;
+        if (dec_geglu(c.wdtype, L.gate, L.up, f_in, d->g, s) != 0) return -1;
+        GemvIn d_in;
+        d_in.resid_in = d->g;
+        if (dec_gemv(c.wdtype, L.down, d_in, d->ffn_out, s) != 0) return -1;
+    }
+    // last finalize + final norm (transformer.c:400-406), LM head + greedy token
+    GemvIn fin;
+    fin.resid_in = d->resid[cur];
+    fin.delta = d->ffn_out;
+    fin.w_delta = d->layers[c.n_layers - 1].n_ffn_post;
+    fin.w_norm = d->norm_final;
+    fin.eps = c.eps;
+    if (dec_prologue_only(fin, H, d->xfin, s) != 0) return -1;
+    if (d->lm_layout == LAYOUT_TILED) {
+        if (launch_gemv_tiled_softmax(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, nullptr, d->state,
+                                      d->lm_scratch, s) != 0)
+            return -1;
+    } else {
+        if (launch_gemv_q(c.lm_dtype, LAYOUT_PACKED, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
+        if (launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
+            return -1;
+    }
+    return dec_advance(d->state, d->state + 1, d->state + 2, d->log, s);
+}
+
+bool valid_config(const sapphire_decoder_config_t &c) {
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.ffn <= 0 ||
+        c.vocab <= 0 || c.max_ctx <= 0) {
+        set_error("decoder config: non-positive dimension");
+        return false;
+    }
+    if (!is_quant(c.wdtype) || !is_quant(c.lm_dtype)) {
+        set_error("decoder config: weights must be Q4_0 or Q8_0");
+        return false;
+    }
+    if (c.hidden % kBlock || (c.n_heads * c.head_dim) % kBlock || c.ffn % kBlock) {
+        set_error("decoder config: hidden, n_heads*head_dim and ffn must be multiples of 32");
+        return false;
+    }
+    if (c.hidden > kDecMaxK || c.n_heads * c.head_dim > kDecMaxK || c.ffn > kDecMaxK) {
+        set_error("decoder config: GEMV inputs longer than %d are not supported", kDecMaxK);
+        return false;
+    }
+    if (c.n_heads % c.n_kv_heads || (c.head_dim & 1)) {
+        set_error("decoder config: heads must group evenly and head_dim be even");
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+void sapphire_decoder_destroy(sapphire_decoder_t *d) {
+    if (!d) return;
+    (void)hipSetDevice(d->device);
+    if (d->stream) (void)hipStreamSynchronize(d->stream);
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    for (void *p : d->allocs) (void)hipFree(p);
+    if (d->stream) (void)hipStreamDestroy(d->stream);
+    delete d;
+}
+
+sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg, const sapphire_decoder_weights_t *w) {
+    if (!cfg || !w) {
+        set_error("sapphire_decoder_create: NULL argument");
+        return nullptr;
+    }
+    if (!valid_config(*cfg)) return nullptr;
+    sapphire_decoder *d = new (std::nothrow) sapphire_decoder();
+    if (!d) return nullptr;
+    d->cfg = *cfg;
+    const auto &c = d->cfg;
+    auto fail = [&]() -> sapphire_decoder_t * {
+        sapphire_decoder_destroy(d);
+        return nullptr;
+    };
+    if (!hip_ok(hipGetDevice(&d->device), "hipGetDevice") ||
+        !hip_ok(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate"))
+        return fail();
+    const int H = c.hidden, hd = c.head_dim, nq = c.n_heads * hd, nk = c.n_kv_heads * hd;
+    d->layers.resize((size_t)c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer &L = d->layers[l];
+        L.global = layer_is_global(c, l);
+        if (!w->wq || !w->wk || !w->wv || !w->wo || !w->wgate || !w->wup || !w->wdown || !w->norm_attn ||
+            !w->norm_attn_post || !w->norm_ffn || !w->norm_ffn_post || !w->q_norm || !w->k_norm) {
+            set_error("decoder weights: a per-layer array is NULL");
+            return fail();
+        }
+        if (!upload_packed(d, c.wdtype, {{w->wq[l], nq}, {w->wk[l], nk}, {w->wv[l], nk}}, H, &L.qkv, "wqkv") ||
+            !upload_packed(d, c.wdtype, {{w->wo[l], H}}, nq, &L.o, "wo") ||
+            !upload_packed(d, c.wdtype, {{w->wgate[l], c.ffn}}, H, &L.gate, "wgate") ||
+            !upload_packed(d, c.wdtype, {{w->wup[l], c.ffn}}, H, &L.up, "wup") ||
+            !upload_packed(d, c.wdtype, {{w->wdown[l], H}}, c.ffn, &L.down, "wdown"))
+            return fail();
+        if (!(L.n_attn = upload_f32(d, w->norm_attn[l], H, "norm_attn")) ||
+            !(L.n_attn_post = upload_f32(d, w->norm_attn_post[l], H, "norm_attn_post")) ||
+            !(L.n_ffn = upload_f32(d, w->norm_ffn[l], H, "norm_ffn")) ||
+            !(L.n_ffn_post = upload_f32(d, w->norm_ffn_post[l], H, "norm_ffn_post")) ||
+            !(L.qn = upload_f32(d, w->q_norm[l], hd, "q_norm")) || !(L.kn = upload_f32(d, w->k_norm[l], hd, "k_norm")))
+            return fail();
+    }
+    void *p = nullptr;
+    if (!upload(d, w->embed_bf16, (size_t)c.vocab * H * sizeof(uint16_t), &p, "embed")) return fail();
+    d->embed = static_cast<const uint16_t *>(p);
+    if (!(d->norm_final = upload_f32(d, w->norm_final, H, "norm_final"))) return fail();
+    // LM head
+    {
+        if (!w->lm_head) {
+            set_error("decoder weights: lm_head is NULL");
+            return fail();
+        }
+        void *aos = nullptr;
+        const size_t ab = q_aos_bytes(c.lm_dtype, c.vocab, H);
+        if (!hip_ok(hipMalloc(&aos, ab), "lm aos")) return fail();
+        bool ok = hip_ok(hipMemcpy(aos, w->lm_head, ab, hipMemcpyHostToDevice), "lm upload");
+        d->lm_layout = tiled_supported(c.lm_dtype, c.vocab, H) ? LAYOUT_TILED : LAYOUT_PACKED;
+        const size_t lb = d->lm_layout == LAYOUT_TILED ? q_tiled_bytes(c.lm_dtype, c.vocab, H)
+                                                       : q_packed_bytes(c.lm_dtype, c.vocab, H);
+        void *lm = nullptr;
+        ok = ok && dev_alloc(d, &lm, lb, "lm") &&
+             (d->lm_layout == LAYOUT_TILED ? launch_to_tiled(c.lm_dtype, aos, c.vocab, H, lm, d->stream)
+                                           : launch_repack(c.lm_dtype, aos, c.vocab, H, lm, d->stream)) == 0 &&
+             hip_ok(hipStreamSynchronize(d->stream), "lm repack");
+        (void)hipFree(aos);
+        if (!ok) return fail();
+        d->lm = lm;
+        const size_t sb = d->lm_layout == LAYOUT_TILED ? tiled_softmax_scratch_bytes(c.vocab)
+                                                       : softmax_scratch_floats(c.vocab) * sizeof(float);
+        if (!dev_alloc(d, &d->lm_scratch, sb, "lm scratch")) return fail();
+    }
+    // RoPE tables and the KV caches
+    {
+        std::vector<float> cs, sn;
+        rope_tables(hd, c.max_ctx, c.rope_theta, cs, sn);
+        if (!(d->cos_g = const_cast<float *>(upload_f32(d, cs.data(), cs.size(), "rope"))) ||
+            !(d->sin_g = const_cast<float *>(upload_f32(d, sn.data(), sn.size(), "rope"))))
+            return fail();
+        rope_tables(hd, c.max_ctx, c.rope_local_base, cs, sn);
+        if (!(d->cos_l = const_cast<float *>(upload_f32(d, cs.data(), cs.size(), "rope"))) ||
+            !(d->sin_l = const_cast<float *>(upload_f32(d, sn.data(), sn.size(), "rope"))))
+            return fail();
+    }
+    const size_t kv = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * hd;
+    if (!dev_alloc_t(d, &d->kc, kv, "k cache") || !dev_alloc_t(d, &d->vc, kv, "v cache") ||
+        !hip_ok(hipMemset(d->kc, 0, kv * sizeof(float)), "kv zero") ||
+        !hip_ok(hipMemset(d->vc, 0, kv * sizeof(float)), "kv zero"))
+        return fail();
+    if (!dev_alloc_t(d, &d->resid[0], H, "resid") || !dev_alloc_t(d, &d->resid[1], H, "resid") ||
+        !dev_alloc_t(d, &d->qkv, (size_t)nq + 2 * nk, "qkv") || !dev_alloc_t(d, &d->attn, nq, "attn") ||
+        !dev_alloc_t(d, &d->o, H, "o") || !dev_alloc_t(d, &d->g, c.ffn, "g") ||
+        !dev_alloc_t(d, &d->ffn_out, H, "ffn_out") || !dev_alloc_t(d, &d->xfin, H, "xfin") ||
+        !dev_alloc_t(d, &d->logits, c.vocab, "logits") ||
+        !dev_alloc_t(d, &d->attn_part, (size_t)kAttnSplit * c.n_heads * (hd + 2), "attn partials") ||
+        !dev_alloc_t(d, &d->state, 4, "state") || !dev_alloc_t(d, &d->log, c.max_ctx, "token log"))
+        return fail();
+    return d;
+}
+
+int sapphire_decoder_set_kv(sapphire_decoder_t *d, const float *k, const float *v) {
+    if (!d || !k || !v) {
+        set_error("sapphire_decoder_set_kv: NULL argument");
+        return -1;
+    }
+    const auto &c = d->cfg;
+    const size_t b = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim * sizeof(float);
+    SPH_CHECK(hipSetDevice(d->device));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    SPH_CHECK(hipMemcpy(d->kc, k, b, hipMemcpyHostToDevice));
+    SPH_CHECK(hipMemcpy(d->vc, v, b, hipMemcpyHostToDevice));
+    return 0;
+}
+
+int sapphire_decoder_get_kv(sapphire_decoder_t *d, float *k, float *v) {
+    if (!d || !k || !v) {
+        set_error("sapphire_decoder_get_kv: NULL argument");
+        return -1;
+    }
+    const auto &c = d->cfg;
+    const size_t b = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim * sizeof(float);
+    SPH_CHECK(hipSetDevice(d->device));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    SPH_CHECK(hipMemcpy(k, d->kc, b, hipMemcpyDeviceToHost));
+    SPH_CHECK(hipMemcpy(v, d->vc, b, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int sapphire_decoder_generate(sapphire_decoder_t *d, int token, int pos, int steps, int *tokens_out, float *logits_out,
+                              float *elapsed_ms) {
+    if (!d || !tokens_out || steps <= 0) {
+        set_error("sapphire_decoder_generate: bad arguments");
+        return -1;
+    }
+    const auto &c = d->cfg;
+    if (token < 0 || token >= c.vocab || pos < 0 || pos + steps > c.max_ctx) {
+        set_error("sapphire_decoder_generate: token %d / positions %d..%d out of range", token, pos, pos + steps - 1);
+        return -1;
+    }
+    SPH_CHECK(hipSetDevice(d->device));
+    if (!d->exec) {
+        SPH_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_step(d);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(d->stream, &g);
+        if (rc != 0 || !hip_ok(e, "hipStreamEndCapture")) {
+            if (g) (void)hipGraphDestroy(g);
+            return -1;
+        }
+        d->graph = g;
+        SPH_CHECK(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
+    }
+    const int st[4] = {token, pos, 0, 0};
+    SPH_CHECK(hipMemcpy(d->state, st, sizeof st, hipMemcpyHostToDevice));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (elapsed_ms) {
+        SPH_CHECK(hipEventCreate(&e0));
+        SPH_CHECK(hipEventCreate(&e1));
+        SPH_CHECK(hipEventRecord(e0, d->stream));
+    }
+    for (int s = 0; s < steps; ++s) {
+        SPH_CHECK(hipGraphLaunch(d->exec, d->stream));
+        if (logits_out)
+            SPH_CHECK(hipMemcpyAsync(logits_out + (size_t)s * c.vocab, d->logits, sizeof(float) * (size_t)c.vocab,
+                                     hipMemcpyDeviceToHost, d->stream));
+    }
+    if (elapsed_ms) SPH_CHECK(hipEventRecord(e1, d->stream));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    if (elapsed_ms) {
+        SPH_CHECK(hipEventElapsedTime(elapsed_ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+    }
+    SPH_CHECK(hipMemcpy(tokens_out, d->log, sizeof(int) * (size_t)steps, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,139 @@
+"""The device-resident decode engine (include/decoder.h) from Python.
+
+:class:`Decoder` uploads a :class:`sapphire_amd.model.SyntheticModel` (or any object with
+the same fields) once and runs greedy decode steps as HIP graph replays; weights,
+activations, the KV cache and the sampled tokens stay in HBM.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import load
+from . import model as smodel
+
+_VPP = C.POINTER(C.c_void_p)
+_FPP = C.POINTER(C.POINTER(C.c_float))
+
+
+class DecoderConfig(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+        ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("max_ctx", C.c_int),
+        ("sliding_window", C.c_int), ("global_mask", C.c_ulonglong),
+        ("query_pre_attn_scalar", C.c_float), ("rope_theta", C.c_float), ("rope_local_base", C.c_float),
+        ("eps", C.c_float), ("wdtype", C.c_int), ("lm_dtype", C.c_int),
+    ]
+
+
+class DecoderWeights(C.Structure):
+    _fields_ = [(n, _VPP) for n in smodel.PROJ] + \
+               [(n, _FPP) for n in ("norm_attn", "norm_attn_post", "norm_ffn", "norm_ffn_post", "q_norm", "k_norm")] + \
+               [("embed_bf16", C.c_void_p), ("norm_final", C.c_void_p), ("lm_head", C.c_void_p)]
+
+
+def _protos(L):
+    L.sapphire_decoder_create.restype = C.c_void_p
+    L.sapphire_decoder_create.argtypes = [C.POINTER(DecoderConfig), C.POINTER(DecoderWeights)]
+    L.sapphire_decoder_destroy.restype = None
+    L.sapphire_decoder_destroy.argtypes = [C.c_void_p]
+    L.sapphire_decoder_set_kv.restype = C.c_int
+    L.sapphire_decoder_set_kv.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+    L.sapphire_decoder_get_kv.restype = C.c_int
+    L.sapphire_decoder_get_kv.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+    L.sapphire_decoder_generate.restype = C.c_int
+    L.sapphire_decoder_generate.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                            C.POINTER(C.c_float)]
+
+
+class Decoder:
+    def __init__(self, m: "smodel.SyntheticModel"):
+        self.lib = L = load()
+        _protos(L)
+        cfg = m.cfg
+        self.cfg = cfg
+        self._keep = []
+        c = DecoderConfig(cfg.n_layers, cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn, cfg.vocab,
+                          cfg.max_ctx, cfg.sliding_window, cfg.global_mask, cfg.query_pre_attn_scalar,
+                          cfg.rope_theta, cfg.rope_local_base, cfg.eps, cfg.wdtype, cfg.lm_dtype)
+        w = DecoderWeights()
+        for n in smodel.PROJ:
+            arrs = [np.ascontiguousarray(m.weights[n][l]) for l in range(cfg.n_layers)]
+            self._keep.append(arrs)
+            setattr(w, n, (C.c_void_p * cfg.n_layers)(*[a.ctypes.data for a in arrs]))
+        for n in ("norm_attn", "norm_attn_post", "norm_ffn", "norm_ffn_post", "q_norm", "k_norm"):
+            arrs = [np.ascontiguousarray(m.norms[n][l], np.float32) for l in range(cfg.n_layers)]
+            self._keep.append(arrs)
+            setattr(w, n, (C.POINTER(C.c_float) * cfg.n_layers)(
+                *[C.cast(a.ctypes.data, C.POINTER(C.c_float)) for a in arrs]))
+        for n, a in (("embed_bf16", m.embed_bf16), ("norm_final", m.norm_final), ("lm_head", m.lm_head)):
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            setattr(w, n, a.ctypes.data)
+        self.ptr = L.sapphire_decoder_create(C.byref(c), C.byref(w))
+        self._keep = None      # the library copied the weights
+        if not self.ptr:
+            raise RuntimeError("sapphire_decoder_create: " + L.sapphire_last_error().decode())
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: " + self.lib.sapphire_last_error().decode())
+
+    def set_kv(self, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        self._check(self.lib.sapphire_decoder_set_kv(self.ptr, k.ctypes.data, v.ctypes.data), "set_kv")
+
+    def get_kv(self):
+        c = self.cfg
+        shape = (c.n_layers, c.n_kv_heads, c.max_ctx, c.head_dim)
+        k, v = np.empty(shape, np.float32), np.empty(shape, np.float32)
+        self._check(self.lib.sapphire_decoder_get_kv(self.ptr, k.ctypes.data, v.ctypes.data), "get_kv")
+        return k, v
+
+    def generate(self, token: int, pos: int, steps: int, keep_logits: bool = False):
+        """(tokens[steps], logits[steps, vocab] or None, device milliseconds)."""
+        toks = np.empty(steps, np.int32)
+        logits = np.empty((steps, self.cfg.vocab), np.float32) if keep_logits else None
+        ms = C.c_float(0.0)
+        self._check(self.lib.sapphire_decoder_generate(self.ptr, int(token), int(pos), int(steps), toks.ctypes.data,
+                                                       logits.ctypes.data if logits is not None else None,
+                                                       C.byref(ms)), "generate")
+        return toks, logits, float(ms.value)
+
+    def close(self):
+        if getattr(self, "ptr", None):
+            self.lib.sapphire_decoder_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, reps: int = 3):
+    """Greedy decode of the Gemma-3-270M-shaped Q4_0 model (KV prefilled to `prefill` of
+    2048 positions): tokens/s over `steps` steps, best of `reps` runs after a warm-up."""
+    cfg = smodel.GEMMA3_270M
+    m = smodel.synthetic_model(cfg, seed)
+    k, v = m.kv_prefill(prefill)
+    dec = Decoder(m)
+    tok = smodel.start_token(cfg, seed)
+    dec.set_kv(k, v)
+    dec.generate(tok, prefill, steps)                 # graph capture + warm-up
+    best = None
+    for _ in range(reps):
+        dec.set_kv(k, v)
+        toks, _, ms = dec.generate(tok, prefill, steps)
+        best = ms if best is None else min(best, ms)
+    dec.close()
+    layer_bytes = sum(int(m.weights[n][0].nbytes) for n in smodel.PROJ) * cfg.n_layers
+    return {
+        "model": "Gemma-3-270M-shaped, Q4_0 weights (random init), 18 layers, hidden 640, vocab 262144",
+        "steps": steps, "kv_prefill": prefill, "ms_total": round(best, 3), "ms_per_token": round(best / steps, 4),
+        "tok_per_s": round(steps / (best * 1e-3), 1), "first_tokens": [int(t) for t in toks[:8]],
+        "weight_bytes_per_token": layer_bytes + int(m.lm_head.nbytes),
+    }

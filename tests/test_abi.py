@@ -182,3 +182,21 @@ def test_parallel_for_runs_each_index_once(lib):
         assert (hits == 1).all()
         lib.kernel_ctx_destroy(ctx)
     assert lib.kernel_parallel_for(None, fn, None, n) == -1
+
+
+def test_decoder_argument_validation(lib):
+    """The decode engine refuses bad arguments before touching a device."""
+    from sapphire_amd.engine import DecoderConfig, _protos
+    _protos(lib)
+    assert not lib.sapphire_decoder_create(None, None)
+    bad = DecoderConfig(0, 640, 4, 1, 256, 2048, 262144, 2048, 512, 0, 256.0, 1e6, 1e4, 1e-6, 3, 3)
+    assert not lib.sapphire_decoder_create(C.byref(bad), None)
+    cfg = DecoderConfig(18, 640, 4, 1, 256, 2048, 262144, 2048, 512, 0, 256.0, 1e6, 1e4, 1e-6, 0, 3)
+    from sapphire_amd.engine import DecoderWeights
+    w = DecoderWeights()
+    assert not lib.sapphire_decoder_create(C.byref(cfg), C.byref(w))      # F32 projections: not Q4_0/Q8_0
+    assert b"Q4_0 or Q8_0" in lib.sapphire_last_error()
+    toks = np.zeros(4, np.int32)
+    assert lib.sapphire_decoder_generate(None, 0, 0, 4, toks.ctypes.data, None, None) == -1
+    assert lib.sapphire_decoder_set_kv(None, None, None) == -1
+    lib.sapphire_decoder_destroy(None)
