@@ -79,6 +79,36 @@ def cpu_baseline(x, w8, w4, budget_s: float = 12.0):
     }
 
 
+def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024):
+    """Greedy decode of the Gemma-3-270M-shaped Q4_0 model on the GPU (device-resident engine,
+    one HIP graph per step), and the reference engine compiled from its sources (oracle/_ref)
+    on this host's cores for a few steps of the same model as the CPU baseline."""
+    from sapphire_amd import model as smodel
+    from sapphire_amd.engine import bench_decode
+    m = smodel.synthetic_model(smodel.GEMMA3_270M, seed)
+    k, v = m.kv_prefill(prefill)
+    out = bench_decode(steps, seed=seed, prefill=prefill, m=m, kv=(k, v))
+    if cpu:
+        from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
+        tok = smodel.start_token(m.cfg, seed)
+        n = 6
+        t0 = time.perf_counter()
+        if ref_decode_available():
+            toks, _ = ref_decode(m, k.copy(), v.copy(), tok, prefill, n)
+            kind = "reference"
+        else:
+            toks, _ = oracle_decode(Oracle(), m, k.copy(), v.copy(), tok, prefill, n, nthreads=os.cpu_count() or 1)
+            kind = "port"
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {
+            "tok_per_s": round(n / dt, 2), "kind": kind, "cores": os.cpu_count(),
+            "sample": f"{n} greedy steps of the same model and KV cache through the reference's session and "
+                      f"layer functions ({dt:.2f} s, thread pool of nproc threads)",
+            "tokens_match_gpu": [int(t) for t in toks] == out["first_tokens"][:n],
+        }
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,11 +205,7 @@ def main() -> int:
 
     decode = None
     if args.decode_steps > 0:
-        try:
-            from sapphire_amd.engine import bench_decode
-            decode = bench_decode(args.decode_steps)
-        except ImportError:
-            decode = None
+        decode = decode_leg(args.decode_steps, cpu=not args.no_cpu)
 
     out = {
         "metric": METRIC,

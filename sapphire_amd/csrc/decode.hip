@@ -38,19 +38,56 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// xs[0..K) = x(in) (see GemvIn); every thread of the workgroup takes part.
-__device__ void stage_input(const GemvIn &in, int K, float *xs, float *sh) {
-    for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = in.resid_in[i];
-    if (in.delta) {
-        const float r = rms_inv_of(block_sum_sq_ref(in.delta, K, sh), K, in.eps);
-        for (int i = threadIdx.x; i < K; i += blockDim.x)
-            xs[i] = __fadd_rn(xs[i], __fmul_rn(__fmul_rn(in.delta[i], r), __fadd_rn(1.0f, in.w_delta[i])));
+// Sum of squares of v[0..n) (LDS) in the reference order of sum_sq_avx2
+// (normalization.c:12-32): eight sequential FMA lanes over elements l, l+8, ..., then
+// ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)) and a sequential fused tail. Threads 0..7 run the
+// lanes, loading eight elements ahead of their FMA chain; the result is returned to every
+// thread (the call synchronises the workgroup).
+__device__ float lds_sum_sq(const float *v, int n, float *sh) {
+    const int t = threadIdx.x;
+    if (t < 8) {
+        float s = 0.f;
+        const int full = n & ~7;
+        int i = t;
+        for (; i + 56 < full; i += 64) {
+            float w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = v[i + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s = __builtin_fmaf(w[u], w[u], s);
+        }
+        for (; i < full; i += 8) s = __builtin_fmaf(v[i], v[i], s);
+        sh[t] = s;
     }
     __syncthreads();
+    if (t == 0) {
+        const float a0 = sh[0] + sh[4], a1 = sh[1] + sh[5], a2 = sh[2] + sh[6], a3 = sh[3] + sh[7];
+        float s = (a0 + a1) + (a2 + a3);
+        for (int i = n & ~7; i < n; ++i) s = __builtin_fmaf(v[i], v[i], s);
+        sh[8] = s;
+    }
+    __syncthreads();
+    return sh[8];
+}
+
+// xs[0..K) = x(in) (see GemvIn); every thread of the workgroup takes part. dl is LDS
+// scratch of K floats for the delta vector.
+__device__ void stage_input(const GemvIn &in, int K, float *xs, float *dl, float *sh) {
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+        xs[i] = in.resid_in[i];
+        if (in.delta) dl[i] = in.delta[i];
+    }
+    __syncthreads();
+    if (in.delta) {
+        const float r = rms_inv_of(lds_sum_sq(dl, K, sh), K, in.eps);
+        for (int i = threadIdx.x; i < K; i += blockDim.x)
+            xs[i] = __fadd_rn(xs[i], __fmul_rn(__fmul_rn(dl[i], r), __fadd_rn(1.0f, in.w_delta[i])));
+        __syncthreads();
+    }
     if (in.resid_out && blockIdx.x == 0)
         for (int i = threadIdx.x; i < K; i += blockDim.x) in.resid_out[i] = xs[i];
     if (in.w_norm) {
-        const float r = rms_inv_of(block_sum_sq_ref(xs, K, sh), K, in.eps);   // synchronises
+        const float r = rms_inv_of(lds_sum_sq(xs, K, sh), K, in.eps);   // synchronises
         for (int i = threadIdx.x; i < K; i += blockDim.x)
             xs[i] = __fmul_rn(__fmul_rn(xs[i], r), __fadd_rn(1.0f, in.w_norm[i]));
     }
@@ -61,34 +98,50 @@ template <int DT> struct QB;
 template <> struct QB<DT_Q4_0> { static constexpr int BYTES = 16, WORDS = 4; };
 template <> struct QB<DT_Q8_0> { static constexpr int BYTES = 32, WORDS = 8; };
 
-// This lane's block of `row` times x: scale * sum(int * x) (0 for a lane off the matrix).
+// The quants and scale of this lane's block of `row` (zeros for a lane off the matrix),
+// loaded before the input vector is staged so their latency overlaps the prologue.
 template <int DT>
-__device__ __forceinline__ float lane_block(const QMat &w, int row, int blk, int nb, const float (&xv)[32], float xsum,
-                                            bool on) {
-    if (!on || row >= w.M) return 0.f;
-    const size_t bi = (size_t)row * nb + blk;
+struct LaneBlock {
     uint32_t q[QB<DT>::WORDS];
+    float s;
+};
+
+template <int DT>
+__device__ __forceinline__ void load_lane_block(const QMat &w, int row, int blk, int nb, bool on, LaneBlock<DT> &b) {
+    const bool ok = on && row < w.M;
+    const size_t bi = ok ? (size_t)row * nb + blk : 0;
     const u32x4 *qp = reinterpret_cast<const u32x4 *>(w.q + bi * QB<DT>::BYTES);
 #pragma unroll
     for (int i = 0; i < QB<DT>::WORDS / 4; ++i) {
         const u32x4 t = __builtin_nontemporal_load(qp + i);
-        q[4 * i + 0] = t.x; q[4 * i + 1] = t.y; q[4 * i + 2] = t.z; q[4 * i + 3] = t.w;
+        b.q[4 * i + 0] = t.x; b.q[4 * i + 1] = t.y; b.q[4 * i + 2] = t.z; b.q[4 * i + 3] = t.w;
     }
-    const float s = w.s[bi];
-    if constexpr (DT == DT_Q4_0) return s * dot_q4(q, xv, xsum);
-    else return s * dot_q8(q, xv, xsum);
+    b.s = ok ? w.s[bi] : 0.f;
 }
 
+template <int DT>
+__device__ __forceinline__ float block_value(const LaneBlock<DT> &b, const float (&xv)[32], float xsum) {
+    if constexpr (DT == DT_Q4_0) return b.s * dot_q4(b.q, xv, xsum);
+    else return b.s * dot_q8(b.q, xv, xsum);
+}
+
+// One wave-step per wave: rps rows of w0 (and of w1 for the GeGLU form).
 template <int DT, bool GEGLU>
 __global__ __launch_bounds__(kThreads) void dec_gemv_kernel(QMat w0, QMat w1, GemvIn in, float *__restrict__ y) {
     __shared__ float xs[kDecMaxK];
+    __shared__ float dl[kDecMaxK];
     __shared__ float sh[16];
     const int K = w0.K, M = w0.M;
-    stage_input(in, K, xs, sh);
     const int nb = K / kBlock, rps = kWave / nb;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int r_in = lane / nb, blk = lane - r_in * nb;
     const bool on = r_in < rps;
+    const int st = blockIdx.x * (kThreads / kWave) + wid;
+    const int row = st * rps + r_in;
+    LaneBlock<DT> b0, b1;
+    load_lane_block<DT>(w0, row, blk, nb, on, b0);
+    if constexpr (GEGLU) load_lane_block<DT>(w1, row, blk, nb, on, b1);
+    stage_input(in, K, xs, dl, sh);
     float xv[32];
     float xsum = 0.f;
 #pragma unroll
@@ -96,41 +149,47 @@ __global__ __launch_bounds__(kThreads) void dec_gemv_kernel(QMat w0, QMat w1, Ge
         xv[i] = on ? xs[blk * kBlock + i] : 0.f;
         xsum += xv[i];
     }
-    const int wsteps = (M + rps - 1) / rps;
-    for (int st = blockIdx.x * (kThreads / kWave) + wid; st < wsteps; st += gridDim.x * (kThreads / kWave)) {
-        const int row = st * rps + r_in;
-        const float p0 = lane_block<DT>(w0, row, blk, nb, xv, xsum, on);
-        float p1 = 0.f;
-        if constexpr (GEGLU) p1 = lane_block<DT>(w1, row, blk, nb, xv, xsum, on);
-        for (int r = 0; r < rps; ++r) {
-            const float t0 = wave_sum(r_in == r ? p0 : 0.f);
-            float v = t0;
-            if constexpr (GEGLU) v = __fmul_rn(gelu_ref(t0), wave_sum(r_in == r ? p1 : 0.f));
-            const int orow = st * rps + r;
-            if (lane == r && orow < M) y[orow] = v;
-        }
+    const float p0 = block_value<DT>(b0, xv, xsum);
+    float p1 = 0.f;
+    if constexpr (GEGLU) p1 = block_value<DT>(b1, xv, xsum);
+    for (int r = 0; r < rps; ++r) {
+        const float t0 = wave_sum(r_in == r ? p0 : 0.f);
+        float v = t0;
+        if constexpr (GEGLU) v = __fmul_rn(gelu_ref(t0), wave_sum(r_in == r ? p1 : 0.f));
+        const int orow = st * rps + r;
+        if (lane == r && orow < M) y[orow] = v;
     }
 }
 
 __global__ __launch_bounds__(kThreads) void dec_prologue_kernel(GemvIn in, int K, float *__restrict__ out) {
     __shared__ float xs[kDecMaxK];
+    __shared__ float dl[kDecMaxK];
     __shared__ float sh[16];
-    stage_input(in, K, xs, sh);
+    stage_input(in, K, xs, dl, sh);
     for (int i = threadIdx.x; i < K; i += blockDim.x) out[i] = xs[i];
 }
 
 // ---- attention ----
 
-// Sums of squares of nv consecutive vectors of length hd, each in the reference order of
-// sum_sq_avx2 (eight sequential lanes, then the fixed tree and a sequential tail); eight
-// threads per vector. Result in ss[v].
-__device__ void vectors_sum_sq(const float *__restrict__ base, int nv, int hd, float *part8, float *ss) {
+// Sums of squares of nv consecutive vectors of length hd in LDS, each in the reference
+// order of sum_sq_avx2 (eight sequential lanes, then the fixed tree and a sequential
+// tail); eight threads per vector, loading eight elements ahead. Result in ss[v].
+__device__ void vectors_sum_sq(const float *base, int nv, int hd, float *part8, float *ss) {
     const int t = threadIdx.x;
     if (t < 8 * nv) {
         const int v = t / 8, l = t - 8 * v;
         const float *p = base + (size_t)v * hd;
+        const int full = hd & ~7;
         float s = 0.f;
-        for (int i = l; i < (hd & ~7); i += 8) s = __builtin_fmaf(p[i], p[i], s);
+        int i = l;
+        for (; i + 56 < full; i += 64) {
+            float w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = p[i + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s = __builtin_fmaf(w[u], w[u], s);
+        }
+        for (; i < full; i += 8) s = __builtin_fmaf(p[i], p[i], s);
         part8[t] = s;
     }
     __syncthreads();
@@ -145,9 +204,9 @@ __device__ void vectors_sum_sq(const float *__restrict__ base, int nv, int hd, f
     __syncthreads();
 }
 
-// dst[v] = rope(rmsnorm_delta(src[v], g)) for nv head vectors, into LDS (attention.c:221-309;
-// rope_apply_fast rope.c:99-117 with the fused forms of the reference build).
-__device__ void norm_rope_heads(const float *__restrict__ src, int nv, int hd, const float *__restrict__ g,
+// dst[v] = rope(rmsnorm_delta(src[v], g)) for nv head vectors held in LDS (attention.c:
+// 221-309; rope_apply_fast rope.c:99-117 with the fused forms of the reference build).
+__device__ void norm_rope_heads(const float *src, int nv, int hd, const float *__restrict__ g,
                                 const float *__restrict__ cs, const float *__restrict__ sn, float eps, float *dst,
                                 float *part8, float *ss) {
     vectors_sum_sq(src, nv, hd, part8, ss);
@@ -172,6 +231,7 @@ __device__ void norm_rope_heads(const float *__restrict__ src, int nv, int hd, c
 // merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL).
 template <int DPL, int NH>
 __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
+    __shared__ float raw[kAttnMaxQ + 2 * kAttnMaxKV];   // q | k | v as projected
     __shared__ float qs[kAttnMaxQ];
     __shared__ float ks[kAttnMaxKV];
     __shared__ float part8[8 * 16];
@@ -181,10 +241,41 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     const int hd = a.hd, nkv = a.nkv;
     const int pos = *a.d_pos, seq = pos + 1;
     const int start = (a.window > 0 && seq > a.window) ? seq - a.window : 0;
+    const int len = seq - start, nsplit = gridDim.x;
+    const int chunk = (len + nsplit - 1) / nsplit;
+    const int t0 = start + blockIdx.x * chunk, t1 = min(seq, t0 + chunk);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int group = NH / nkv;
+    // The wave's positions t0 + wid + 4j, PF at a time: every K/V row of a batch is loaded
+    // before its first score is formed. Rows come from the cache; the row of the current
+    // position is taken from this kernel's own K (after RoPE) and V.
+    constexpr int PF = 4;
+    constexpr int NW = kThreads / kWave;
+    float kr[PF][2][DPL], vr[PF][2][DPL];   // up to two K/V heads per row
+    auto load_batch = [&](int tb) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const int t = tb + j * NW;
+#pragma unroll
+            for (int hk = 0; hk < 2; ++hk) {
+                const bool ok = t < t1 && t != pos && hk < nkv;
+                const size_t off = ok ? ((size_t)hk * a.max_ctx + t) * hd : 0;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) {
+                    kr[j][hk][d] = ok ? a.kc[off + lane * DPL + d] : 0.f;
+                    vr[j][hk][d] = ok ? a.vc[off + lane * DPL + d] : 0.f;
+                }
+            }
+        }
+    };
+    if (t0 + wid < t1) load_batch(t0 + wid);   // in flight during the prologue
+
+    for (int i = threadIdx.x; i < (NH + 2 * nkv) * hd; i += blockDim.x) raw[i] = a.qkv[i];
+    __syncthreads();
     const float *cs = a.cos_t + (size_t)pos * hd, *sn = a.sin_t + (size_t)pos * hd;
-    norm_rope_heads(a.qkv, NH, hd, a.qn, cs, sn, a.eps, qs, part8, ss);
-    norm_rope_heads(a.qkv + NH * hd, nkv, hd, a.kn, cs, sn, a.eps, ks, part8, ss);
-    const float *vnew = a.qkv + (NH + nkv) * hd;
+    norm_rope_heads(raw, NH, hd, a.qn, cs, sn, a.eps, qs, part8, ss);
+    norm_rope_heads(raw + NH * hd, nkv, hd, a.kn, cs, sn, a.eps, ks, part8, ss);
+    const float *vnew = raw + (NH + nkv) * hd;
     if (blockIdx.x == 0)   // kv_cache_write_token: [head][pos][dim]
         for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) {
             const int h = i / hd, d = i - h * hd;
@@ -193,11 +284,6 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
             a.vc[off] = vnew[i];
         }
 
-    const int len = seq - start, nsplit = gridDim.x;
-    const int chunk = (len + nsplit - 1) / nsplit;
-    const int t0 = start + blockIdx.x * chunk, t1 = min(seq, t0 + chunk);
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    const int group = NH / nkv;
     float m[NH], s[NH], o[NH][DPL];
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -206,31 +292,38 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 #pragma unroll
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
-    for (int t = t0 + wid; t < t1; t += kThreads / kWave) {
-        float kv[DPL], vv[DPL];
+    for (int tb = t0 + wid; tb < t1; tb += PF * NW) {
+        if (tb != t0 + wid) load_batch(tb);
 #pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            if (h % group == 0) {   // the heads of one group share a K/V row
-                const int hk = h / group;
-                const float *krow = t == pos ? ks + hk * hd : a.kc + ((size_t)hk * a.max_ctx + t) * hd;
-                const float *vrow = t == pos ? vnew + hk * hd : a.vc + ((size_t)hk * a.max_ctx + t) * hd;
+        for (int j = 0; j < PF; ++j) {
+            const int t = tb + j * NW;
+            if (t >= t1) break;
+            if (t == pos) {
 #pragma unroll
-                for (int d = 0; d < DPL; ++d) {
-                    kv[d] = krow[lane * DPL + d];
-                    vv[d] = vrow[lane * DPL + d];
-                }
+                for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+                    for (int d = 0; d < DPL; ++d) {
+                        kr[j][hk][d] = hk < nkv ? ks[hk * hd + lane * DPL + d] : 0.f;
+                        vr[j][hk][d] = hk < nkv ? vnew[hk * hd + lane * DPL + d] : 0.f;
+                    }
             }
-            float dp = 0.f;
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) dp = __builtin_fmaf(qs[h * hd + lane * DPL + d], kv[d], dp);
-            const float score = __fmul_rn(wave_sum(dp), a.scale);
-            const float mn = fmaxf(m[h], score);
-            const float c = m[h] == -INFINITY ? 0.f : expf(m[h] - mn);
-            const float p = expf(score - mn);
-            s[h] = __builtin_fmaf(s[h], c, p);
+            for (int h = 0; h < NH; ++h) {
+                const int hk = h / group;
+                float dp = 0.f;
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) o[h][d] = __builtin_fmaf(o[h][d], c, p * vv[d]);
-            m[h] = mn;
+                for (int d = 0; d < DPL; ++d)
+                    dp = __builtin_fmaf(qs[h * hd + lane * DPL + d], hk == 0 ? kr[j][0][d] : kr[j][1][d], dp);
+                const float score = __fmul_rn(wave_sum(dp), a.scale);
+                const float mn = fmaxf(m[h], score);
+                const float c = m[h] == -INFINITY ? 0.f : expf(m[h] - mn);
+                const float p = expf(score - mn);
+                s[h] = __builtin_fmaf(s[h], c, p);
+#pragma unroll
+                for (int d = 0; d < DPL; ++d)
+                    o[h][d] = __builtin_fmaf(o[h][d], c, p * (hk == 0 ? vr[j][0][d] : vr[j][1][d]));
+                m[h] = mn;
+            }
         }
     }
     // merge the four waves
@@ -267,21 +360,32 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 // out[h*hd + d] = sum_b e_b o_b[d] / sum_b e_b s_b with e_b = exp(m_b - max_b m_b): the
 // softmax-weighted sum of values of attention.c:140-158 over all slices. One workgroup per
 // head, one thread per dim.
-__global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float *__restrict__ part, int nsplit, int nh,
-                                                                    int hd, float *__restrict__ out) {
-    const int h = blockIdx.x;
-    float M = -INFINITY;
-    for (int b = 0; b < nsplit; ++b) M = fmaxf(M, part[((size_t)b * nh + h) * (hd + 2) + hd]);
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float S = 0.f, O = 0.f;
-        for (int b = 0; b < nsplit; ++b) {
-            const float *p = part + ((size_t)b * nh + h) * (hd + 2);
-            if (p[hd] == -INFINITY) continue;
-            const float e = expf(p[hd] - M);
-            S = __builtin_fmaf(p[hd + 1], e, S);
-            O = __builtin_fmaf(p[d], e, O);
-        }
-        out[h * hd + d] = O / S;
+template <int NS>
+__global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float *__restrict__ part, int nh, int hd,
+                                                                    float *__restrict__ out) {
+    static_assert(NS <= kWave, "one lane of wave 0 per slice");
+    __shared__ float es[NS];
+    __shared__ float S;
+    const int h = blockIdx.x, t = threadIdx.x;
+    if (t < kWave) {
+        const float *p = part + ((size_t)t * nh + h) * (hd + 2);
+        const float mb = t < NS ? p[hd] : -INFINITY;
+        const float sb = t < NS ? p[hd + 1] : 0.f;
+        float M = mb;
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
+        const float e = mb == -INFINITY ? 0.f : expf(mb - M);
+        if (t < NS) es[t] = e;
+        const float tot = wave_sum(e * sb);
+        if (t == 0) S = tot;
+    }
+    __syncthreads();
+    const float inv = 1.0f / S;
+    for (int d = t; d < hd; d += blockDim.x) {
+        float O = 0.f;
+#pragma unroll 16
+        for (int b = 0; b < NS; ++b) O = __builtin_fmaf(part[((size_t)b * nh + h) * (hd + 2) + d], es[b], O);
+        out[h * hd + d] = O * inv;
     }
 }
 
@@ -313,7 +417,7 @@ int launch_gemv_kernel(const QMat &w0, const QMat &w1, const GemvIn &in, float *
     }
     const int rps = kWave / nb;
     const int wsteps = (w0.M + rps - 1) / rps;
-    const int blocks = (wsteps + 3) / 4;
+    const int blocks = (wsteps + 3) / 4;   // one wave-step per wave
     hipLaunchKernelGGL((dec_gemv_kernel<DT, GEGLU>), dim3(blocks), dim3(kThreads), 0, st, w0, w1, in, y);
     return hip_ok(hipGetLastError(), "dec_gemv launch") ? 0 : -1;
 }
@@ -344,7 +448,7 @@ int dec_prologue_only(const GemvIn &in, int K, float *out, hipStream_t s) {
 }
 
 int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
-    if (a.nh * a.hd > kAttnMaxQ || a.nkv * a.hd > kAttnMaxKV || a.nkv <= 0 || a.nh % a.nkv != 0 ||
+    if (a.nh * a.hd > kAttnMaxQ || a.nkv * a.hd > kAttnMaxKV || a.nkv <= 0 || a.nkv > 2 || a.nh % a.nkv != 0 ||
         a.hd % kWave != 0 || a.hd > 4 * kWave || a.nh + a.nkv > 16) {
         set_error("attention shape not supported (heads %d/%d, head_dim %d)", a.nh, a.nkv, a.hd);
         return -1;
@@ -360,7 +464,7 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     }
 #undef SPH_ATTN
     if (!hip_ok(hipGetLastError(), "attention launch")) return -1;
-    hipLaunchKernelGGL(dec_attn_combine_kernel, dim3(a.nh), dim3(kThreads), 0, s, a.part, kAttnSplit, a.nh, a.hd, out);
+    hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplit>, dim3(a.nh), dim3(kThreads), 0, s, a.part, a.nh, a.hd, out);
     return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
 }
 

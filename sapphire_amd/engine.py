@@ -114,12 +114,14 @@ class Decoder:
             pass
 
 
-def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, reps: int = 3):
+def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, reps: int = 3, m=None, kv=None):
     """Greedy decode of the Gemma-3-270M-shaped Q4_0 model (KV prefilled to `prefill` of
-    2048 positions): tokens/s over `steps` steps, best of `reps` runs after a warm-up."""
+    2048 positions): tokens/s over `steps` steps, best of `reps` runs after a warm-up.
+    `m` / `kv` reuse an already generated model and prefilled caches."""
     cfg = smodel.GEMMA3_270M
-    m = smodel.synthetic_model(cfg, seed)
-    k, v = m.kv_prefill(prefill)
+    if m is None:
+        m = smodel.synthetic_model(cfg, seed)
+    k, v = kv if kv is not None else m.kv_prefill(prefill)
     dec = Decoder(m)
     tok = smodel.start_token(cfg, seed)
     dec.set_kv(k, v)
