@@ -33,10 +33,11 @@ enum { SAPPHIRE_F32 = 0, SAPPHIRE_BF16 = 1, SAPPHIRE_F16 = 2, SAPPHIRE_Q4_0 = 3,
  *           sapphire_q_repack_dev: quants [M][nb][16|32] bytes (byte order of the
  *           reference block), then, at offset sapphire_q_scales_offset(), fp32
  *           scales [M][nb]. Values are bit-identical; only their placement differs.
- *  TILED  : the matrix-core layout of long matrices (K/128 in {5, 8, 9}): 16-row tiles,
- *           4-block groups, each group's quants stored in the order the MFMA operand
- *           registers of a wave take them (one contiguous KiB per load instruction),
- *           then fp32 scales [tile][group][block][row]. Rows past M are zero. */
+ *  TILED  : the matrix-core layout (K a multiple of 128): 16-row tiles, 4-block groups,
+ *           each group's quants stored in the order the MFMA operand registers of a wave
+ *           take them (one contiguous KiB per load instruction), then fp32 scales
+ *           [tile][group][block][row]. Rows past M are zero. The batch-1 GEMV runs on it
+ *           for K/128 in {5, 8, 9}; the batched GEMM for every K. */
 enum { SAPPHIRE_LAYOUT_AOS = 0, SAPPHIRE_LAYOUT_PACKED = 1, SAPPHIRE_LAYOUT_TILED = 2 };
 
 const char *sapphire_last_error(void);
@@ -84,6 +85,17 @@ int sapphire_gemv_q_dev(int dtype, int layout, const void *w, int M, int K,
                         const float *x, float *y, void *stream);
 /* y[M] = W[M,K] . x[K] for F32 or BF16 row-major W (f32_avx.c:44-83, bf16_avx.c:55-108). */
 int sapphire_gemv_f_dev(int dtype, const void *w, int M, int K, const float *x, float *y, void *stream);
+
+/* Y[b][M] = W[M,K] . X[b][K] for b < batch: the batched GEMV of kernel_gemm /
+ * kernel_gemv_batch (dispatch.c:87-99, 234-266) for Q4_0/Q8_0, which the reference
+ * itself rejects (pool.c:318-321); its meaning is `batch` independent kernel_gemv calls.
+ * X and Y are row-major [batch][K] / [batch][M]. On the TILED layout the rows run on the
+ * fp16 matrix cores, 16 sequences per pass (longer batches loop), with `ws` holding
+ * sapphire_gemm_workspace_bytes(dtype, M, K) bytes of device memory; on AOS/PACKED it is
+ * the vector kernel and ws may be NULL. */
+size_t sapphire_gemm_workspace_bytes(int dtype, int M, int K);
+int sapphire_gemm_q_dev(int dtype, int layout, const void *w, int M, int K, const float *X, int batch,
+                        float *Y, void *ws, void *stream);
 
 /* ---- LM-head epilogue ----
  * probs = softmax(logits) (utils.c:18-59) written to probs (may equal logits) and the

@@ -13,8 +13,8 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libsapphire_hip.so")
-SOURCES = ["runtime.cpp", "tensor.cpp", "dispatch.cpp", "decoder.cpp", "gemv.hip", "gemv_mfma.hip", "ops.hip",
-           "decode.hip"]
+SOURCES = ["runtime.cpp", "tensor.cpp", "dispatch.cpp", "decoder.cpp", "gemv.hip", "gemv_mfma.hip", "gemm_mfma.hip",
+           "ops.hip", "decode.hip"]
 ARCH = os.environ.get("SAPPHIRE_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [

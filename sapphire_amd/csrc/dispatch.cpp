@@ -133,10 +133,13 @@ int gemv_exec(kernel_context_t *c, const tensor_t *A, const float *X, float *Y, 
     std::lock_guard<std::mutex> g(c->mu);
     if (!hip_ok(hipSetDevice(c->device), "hipSetDevice")) return -1;
     int layout = 0;
-    const void *w = tensor_device_weights(A, &layout, c->stream);
+    // batches of quantized rows run on the matrix cores from a TILED copy when K allows it
+    const bool mm = is_quant(dt) && batch > 1 && tiled_layout_ok(dt, M, Kp);
+    const void *w = mm ? tensor_device_tiled(A, c->stream) : tensor_device_weights(A, &layout, c->stream);
     if (!w) return -1;
     const size_t xb = (size_t)batch * Kp * sizeof(float), yb = (size_t)batch * M * sizeof(float);
-    if (!ensure_staging(c, align256(xb) + align256(yb), align256(xb) + align256(yb))) return -1;
+    const size_t wsb = mm ? gemm_workspace_bytes(M, Kp) : 0;
+    if (!ensure_staging(c, align256(xb) + align256(yb), align256(xb) + align256(yb) + wsb)) return -1;
     char *hb = static_cast<char *>(c->h_stage);
     char *db = static_cast<char *>(c->d_stage);
     float *hx = reinterpret_cast<float *>(hb), *hy = reinterpret_cast<float *>(hb + align256(xb));
@@ -148,8 +151,11 @@ int gemv_exec(kernel_context_t *c, const tensor_t *A, const float *X, float *Y, 
     if (!hip_ok(hipMemcpyAsync(dx, hx, xb, hipMemcpyHostToDevice, c->stream), "H2D x")) return -1;
     int rc;
     if (is_quant(dt)) {
-        rc = batch == 1 ? launch_gemv_q(dt, layout, w, M, Kp, dx, dy, c->stream)
-                        : launch_gemm_q(dt, layout, w, M, Kp, dx, dy, batch, c->stream);
+        if (mm)
+            rc = launch_gemm_tiled(dt, w, M, Kp, dx, batch, dy, db + align256(xb) + align256(yb), c->stream);
+        else
+            rc = batch == 1 ? launch_gemv_q(dt, layout, w, M, Kp, dx, dy, c->stream)
+                            : launch_gemm_q(dt, layout, w, M, Kp, dx, dy, batch, c->stream);
     } else {
         rc = 0;
         for (int b = 0; b < batch && rc == 0; ++b)

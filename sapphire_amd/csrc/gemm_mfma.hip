@@ -1,0 +1,362 @@
+// gemm_mfma.hip - Q4_0 / Q8_0 weights times a batch of up to 16 activation vectors on the
+// CDNA4 matrix cores: Y[b][r] = sum_k W[r][k] * X[b][k], the batched form of kernel_gemv
+// (dispatch.c:101-156; the reference itself rejects quantized batches, pool.c:318-321, so
+// its meaning here is 16 independent GEMVs).
+//
+// Operands of v_mfma_f32_16x16x32_f16, one MFMA per 32-weight block and activation term:
+//  * B (16 columns = 16 weight rows of a TILED tile): the integer weights, converted exactly
+//    to fp16 in registers: a nibble or a sign-flipped byte is placed under the fp16 exponent
+//    of 1024 (0x64nn) with v_perm and the bias removed with one packed fp16 subtract.
+//  * A (16 rows = the sequences): x split into fp16 hi + lo terms, x * 2^-e = hi + lo to
+//    about 22 bits, with one power-of-two range scale e per sequence and K chunk, so that
+//    the largest |x| of the chunk sits in [2^14, 2^15). Two MFMAs (hi, lo) per block.
+//  * C: per lane the four sequences 4m..4m+3 of weight row n; the block's weight scale is
+//    applied with one FMA per value, the chunk's 2^e when the tile's result is stored.
+//
+// A workgroup of eight waves converts its K chunk (at most 36 blocks) of the 16 activation
+// vectors into the A operands in LDS once, then each wave streams whole tiles through it.
+// A wave's (tile, 4-block group) units run through a ring of register buffers: the loads of
+// the next kRing-1 units are in flight while one unit is multiplied. K longer than one
+// chunk is split over workgroups (grid.y) and gemm_reduce_kernel adds the partial sums.
+#include <algorithm>
+
+#include "internal.h"
+
+namespace sapphire {
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWaves = 8;                              // waves per workgroup
+constexpr int kThreads = kWave * kWaves;
+constexpr int kTileRows = 16;
+constexpr int kGroupBlocks = 4;
+constexpr int kChunkBlocks = 36;                       // A operands staged per workgroup (72 KiB)
+constexpr int kBatchMax = 16;
+constexpr int kRing = 6;                               // units in flight per wave
+constexpr int kNT = 2;                                 // streaming (non-temporal) weight loads
+// (block, quarter) pairs of a chunk handled by one staging thread
+constexpr int kStagePairs = (kChunkBlocks * 4 + kThreads / kBatchMax - 1) / (kThreads / kBatchMax);
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// k order of the 8 values a lane holds for one block, and the factor of its weight. Q8_0:
+// elements 8m+0..7 in order, weights as they are. Q4_0: elements 8m + {0,4,1,5,2,6,3,7},
+// the high nibbles (odd elements) left in place as 16 * (nib - 8), so their activations
+// are staged divided by 16 (exact: a power of two).
+template <int DT>
+__device__ __forceinline__ int k_order(int i) {
+    if constexpr (DT == DT_Q8_0) return i;
+    else return (i >> 1) + 4 * (i & 1);
+}
+template <int DT>
+__device__ __forceinline__ float k_factor(int i) {
+    if constexpr (DT == DT_Q8_0) return 1.0f;
+    else return (i & 2) ? 0.0625f : 1.0f;
+}
+
+// a ? (q ^ b) : b for every bit, in one v_bitop3_b32. Its 8-bit table is indexed by
+// {S0, S1, S2} (S0 the most significant bit): with S0 = q, S1 = a, S2 = b that is
+// ((0xf0 ^ 0xaa) & 0xcc) | (0xaa & ~0xcc) = 0x6a.
+__device__ __forceinline__ uint32_t mask_xor_or(uint32_t q, uint32_t a, uint32_t b) {
+    uint32_t d;
+    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(d) : "v"(q), "v"(a), "v"(b));
+    return d;
+}
+
+// Exact fp16 weights of block j of a lane's group registers, for the MFMA B operand.
+template <int DT>
+__device__ __forceinline__ h8 b_operand(const u32x4 (&a)[2], int j, uint32_t kLoMask, uint32_t kHiMask,
+                                        uint32_t kLoBits, uint32_t kHiBits) {
+    uint32_t w[4];
+    _Float16 bias[4];
+    if constexpr (DT == DT_Q4_0) {
+        // TILED holds nib ^ 8. Halves 0x6400 | nib = 1024 + nib (low nibbles of bytes 0, 2 /
+        // 1, 3) and 0x6400 | nib << 4 = 1024 + 16 nib (high nibbles)
+        const uint32_t q = a[0][j], q8 = q >> 8;
+        w[0] = mask_xor_or(q, kLoMask, kLoBits);
+        w[1] = mask_xor_or(q, kHiMask, kHiBits);
+        w[2] = mask_xor_or(q8, kLoMask, kLoBits);
+        w[3] = mask_xor_or(q8, kHiMask, kHiBits);
+        bias[0] = bias[2] = (_Float16)1032.0f;             // 1024 + 8
+        bias[1] = bias[3] = (_Float16)1152.0f;             // 1024 + 16 * 8
+    } else {
+        const u32x4 h = a[j >> 1];
+        const uint32_t lo = ((j & 1) ? h.z : h.x) ^ 0x80808080u, hi = ((j & 1) ? h.w : h.y) ^ 0x80808080u;
+        // halves 0x64uu = 1024 + (q + 128)
+        w[0] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+        w[1] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+        w[2] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+        w[3] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+        bias[0] = bias[1] = bias[2] = bias[3] = (_Float16)1152.0f;   // 1024 + 128
+    }
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h2 v = __builtin_bit_cast(h2, w[i]) - h2{bias[i], bias[i]};   // exact small integers
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+// One ring slot: the weight quants (1 or 2 KiB per wave) and the four block scales of row n.
+struct Unit {
+    u32x4 a[2];
+    float s[4];
+};
+
+// Loads of unit (tile, group) gb: the lane's 16 (or 2 x 16) quant bytes and row n's four
+// block scales. The unit offset is wave-uniform (scalar offset), the lane part constant.
+template <int DT>
+__device__ __forceinline__ void unit_issue(Unit &u, __amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rs,
+                                           uint32_t gb, int lane, int n) {
+    constexpr int NQ = DT == DT_Q8_0 ? 2 : 1;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h)
+        u.a[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16u + h * 1024u, gb * (NQ * 1024u), kNT));
+    if constexpr (NQ == 1) u.a[1] = u.a[0];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        u.s[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, n * 4u + j * 64u, gb * 256u, kNT));
+}
+
+struct BConst {
+    uint32_t lo_mask, hi_mask, lo_bits, hi_bits;
+};
+
+template <int DT>
+__device__ __forceinline__ void unit_mfma(const Unit &u, const h8 *__restrict__ xs, int bl, int lane, f4 &acc,
+                                          const BConst &k) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const h8 bop = b_operand<DT>(u.a, j, k.lo_mask, k.hi_mask, k.lo_bits, k.hi_bits);
+        f4 C = {0.f, 0.f, 0.f, 0.f};
+        C = __builtin_amdgcn_mfma_f32_16x16x32_f16(xs[((bl + j) * 2 + 0) * kWave + lane], bop, C, 0, 0, 0);
+        C = __builtin_amdgcn_mfma_f32_16x16x32_f16(xs[((bl + j) * 2 + 1) * kWave + lane], bop, C, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(C[r], u.s[j], acc[r]);
+    }
+}
+
+// grid.x: workgroups over the tiles (grid-stride), grid.y: K chunks of `cb` blocks.
+// Y[b][r] = sum over the chunk (grid.y == 1), else Yp[chunk][b][r].
+template <int DT>
+__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const uint8_t *__restrict__ wq, uint32_t q_bytes,
+                                                             const uint8_t *__restrict__ wsc, uint32_t s_bytes,
+                                                             const float *__restrict__ X, int batch, int M, int K,
+                                                             int cb, float *__restrict__ Y, float *__restrict__ Yp) {
+    __shared__ h8 xs[kChunkBlocks * 2 * kWave];        // [block][hi/lo][lane 16m + seq]
+    __shared__ float wmax[kWaves][kBatchMax];
+    __shared__ float xsc[kBatchMax];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    const int nb = K / kBlock, G = nb / kGroupBlocks;
+    const int b0 = blockIdx.y * cb, b1 = min(nb, b0 + cb);
+
+    // ---- the first kRing-1 units' weight loads go out before the staging ----
+    // Unit counters are wave-uniform (scalar registers, scalar branches).
+    const int n = lane & 15, m = lane >> 4;
+    const int ntiles = (M + kTileRows - 1) / kTileRows;
+    const int g0 = b0 / kGroupBlocks, gc = (b1 - b0) / kGroupBlocks;
+    const int tstride = gridDim.x * kWaves;
+    const int t0 = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(wid);
+    const bool idle = t0 >= ntiles;           // no tile: stages, then leaves
+    const int U = idle ? 0 : (ntiles - t0 + tstride - 1) / tstride * gc;   // units of this wave
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(wq, q_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(wsc, s_bytes);
+
+    // bit masks of the Q4_0 expansion: nibble fields (low / high nibble of bytes 0 and 2),
+    // and outside them the fp16 exponent of 1024, inside them the bits that undo nib ^ 8
+    BConst bk = {0x000F000Fu, 0x00F000F0u, 0x64086408u, 0x64806480u};
+    asm volatile("" : "+v"(bk.lo_mask), "+v"(bk.hi_mask), "+v"(bk.lo_bits), "+v"(bk.hi_bits));
+    Unit ring[kRing];
+    // issue pointer: group offset (tile * G + g) of unit u + kRing - 1; loads past the last
+    // unit repeat it. The offset goes in the scalar offset field, which the buffer range
+    // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
+    int igb = (idle ? 0 : t0) * G + g0, ig = 0, issued = 0;
+#pragma unroll
+    for (int p = 0; p < kRing - 1; ++p) {
+        unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
+        if (issued < U - 1) {
+            ++issued;
+            if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
+        }
+    }
+    // ---- stage the chunk: range scale per sequence, then the hi/lo operands ----
+    {
+        const int seq = tid & (kBatchMax - 1), q = tid / kBatchMax;   // q: 0..31
+        const int pairs = (b1 - b0) * 4;
+        float v[kStagePairs][8];
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < kStagePairs; ++i) {
+            const int p = q + i * (kThreads / kBatchMax);
+            if (p < pairs && seq < batch) {
+                const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)seq * K + (size_t)b0 * kBlock + p * 8);
+                const float4 lo = src[0], hi = src[1];
+                v[i][0] = lo.x; v[i][1] = lo.y; v[i][2] = lo.z; v[i][3] = lo.w;
+                v[i][4] = hi.x; v[i][5] = hi.y; v[i][6] = hi.z; v[i][7] = hi.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[i][e]));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        if (lane < kBatchMax) wmax[wid][lane] = mx;
+        __syncthreads();
+        mx = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wmax[w][seq]);
+        // e: the chunk's largest |x| * 2^-e in [2^14, 2^15) (finite in fp16, lo term normal)
+        int e = 0;
+        if (mx > 0.f) {
+            int ex;
+            frexpf(mx, &ex);
+            e = ex - 15;
+        }
+        if (q == 0) xsc[seq] = ldexpf(1.0f, e);
+#pragma unroll
+        for (int i = 0; i < kStagePairs; ++i) {
+            const int p = q + i * (kThreads / kBatchMax);
+            if (p < pairs) {
+                h8 hv, lv;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float s = ldexpf(v[i][k_order<DT>(k)], -e) * k_factor<DT>(k);
+                    const _Float16 h = (_Float16)s;
+                    hv[k] = h;
+                    lv[k] = (_Float16)(s - (float)h);
+                }
+                const int bl = p >> 2, m = p & 3;
+                xs[(bl * 2 + 0) * kWave + m * 16 + seq] = hv;
+                xs[(bl * 2 + 1) * kWave + m * 16 + seq] = lv;
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- stream the tiles: units (tile, group) through the register ring ----
+    if (idle) return;
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = xsc[4 * m + r];
+    int ct = t0, cg = 0;                               // tile and group of the unit multiplied
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    // Every pass issues the loads of all kRing slots (past the last unit they repeat it), so
+    // each path through the loop has the same load order and the waits stay kRing-1 units
+    // deep; only the multiplication of units past the end is skipped.
+    for (int base = 0; base < U; base += kRing) {
+#pragma unroll
+        for (int p = 0; p < kRing; ++p) {
+            unit_issue<DT>(ring[(p + kRing - 1) % kRing], rq, rs, (uint32_t)igb, lane, n);
+            if (issued < U - 1) {
+                ++issued;
+                if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
+            }
+            if (base + p < U) {
+                unit_mfma<DT>(ring[p], xs, cg * kGroupBlocks, lane, acc, bk);
+                if (++cg == gc) {
+                    const int row = ct * kTileRows + n;
+                    if (row < M) {
+                        float *dst = gridDim.y == 1 ? Y : Yp + (size_t)blockIdx.y * batch * M;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (4 * m + r < batch) dst[(size_t)(4 * m + r) * M + row] = acc[r] * sc[r];
+                    }
+                    acc = f4{0.f, 0.f, 0.f, 0.f};
+                    cg = 0;
+                    ct += tstride;
+                }
+            }
+        }
+    }
+}
+
+__global__ void gemm_reduce_kernel(const float *__restrict__ Yp, int nsplit, size_t n, float *__restrict__ Y) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float s = 0.f;
+        for (int c = 0; c < nsplit; ++c) s += Yp[(size_t)c * n + i];
+        Y[i] = s;
+    }
+}
+
+int cus() {
+    int dev = 0, c = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+        return 256;
+    return c;
+}
+
+// K chunking: as few chunks of at most kChunkBlocks blocks as cover K, in whole groups,
+// every chunk non-empty (only the last may be shorter).
+void k_chunks(int K, int *nsplit, int *cb) {
+    const int nb = K / kBlock;
+    const int parts = (nb + kChunkBlocks - 1) / kChunkBlocks;
+    const int per = (nb + parts - 1) / parts;
+    *cb = (per + kGroupBlocks - 1) / kGroupBlocks * kGroupBlocks;
+    *nsplit = (nb + *cb - 1) / *cb;
+}
+
+int gemm_pass(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws, hipStream_t st) {
+    int nsplit = 1, cb = 0;
+    k_chunks(K, &nsplit, &cb);
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    const size_t so = q_tiled_scales_offset(dt, M, K);
+    const size_t sbytes = q_tiled_bytes(dt, M, K) - so;
+    const int ntiles = (M + kTileRows - 1) / kTileRows;
+    const int sets = (ntiles + kWaves - 1) / kWaves;
+    // two 72 KiB workgroups per CU
+    const int gx = std::max(1, std::min(sets, (2 * cus() + nsplit - 1) / nsplit));
+    const dim3 grid((unsigned)gx, (unsigned)nsplit);
+    float *Yp = static_cast<float *>(ws);
+    if (dt == DT_Q4_0)
+        hipLaunchKernelGGL(gemm_mfma_kernel<DT_Q4_0>, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so,
+                           (uint32_t)sbytes, X, batch, M, K, cb, Y, Yp);
+    else
+        hipLaunchKernelGGL(gemm_mfma_kernel<DT_Q8_0>, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so,
+                           (uint32_t)sbytes, X, batch, M, K, cb, Y, Yp);
+    if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
+    if (nsplit > 1) {
+        const size_t n = (size_t)batch * M;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)std::min<size_t>(2048, (n + 255) / 256)), dim3(256), 0, st,
+                           Yp, nsplit, n, Y);
+        if (!hip_ok(hipGetLastError(), "gemm_reduce launch")) return -1;
+    }
+    return 0;
+}
+
+}  // namespace
+
+size_t gemm_workspace_bytes(int M, int K) {
+    int nsplit = 1, cb = 0;
+    k_chunks(K, &nsplit, &cb);
+    return 256 + (nsplit > 1 ? (size_t)nsplit * kBatchMax * M * sizeof(float) : 0);
+}
+
+int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws,
+                      hipStream_t st) {
+    if (batch < 1 || K % (kGroupBlocks * kBlock) != 0 || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0 ||
+        (reinterpret_cast<uintptr_t>(X) & 15u) != 0) {
+        set_error("batched GEMM: bad arguments (batch=%d K=%d ws=%p X=%p; K %% 128 == 0, ws 256-byte and X "
+                  "16-byte aligned)", batch, K, ws, (const void *)X);
+        return -1;
+    }
+    // passes of 16 sequences share the workspace; the stream orders them
+    for (int b0 = 0; b0 < batch; b0 += kBatchMax)
+        if (gemm_pass(dt, w, M, K, X + (size_t)b0 * K, std::min(kBatchMax, batch - b0), Y + (size_t)b0 * M, ws, st))
+            return -1;
+    return 0;
+}
+
+}  // namespace sapphire

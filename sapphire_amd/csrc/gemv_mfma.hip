@@ -448,11 +448,14 @@ int launch_tiled(int dt, const void *w, int M, int K, const float *x, float *y, 
 
 }  // namespace
 
-bool tiled_supported(int dt, int M, int K) {
+bool tiled_layout_ok(int dt, int M, int K) {
     if (!is_quant(dt) || M <= 0 || K <= 0 || K % (kGroupBlocks * kBlock) != 0) return false;
-    const int ng = K / (kGroupBlocks * kBlock);
-    if (ng != 5 && ng != 8 && ng != 9) return false;
     return q_tiled_bytes(dt, M, K) < (size_t(1) << 32) - 256;   // 32-bit buffer offsets
+}
+
+bool tiled_supported(int dt, int M, int K) {
+    const int ng = K / (kGroupBlocks * kBlock);
+    return tiled_layout_ok(dt, M, K) && (ng == 5 || ng == 8 || ng == 9);
 }
 
 size_t q_tiled_scales_offset(int dt, int M, int K) {

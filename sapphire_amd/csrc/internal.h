@@ -39,7 +39,9 @@ int launch_dequant(int dt, int layout, const void *w, int M, int K, float *out, 
 int launch_gemv_q(int dt, int layout, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 int launch_gemm_q(int dt, int layout, const void *w, int M, int K, const float *X, float *Y, int batch,
                   hipStream_t s);
-// TILED layout + matrix-core GEMV (gemv_mfma.hip)
+// TILED layout + matrix-core GEMV (gemv_mfma.hip). The layout needs K % 128 == 0 and
+// fewer than 4 GiB (tiled_layout_ok); the GEMV also needs K/128 in {5, 8, 9} (tiled_supported).
+bool tiled_layout_ok(int dt, int M, int K);
 bool tiled_supported(int dt, int M, int K);
 size_t q_tiled_scales_offset(int dt, int M, int K);
 size_t q_tiled_bytes(int dt, int M, int K);
@@ -52,6 +54,12 @@ int launch_gemv_tiled(int dt, const void *w, int M, int K, const float *x, float
 size_t tiled_softmax_scratch_bytes(int M);
 int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *x, float *logits, float *probs,
                               int *argmax, void *scratch, hipStream_t s);
+// Batched GEMM on the TILED layout (gemm_mfma.hip): Y[b][r] = W[r] . X[b] for b < batch, 16
+// sequences per pass. ws: gemm_workspace_bytes(M, K) bytes of 256-byte aligned device memory
+// (activation operands, K-split partials).
+size_t gemm_workspace_bytes(int M, int K);
+int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws,
+                      hipStream_t s);
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 
 int launch_rmsnorm(float *out, const float *in, const float *w, float eps, int dim, int batch, bool delta,

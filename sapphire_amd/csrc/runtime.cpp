@@ -127,7 +127,7 @@ size_t sapphire_q_layout_bytes(int dt, int layout, int M, int K) {
     if (!is_quant(dt) || M <= 0 || K <= 0) return 0;
     if (layout == LAYOUT_AOS) return q_aos_bytes(dt, M, K);
     if (layout == LAYOUT_PACKED) return q_packed_bytes(dt, M, K);
-    if (layout == LAYOUT_TILED && tiled_supported(dt, M, K)) return q_tiled_bytes(dt, M, K);
+    if (layout == LAYOUT_TILED && tiled_layout_ok(dt, M, K)) return q_tiled_bytes(dt, M, K);
     return 0;
 }
 
@@ -135,8 +135,8 @@ int sapphire_q_convert_dev(int dt, const void *w_aos, int M, int K, int layout, 
     if (!valid_quant_args(dt, w_aos, M, K) || !out) return -1;
     if (layout == LAYOUT_PACKED) return launch_repack(dt, w_aos, M, K, out, as_stream(stream));
     if (layout == LAYOUT_TILED) {
-        if (!tiled_supported(dt, M, K)) {
-            set_error("TILED layout needs K/128 in {5, 8, 9} (K=%d)", K);
+        if (!tiled_layout_ok(dt, M, K)) {
+            set_error("TILED layout needs K to be a multiple of 128 (K=%d)", K);
             return -1;
         }
         return launch_to_tiled(dt, w_aos, M, K, out, as_stream(stream));
@@ -147,7 +147,7 @@ int sapphire_q_convert_dev(int dt, const void *w_aos, int M, int K, int layout, 
 
 static bool valid_layout(int dt, int layout, int M, int K) {
     if (layout == LAYOUT_AOS || layout == LAYOUT_PACKED) return true;
-    if (layout == LAYOUT_TILED && tiled_supported(dt, M, K)) return true;
+    if (layout == LAYOUT_TILED && tiled_layout_ok(dt, M, K)) return true;
     set_error("layout %d is not valid for a %d x %d matrix", layout, M, K);
     return false;
 }
@@ -167,6 +167,25 @@ int sapphire_gemv_q_dev(int dt, int layout, const void *w, int M, int K, const f
     if (K % kBlock != 0) { set_error("K=%d is not a multiple of 32", K); return -1; }
     if (!valid_layout(dt, layout, M, K)) return -1;
     return launch_gemv_q(dt, layout, w, M, K, x, y, as_stream(stream));
+}
+
+size_t sapphire_gemm_workspace_bytes(int dt, int M, int K) {
+    if (!is_quant(dt) || M <= 0 || K <= 0 || K % kBlock != 0) return 0;
+    return gemm_workspace_bytes(M, K);
+}
+
+int sapphire_gemm_q_dev(int dt, int layout, const void *w, int M, int K, const float *X, int batch, float *Y,
+                        void *ws, void *stream) {
+    if (!valid_quant_args(dt, w, M, K) || !X || !Y || batch <= 0) {
+        if (batch <= 0) set_error("batch must be positive (got %d)", batch);
+        return -1;
+    }
+    if (K % kBlock != 0) { set_error("K=%d is not a multiple of 32", K); return -1; }
+    if (!valid_layout(dt, layout, M, K)) return -1;
+    hipStream_t s = as_stream(stream);
+    if (layout != LAYOUT_TILED) return launch_gemm_q(dt, layout, w, M, K, X, Y, batch, s);
+    if (!ws) { set_error("the TILED GEMM needs a workspace"); return -1; }
+    return launch_gemm_tiled(dt, w, M, K, X, batch, Y, ws, s);
 }
 
 int sapphire_gemv_f_dev(int dt, const void *w, int M, int K, const float *x, float *y, void *stream) {

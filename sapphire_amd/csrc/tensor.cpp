@@ -3,8 +3,9 @@
 // Host-side semantics follow the reference src/tensor/tensor.c (create, view, clone,
 // refcount, accessors, the Q4_0 numel/2 allocation, view nbytes = numel * elem size).
 // The private struct adds the device copy used by the GEMV entry points: quantized
-// weights are uploaded once and repacked into the PACKED layout, F32/BF16 uploaded as
-// is. The copy is freed with the tensor.
+// weights are uploaded once and repacked into the PACKED (or, for the LM head, TILED)
+// layout, F32/BF16 uploaded as is; batched calls add a TILED copy. The copies are freed
+// with the tensor.
 #include <cstdlib>
 #include <cstring>
 
@@ -160,16 +161,39 @@ namespace sapphire {
 
 void tensor_drop_device(tensor_t *t) {
     std::lock_guard<std::mutex> g(t->dev_mu);
-    if (t->dev) {
+    if (t->dev || t->dev_tiled) {
         int cur = 0;
         (void)hipGetDevice(&cur);
         (void)hipSetDevice(t->dev_device);
-        (void)hipFree(t->dev);
+        if (t->dev) (void)hipFree(t->dev);
+        if (t->dev_tiled) (void)hipFree(t->dev_tiled);
         (void)hipSetDevice(cur);
     }
     t->dev = nullptr;
+    t->dev_tiled = nullptr;
     t->dev_bytes = 0;
 }
+
+namespace {
+
+// Uploads the AoS blocks of a quantized tensor and converts them to `lay` on the device.
+void *upload_quant(const tensor_t *t, int lay, hipStream_t s) {
+    const int M = t->shape[0], K = t->shape[t->ndim - 1];
+    const size_t aos = q_aos_bytes(t->dtype, M, K);
+    const size_t bytes = lay == LAYOUT_TILED ? q_tiled_bytes(t->dtype, M, K) : q_packed_bytes(t->dtype, M, K);
+    void *dst = nullptr, *tmp = nullptr;
+    if (!hip_ok(hipMalloc(&dst, bytes), "hipMalloc(weights)")) return nullptr;
+    if (!hip_ok(hipMalloc(&tmp, aos), "hipMalloc(staging)")) { (void)hipFree(dst); return nullptr; }
+    bool ok = hip_ok(hipMemcpyAsync(tmp, t->data, aos, hipMemcpyHostToDevice, s), "upload weights") &&
+              (lay == LAYOUT_TILED ? launch_to_tiled(t->dtype, tmp, M, K, dst, s)
+                                   : launch_repack(t->dtype, tmp, M, K, dst, s)) == 0 &&
+              hip_ok(hipStreamSynchronize(s), "repack sync");
+    (void)hipFree(tmp);
+    if (!ok) { (void)hipFree(dst); return nullptr; }
+    return dst;
+}
+
+}  // namespace
 
 const void *tensor_device_weights(const tensor_t *tc, int *layout, hipStream_t s) {
     tensor_t *t = const_cast<tensor_t *>(tc);
@@ -189,19 +213,10 @@ const void *tensor_device_weights(const tensor_t *tc, int *layout, hipStream_t s
     if (is_quant(t->dtype)) {
         // Long matrices (the LM head) go to the matrix-core TILED layout, the rest to PACKED.
         const int lay = (M >= kTiledMinRows && tiled_supported(t->dtype, M, K)) ? LAYOUT_TILED : LAYOUT_PACKED;
-        const size_t aos = q_aos_bytes(t->dtype, M, K);
-        const size_t bytes = lay == LAYOUT_TILED ? q_tiled_bytes(t->dtype, M, K) : q_packed_bytes(t->dtype, M, K);
-        void *tmp = nullptr;
-        if (!hip_ok(hipMalloc(&dst, bytes), "hipMalloc(weights)")) return nullptr;
-        if (!hip_ok(hipMalloc(&tmp, aos), "hipMalloc(staging)")) { (void)hipFree(dst); return nullptr; }
-        bool ok = hip_ok(hipMemcpyAsync(tmp, t->data, aos, hipMemcpyHostToDevice, s), "upload weights") &&
-                  (lay == LAYOUT_TILED ? launch_to_tiled(t->dtype, tmp, M, K, dst, s)
-                                       : launch_repack(t->dtype, tmp, M, K, dst, s)) == 0 &&
-                  hip_ok(hipStreamSynchronize(s), "repack sync");
-        (void)hipFree(tmp);
-        if (!ok) { (void)hipFree(dst); return nullptr; }
+        dst = upload_quant(t, lay, s);
+        if (!dst) return nullptr;
         t->dev_layout = lay;
-        t->dev_bytes = bytes;
+        t->dev_bytes = lay == LAYOUT_TILED ? q_tiled_bytes(t->dtype, M, K) : q_packed_bytes(t->dtype, M, K);
     } else {
         const size_t bytes = (size_t)M * (size_t)K * dtype_element_size(t->dtype);
         if (!hip_ok(hipMalloc(&dst, bytes), "hipMalloc(weights)")) return nullptr;
@@ -217,6 +232,22 @@ const void *tensor_device_weights(const tensor_t *tc, int *layout, hipStream_t s
     t->dev_device = dev;
     *layout = t->dev_layout;
     return dst;
+}
+
+const void *tensor_device_tiled(const tensor_t *tc, hipStream_t s) {
+    int layout = 0;
+    const void *w = tensor_device_weights(tc, &layout, s);
+    if (!w) return nullptr;
+    if (layout == LAYOUT_TILED) return w;
+    tensor_t *t = const_cast<tensor_t *>(tc);
+    const int M = t->shape[0], K = t->shape[t->ndim - 1];
+    if (!is_quant(t->dtype) || !tiled_layout_ok(t->dtype, M, K)) {
+        set_error("no TILED layout for this tensor (dtype %d, K=%d)", (int)t->dtype, K);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(t->dev_mu);
+    if (!t->dev_tiled) t->dev_tiled = upload_quant(t, LAYOUT_TILED, s);
+    return t->dev_tiled;
 }
 
 }  // namespace sapphire

@@ -19,12 +19,17 @@ struct tensor_t {
     std::mutex dev_mu;
     void *dev = nullptr;
     size_t dev_bytes = 0;
-    int dev_layout = 0;           // sapphire::LAYOUT_AOS for F32/BF16, LAYOUT_PACKED for Q4_0/Q8_0
+    int dev_layout = 0;           // sapphire::LAYOUT_AOS for F32/BF16, PACKED or TILED for Q4_0/Q8_0
     int dev_device = -1;
+    // TILED copy for batched calls when the GEMV copy is PACKED (same device as dev)
+    void *dev_tiled = nullptr;
 };
 
 namespace sapphire {
 // Device copy of a 2-D weight tensor on the current device (uploaded on first use).
 const void *tensor_device_weights(const tensor_t *t, int *layout, hipStream_t s);
+// TILED copy of a Q4_0/Q8_0 weight tensor for the batched matrix-core GEMM (K % 128 == 0):
+// the GEMV copy when that is TILED, else a second copy made on first use.
+const void *tensor_device_tiled(const tensor_t *t, hipStream_t s);
 void tensor_drop_device(tensor_t *t);
 }  // namespace sapphire
