@@ -97,6 +97,44 @@ size_t sapphire_gemm_workspace_bytes(int dtype, int M, int K);
 int sapphire_gemm_q_dev(int dtype, int layout, const void *w, int M, int K, const float *X, int batch,
                         float *Y, void *ws, void *stream);
 
+/* The batched GEMM with its input and output transforms, for a host engine that runs a
+ * batched decode step (TILED weights only). Per sequence row b the input is formed while
+ * the activations are staged:
+ *   d = sum of the `nparts` rows parts[c * part_stride + b * ldp + k] (when parts is set),
+ *   d = rmsnorm_delta(d, w_delta) when w_delta is set; h = x[b * ldx + k] (+ d);
+ *   resid_out[b * ldr + k] = h when resid_out is set;
+ *   input = rmsnorm_delta(h, w_norm) when w_norm is set, else h
+ * (the residual of attention.c:356-366 / transformer.c:231-239 and the pre-norms of
+ * attention.c:316-325 / transformer.c:119-121; rmsnorm_delta of normalization.c:104-117).
+ * The norms need whole rows: K <= 1152 when w_delta or w_norm is set. Output: with
+ * out.parts set, the K chunks' partial sums are left in parts[c][b][M] (c < the number
+ * sapphire_gemm_splits(K) returns) for the next call's input; else y[b * ldy + r]. With
+ * out.geglu, W's rows are gate and up rows interleaved by eight and y[b * ldy + j] =
+ * gelu(gate_j) * up_j for j < M/2 (transformer.c:141-157). Pointers 16-byte aligned,
+ * leading dimensions multiples of 4; ws as for sapphire_gemm_q_dev (NULL allowed when
+ * K <= 1152 or out.parts is set). batch <= 16. */
+typedef struct {
+    const float *x;
+    int ldx;
+    const float *parts;
+    int nparts, ldp;
+    size_t part_stride;
+    const float *w_delta;
+    float *resid_out;
+    int ldr;
+    const float *w_norm;
+    float eps;
+} sapphire_gemm_input_t;
+typedef struct {
+    float *y;
+    int ldy;
+    float *parts;
+    int geglu;
+} sapphire_gemm_output_t;
+int sapphire_gemm_splits(int K);
+int sapphire_gemm_q_fused_dev(int dtype, const void *w_tiled, int M, int K, int batch, const sapphire_gemm_input_t *in,
+                              const sapphire_gemm_output_t *out, void *ws, void *stream);
+
 /* ---- LM-head epilogue ----
  * probs = softmax(logits) (utils.c:18-59) written to probs (may equal logits) and the
  * greedy token (utils.c:145-156: first index of the maximum) written to *argmax_dev.

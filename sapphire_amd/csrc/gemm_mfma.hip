@@ -20,6 +20,7 @@
 // chunk is split over workgroups (grid.y) and gemm_reduce_kernel adds the partial sums.
 #include <algorithm>
 
+#include "devmath.h"
 #include "internal.h"
 
 namespace sapphire {
@@ -146,16 +147,53 @@ __device__ __forceinline__ void unit_mfma(const Unit &u, const h8 *__restrict__ 
     }
 }
 
+// Reference-order sums of squares of the staged rows (sum_sq_avx2, normalization.c:12-32:
+// eight strided chains, then ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)) and the tail), turned into
+// the rmsnorm factor 1/sqrtf(sum/dim + eps) of every sequence. raw: [seq][ld] fp32 in LDS.
+__device__ void rows_rms_inv(const float *raw, int ld, int dim, int batch, float eps, float (*part)[8], float *rinv) {
+    const int t = threadIdx.x;
+    if (t < kBatchMax * 8) {
+        const int seq = t >> 3, l = t & 7;
+        float s = 0.f;
+        if (seq < batch)
+            for (int i = l; i < (dim & ~7); i += 8) s = __builtin_fmaf(raw[seq * ld + i], raw[seq * ld + i], s);
+        part[seq][l] = s;
+    }
+    __syncthreads();
+    if (t < batch) {
+        const float *pp = part[t];
+        const float a0 = pp[0] + pp[4], a1 = pp[1] + pp[5], a2 = pp[2] + pp[6], a3 = pp[3] + pp[7];
+        float sum = (a0 + a1) + (a2 + a3);
+        for (int i = dim & ~7; i < dim; ++i) sum = __builtin_fmaf(raw[t * ld + i], raw[t * ld + i], sum);
+        rinv[t] = devmath::rms_inv_of(sum, dim, eps);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
+    const float4 lo = reinterpret_cast<const float4 *>(p)[0], hi = reinterpret_cast<const float4 *>(p)[1];
+    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+}
+
+// LDS of the staging: the A operands [block][hi/lo][lane 16m + seq] of a chunk, and, before
+// them (same memory), the rows as fp32 [seq][K + 4] for the reference-order norm sums.
+constexpr int kRawLd = kChunkBlocks * kBlock + 4;
+constexpr int kStageH8 = (kBatchMax * kRawLd * 4 + 15) / 16 > kChunkBlocks * 2 * kWave
+                             ? (kBatchMax * kRawLd * 4 + 15) / 16
+                             : kChunkBlocks * 2 * kWave;
+
 // grid.x: workgroups over the tiles (grid-stride), grid.y: K chunks of `cb` blocks.
-// Y[b][r] = sum over the chunk (grid.y == 1), else Yp[chunk][b][r].
+// Four waves per SIMD (two workgroups per CU): at most 128 VGPRs.
 template <int DT>
-__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const uint8_t *__restrict__ wq, uint32_t q_bytes,
-                                                             const uint8_t *__restrict__ wsc, uint32_t s_bytes,
-                                                             const float *__restrict__ X, int batch, int M, int K,
-                                                             int cb, float *__restrict__ Y, float *__restrict__ Yp) {
-    __shared__ h8 xs[kChunkBlocks * 2 * kWave];        // [block][hi/lo][lane 16m + seq]
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_mfma_kernel(
+    const uint8_t *__restrict__ wq, uint32_t q_bytes, const uint8_t *__restrict__ wsc, uint32_t s_bytes, GemmIn in,
+    int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp) {
+    __shared__ h8 xs[kStageH8];
     __shared__ float wmax[kWaves][kBatchMax];
     __shared__ float xsc[kBatchMax];
+    __shared__ float npart[kBatchMax][8];
+    __shared__ float rinv[kBatchMax];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int nb = K / kBlock, G = nb / kGroupBlocks;
     const int b0 = blockIdx.y * cb, b1 = min(nb, b0 + cb);
@@ -189,31 +227,110 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const uint8_t *__re
             if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
         }
     }
-    // ---- stage the chunk: range scale per sequence, then the hi/lo operands ----
+    // ---- stage the chunk: input transform, range scale per sequence, hi/lo operands ----
     {
         const int seq = tid & (kBatchMax - 1), q = tid / kBatchMax;   // q: 0..31
         const int pairs = (b1 - b0) * 4;
+        const int kb = b0 * kBlock;
+        float *raw = reinterpret_cast<float *>(xs);
         float v[kStagePairs][8];
-        float mx = 0.f;
+        // h (or the delta) of this thread's 8-element pieces
 #pragma unroll
         for (int i = 0; i < kStagePairs; ++i) {
             const int p = q + i * (kThreads / kBatchMax);
-            if (p < pairs && seq < batch) {
-                const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)seq * K + (size_t)b0 * kBlock + p * 8);
-                const float4 lo = src[0], hi = src[1];
-                v[i][0] = lo.x; v[i][1] = lo.y; v[i][2] = lo.z; v[i][3] = lo.w;
-                v[i][4] = hi.x; v[i][5] = hi.y; v[i][6] = hi.z; v[i][7] = hi.w;
-            } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+            for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+            if (p < pairs && seq < batch) {
+                const int k = kb + p * 8;
+                if (in.parts) {
+                    for (int c = 0; c < in.nparts; ++c) {
+                        float t[8];
+                        load8(in.parts + c * in.part_stride + (size_t)seq * in.ldp + k, t);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(v[i][e], t[e]);
+                    }
+                } else {
+                    load8(in.x + (size_t)seq * in.ldx + k, v[i]);
+                }
             }
+        }
+        if (in.parts) {
+            if (in.w_delta) {
+#pragma unroll
+                for (int i = 0; i < kStagePairs; ++i) {
+                    const int p = q + i * (kThreads / kBatchMax);
+                    if (p < pairs)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) raw[seq * kRawLd + p * 8 + e] = v[i][e];
+                }
+                __syncthreads();
+                rows_rms_inv(raw, kRawLd, K, batch, in.eps, npart, rinv);
+                const float r = rinv[seq];
+#pragma unroll
+                for (int i = 0; i < kStagePairs; ++i) {
+                    const int p = q + i * (kThreads / kBatchMax);
+                    if (p < pairs && seq < batch) {
+                        float w[8];
+                        load8(in.w_delta + kb + p * 8, w);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[i][e] = __fmul_rn(__fmul_rn(v[i][e], r), __fadd_rn(1.0f, w[e]));
+                    }
+                }
+            }
+            if (in.x)
+#pragma unroll
+                for (int i = 0; i < kStagePairs; ++i) {
+                    const int p = q + i * (kThreads / kBatchMax);
+                    if (p < pairs && seq < batch) {
+                        float t[8];
+                        load8(in.x + (size_t)seq * in.ldx + kb + p * 8, t);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(t[e], v[i][e]);
+                    }
+                }
+        }
+        if (in.resid_out && blockIdx.x == 0 && blockIdx.y == 0)
+#pragma unroll
+            for (int i = 0; i < kStagePairs; ++i) {
+                const int p = q + i * (kThreads / kBatchMax);
+                if (p < pairs && seq < batch) {
+                    float4 *dst = reinterpret_cast<float4 *>(in.resid_out + (size_t)seq * in.ldr + kb + p * 8);
+                    dst[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+                    dst[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+                }
+            }
+        if (in.w_norm) {
+            __syncthreads();                           // raw may still be read by the delta norm
+#pragma unroll
+            for (int i = 0; i < kStagePairs; ++i) {
+                const int p = q + i * (kThreads / kBatchMax);
+                if (p < pairs)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) raw[seq * kRawLd + p * 8 + e] = v[i][e];
+            }
+            __syncthreads();
+            rows_rms_inv(raw, kRawLd, K, batch, in.eps, npart, rinv);
+            const float r = rinv[seq];
+#pragma unroll
+            for (int i = 0; i < kStagePairs; ++i) {
+                const int p = q + i * (kThreads / kBatchMax);
+                if (p < pairs && seq < batch) {
+                    float w[8];
+                    load8(in.w_norm + kb + p * 8, w);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[i][e] = __fmul_rn(__fmul_rn(v[i][e], r), __fadd_rn(1.0f, w[e]));
+                }
+            }
+        }
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < kStagePairs; ++i)
 #pragma unroll
             for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[i][e]));
-        }
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         if (lane < kBatchMax) wmax[wid][lane] = mx;
-        __syncthreads();
+        __syncthreads();                               // also ends every read of raw
         mx = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wmax[w][seq]);
@@ -250,6 +367,16 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const uint8_t *__re
     float sc[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) sc[r] = xsc[4 * m + r];
+    // where this chunk's results go: final rows, or the partial sums of chunk blockIdx.y
+    float *dst = out.y;
+    int ldd = out.ldy;
+    if (out.parts) {
+        dst = out.parts + (size_t)blockIdx.y * batch * M;
+        ldd = M;
+    } else if (gridDim.y > 1) {
+        dst = Yp + (size_t)blockIdx.y * batch * M;
+        ldd = M;
+    }
     int ct = t0, cg = 0;                               // tile and group of the unit multiplied
     f4 acc = {0.f, 0.f, 0.f, 0.f};
     // Every pass issues the loads of all kRing slots (past the last unit they repeat it), so
@@ -266,12 +393,22 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const uint8_t *__re
             if (base + p < U) {
                 unit_mfma<DT>(ring[p], xs, cg * kGroupBlocks, lane, acc, bk);
                 if (++cg == gc) {
-                    const int row = ct * kTileRows + n;
-                    if (row < M) {
-                        float *dst = gridDim.y == 1 ? Y : Yp + (size_t)blockIdx.y * batch * M;
+                    if (out.geglu) {
+                        // lanes n < 8 hold gate rows 8t'+n, lanes n + 8 the matching up rows
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            if (4 * m + r < batch) dst[(size_t)(4 * m + r) * M + row] = acc[r] * sc[r];
+                        for (int r = 0; r < 4; ++r) {
+                            const float val = acc[r] * sc[r];
+                            const float up = __shfl_xor(val, 8, kWave);
+                            const int j = ct * 8 + n;
+                            if (n < 8 && 4 * m + r < batch && 2 * j < M)
+                                dst[(size_t)(4 * m + r) * ldd + j] = __fmul_rn(devmath::gelu_ref(val), up);
+                        }
+                    } else {
+                        const int row = ct * kTileRows + n;
+                        if (row < M)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (4 * m + r < batch) dst[(size_t)(4 * m + r) * ldd + row] = acc[r] * sc[r];
                     }
                     acc = f4{0.f, 0.f, 0.f, 0.f};
                     cg = 0;
@@ -282,11 +419,13 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(const uint8_t *__re
     }
 }
 
-__global__ void gemm_reduce_kernel(const float *__restrict__ Yp, int nsplit, size_t n, float *__restrict__ Y) {
+__global__ void gemm_reduce_kernel(const float *__restrict__ Yp, int nsplit, int batch, int M, float *__restrict__ Y,
+                                   int ldy) {
+    const size_t n = (size_t)batch * M;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         float s = 0.f;
         for (int c = 0; c < nsplit; ++c) s += Yp[(size_t)c * n + i];
-        Y[i] = s;
+        Y[(i / M) * ldy + i % M] = s;
     }
 }
 
@@ -308,7 +447,11 @@ void k_chunks(int K, int *nsplit, int *cb) {
     *nsplit = (nb + *cb - 1) / *cb;
 }
 
-int gemm_pass(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws, hipStream_t st) {
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// One pass of at most 16 sequences.
+int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out, void *ws,
+              hipStream_t st) {
     int nsplit = 1, cb = 0;
     k_chunks(K, &nsplit, &cb);
     const uint8_t *wb = static_cast<const uint8_t *>(w);
@@ -322,15 +465,15 @@ int gemm_pass(int dt, const void *w, int M, int K, const float *X, int batch, fl
     float *Yp = static_cast<float *>(ws);
     if (dt == DT_Q4_0)
         hipLaunchKernelGGL(gemm_mfma_kernel<DT_Q4_0>, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so,
-                           (uint32_t)sbytes, X, batch, M, K, cb, Y, Yp);
+                           (uint32_t)sbytes, in, batch, M, K, cb, out, Yp);
     else
         hipLaunchKernelGGL(gemm_mfma_kernel<DT_Q8_0>, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so,
-                           (uint32_t)sbytes, X, batch, M, K, cb, Y, Yp);
+                           (uint32_t)sbytes, in, batch, M, K, cb, out, Yp);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
-    if (nsplit > 1) {
+    if (nsplit > 1 && !out.parts) {
         const size_t n = (size_t)batch * M;
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)std::min<size_t>(2048, (n + 255) / 256)), dim3(256), 0, st,
-                           Yp, nsplit, n, Y);
+                           Yp, nsplit, batch, M, out.y, out.ldy);
         if (!hip_ok(hipGetLastError(), "gemm_reduce launch")) return -1;
     }
     return 0;
@@ -338,24 +481,56 @@ int gemm_pass(int dt, const void *w, int M, int K, const float *X, int batch, fl
 
 }  // namespace
 
-size_t gemm_workspace_bytes(int M, int K) {
+int gemm_splits(int K) {
     int nsplit = 1, cb = 0;
     k_chunks(K, &nsplit, &cb);
+    return nsplit;
+}
+
+size_t gemm_workspace_bytes(int M, int K) {
+    const int nsplit = gemm_splits(K);
     return 256 + (nsplit > 1 ? (size_t)nsplit * kBatchMax * M * sizeof(float) : 0);
+}
+
+int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
+                         void *ws, hipStream_t st) {
+    const int nsplit = gemm_splits(K);
+    const bool norms = in.w_delta || in.w_norm;
+    const bool ok = batch >= 1 && batch <= kBatchMax && M > 0 && K > 0 && K % (kGroupBlocks * kBlock) == 0 &&
+                    (in.x || in.parts) && (!in.x || (aligned16(in.x) && in.ldx % 4 == 0 && in.ldx >= K)) &&
+                    (!in.parts || (aligned16(in.parts) && in.nparts >= 1 && in.ldp % 4 == 0 && in.ldp >= K &&
+                                   in.part_stride % 4 == 0)) &&
+                    (!in.w_delta || in.parts) && (!in.resid_out || (aligned16(in.resid_out) && in.ldr % 4 == 0)) &&
+                    (!norms || (nsplit == 1 && aligned16(in.w_delta ? in.w_delta : in.w_norm) &&
+                                (!in.w_norm || aligned16(in.w_norm)))) &&
+                    (out.parts || (out.y && out.ldy >= (out.geglu ? M / 2 : M))) &&
+                    (!out.geglu || (nsplit == 1 && M % 16 == 0 && !out.parts)) &&
+                    (out.parts || nsplit == 1 || ((reinterpret_cast<uintptr_t>(ws) & 255u) == 0 && ws));
+    if (!ok) {
+        set_error("batched GEMM: unsupported arguments (batch=%d M=%d K=%d nsplit=%d)", batch, M, K, nsplit);
+        return -1;
+    }
+    return gemm_pass(dt, w, M, K, batch, in, out, ws, st);
 }
 
 int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws,
                       hipStream_t st) {
     if (batch < 1 || K % (kGroupBlocks * kBlock) != 0 || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0 ||
-        (reinterpret_cast<uintptr_t>(X) & 15u) != 0) {
+        !aligned16(X)) {
         set_error("batched GEMM: bad arguments (batch=%d K=%d ws=%p X=%p; K %% 128 == 0, ws 256-byte and X "
                   "16-byte aligned)", batch, K, ws, (const void *)X);
         return -1;
     }
     // passes of 16 sequences share the workspace; the stream orders them
-    for (int b0 = 0; b0 < batch; b0 += kBatchMax)
-        if (gemm_pass(dt, w, M, K, X + (size_t)b0 * K, std::min(kBatchMax, batch - b0), Y + (size_t)b0 * M, ws, st))
-            return -1;
+    for (int b0 = 0; b0 < batch; b0 += kBatchMax) {
+        GemmIn in;
+        in.x = X + (size_t)b0 * K;
+        in.ldx = K;
+        GemmOut out;
+        out.y = Y + (size_t)b0 * M;
+        out.ldy = M;
+        if (gemm_pass(dt, w, M, K, std::min(kBatchMax, batch - b0), in, out, ws, st)) return -1;
+    }
     return 0;
 }
 

@@ -56,10 +56,43 @@ int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *
                               int *argmax, void *scratch, hipStream_t s);
 // Batched GEMM on the TILED layout (gemm_mfma.hip): Y[b][r] = W[r] . X[b] for b < batch, 16
 // sequences per pass. ws: gemm_workspace_bytes(M, K) bytes of 256-byte aligned device memory
-// (activation operands, K-split partials).
+// (the K-split partial sums).
 size_t gemm_workspace_bytes(int M, int K);
 int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws,
                       hipStream_t s);
+// Number of K chunks (partial sums) of a batched GEMM with inner dimension K.
+int gemm_splits(int K);
+// Input of a batched GEMM, formed per sequence row while the activations are staged (the
+// residual pattern of attention.c:356-366 / transformer.c:231-239 and the pre-norms of
+// attention.c:316-325 / transformer.c:119-121):
+//   d = sum of `nparts` partial rows (when parts is set), d = rmsnorm_delta(d, w_delta) when
+//   w_delta is set; h = x (+ d); resid_out <- h (workgroup (0, 0)); the GEMM input is
+//   rmsnorm_delta(h, w_norm) when w_norm is set, else h.
+// The norms need whole rows: K at most 36 blocks (one K chunk) when w_delta or w_norm is set.
+struct GemmIn {
+    const float *x = nullptr;        // [b * ldx + k]; may be NULL when parts is set
+    int ldx = 0;
+    const float *parts = nullptr;    // [c * part_stride + b * ldp + k], c < nparts
+    int nparts = 0, ldp = 0;
+    size_t part_stride = 0;
+    const float *w_delta = nullptr;
+    float *resid_out = nullptr;      // [b * ldr + k]
+    int ldr = 0;
+    const float *w_norm = nullptr;
+    float eps = 1e-6f;
+};
+// Output of a batched GEMM. parts set: the K chunks' partial sums go to parts[c][b][M] (an
+// input of the next GEMM's GemmIn), nothing else is written. geglu: the weight rows are
+// interleaved by eight (gate rows 8i..8i+7, then the matching up rows) and
+// y[b * ldy + j] = gelu(gate_j) * up_j for j < M / 2 (transformer.c:141-157).
+struct GemmOut {
+    float *y = nullptr;
+    int ldy = 0;
+    float *parts = nullptr;
+    bool geglu = false;
+};
+int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
+                         void *ws, hipStream_t s);
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 
 int launch_rmsnorm(float *out, const float *in, const float *w, float eps, int dim, int batch, bool delta,

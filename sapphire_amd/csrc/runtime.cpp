@@ -188,6 +188,35 @@ int sapphire_gemm_q_dev(int dt, int layout, const void *w, int M, int K, const f
     return launch_gemm_tiled(dt, w, M, K, X, batch, Y, ws, s);
 }
 
+int sapphire_gemm_splits(int K) { return K > 0 && K % kBlock == 0 ? gemm_splits(K) : 0; }
+
+int sapphire_gemm_q_fused_dev(int dt, const void *w, int M, int K, int batch, const sapphire_gemm_input_t *in,
+                              const sapphire_gemm_output_t *out, void *ws, void *stream) {
+    if (!valid_quant_args(dt, w, M, K) || !in || !out) return -1;
+    if (!tiled_layout_ok(dt, M, K)) {
+        set_error("the fused GEMM takes TILED weights (K a multiple of 128; K=%d)", K);
+        return -1;
+    }
+    GemmIn gi;
+    gi.x = in->x;
+    gi.ldx = in->ldx;
+    gi.parts = in->parts;
+    gi.nparts = in->nparts;
+    gi.ldp = in->ldp;
+    gi.part_stride = in->part_stride;
+    gi.w_delta = in->w_delta;
+    gi.resid_out = in->resid_out;
+    gi.ldr = in->ldr;
+    gi.w_norm = in->w_norm;
+    gi.eps = in->eps;
+    GemmOut go;
+    go.y = out->y;
+    go.ldy = out->ldy;
+    go.parts = out->parts;
+    go.geglu = out->geglu != 0;
+    return launch_gemm_tiled_ex(dt, w, M, K, batch, gi, go, ws, as_stream(stream));
+}
+
 int sapphire_gemv_f_dev(int dt, const void *w, int M, int K, const float *x, float *y, void *stream) {
     if ((dt != DT_F32 && dt != DT_BF16) || !w || !x || !y || M <= 0 || K <= 0) {
         set_error("bad F32/BF16 GEMV arguments");

@@ -180,3 +180,147 @@ def test_kernel_gemm_tensor_api(hip, oracle, dtype, shape, batch):
     finally:
         hip.tensor_release(A)
         hip.kernel_ctx_destroy(ctx)
+
+
+# ---- the fused input / output transforms (sapphire_gemm_q_fused_dev) ----
+
+class _GemmIn(C.Structure):
+    _fields_ = [("x", C.c_void_p), ("ldx", C.c_int), ("parts", C.c_void_p), ("nparts", C.c_int), ("ldp", C.c_int),
+                ("part_stride", C.c_size_t), ("w_delta", C.c_void_p), ("resid_out", C.c_void_p), ("ldr", C.c_int),
+                ("w_norm", C.c_void_p), ("eps", C.c_float)]
+
+
+class _GemmOut(C.Structure):
+    _fields_ = [("y", C.c_void_p), ("ldy", C.c_int), ("parts", C.c_void_p), ("geglu", C.c_int)]
+
+
+def _fused(hip, qm, batch, gin, gout, ws=None):
+    from sapphire_amd.device import check
+    check(hip.sapphire_gemm_q_fused_dev(qm.dtype, qm.ptr(), qm.M, qm.K, batch, C.byref(gin), C.byref(gout),
+                                        ws.ptr if ws is not None else None, None))
+    check(hip.sapphire_synchronize())
+
+
+def _norm_w(n, tid):
+    return synth.normal_f32(n, 40, tid, 1.0, 0.1)
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("batch", [16, 5])
+def test_gemm_fused_residual_and_norms(hip, oracle, dtype, batch):
+    """h = x + rmsnorm_delta(p0 + p1 + p2, w_delta); resid_out = h (bit for bit: the norm sums
+    run in the reference's order); y = W . rmsnorm_delta(h, w_norm) against the oracle."""
+    from sapphire_amd.device import DeviceArray, QMatrix
+    m, k = 1536, 1152
+    W = synth.quant_matrix(dtype, m, k, seed=41, tensor_id=1)
+    qm = QMatrix(dtype, W, layout=TILED)
+    x = synth.normal_f32((batch, k), 41, 2)
+    parts = synth.normal_f32((3, 16, k), 41, 3)
+    wd, wn = _norm_w(k, 1), _norm_w(k, 2)
+    d = ((parts[0, :batch] + parts[1, :batch]) + parts[2, :batch]).astype(np.float32)
+    h = np.stack([x[b] + oracle.rmsnorm_delta(d[b], wd) for b in range(batch)]).astype(np.float32)
+    xin = np.stack([oracle.rmsnorm_delta(h[b], wn) for b in range(batch)])
+    ref = _ref(oracle, dtype, W, xin)
+    dx, dp, dwd, dwn = (DeviceArray.from_numpy(a) for a in (x, parts, wd, wn))
+    dr, dy = DeviceArray.empty(batch * k), DeviceArray.empty(batch * m)
+    gin = _GemmIn(dx.ptr, k, dp.ptr, 3, k, 16 * k, dwd.ptr, dr.ptr, k, dwn.ptr, 1e-6)
+    gout = _GemmOut(dy.ptr, m, None, 0)
+    _fused(hip, qm, batch, gin, gout)
+    assert np.array_equal(dr.numpy().reshape(batch, k).view(np.uint32), h.view(np.uint32))
+    ok, err = close(dy.numpy().reshape(batch, m), ref)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("ffn", [6912, 200])
+def test_gemm_fused_geglu(hip, oracle, dtype, ffn):
+    """Gate and up rows interleaved by eight in one matrix; y = gelu(W_g . x) * (W_u . x)
+    (transformer.c:141-157) from the GEMM epilogue. Each projection is held to the GEMV
+    tolerance t(v) = 1e-4 + 1e-3|v|; the product to what that propagates to:
+    |u| t(g) max|gelu'| + |gelu(g)| t(u) (max|gelu'| < 1.13)."""
+    from sapphire_amd.device import DeviceArray, QMatrix
+    k, batch = 1152, 16
+    Wg = synth.quant_matrix(dtype, ffn, k, seed=42, tensor_id=1)
+    Wu = synth.quant_matrix(dtype, ffn, k, seed=42, tensor_id=2)
+    st = np.empty((2 * ffn, k // 32), dtype=Wg.dtype)
+    st.reshape(ffn // 8, 2, 8, k // 32)[:, 0] = Wg.reshape(ffn // 8, 8, k // 32)
+    st.reshape(ffn // 8, 2, 8, k // 32)[:, 1] = Wu.reshape(ffn // 8, 8, k // 32)
+    qm = QMatrix(dtype, st, layout=TILED)
+    x = synth.normal_f32((batch, k), 42, 3)
+    gate, up = _ref(oracle, dtype, Wg, x), _ref(oracle, dtype, Wu, x)
+    ref = np.stack([oracle.gelu_mul(gate[b], up[b]) for b in range(batch)])
+    dx, dy = DeviceArray.from_numpy(x), DeviceArray.empty(batch * ffn)
+    _fused(hip, qm, batch, _GemmIn(dx.ptr, k, None, 0, 0, 0, None, None, 0, None, 1e-6), _GemmOut(dy.ptr, ffn, None, 1))
+    got = dy.numpy().reshape(batch, ffn).astype(np.float64)
+    g64, u64 = gate.astype(np.float64), up.astype(np.float64)
+    gelu = np.stack([oracle.gelu_mul(gate[b], np.ones(ffn, np.float32)) for b in range(batch)]).astype(np.float64)
+    t = lambda v: 1e-4 + 1e-3 * np.abs(v)
+    bound = 1.13 * t(g64) * np.abs(u64) + np.abs(gelu) * t(u64) + t(ref.astype(np.float64))
+    err = np.abs(got - ref)
+    assert np.all(err <= bound), f"max abs err {err.max()}, worst excess {(err - bound).max()}"
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+def test_gemm_fused_partials_chain(hip, oracle, dtype):
+    """The down projection (K = 6912, six K chunks) leaves partial sums; the next GEMM adds
+    them while staging (residual + post-norm + pre-norm), as a decode step chains them."""
+    from sapphire_amd.device import DeviceArray, QMatrix
+    hdim, ffn, batch = 1152, 6912, 16
+    Wd = synth.quant_matrix(dtype, hdim, ffn, seed=43, tensor_id=1)
+    W2 = synth.quant_matrix(dtype, 1536, hdim, seed=43, tensor_id=2)
+    qd, q2 = QMatrix(dtype, Wd, layout=TILED), QMatrix(dtype, W2, layout=TILED)
+    g = synth.normal_f32((batch, ffn), 43, 3)
+    x = synth.normal_f32((batch, hdim), 43, 4)
+    wd, wn = _norm_w(hdim, 3), _norm_w(hdim, 4)
+    ns = hip.sapphire_gemm_splits(ffn)
+    assert ns == 6
+    dg, dx, dwd, dwn = (DeviceArray.from_numpy(a) for a in (g, x, wd, wn))
+    dparts = DeviceArray.empty(ns * batch * hdim)
+    _fused(hip, qd, batch, _GemmIn(dg.ptr, ffn, None, 0, 0, 0, None, None, 0, None, 1e-6),
+           _GemmOut(None, 0, dparts.ptr, 0))
+    dr, dy = DeviceArray.empty(batch * hdim), DeviceArray.empty(batch * 1536)
+    _fused(hip, q2, batch, _GemmIn(dx.ptr, hdim, dparts.ptr, ns, hdim, batch * hdim, dwd.ptr, dr.ptr, hdim, dwn.ptr,
+                                   1e-6), _GemmOut(dy.ptr, 1536, None, 0))
+    d = _ref(oracle, dtype, Wd, g)
+    partsum = dparts.numpy().reshape(ns, batch, hdim).sum(axis=0, dtype=np.float64)
+    ok, err = close(partsum, d)
+    assert ok, f"partial sums: max abs err {err}"
+    h = np.stack([x[b] + oracle.rmsnorm_delta(d[b], wd) for b in range(batch)]).astype(np.float32)
+    ok, err = close(dr.numpy().reshape(batch, hdim), h)
+    assert ok, f"residual: max abs err {err}"
+    ref = _ref(oracle, dtype, W2, np.stack([oracle.rmsnorm_delta(h[b], wn) for b in range(batch)]))
+    ok, err = close(dy.numpy().reshape(batch, 1536), ref)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+def test_gemm_fused_strided_input(hip, oracle, dtype):
+    """Input rows read with a leading dimension larger than K (the first 1024 columns of a
+    [batch][1536] buffer) and output rows written with one larger than M."""
+    from sapphire_amd.device import DeviceArray, QMatrix
+    m, k, batch = 1152, 1024, 7
+    W = synth.quant_matrix(dtype, m, k, seed=44, tensor_id=1)
+    qm = QMatrix(dtype, W, layout=TILED)
+    buf = synth.normal_f32((batch, 1536), 44, 2)
+    ref = _ref(oracle, dtype, W, np.ascontiguousarray(buf[:, :k]))
+    dx = DeviceArray.from_numpy(buf)
+    dy = DeviceArray.from_numpy(np.full((batch, m + 4), 7.0, np.float32))
+    _fused(hip, qm, batch, _GemmIn(dx.ptr, 1536, None, 0, 0, 0, None, None, 0, None, 1e-6), _GemmOut(dy.ptr, m + 4, None, 0))
+    got = dy.numpy().reshape(batch, m + 4)
+    ok, err = close(got[:, :m], ref)
+    assert ok, f"max abs err {err}"
+    assert np.all(got[:, m:] == 7.0)
+
+
+def test_gemm_fused_rejects(hip):
+    from sapphire_amd.device import DeviceArray, QMatrix
+    W = synth.quant_matrix(synth.Q4_0, 64, 6912, seed=45, tensor_id=1)
+    qm = QMatrix(synth.Q4_0, W, layout=TILED)
+    dx, dy, dw = DeviceArray.empty(4 * 6912), DeviceArray.empty(4 * 64), DeviceArray.empty(6912)
+    # a norm over K = 6912 needs whole rows in one K chunk
+    gin = _GemmIn(dx.ptr, 6912, None, 0, 0, 0, None, None, 0, dw.ptr, 1e-6)
+    assert hip.sapphire_gemm_q_fused_dev(qm.dtype, qm.ptr(), 64, 6912, 4, C.byref(gin),
+                                         C.byref(_GemmOut(dy.ptr, 64, None, 0)), None, None) == -1
+    gin = _GemmIn(dx.ptr, 6912, None, 0, 0, 0, None, None, 0, None, 1e-6)
+    assert hip.sapphire_gemm_q_fused_dev(qm.dtype, qm.ptr(), 64, 6912, 17, C.byref(gin),
+                                         C.byref(_GemmOut(dy.ptr, 64, None, 0)), None, None) == -1   # batch > 16
