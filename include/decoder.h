@@ -59,7 +59,8 @@ sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg
                                             const sapphire_decoder_weights_t *w);
 void sapphire_decoder_destroy(sapphire_decoder_t *dec);
 
-/* The KV caches as [n_layers][n_kv_heads][max_ctx][head_dim] fp32 (kv_cache.c:101-106). */
+/* The KV caches as [n_layers][n_kv_heads][max_ctx][head_dim] fp32 (kv_cache.c:101-106);
+ * for a batched decoder [batch][n_layers][n_kv_heads][max_ctx][head_dim]. */
 int sapphire_decoder_set_kv(sapphire_decoder_t *dec, const float *k, const float *v);
 int sapphire_decoder_get_kv(sapphire_decoder_t *dec, float *k, float *v);
 
@@ -70,6 +71,25 @@ int sapphire_decoder_get_kv(sapphire_decoder_t *dec, float *k, float *v);
  * device time of the steps (HIP events on the decoder's stream). 0 / -1. */
 int sapphire_decoder_generate(sapphire_decoder_t *dec, int token, int pos, int steps, int *tokens_out,
                               float *logits_out, float *elapsed_ms);
+
+/* ---- batched decode ----
+ * `batch` (2..16) independent sequences decoded in lock step, each with its own KV cache,
+ * position and greedy token: one step runs every projection as one matrix-core GEMM over
+ * the batch (the reference decodes one sequence per inference_forward call). Shapes:
+ * hidden, n_heads*head_dim and ffn multiples of 128, hidden <= 1152. Weights as for
+ * sapphire_decoder_create. A decoder made by sapphire_decoder_create has batch 1; the
+ * functions below accept it too. */
+sapphire_decoder_t *sapphire_decoder_create_batch(const sapphire_decoder_config_t *cfg,
+                                                  const sapphire_decoder_weights_t *w, int batch);
+int sapphire_decoder_batch(const sapphire_decoder_t *dec);
+/* The KV caches of sequence `seq`, [n_layers][n_kv_heads][max_ctx][head_dim] fp32.
+ * sapphire_decoder_set_kv / get_kv move all sequences at once, [batch][n_layers]... */
+int sapphire_decoder_set_kv_seq(sapphire_decoder_t *dec, int seq, const float *k, const float *v);
+int sapphire_decoder_get_kv_seq(sapphire_decoder_t *dec, int seq, float *k, float *v);
+/* tokens[batch] and pos[batch] start every sequence; tokens_out receives [steps][batch]
+ * greedy tokens; logits_out, if not NULL, [steps][batch][vocab]. */
+int sapphire_decoder_generate_batch(sapphire_decoder_t *dec, const int *tokens, const int *pos, int steps,
+                                    int *tokens_out, float *logits_out, float *elapsed_ms);
 
 #ifdef __cplusplus
 }

@@ -231,6 +231,14 @@ __device__ void norm_rope_heads(const float *src, int nv, int hd, const float *_
 // merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL).
 template <int DPL, int NH>
 __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
+    {   // sequence blockIdx.y of a batch
+        const size_t b = blockIdx.y;
+        a.qkv += b * a.qkv_stride;
+        a.kc += b * a.kv_stride;
+        a.vc += b * a.kv_stride;
+        a.d_pos += b;
+        a.part += b * (size_t)gridDim.x * NH * (a.hd + 2);
+    }
     __shared__ float raw[kAttnMaxQ + 2 * kAttnMaxKV];   // q | k | v as projected
     __shared__ float qs[kAttnMaxQ];
     __shared__ float ks[kAttnMaxKV];
@@ -362,11 +370,13 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 // head, one thread per dim.
 template <int NS>
 __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float *__restrict__ part, int nh, int hd,
-                                                                    float *__restrict__ out) {
+                                                                    float *__restrict__ out, size_t out_stride) {
     static_assert(NS <= kWave, "one lane of wave 0 per slice");
     __shared__ float es[NS];
     __shared__ float S;
     const int h = blockIdx.x, t = threadIdx.x;
+    part += (size_t)blockIdx.y * NS * nh * (hd + 2);   // sequence blockIdx.y
+    out += (size_t)blockIdx.y * out_stride;
     if (t < kWave) {
         const float *p = part + ((size_t)t * nh + h) * (hd + 2);
         const float mb = t < NS ? p[hd] : -INFINITY;
@@ -408,6 +418,85 @@ __global__ void dec_advance_kernel(const int *__restrict__ tok, int *__restrict_
     }
 }
 
+// ---- batched decode: embedding, greedy token and position of a batch of sequences ----
+
+__global__ void dec_embed_batch_kernel(const uint16_t *__restrict__ embed, int hidden, float es,
+                                       const int *__restrict__ tok, float *__restrict__ resid) {
+    const size_t row = (size_t)tok[blockIdx.y] * hidden;
+    float *out = resid + (size_t)blockIdx.y * hidden;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x) {
+        const float v = __uint_as_float((uint32_t)embed[row + i] << 16);
+        out[i] = es != 1.0f ? __fmul_rn(v, es) : v;
+    }
+}
+
+constexpr int kArgmaxParts = 64;     // workgroups per sequence in the first argmax pass
+
+// (value, index) order of sample_greedy (utils.c:145-156): a larger value wins, and of
+// equal values the lower index.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__device__ __forceinline__ void wave_best(float &v, int &i) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, kWave);
+        const int oi = __shfl_xor(i, off, kWave);
+        if (better(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+}
+
+// grid (kArgmaxParts, batch): part[b][p] = best (value, index) of slice p of logits[b]
+__global__ __launch_bounds__(kThreads) void dec_argmax_part_kernel(const float *__restrict__ logits, int n,
+                                                                   float *__restrict__ part) {
+    __shared__ float sv[kThreads / kWave];
+    __shared__ int si[kThreads / kWave];
+    const float *x = logits + (size_t)blockIdx.y * n;
+    const int chunk = (n + gridDim.x - 1) / gridDim.x;
+    const int i0 = blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+    float bv = -INFINITY;
+    int bi = n;
+    for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+        const float v = x[i];
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    wave_best(bv, bi);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    if (lane == 0) { sv[wid] = bv; si[wid] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / kWave; ++w)
+            if (better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+        float *o = part + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 2;
+        o[0] = bv;
+        o[1] = __int_as_float(bi);
+    }
+}
+
+// grid (batch), one wave: tokens[b] = best of the sequence's partials
+__global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int nparts, int *__restrict__ tokens) {
+    const float *p = part + (size_t)blockIdx.x * nparts * 2;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = threadIdx.x; j < nparts; j += kWave) {
+        const float v = p[2 * j];
+        const int i = __float_as_int(p[2 * j + 1]);
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    wave_best(bv, bi);
+    if (threadIdx.x == 0) tokens[blockIdx.x] = bi;
+}
+
+__global__ void dec_advance_batch_kernel(const int *__restrict__ tok, int *__restrict__ pos, int *__restrict__ step,
+                                         int batch, int *__restrict__ log) {
+    const int s = *step;
+    for (int b = threadIdx.x; b < batch; b += blockDim.x) {
+        log[(size_t)s * batch + b] = tok[b];
+        pos[b] = pos[b] + 1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *step = s + 1;
+}
+
 template <int DT, bool GEGLU>
 int launch_gemv_kernel(const QMat &w0, const QMat &w1, const GemvIn &in, float *y, hipStream_t st) {
     const int nb = w0.K / kBlock;
@@ -447,16 +536,18 @@ int dec_prologue_only(const GemvIn &in, int K, float *out, hipStream_t s) {
     return hip_ok(hipGetLastError(), "dec_prologue launch") ? 0 : -1;
 }
 
+size_t attn_part_floats(int nh, int hd) { return (size_t)kAttnSplit * nh * (hd + 2); }
+
 int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     if (a.nh * a.hd > kAttnMaxQ || a.nkv * a.hd > kAttnMaxKV || a.nkv <= 0 || a.nkv > 2 || a.nh % a.nkv != 0 ||
-        a.hd % kWave != 0 || a.hd > 4 * kWave || a.nh + a.nkv > 16) {
+        a.hd % kWave != 0 || a.hd > 4 * kWave || a.nh + a.nkv > 16 || a.batch < 1 || a.batch > 65535) {
         set_error("attention shape not supported (heads %d/%d, head_dim %d)", a.nh, a.nkv, a.hd);
         return -1;
     }
     const int dpl = a.hd / kWave;
 #define SPH_ATTN(DPLV, NHV)                                                                                  \
     if (dpl == DPLV && a.nh == NHV) {                                                                        \
-        hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV>), dim3(kAttnSplit), dim3(kThreads), 0, s, a); \
+        hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV>), dim3(kAttnSplit, a.batch), dim3(kThreads), 0, s, a); \
     } else
     SPH_ATTN(1, 4) SPH_ATTN(2, 4) SPH_ATTN(4, 4) SPH_ATTN(1, 8) SPH_ATTN(2, 8) SPH_ATTN(4, 8) {
         set_error("attention with %d heads of dim %d not instantiated", a.nh, a.hd);
@@ -464,7 +555,8 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     }
 #undef SPH_ATTN
     if (!hip_ok(hipGetLastError(), "attention launch")) return -1;
-    hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplit>, dim3(a.nh), dim3(kThreads), 0, s, a.part, a.nh, a.hd, out);
+    hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplit>, dim3(a.nh, a.batch), dim3(kThreads), 0, s, a.part, a.nh,
+                       a.hd, out, a.out_stride);
     return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
 }
 
@@ -477,6 +569,30 @@ int dec_embed(const uint16_t *embed, int hidden, float es, const int *d_token, f
 int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, hipStream_t s) {
     hipLaunchKernelGGL(dec_advance_kernel, dim3(1), dim3(64), 0, s, d_token, d_pos, d_step, log);
     return hip_ok(hipGetLastError(), "advance launch") ? 0 : -1;
+}
+
+int dec_embed_batch(const uint16_t *embed, int hidden, float es, const int *d_tokens, int batch, float *resid,
+                    hipStream_t s) {
+    hipLaunchKernelGGL(dec_embed_batch_kernel, dim3((hidden + kThreads - 1) / kThreads, batch), dim3(kThreads), 0, s,
+                       embed, hidden, es, d_tokens, resid);
+    return hip_ok(hipGetLastError(), "batched embed launch") ? 0 : -1;
+}
+
+size_t argmax_batch_part_floats(int n, int batch) {
+    (void)n;
+    return (size_t)batch * kArgmaxParts * 2;
+}
+
+int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_tokens, hipStream_t s) {
+    hipLaunchKernelGGL(dec_argmax_part_kernel, dim3(kArgmaxParts, batch), dim3(kThreads), 0, s, logits, n, part);
+    if (!hip_ok(hipGetLastError(), "argmax launch")) return -1;
+    hipLaunchKernelGGL(dec_argmax_finish_kernel, dim3(batch), dim3(kWave), 0, s, part, kArgmaxParts, d_tokens);
+    return hip_ok(hipGetLastError(), "argmax finish launch") ? 0 : -1;
+}
+
+int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, hipStream_t s) {
+    hipLaunchKernelGGL(dec_advance_batch_kernel, dim3(1), dim3(kWave), 0, s, d_tokens, d_pos, d_step, batch, log);
+    return hip_ok(hipGetLastError(), "batched advance launch") ? 0 : -1;
 }
 
 }  // namespace sapphire

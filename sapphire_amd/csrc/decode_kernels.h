@@ -47,14 +47,31 @@ struct AttnArgs {
     int nh = 0, nkv = 0, hd = 0, max_ctx = 0;
     int window = 0;                  // sliding window of a local layer, 0 for a global one
     float scale = 1.f, eps = 1e-6f;
+    // a batch of independent sequences: sequence b uses qkv + b*qkv_stride, the caches at
+    // + b*kv_stride, d_pos[b], and its own partials; out + b*out_stride
+    int batch = 1;
+    size_t qkv_stride = 0, kv_stride = 0, out_stride = 0;
 };
 // QK-norm, RoPE, KV write and split attention partials, then their combination into
-// out[nh*hd] (attention.c:93-163, 271-309; kv_cache.c:252-278).
+// out[nh*hd] (attention.c:93-163, 271-309; kv_cache.c:252-278). part holds
+// attn_part_floats(nh, hd) floats per sequence.
+size_t attn_part_floats(int nh, int hd);
 int dec_attention(const AttnArgs &a, float *out, hipStream_t s);
 
 // resid[i] = bf16 row of *d_token * es (transformer.c:347-365)
 int dec_embed(const uint16_t *embed, int hidden, float es, const int *d_token, float *resid, hipStream_t s);
 // log[*d_step] = *d_token; ++*d_step; ++*d_pos
 int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, hipStream_t s);
+
+// ---- batched decode (a batch of sequences in lock step) ----
+// resid[b][i] = bf16 row of tokens[b] * es
+int dec_embed_batch(const uint16_t *embed, int hidden, float es, const int *d_tokens, int batch, float *resid,
+                    hipStream_t s);
+// tokens[b] = first index of the maximum of logits[b][0..n) (utils.c:145-156); part holds
+// argmax_batch_part_floats(n, batch) floats
+size_t argmax_batch_part_floats(int n, int batch);
+int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_tokens, hipStream_t s);
+// log[*d_step][b] = tokens[b]; ++pos[b]; ++*d_step
+int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, hipStream_t s);
 
 }  // namespace sapphire

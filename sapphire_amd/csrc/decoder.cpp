@@ -7,6 +7,13 @@
 // gate/up GEMV, down GEMV), final norm, LM head with its argmax epilogue writing the next
 // token, and a one-thread kernel that logs the token and advances the position. The host
 // only launches the graph; nothing crosses PCIe between steps.
+//
+// A batched decoder (sapphire_decoder_create_batch) runs 2..16 sequences in lock step, each
+// with its own KV cache and position. Its projections are TILED matrices multiplied on the
+// matrix cores as one GEMM over the batch (QKV stacked, gate and up interleaved by eight
+// rows so that the GeGLU is the GEMM's epilogue), and the residual adds and RMSNorms are
+// formed while each GEMM stages its input; a step is 4 GEMMs and 2 attention launches per
+// layer, the LM-head GEMM, a batched argmax and the advance.
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -22,6 +29,8 @@ namespace {
 
 struct Layer {
     QMat qkv, o, gate, up, down;
+    // batched decoder: TILED matrices (QKV stacked; gate/up interleaved by eight rows)
+    const void *t_qkv = nullptr, *t_o = nullptr, *t_gu = nullptr, *t_down = nullptr;
     const float *n_attn = nullptr, *n_attn_post = nullptr, *n_ffn = nullptr, *n_ffn_post = nullptr;
     const float *qn = nullptr, *kn = nullptr;
     bool global = false;
@@ -45,10 +54,15 @@ struct sapphire_decoder {
     float *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr, *ffn_out = nullptr, *xfin = nullptr;
     float *logits = nullptr, *attn_part = nullptr;
     void *lm_scratch = nullptr;
-    int *state = nullptr;   // [0] token, [1] position, [2] step
-    int *log = nullptr;     // [max_ctx] tokens of the steps
+    int *state = nullptr;   // [0] token, [1] position, [2] step; batched: tokens[B], pos[B], step
+    int *log = nullptr;     // [max_ctx] tokens of the steps; batched: [max_ctx][B]
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // batched decoder
+    int batch = 1;
+    float *dparts = nullptr;     // the down projection's K-chunk partial sums [splits][B][hidden]
+    float *amax_part = nullptr;  // argmax partials
+    void *gws = nullptr;         // GEMM workspace
 };
 
 namespace {
@@ -110,6 +124,49 @@ bool upload_packed(sapphire_decoder *d, int dt, std::initializer_list<std::pair<
     out->s = reinterpret_cast<const float *>(static_cast<const uint8_t *>(packed) + q_scales_offset(dt, M, K));
     out->M = M;
     out->K = K;
+    return true;
+}
+
+// Block arrays (AOS) -> one TILED matrix: the parts' rows concatenated in order, or, with
+// interleave8, two equally long parts interleaved by eight rows (a0..a7, b0..b7, a8..).
+bool upload_tiled(sapphire_decoder *d, int dt, std::initializer_list<std::pair<const void *, int>> parts, int K,
+                  bool interleave8, const void **out, const char *what) {
+    int M = 0;
+    for (const auto &p : parts) {
+        if (!p.first) {
+            set_error("decoder weights: %s is NULL", what);
+            return false;
+        }
+        M += p.second;
+    }
+    const size_t rb = q_aos_bytes(dt, 1, K);
+    void *aos = nullptr;
+    if (!hip_ok(hipMalloc(&aos, rb * M), what)) return false;
+    bool ok = true;
+    if (interleave8) {
+        int i = 0;
+        for (const auto &p : parts) {
+            ok = ok && p.second % 8 == 0 && p.second * 2 == M &&
+                 hip_ok(hipMemcpy2D(static_cast<char *>(aos) + (size_t)i * 8 * rb, 16 * rb, p.first, 8 * rb, 8 * rb,
+                                    p.second / 8, hipMemcpyHostToDevice),
+                        what);
+            ++i;
+        }
+        if (!ok) set_error("decoder weights: %s cannot be interleaved", what);
+    } else {
+        size_t off = 0;
+        for (const auto &p : parts) {
+            ok = ok && hip_ok(hipMemcpy(static_cast<char *>(aos) + off, p.first, rb * p.second, hipMemcpyHostToDevice),
+                              what);
+            off += rb * p.second;
+        }
+    }
+    void *t = nullptr;
+    ok = ok && dev_alloc(d, &t, q_tiled_bytes(dt, M, K), what) && launch_to_tiled(dt, aos, M, K, t, d->stream) == 0 &&
+         hip_ok(hipStreamSynchronize(d->stream), what);
+    (void)hipFree(aos);
+    if (!ok) return false;
+    *out = t;
     return true;
 }
 
@@ -214,6 +271,115 @@ int enqueue_step(sapphire_decoder *d) {
     return dec_advance(d->state, d->state + 1, d->state + 2, d->log, s);
 }
 
+// One step of the batched decoder, enqueued on d->stream (recorded into the graph).
+int enqueue_step_batch(sapphire_decoder *d) {
+    const auto &c = d->cfg;
+    hipStream_t s = d->stream;
+    const int B = d->batch, H = c.hidden, hd = c.head_dim;
+    const int nq = c.n_heads * hd, nqkv = nq + 2 * c.n_kv_heads * hd;
+    const float es = sqrtf((float)H);
+    const float scale = 1.0f / sqrtf(c.query_pre_attn_scalar > 0.f ? c.query_pre_attn_scalar : (float)hd);
+    const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
+    const int nsd = gemm_splits(c.ffn);
+    const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
+    if (dec_embed_batch(d->embed, H, es, d->state, B, d->resid[0], s) != 0) return -1;
+    int cur = 0;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer &L = d->layers[l];
+        // previous layer's finalize (transformer.c:231-239) + attention pre-norm (attention.c:316-325)
+        GemmIn qi;
+        qi.x = d->resid[cur];
+        qi.ldx = H;
+        qi.w_norm = L.n_attn;
+        qi.eps = c.eps;
+        if (l > 0) {
+            qi.parts = d->dparts;
+            qi.nparts = nsd;
+            qi.ldp = H;
+            qi.part_stride = (size_t)B * H;
+            qi.w_delta = d->layers[l - 1].n_ffn_post;
+            qi.resid_out = d->resid[1 - cur];
+            qi.ldr = H;
+            cur = 1 - cur;
+        }
+        GemmOut qo;
+        qo.y = d->qkv;
+        qo.ldy = nqkv;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_qkv, nqkv, H, B, qi, qo, d->gws, s) != 0) return -1;
+        AttnArgs at;
+        at.qkv = d->qkv;
+        at.qn = L.qn;
+        at.kn = L.kn;
+        at.cos_t = L.global ? d->cos_g : d->cos_l;
+        at.sin_t = L.global ? d->sin_g : d->sin_l;
+        at.kc = d->kc + (size_t)l * layer_kv;
+        at.vc = d->vc + (size_t)l * layer_kv;
+        at.d_pos = d->state + B;
+        at.part = d->attn_part;
+        at.nh = c.n_heads;
+        at.nkv = c.n_kv_heads;
+        at.hd = hd;
+        at.max_ctx = c.max_ctx;
+        at.window = L.global ? 0 : win;
+        at.scale = scale;
+        at.eps = c.eps;
+        at.batch = B;
+        at.qkv_stride = (size_t)nqkv;
+        at.kv_stride = (size_t)c.n_layers * layer_kv;
+        at.out_stride = (size_t)nq;
+        if (dec_attention(at, d->attn, s) != 0) return -1;
+        GemmIn oi;
+        oi.x = d->attn;
+        oi.ldx = nq;
+        GemmOut oo;
+        oo.y = d->o;
+        oo.ldy = H;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_o, H, nq, B, oi, oo, d->gws, s) != 0) return -1;
+        // post-attention norm + residual (attention.c:356-366), FFN pre-norm (transformer.c:119-121),
+        // gate/up projections with the GeGLU (transformer.c:126-157)
+        GemmIn fi;
+        fi.x = d->resid[cur];
+        fi.ldx = H;
+        fi.parts = d->o;
+        fi.nparts = 1;
+        fi.ldp = H;
+        fi.w_delta = L.n_attn_post;
+        fi.resid_out = d->resid[1 - cur];
+        fi.ldr = H;
+        fi.w_norm = L.n_ffn;
+        fi.eps = c.eps;
+        cur = 1 - cur;
+        GemmOut fo;
+        fo.y = d->g;
+        fo.ldy = c.ffn;
+        fo.geglu = true;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_gu, 2 * c.ffn, H, B, fi, fo, d->gws, s) != 0) return -1;
+        GemmIn di;
+        di.x = d->g;
+        di.ldx = c.ffn;
+        GemmOut dout;
+        dout.parts = d->dparts;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_down, H, c.ffn, B, di, dout, d->gws, s) != 0) return -1;
+    }
+    // last finalize + final norm (transformer.c:400-406), LM head, greedy tokens
+    GemmIn li;
+    li.x = d->resid[cur];
+    li.ldx = H;
+    li.parts = d->dparts;
+    li.nparts = nsd;
+    li.ldp = H;
+    li.part_stride = (size_t)B * H;
+    li.w_delta = d->layers[c.n_layers - 1].n_ffn_post;
+    li.w_norm = d->norm_final;
+    li.eps = c.eps;
+    GemmOut lo;
+    lo.y = d->logits;
+    lo.ldy = c.vocab;
+    if (launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s) != 0) return -1;
+    if (dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s) != 0) return -1;
+    return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
+}
+
 bool valid_config(const sapphire_decoder_config_t &c) {
     if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.ffn <= 0 ||
         c.vocab <= 0 || c.max_ctx <= 0) {
@@ -254,15 +420,47 @@ void sapphire_decoder_destroy(sapphire_decoder_t *d) {
     delete d;
 }
 
-sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg, const sapphire_decoder_weights_t *w) {
+}  // extern "C"
+
+namespace {
+
+// The batched decoder's extra shape rules: every projection K a multiple of 128 (TILED),
+// the hidden size at most 36 blocks (the norms are formed inside one K chunk).
+bool valid_batch_config(const sapphire_decoder_config_t &c, int batch) {
+    const int nq = c.n_heads * c.head_dim;
+    if (batch < 2 || batch > 16) {
+        set_error("batched decoder: batch must be 2..16 (got %d)", batch);
+        return false;
+    }
+    if (c.hidden % 128 || nq % 128 || c.ffn % 128 || c.hidden > 1152) {
+        set_error("batched decoder: hidden, n_heads*head_dim and ffn must be multiples of 128, hidden <= 1152");
+        return false;
+    }
+    if (c.n_heads % c.n_kv_heads || (c.head_dim & 1)) {
+        set_error("decoder config: heads must group evenly and head_dim be even");
+        return false;
+    }
+    return true;
+}
+
+sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const sapphire_decoder_weights_t *w,
+                                   int batch) {
     if (!cfg || !w) {
         set_error("sapphire_decoder_create: NULL argument");
         return nullptr;
     }
-    if (!valid_config(*cfg)) return nullptr;
+    if (batch == 1 ? !valid_config(*cfg) : !valid_batch_config(*cfg, batch)) return nullptr;
+    if (batch > 1 && (cfg->n_layers <= 0 || cfg->hidden <= 0 || cfg->n_heads <= 0 || cfg->n_kv_heads <= 0 ||
+                      cfg->head_dim <= 0 || cfg->ffn <= 0 || cfg->vocab <= 0 || cfg->max_ctx <= 0 ||
+                      !is_quant(cfg->wdtype) || !is_quant(cfg->lm_dtype))) {
+        set_error("decoder config: non-positive dimension or weights not Q4_0/Q8_0");
+        return nullptr;
+    }
     sapphire_decoder *d = new (std::nothrow) sapphire_decoder();
     if (!d) return nullptr;
     d->cfg = *cfg;
+    d->batch = batch;
+    const int B = batch;
     const auto &c = d->cfg;
     auto fail = [&]() -> sapphire_decoder_t * {
         sapphire_decoder_destroy(d);
@@ -281,12 +479,21 @@ sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg
             set_error("decoder weights: a per-layer array is NULL");
             return fail();
         }
-        if (!upload_packed(d, c.wdtype, {{w->wq[l], nq}, {w->wk[l], nk}, {w->wv[l], nk}}, H, &L.qkv, "wqkv") ||
-            !upload_packed(d, c.wdtype, {{w->wo[l], H}}, nq, &L.o, "wo") ||
-            !upload_packed(d, c.wdtype, {{w->wgate[l], c.ffn}}, H, &L.gate, "wgate") ||
-            !upload_packed(d, c.wdtype, {{w->wup[l], c.ffn}}, H, &L.up, "wup") ||
-            !upload_packed(d, c.wdtype, {{w->wdown[l], H}}, c.ffn, &L.down, "wdown"))
-            return fail();
+        if (B == 1) {
+            if (!upload_packed(d, c.wdtype, {{w->wq[l], nq}, {w->wk[l], nk}, {w->wv[l], nk}}, H, &L.qkv, "wqkv") ||
+                !upload_packed(d, c.wdtype, {{w->wo[l], H}}, nq, &L.o, "wo") ||
+                !upload_packed(d, c.wdtype, {{w->wgate[l], c.ffn}}, H, &L.gate, "wgate") ||
+                !upload_packed(d, c.wdtype, {{w->wup[l], c.ffn}}, H, &L.up, "wup") ||
+                !upload_packed(d, c.wdtype, {{w->wdown[l], H}}, c.ffn, &L.down, "wdown"))
+                return fail();
+        } else {
+            if (!upload_tiled(d, c.wdtype, {{w->wq[l], nq}, {w->wk[l], nk}, {w->wv[l], nk}}, H, false, &L.t_qkv,
+                              "wqkv") ||
+                !upload_tiled(d, c.wdtype, {{w->wo[l], H}}, nq, false, &L.t_o, "wo") ||
+                !upload_tiled(d, c.wdtype, {{w->wgate[l], c.ffn}, {w->wup[l], c.ffn}}, H, true, &L.t_gu, "wgate/wup") ||
+                !upload_tiled(d, c.wdtype, {{w->wdown[l], H}}, c.ffn, false, &L.t_down, "wdown"))
+                return fail();
+        }
         if (!(L.n_attn = upload_f32(d, w->norm_attn[l], H, "norm_attn")) ||
             !(L.n_attn_post = upload_f32(d, w->norm_attn_post[l], H, "norm_attn_post")) ||
             !(L.n_ffn = upload_f32(d, w->norm_ffn[l], H, "norm_ffn")) ||
@@ -308,7 +515,14 @@ sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg
         const size_t ab = q_aos_bytes(c.lm_dtype, c.vocab, H);
         if (!hip_ok(hipMalloc(&aos, ab), "lm aos")) return fail();
         bool ok = hip_ok(hipMemcpy(aos, w->lm_head, ab, hipMemcpyHostToDevice), "lm upload");
-        d->lm_layout = tiled_supported(c.lm_dtype, c.vocab, H) ? LAYOUT_TILED : LAYOUT_PACKED;
+        d->lm_layout = (B > 1 ? tiled_layout_ok(c.lm_dtype, c.vocab, H) : tiled_supported(c.lm_dtype, c.vocab, H))
+                           ? LAYOUT_TILED
+                           : LAYOUT_PACKED;
+        if (B > 1 && d->lm_layout != LAYOUT_TILED) {
+            (void)hipFree(aos);
+            set_error("batched decoder: the LM head does not fit the TILED layout");
+            return fail();
+        }
         const size_t lb = d->lm_layout == LAYOUT_TILED ? q_tiled_bytes(c.lm_dtype, c.vocab, H)
                                                        : q_packed_bytes(c.lm_dtype, c.vocab, H);
         void *lm = nullptr;
@@ -335,34 +549,69 @@ sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg
             !(d->sin_l = const_cast<float *>(upload_f32(d, sn.data(), sn.size(), "rope"))))
             return fail();
     }
-    const size_t kv = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * hd;
+    const size_t kv = (size_t)B * c.n_layers * c.n_kv_heads * c.max_ctx * hd;
     if (!dev_alloc_t(d, &d->kc, kv, "k cache") || !dev_alloc_t(d, &d->vc, kv, "v cache") ||
         !hip_ok(hipMemset(d->kc, 0, kv * sizeof(float)), "kv zero") ||
         !hip_ok(hipMemset(d->vc, 0, kv * sizeof(float)), "kv zero"))
         return fail();
-    if (!dev_alloc_t(d, &d->resid[0], H, "resid") || !dev_alloc_t(d, &d->resid[1], H, "resid") ||
-        !dev_alloc_t(d, &d->qkv, (size_t)nq + 2 * nk, "qkv") || !dev_alloc_t(d, &d->attn, nq, "attn") ||
-        !dev_alloc_t(d, &d->o, H, "o") || !dev_alloc_t(d, &d->g, c.ffn, "g") ||
+    const size_t b = (size_t)B;
+    if (!dev_alloc_t(d, &d->resid[0], b * H, "resid") || !dev_alloc_t(d, &d->resid[1], b * H, "resid") ||
+        !dev_alloc_t(d, &d->qkv, b * (nq + 2 * nk), "qkv") || !dev_alloc_t(d, &d->attn, b * nq, "attn") ||
+        !dev_alloc_t(d, &d->o, b * H, "o") || !dev_alloc_t(d, &d->g, b * c.ffn, "g") ||
         !dev_alloc_t(d, &d->ffn_out, H, "ffn_out") || !dev_alloc_t(d, &d->xfin, H, "xfin") ||
-        !dev_alloc_t(d, &d->logits, c.vocab, "logits") ||
-        !dev_alloc_t(d, &d->attn_part, (size_t)kAttnSplit * c.n_heads * (hd + 2), "attn partials") ||
-        !dev_alloc_t(d, &d->state, 4, "state") || !dev_alloc_t(d, &d->log, c.max_ctx, "token log"))
+        !dev_alloc_t(d, &d->logits, b * c.vocab, "logits") ||
+        !dev_alloc_t(d, &d->attn_part, b * attn_part_floats(c.n_heads, hd), "attn partials") ||
+        !dev_alloc_t(d, &d->state, 2 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log"))
         return fail();
+    if (B > 1) {
+        if (!dev_alloc_t(d, &d->dparts, (size_t)gemm_splits(c.ffn) * b * H, "down partials") ||
+            !dev_alloc_t(d, &d->amax_part, argmax_batch_part_floats(c.vocab, B), "argmax partials") ||
+            !dev_alloc(d, &d->gws, gemm_workspace_bytes(std::max(H, c.vocab), std::max(nq, c.ffn)), "gemm workspace"))
+            return fail();
+    }
     return d;
 }
+
+size_t seq_kv_floats(const sapphire_decoder_config_t &c) {
+    return (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim;
+}
+
+int kv_copy(sapphire_decoder_t *d, int seq, int nseq, const float *k_in, const float *v_in, float *k_out,
+            float *v_out) {
+    const size_t n = seq_kv_floats(d->cfg), off = (size_t)seq * n, bytes = (size_t)nseq * n * sizeof(float);
+    SPH_CHECK(hipSetDevice(d->device));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    if (k_in) {
+        SPH_CHECK(hipMemcpy(d->kc + off, k_in, bytes, hipMemcpyHostToDevice));
+        SPH_CHECK(hipMemcpy(d->vc + off, v_in, bytes, hipMemcpyHostToDevice));
+    } else {
+        SPH_CHECK(hipMemcpy(k_out, d->kc + off, bytes, hipMemcpyDeviceToHost));
+        SPH_CHECK(hipMemcpy(v_out, d->vc + off, bytes, hipMemcpyDeviceToHost));
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+sapphire_decoder_t *sapphire_decoder_create(const sapphire_decoder_config_t *cfg, const sapphire_decoder_weights_t *w) {
+    return create_decoder(cfg, w, 1);
+}
+
+sapphire_decoder_t *sapphire_decoder_create_batch(const sapphire_decoder_config_t *cfg,
+                                                  const sapphire_decoder_weights_t *w, int batch) {
+    return create_decoder(cfg, w, batch);
+}
+
+int sapphire_decoder_batch(const sapphire_decoder_t *d) { return d ? d->batch : 0; }
 
 int sapphire_decoder_set_kv(sapphire_decoder_t *d, const float *k, const float *v) {
     if (!d || !k || !v) {
         set_error("sapphire_decoder_set_kv: NULL argument");
         return -1;
     }
-    const auto &c = d->cfg;
-    const size_t b = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim * sizeof(float);
-    SPH_CHECK(hipSetDevice(d->device));
-    SPH_CHECK(hipStreamSynchronize(d->stream));
-    SPH_CHECK(hipMemcpy(d->kc, k, b, hipMemcpyHostToDevice));
-    SPH_CHECK(hipMemcpy(d->vc, v, b, hipMemcpyHostToDevice));
-    return 0;
+    return kv_copy(d, 0, d->batch, k, v, nullptr, nullptr);
 }
 
 int sapphire_decoder_get_kv(sapphire_decoder_t *d, float *k, float *v) {
@@ -370,30 +619,43 @@ int sapphire_decoder_get_kv(sapphire_decoder_t *d, float *k, float *v) {
         set_error("sapphire_decoder_get_kv: NULL argument");
         return -1;
     }
-    const auto &c = d->cfg;
-    const size_t b = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim * sizeof(float);
-    SPH_CHECK(hipSetDevice(d->device));
-    SPH_CHECK(hipStreamSynchronize(d->stream));
-    SPH_CHECK(hipMemcpy(k, d->kc, b, hipMemcpyDeviceToHost));
-    SPH_CHECK(hipMemcpy(v, d->vc, b, hipMemcpyDeviceToHost));
-    return 0;
+    return kv_copy(d, 0, d->batch, nullptr, nullptr, k, v);
 }
 
-int sapphire_decoder_generate(sapphire_decoder_t *d, int token, int pos, int steps, int *tokens_out, float *logits_out,
-                              float *elapsed_ms) {
-    if (!d || !tokens_out || steps <= 0) {
+int sapphire_decoder_set_kv_seq(sapphire_decoder_t *d, int seq, const float *k, const float *v) {
+    if (!d || !k || !v || seq < 0 || seq >= d->batch) {
+        set_error("sapphire_decoder_set_kv_seq: bad arguments");
+        return -1;
+    }
+    return kv_copy(d, seq, 1, k, v, nullptr, nullptr);
+}
+
+int sapphire_decoder_get_kv_seq(sapphire_decoder_t *d, int seq, float *k, float *v) {
+    if (!d || !k || !v || seq < 0 || seq >= d->batch) {
+        set_error("sapphire_decoder_get_kv_seq: bad arguments");
+        return -1;
+    }
+    return kv_copy(d, seq, 1, nullptr, nullptr, k, v);
+}
+
+int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, const int *pos, int steps,
+                                    int *tokens_out, float *logits_out, float *elapsed_ms) {
+    if (!d || !tokens || !pos || !tokens_out || steps <= 0) {
         set_error("sapphire_decoder_generate: bad arguments");
         return -1;
     }
     const auto &c = d->cfg;
-    if (token < 0 || token >= c.vocab || pos < 0 || pos + steps > c.max_ctx) {
-        set_error("sapphire_decoder_generate: token %d / positions %d..%d out of range", token, pos, pos + steps - 1);
-        return -1;
-    }
+    const int B = d->batch;
+    for (int b = 0; b < B; ++b)
+        if (tokens[b] < 0 || tokens[b] >= c.vocab || pos[b] < 0 || pos[b] + steps > c.max_ctx) {
+            set_error("sapphire_decoder_generate: sequence %d: token %d / positions %d..%d out of range", b, tokens[b],
+                      pos[b], pos[b] + steps - 1);
+            return -1;
+        }
     SPH_CHECK(hipSetDevice(d->device));
     if (!d->exec) {
         SPH_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = enqueue_step(d);
+        const int rc = B == 1 ? enqueue_step(d) : enqueue_step_batch(d);
         hipGraph_t g = nullptr;
         const hipError_t e = hipStreamEndCapture(d->stream, &g);
         if (rc != 0 || !hip_ok(e, "hipStreamEndCapture")) {
@@ -403,18 +665,29 @@ int sapphire_decoder_generate(sapphire_decoder_t *d, int token, int pos, int ste
         d->graph = g;
         SPH_CHECK(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
     }
-    const int st[4] = {token, pos, 0, 0};
-    SPH_CHECK(hipMemcpy(d->state, st, sizeof st, hipMemcpyHostToDevice));
+    // state: token, position, step (one sequence) or tokens[B], positions[B], step
+    std::vector<int> st((size_t)2 * B + 2, 0);
+    if (B == 1) {
+        st[0] = tokens[0];
+        st[1] = pos[0];
+    } else {
+        for (int b = 0; b < B; ++b) {
+            st[b] = tokens[b];
+            st[B + b] = pos[b];
+        }
+    }
+    SPH_CHECK(hipMemcpy(d->state, st.data(), sizeof(int) * st.size(), hipMemcpyHostToDevice));
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (elapsed_ms) {
         SPH_CHECK(hipEventCreate(&e0));
         SPH_CHECK(hipEventCreate(&e1));
         SPH_CHECK(hipEventRecord(e0, d->stream));
     }
+    const size_t lstep = (size_t)B * c.vocab;
     for (int s = 0; s < steps; ++s) {
         SPH_CHECK(hipGraphLaunch(d->exec, d->stream));
         if (logits_out)
-            SPH_CHECK(hipMemcpyAsync(logits_out + (size_t)s * c.vocab, d->logits, sizeof(float) * (size_t)c.vocab,
+            SPH_CHECK(hipMemcpyAsync(logits_out + (size_t)s * lstep, d->logits, sizeof(float) * lstep,
                                      hipMemcpyDeviceToHost, d->stream));
     }
     if (elapsed_ms) SPH_CHECK(hipEventRecord(e1, d->stream));
@@ -424,8 +697,17 @@ int sapphire_decoder_generate(sapphire_decoder_t *d, int token, int pos, int ste
         (void)hipEventDestroy(e0);
         (void)hipEventDestroy(e1);
     }
-    SPH_CHECK(hipMemcpy(tokens_out, d->log, sizeof(int) * (size_t)steps, hipMemcpyDeviceToHost));
+    SPH_CHECK(hipMemcpy(tokens_out, d->log, sizeof(int) * (size_t)steps * B, hipMemcpyDeviceToHost));
     return 0;
+}
+
+int sapphire_decoder_generate(sapphire_decoder_t *d, int token, int pos, int steps, int *tokens_out, float *logits_out,
+                              float *elapsed_ms) {
+    if (d && d->batch != 1) {
+        set_error("sapphire_decoder_generate: a batched decoder takes sapphire_decoder_generate_batch");
+        return -1;
+    }
+    return sapphire_decoder_generate_batch(d, &token, &pos, steps, tokens_out, logits_out, elapsed_ms);
 }
 
 }  // extern "C"

@@ -45,10 +45,23 @@ def _protos(L):
     L.sapphire_decoder_generate.restype = C.c_int
     L.sapphire_decoder_generate.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
                                             C.POINTER(C.c_float)]
+    L.sapphire_decoder_create_batch.restype = C.c_void_p
+    L.sapphire_decoder_create_batch.argtypes = [C.POINTER(DecoderConfig), C.POINTER(DecoderWeights), C.c_int]
+    L.sapphire_decoder_batch.restype = C.c_int
+    L.sapphire_decoder_batch.argtypes = [C.c_void_p]
+    for n in ("sapphire_decoder_set_kv_seq", "sapphire_decoder_get_kv_seq"):
+        getattr(L, n).restype = C.c_int
+        getattr(L, n).argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+    L.sapphire_decoder_generate_batch.restype = C.c_int
+    L.sapphire_decoder_generate_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                                  C.c_void_p, C.POINTER(C.c_float)]
 
 
 class Decoder:
-    def __init__(self, m: "smodel.SyntheticModel"):
+    """batch = 1: the one-sequence decoder (sapphire_decoder_create); batch 2..16: the
+    batched decoder (sapphire_decoder_create_batch), sequences decoded in lock step."""
+
+    def __init__(self, m: "smodel.SyntheticModel", batch: int = 1):
         self.lib = L = load()
         _protos(L)
         cfg = m.cfg
@@ -71,7 +84,11 @@ class Decoder:
             a = np.ascontiguousarray(a)
             self._keep.append(a)
             setattr(w, n, a.ctypes.data)
-        self.ptr = L.sapphire_decoder_create(C.byref(c), C.byref(w))
+        self.batch = batch
+        if batch == 1:
+            self.ptr = L.sapphire_decoder_create(C.byref(c), C.byref(w))
+        else:
+            self.ptr = L.sapphire_decoder_create_batch(C.byref(c), C.byref(w), int(batch))
         self._keep = None      # the library copied the weights
         if not self.ptr:
             raise RuntimeError("sapphire_decoder_create: " + L.sapphire_last_error().decode())
@@ -91,6 +108,34 @@ class Decoder:
         k, v = np.empty(shape, np.float32), np.empty(shape, np.float32)
         self._check(self.lib.sapphire_decoder_get_kv(self.ptr, k.ctypes.data, v.ctypes.data), "get_kv")
         return k, v
+
+    def set_kv_seq(self, seq: int, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        self._check(self.lib.sapphire_decoder_set_kv_seq(self.ptr, int(seq), k.ctypes.data, v.ctypes.data),
+                    "set_kv_seq")
+
+    def get_kv_seq(self, seq: int):
+        c = self.cfg
+        shape = (c.n_layers, c.n_kv_heads, c.max_ctx, c.head_dim)
+        k, v = np.empty(shape, np.float32), np.empty(shape, np.float32)
+        self._check(self.lib.sapphire_decoder_get_kv_seq(self.ptr, int(seq), k.ctypes.data, v.ctypes.data),
+                    "get_kv_seq")
+        return k, v
+
+    def generate_batch(self, tokens, pos, steps: int, keep_logits: bool = False):
+        """(tokens[steps, batch], logits[steps, batch, vocab] or None, device milliseconds)."""
+        tk = np.ascontiguousarray(tokens, np.int32)
+        ps = np.ascontiguousarray(pos, np.int32)
+        assert tk.shape == (self.batch,) and ps.shape == (self.batch,)
+        toks = np.empty((steps, self.batch), np.int32)
+        logits = np.empty((steps, self.batch, self.cfg.vocab), np.float32) if keep_logits else None
+        ms = C.c_float(0.0)
+        self._check(self.lib.sapphire_decoder_generate_batch(self.ptr, tk.ctypes.data, ps.ctypes.data, int(steps),
+                                                             toks.ctypes.data,
+                                                             logits.ctypes.data if logits is not None else None,
+                                                             C.byref(ms)), "generate_batch")
+        return toks, logits, float(ms.value)
 
     def generate(self, token: int, pos: int, steps: int, keep_logits: bool = False):
         """(tokens[steps], logits[steps, vocab] or None, device milliseconds)."""

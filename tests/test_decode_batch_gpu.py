@@ -1,0 +1,89 @@
+"""Batched greedy decode (sapphire_decoder_create_batch: sequences in lock step, every
+projection one matrix-core GEMM over the batch) against the oracle's decode step run on each
+sequence on its own. The reference decodes one sequence per inference_forward call
+(inference.c:612-651), so that is the expected result of every sequence.
+
+Bar (north star): per sequence and step, logits within 2e-3 relative and identical greedy
+tokens, except after a near-tie (top-2 gap inside the tolerance), as in test_decode_gpu.
+"""
+import numpy as np
+import pytest
+
+from oracle.oracle import oracle_decode
+from sapphire_amd import model as smodel
+from sapphire_amd import synth
+from tests.test_decode_gpu import MID, _compare
+
+pytestmark = pytest.mark.gpu
+
+REL = 2e-3
+
+
+def _run(oracle, cfg, seed, batch, prefills, steps, nthreads=4, check_kv=True):
+    from sapphire_amd.engine import Decoder
+    m = smodel.synthetic_model(cfg, seed)
+    rng = synth.rng(seed, 4242)
+    toks0 = rng.integers(0, cfg.vocab, size=batch).astype(np.int32)
+    kvs = [m.kv_prefill(prefills[b], seed_offset=100 + b) for b in range(batch)]
+    dec = Decoder(m, batch=batch)
+    for b in range(batch):
+        dec.set_kv_seq(b, *kvs[b])
+    got_toks, got_logits, _ = dec.generate_batch(toks0, np.asarray(prefills, np.int32), steps, keep_logits=True)
+    got_kv = [dec.get_kv_seq(b) for b in range(batch)] if check_kv else None
+    dec.close()
+    print("gpu done; oracle", flush=True)
+    for b in range(batch):
+        k, v = kvs[b]
+        ref_toks, ref_logits = oracle_decode(oracle, m, k, v, int(toks0[b]), prefills[b], steps, nthreads=nthreads,
+                                             keep_logits=True)
+        n = _compare(ref_toks, ref_logits, got_toks[:, b], got_logits[:, b])
+        assert n == steps, f"sequence {b}: near-tie at step {n}"
+        if check_kv:
+            gk, gv = got_kv[b]
+            sl = slice(prefills[b], prefills[b] + steps)
+            for name, g, r in (("K", gk, k), ("V", gv, v)):
+                d = np.abs(g[:, :, sl] - r[:, :, sl]).max() / np.abs(r[:, :, sl]).max()
+                assert d <= REL, f"sequence {b}: {name} cache rows differ: {d:.2e}"
+            assert np.array_equal(gk[:, :, :prefills[b]], k[:, :, :prefills[b]])
+
+
+TINY_Q8 = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "wdtype": synth.Q8_0, "lm_dtype": synth.Q8_0})
+
+
+@pytest.mark.parametrize("cfg,seed,batch,prefills,steps", [
+    (smodel.TINY, 51, 4, [40, 10, 23, 55], 12),              # windows slide at different steps
+    (TINY_Q8, 52, 3, [8, 30, 60], 10),                       # Q8_0 weights
+    (smodel.TINY, 53, 16, [5 + 4 * b for b in range(16)], 8),  # a full batch of 16
+    (MID, 54, 5, [40, 44, 20, 47, 1], 16),                   # head_dim 128, 48-position window
+], ids=["tiny_b4", "tiny_q8_b3", "tiny_b16", "mid_b5"])
+def test_decode_batch_matches_oracle(oracle, cfg, seed, batch, prefills, steps):
+    print(f"batched decode cfg={cfg.n_layers}x{cfg.hidden} batch={batch} steps={steps}", flush=True)
+    _run(oracle, cfg, seed, batch, prefills, steps)
+
+
+def test_decode_batch_gemma3_1b(oracle):
+    """The Gemma-3-1B-shaped Q4_0 model (26 layers, hidden 1152, FFN 6912, vocab 262144),
+    four sequences prefilled to different lengths around 1024 of 2048 positions, 4 steps."""
+    print("batched decode gemma3-1b", flush=True)
+    _run(oracle, smodel.GEMMA3_1B, 20260101, 4, [1024, 1000, 1031, 515], 4, nthreads=16, check_kv=False)
+
+
+def test_decode_batch_repeatable_and_rejects(oracle):
+    from sapphire_amd.engine import Decoder
+    m = smodel.synthetic_model(smodel.TINY, 55)
+    dec = Decoder(m, batch=2)
+    assert dec.lib.sapphire_decoder_batch(dec.ptr) == 2
+    for b in range(2):
+        dec.set_kv_seq(b, *m.kv_prefill(20, seed_offset=b))
+    t1, _, _ = dec.generate_batch([5, 9], [20, 20], 6)
+    for b in range(2):
+        dec.set_kv_seq(b, *m.kv_prefill(20, seed_offset=b))
+    t2, _, _ = dec.generate_batch([5, 9], [20, 20], 6)
+    assert np.array_equal(t1, t2)
+    with pytest.raises(RuntimeError):
+        dec.generate(5, 20, 2)                                     # one-sequence call on a batch
+    with pytest.raises(RuntimeError):
+        dec.generate_batch([5, 9], [20, m.cfg.max_ctx - 1], 4)     # positions past max_ctx
+    dec.close()
+    with pytest.raises(RuntimeError):
+        Decoder(m, batch=17)
