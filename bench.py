@@ -109,6 +109,36 @@ def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024)
     return out
 
 
+def decode_batch_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024, batch: int = 16):
+    """Batched greedy decode of the Gemma-3-1B-shaped Q4_0 model, 16 sequences in lock step
+    (projections as matrix-core GEMMs). CPU baseline: the reference engine (oracle/_ref) decodes
+    one sequence at a time (it has no quantized batch path, pool.c:318-321), so its tokens/s
+    for 16 sequences is its one-sequence rate, timed for a few steps of the same model."""
+    from sapphire_amd import model as smodel
+    from sapphire_amd.engine import bench_decode_batch
+    m = smodel.synthetic_model(smodel.GEMMA3_1B, seed)
+    k, v = m.kv_prefill(prefill)
+    out = bench_decode_batch(steps, batch=batch, seed=seed, prefill=prefill, m=m, kv=(k, v))
+    if cpu:
+        from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
+        n = 3
+        tok = out["first_tokens"][0]
+        t0 = time.perf_counter()
+        if ref_decode_available():
+            ref_decode(m, k.copy(), v.copy(), tok, prefill, n)
+            kind = "reference"
+        else:
+            oracle_decode(Oracle(), m, k.copy(), v.copy(), tok, prefill, n, nthreads=os.cpu_count() or 1)
+            kind = "port"
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {
+            "tok_per_s": round(n / dt, 2), "kind": kind, "cores": os.cpu_count(),
+            "sample": f"{n} greedy steps of one sequence of the same model through the reference's session and "
+                      f"layer functions ({dt:.2f} s incl. session set-up, thread pool of nproc threads)",
+        }
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +146,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--decode-steps", type=int, default=64, help="greedy decode steps (0 skips decode)")
+    ap.add_argument("--batch-steps", type=int, default=32,
+                    help="steps of the 16-sequence Gemma-3-1B-shaped batched decode (0 skips it)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch each LM-head kernel 10 times plus a 256 MiB device copy (the "
                          "calibration kernel of the FETCH_SIZE/WRITE_SIZE counters), for rocprofv3")
@@ -206,6 +238,9 @@ def main() -> int:
     decode = None
     if args.decode_steps > 0:
         decode = decode_leg(args.decode_steps, cpu=not args.no_cpu)
+    decode_batch = None
+    if args.batch_steps > 0:
+        decode_batch = decode_batch_leg(args.batch_steps, cpu=not args.no_cpu)
 
     out = {
         "metric": METRIC,
@@ -239,6 +274,7 @@ def main() -> int:
             "softmax_argmax_262144_standalone": {"us": round(sm_ms * 1e3, 2)},
         },
         "decode": decode,
+        "decode_batch16_gemma3_1b": decode_batch,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(x, w8, w4)

@@ -91,7 +91,8 @@ int sapphire_gemv_f_dev(int dtype, const void *w, int M, int K, const float *x, 
  * itself rejects (pool.c:318-321); its meaning is `batch` independent kernel_gemv calls.
  * X and Y are row-major [batch][K] / [batch][M]. On the TILED layout the rows run on the
  * fp16 matrix cores, 16 sequences per pass (longer batches loop), with `ws` holding
- * sapphire_gemm_workspace_bytes(dtype, M, K) bytes of device memory; on AOS/PACKED it is
+ * sapphire_gemm_workspace_bytes(dtype, M, K) bytes of device memory (K-split partial
+ * sums); calls that share a workspace must be ordered on one stream. On AOS/PACKED it is
  * the vector kernel and ws may be NULL. */
 size_t sapphire_gemm_workspace_bytes(int dtype, int M, int K);
 int sapphire_gemm_q_dev(int dtype, int layout, const void *w, int M, int K, const float *X, int batch,

@@ -545,9 +545,12 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
         return -1;
     }
     const int dpl = a.hd / kWave;
+    // splits per sequence: enough workgroups in total, without cutting a sequence's positions
+    // into slivers once a batch fills the GPU
+    const int ns = a.batch >= 4 ? kAttnSplitBatch : kAttnSplit;
 #define SPH_ATTN(DPLV, NHV)                                                                                  \
     if (dpl == DPLV && a.nh == NHV) {                                                                        \
-        hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV>), dim3(kAttnSplit, a.batch), dim3(kThreads), 0, s, a); \
+        hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV>), dim3(ns, a.batch), dim3(kThreads), 0, s, a);   \
     } else
     SPH_ATTN(1, 4) SPH_ATTN(2, 4) SPH_ATTN(4, 4) SPH_ATTN(1, 8) SPH_ATTN(2, 8) SPH_ATTN(4, 8) {
         set_error("attention with %d heads of dim %d not instantiated", a.nh, a.hd);
@@ -555,8 +558,12 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     }
 #undef SPH_ATTN
     if (!hip_ok(hipGetLastError(), "attention launch")) return -1;
-    hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplit>, dim3(a.nh, a.batch), dim3(kThreads), 0, s, a.part, a.nh,
-                       a.hd, out, a.out_stride);
+    if (ns == kAttnSplit)
+        hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplit>, dim3(a.nh, a.batch), dim3(kThreads), 0, s, a.part,
+                           a.nh, a.hd, out, a.out_stride);
+    else
+        hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplitBatch>, dim3(a.nh, a.batch), dim3(kThreads), 0, s,
+                           a.part, a.nh, a.hd, out, a.out_stride);
     return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
 }
 

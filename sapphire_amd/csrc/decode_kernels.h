@@ -29,6 +29,7 @@ constexpr int kDecMaxK = 2048;       // longest GEMV input of the fused kernels
 constexpr int kAttnMaxQ = 2048;      // n_heads * head_dim
 constexpr int kAttnMaxKV = 512;      // n_kv_heads * head_dim (at most two K/V heads)
 constexpr int kAttnSplit = 64;       // workgroups over the positions of one attention
+constexpr int kAttnSplitBatch = 16;  // the same per sequence of a batch (batch >= 4)
 
 // y = W . x(in)  (rows M of w, K = w.K)
 int dec_gemv(int dt, const QMat &w, const GemvIn &in, float *y, hipStream_t s);

@@ -12,8 +12,10 @@
 // with its own KV cache and position. Its projections are TILED matrices multiplied on the
 // matrix cores as one GEMM over the batch (QKV stacked, gate and up interleaved by eight
 // rows so that the GeGLU is the GEMM's epilogue), and the residual adds and RMSNorms are
-// formed while each GEMM stages its input; a step is 4 GEMMs and 2 attention launches per
-// layer, the LM-head GEMM, a batched argmax and the advance.
+// formed while each GEMM stages its input; a step is 4 GEMMs, 2 attention launches and the
+// sum of the down projection's K-chunk partials per layer, the LM-head GEMM, a batched
+// argmax and the advance.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -61,6 +63,7 @@ struct sapphire_decoder {
     // batched decoder
     int batch = 1;
     float *dparts = nullptr;     // the down projection's K-chunk partial sums [splits][B][hidden]
+    float *dout = nullptr;       // their sum [B][hidden]
     float *amax_part = nullptr;  // argmax partials
     void *gws = nullptr;         // GEMM workspace
 };
@@ -280,8 +283,8 @@ int enqueue_step_batch(sapphire_decoder *d) {
     const float es = sqrtf((float)H);
     const float scale = 1.0f / sqrtf(c.query_pre_attn_scalar > 0.f ? c.query_pre_attn_scalar : (float)hd);
     const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
-    const int nsd = gemm_splits(c.ffn);
     const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
+    const int nsd = gemm_splits(c.ffn);
     if (dec_embed_batch(d->embed, H, es, d->state, B, d->resid[0], s) != 0) return -1;
     int cur = 0;
     for (int l = 0; l < c.n_layers; ++l) {
@@ -293,10 +296,12 @@ int enqueue_step_batch(sapphire_decoder *d) {
         qi.w_norm = L.n_attn;
         qi.eps = c.eps;
         if (l > 0) {
-            qi.parts = d->dparts;
-            qi.nparts = nsd;
+            // the previous down projection's K-chunk partial sums, added once by a short kernel
+            // (cheaper than every staging workgroup adding them)
+            if (launch_sum_parts(d->dparts, nsd, (size_t)B * H, B, H, d->dout, H, s) != 0) return -1;
+            qi.parts = d->dout;
+            qi.nparts = 1;
             qi.ldp = H;
-            qi.part_stride = (size_t)B * H;
             qi.w_delta = d->layers[l - 1].n_ffn_post;
             qi.resid_out = d->resid[1 - cur];
             qi.ldr = H;
@@ -362,13 +367,13 @@ int enqueue_step_batch(sapphire_decoder *d) {
         if (launch_gemm_tiled_ex(c.wdtype, L.t_down, H, c.ffn, B, di, dout, d->gws, s) != 0) return -1;
     }
     // last finalize + final norm (transformer.c:400-406), LM head, greedy tokens
+    if (launch_sum_parts(d->dparts, nsd, (size_t)B * H, B, H, d->dout, H, s) != 0) return -1;
     GemmIn li;
     li.x = d->resid[cur];
     li.ldx = H;
-    li.parts = d->dparts;
-    li.nparts = nsd;
+    li.parts = d->dout;
+    li.nparts = 1;
     li.ldp = H;
-    li.part_stride = (size_t)B * H;
     li.w_delta = d->layers[c.n_layers - 1].n_ffn_post;
     li.w_norm = d->norm_final;
     li.eps = c.eps;
@@ -564,11 +569,16 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
         !dev_alloc_t(d, &d->state, 2 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log"))
         return fail();
     if (B > 1) {
+        const size_t wsb = std::max({gemm_workspace_bytes(H, c.ffn), gemm_workspace_bytes(H, nq),
+                                     gemm_workspace_bytes(c.vocab, H)});
         if (!dev_alloc_t(d, &d->dparts, (size_t)gemm_splits(c.ffn) * b * H, "down partials") ||
+            !dev_alloc_t(d, &d->dout, b * H, "down output") ||
             !dev_alloc_t(d, &d->amax_part, argmax_batch_part_floats(c.vocab, B), "argmax partials") ||
-            !dev_alloc(d, &d->gws, gemm_workspace_bytes(std::max(H, c.vocab), std::max(nq, c.ffn)), "gemm workspace"))
+            !dev_alloc(d, &d->gws, wsb, "gemm workspace"))
             return fail();
     }
+    // the zero fills above run on the null stream; the decoder's stream does not wait for it
+    if (!hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize")) return fail();
     return d;
 }
 

@@ -17,7 +17,10 @@
 // vectors into the A operands in LDS once, then each wave streams whole tiles through it.
 // A wave's (tile, 4-block group) units run through a ring of register buffers: the loads of
 // the next kRing-1 units are in flight while one unit is multiplied. K longer than one
-// chunk is split over workgroups (grid.y) and gemm_reduce_kernel adds the partial sums.
+// chunk is split over workgroups (grid.y): each leaves its partial sums, which a short
+// kernel adds in chunk order (or the next GEMM adds while staging its input). Adding them
+// in the GEMM itself (last workgroup to finish) needs device-scope fences, i.e. L2
+// write-backs across the XCDs, which cost more than the extra launch.
 #include <algorithm>
 
 #include "devmath.h"
@@ -36,6 +39,7 @@ constexpr int kChunkBlocks = 36;                       // A operands staged per 
 constexpr int kBatchMax = 16;
 constexpr int kRing = 6;                               // units in flight per wave
 constexpr int kNT = 2;                                 // streaming (non-temporal) weight loads
+constexpr int kMaxGrid = 1024;                         // workgroups over the tiles
 // (block, quarter) pairs of a chunk handled by one staging thread
 constexpr int kStagePairs = (kChunkBlocks * 4 + kThreads / kBatchMax - 1) / (kThreads / kBatchMax);
 
@@ -155,8 +159,19 @@ __device__ void rows_rms_inv(const float *raw, int ld, int dim, int batch, float
     if (t < kBatchMax * 8) {
         const int seq = t >> 3, l = t & 7;
         float s = 0.f;
-        if (seq < batch)
-            for (int i = l; i < (dim & ~7); i += 8) s = __builtin_fmaf(raw[seq * ld + i], raw[seq * ld + i], s);
+        if (seq < batch) {
+            const float *r = raw + seq * ld + l;
+            const int n8 = dim >> 3;
+            int j = 0;
+            for (; j + 8 <= n8; j += 8) {   // eight loads in flight, then the chain
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) x[u] = r[(j + u) * 8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s = __builtin_fmaf(x[u], x[u], s);
+            }
+            for (; j < n8; ++j) s = __builtin_fmaf(r[j * 8], r[j * 8], s);
+        }
         part[seq][l] = s;
     }
     __syncthreads();
@@ -177,8 +192,9 @@ __device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
 }
 
 // LDS of the staging: the A operands [block][hi/lo][lane 16m + seq] of a chunk, and, before
-// them (same memory), the rows as fp32 [seq][K + 4] for the reference-order norm sums.
-constexpr int kRawLd = kChunkBlocks * kBlock + 4;
+// them (same memory), the rows as fp32 [seq][K + 8] for the reference-order norm sums (the
+// pad puts the rows of four sequences in different banks).
+constexpr int kRawLd = kChunkBlocks * kBlock + 8;
 constexpr int kStageH8 = (kBatchMax * kRawLd * 4 + 15) / 16 > kChunkBlocks * 2 * kWave
                              ? (kBatchMax * kRawLd * 4 + 15) / 16
                              : kChunkBlocks * 2 * kWave;
@@ -198,7 +214,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int nb = K / kBlock, G = nb / kGroupBlocks;
     const int b0 = blockIdx.y * cb, b1 = min(nb, b0 + cb);
 
-    // ---- the first kRing-1 units' weight loads go out before the staging ----
+    // ---- the wave's units: (tile, 4-block group) pairs of this K chunk ----
     // Unit counters are wave-uniform (scalar registers, scalar branches).
     const int n = lane & 15, m = lane >> 4;
     const int ntiles = (M + kTileRows - 1) / kTileRows;
@@ -214,47 +230,38 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // and outside them the fp16 exponent of 1024, inside them the bits that undo nib ^ 8
     BConst bk = {0x000F000Fu, 0x00F000F0u, 0x64086408u, 0x64806480u};
     asm volatile("" : "+v"(bk.lo_mask), "+v"(bk.hi_mask), "+v"(bk.lo_bits), "+v"(bk.hi_bits));
-    Unit ring[kRing];
-    // issue pointer: group offset (tile * G + g) of unit u + kRing - 1; loads past the last
-    // unit repeat it. The offset goes in the scalar offset field, which the buffer range
-    // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
-    int igb = (idle ? 0 : t0) * G + g0, ig = 0, issued = 0;
-#pragma unroll
-    for (int p = 0; p < kRing - 1; ++p) {
-        unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
-        if (issued < U - 1) {
-            ++issued;
-            if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
-        }
-    }
     // ---- stage the chunk: input transform, range scale per sequence, hi/lo operands ----
     {
         const int seq = tid & (kBatchMax - 1), q = tid / kBatchMax;   // q: 0..31
         const int pairs = (b1 - b0) * 4;
         const int kb = b0 * kBlock;
         float *raw = reinterpret_cast<float *>(xs);
-        float v[kStagePairs][8];
-        // h (or the delta) of this thread's 8-element pieces
+        float v[kStagePairs][8];    // the delta (parts given), else h
+        float xv[kStagePairs][8];   // x when it is added to the delta
+        // every load of the staging's first stage goes out before any is used
 #pragma unroll
         for (int i = 0; i < kStagePairs; ++i) {
             const int p = q + i * (kThreads / kBatchMax);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+            for (int e = 0; e < 8; ++e) v[i][e] = xv[i][e] = 0.f;
             if (p < pairs && seq < batch) {
                 const int k = kb + p * 8;
-                if (in.parts) {
-                    for (int c = 0; c < in.nparts; ++c) {
-                        float t[8];
-                        load8(in.parts + c * in.part_stride + (size_t)seq * in.ldp + k, t);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(v[i][e], t[e]);
-                    }
-                } else {
-                    load8(in.x + (size_t)seq * in.ldx + k, v[i]);
-                }
+                if (in.x) load8(in.x + (size_t)seq * in.ldx + k, in.parts ? xv[i] : v[i]);
+                if (in.parts) load8(in.parts + (size_t)seq * in.ldp + k, v[i]);
             }
         }
         if (in.parts) {
+            for (int c = 1; c < in.nparts; ++c)
+#pragma unroll
+                for (int i = 0; i < kStagePairs; ++i) {
+                    const int p = q + i * (kThreads / kBatchMax);
+                    if (p < pairs && seq < batch) {
+                        float t[8];
+                        load8(in.parts + c * in.part_stride + (size_t)seq * in.ldp + kb + p * 8, t);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(v[i][e], t[e]);
+                    }
+                }
             if (in.w_delta) {
 #pragma unroll
                 for (int i = 0; i < kStagePairs; ++i) {
@@ -279,15 +286,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             }
             if (in.x)
 #pragma unroll
-                for (int i = 0; i < kStagePairs; ++i) {
-                    const int p = q + i * (kThreads / kBatchMax);
-                    if (p < pairs && seq < batch) {
-                        float t[8];
-                        load8(in.x + (size_t)seq * in.ldx + kb + p * 8, t);
+                for (int i = 0; i < kStagePairs; ++i)
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(t[e], v[i][e]);
-                    }
-                }
+                    for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(xv[i][e], v[i][e]);
         }
         if (in.resid_out && blockIdx.x == 0 && blockIdx.y == 0)
 #pragma unroll
@@ -362,8 +363,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         __syncthreads();
     }
 
+    // ---- the first kRing-1 units' weight loads ----
+    Unit ring[kRing];
+    // issue pointer: group offset (tile * G + g) of unit u + kRing - 1; loads past the last
+    // unit repeat it. The offset goes in the scalar offset field, which the buffer range
+    // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
+    int igb = (idle ? 0 : t0) * G + g0, ig = 0, issued = 0;
+#pragma unroll
+    for (int p = 0; p < kRing - 1; ++p) {
+        unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
+        if (issued < U - 1) {
+            ++issued;
+            if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
+        }
+    }
     // ---- stream the tiles: units (tile, group) through the register ring ----
-    if (idle) return;
     float sc[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) sc[r] = xsc[4 * m + r];
@@ -381,7 +395,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     f4 acc = {0.f, 0.f, 0.f, 0.f};
     // Every pass issues the loads of all kRing slots (past the last unit they repeat it), so
     // each path through the loop has the same load order and the waits stay kRing-1 units
-    // deep; only the multiplication of units past the end is skipped.
+    // deep; only the multiplication of units past the end is skipped. (An idle wave has
+    // U = 0.)
     for (int base = 0; base < U; base += kRing) {
 #pragma unroll
         for (int p = 0; p < kRing; ++p) {
@@ -419,13 +434,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
 }
 
-__global__ void gemm_reduce_kernel(const float *__restrict__ Yp, int nsplit, int batch, int M, float *__restrict__ Y,
-                                   int ldy) {
+// y[b * ldy + r] = sum over c of parts[c * stride + b * M + r], in chunk order.
+__global__ void sum_parts_kernel(const float *__restrict__ parts, int nparts, size_t stride, int batch, int M,
+                                 float *__restrict__ y, int ldy) {
     const size_t n = (size_t)batch * M;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        float s = 0.f;
-        for (int c = 0; c < nsplit; ++c) s += Yp[(size_t)c * n + i];
-        Y[(i / M) * ldy + i % M] = s;
+        float s = parts[i];
+        for (int c = 1; c < nparts; ++c) s += parts[c * stride + i];
+        y[(i / M) * ldy + i % M] = s;
     }
 }
 
@@ -460,7 +476,7 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
     const int ntiles = (M + kTileRows - 1) / kTileRows;
     const int sets = (ntiles + kWaves - 1) / kWaves;
     // two 72 KiB workgroups per CU
-    const int gx = std::max(1, std::min(sets, (2 * cus() + nsplit - 1) / nsplit));
+    const int gx = std::max(1, std::min({sets, (2 * cus() + nsplit - 1) / nsplit, kMaxGrid}));
     const dim3 grid((unsigned)gx, (unsigned)nsplit);
     float *Yp = static_cast<float *>(ws);
     if (dt == DT_Q4_0)
@@ -470,12 +486,7 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
         hipLaunchKernelGGL(gemm_mfma_kernel<DT_Q8_0>, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so,
                            (uint32_t)sbytes, in, batch, M, K, cb, out, Yp);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
-    if (nsplit > 1 && !out.parts) {
-        const size_t n = (size_t)batch * M;
-        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)std::min<size_t>(2048, (n + 255) / 256)), dim3(256), 0, st,
-                           Yp, nsplit, batch, M, out.y, out.ldy);
-        if (!hip_ok(hipGetLastError(), "gemm_reduce launch")) return -1;
-    }
+    if (nsplit > 1 && !out.parts) return launch_sum_parts(Yp, nsplit, (size_t)batch * M, batch, M, out.y, out.ldy, st);
     return 0;
 }
 
@@ -490,6 +501,14 @@ int gemm_splits(int K) {
 size_t gemm_workspace_bytes(int M, int K) {
     const int nsplit = gemm_splits(K);
     return 256 + (nsplit > 1 ? (size_t)nsplit * kBatchMax * M * sizeof(float) : 0);
+}
+
+int launch_sum_parts(const float *parts, int nparts, size_t stride, int batch, int M, float *y, int ldy,
+                     hipStream_t st) {
+    const size_t n = (size_t)batch * M;
+    hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)std::min<size_t>(1024, (n + 255) / 256)), dim3(256), 0, st,
+                       parts, nparts, stride, batch, M, y, ldy);
+    return hip_ok(hipGetLastError(), "sum_parts launch") ? 0 : -1;
 }
 
 int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,

@@ -56,12 +56,15 @@ int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *
                               int *argmax, void *scratch, hipStream_t s);
 // Batched GEMM on the TILED layout (gemm_mfma.hip): Y[b][r] = W[r] . X[b] for b < batch, 16
 // sequences per pass. ws: gemm_workspace_bytes(M, K) bytes of 256-byte aligned device memory
-// (the K-split partial sums).
+// (the K-split partial sums). Calls sharing a workspace must be ordered.
 size_t gemm_workspace_bytes(int M, int K);
 int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws,
                       hipStream_t s);
 // Number of K chunks (partial sums) of a batched GEMM with inner dimension K.
 int gemm_splits(int K);
+// y[b * ldy + r] = sum over c < nparts of parts[c * stride + b * M + r] (chunk order).
+int launch_sum_parts(const float *parts, int nparts, size_t stride, int batch, int M, float *y, int ldy,
+                     hipStream_t s);
 // Input of a batched GEMM, formed per sequence row while the activations are staged (the
 // residual pattern of attention.c:356-366 / transformer.c:231-239 and the pre-norms of
 // attention.c:316-325 / transformer.c:119-121):

@@ -76,7 +76,13 @@ int sapphire_memcpy_d2d(void *dst, const void *src, size_t n, void *stream) {
     return 0;
 }
 
-int sapphire_memset(void *p, int v, size_t n) { SPH_CHECK(hipMemset(p, v, n)); return 0; }
+// Blocking: the fill is complete on return, so work on any stream (non-blocking ones
+// included) sees it.
+int sapphire_memset(void *p, int v, size_t n) {
+    SPH_CHECK(hipMemset(p, v, n));
+    SPH_CHECK(hipDeviceSynchronize());
+    return 0;
+}
 int sapphire_synchronize(void) { SPH_CHECK(hipDeviceSynchronize()); return 0; }
 
 void *sapphire_stream_create(void) {
@@ -246,7 +252,12 @@ void *partial_scratch() {
     if (!scratch[dev]) {
         void *p = nullptr;
         if (!hip_ok(hipMalloc(&p, kPartialBytes), "hipMalloc(partials)")) return nullptr;
-        if (!hip_ok(hipMemset(p, 0, kPartialBytes), "hipMemset(partials)")) { (void)hipFree(p); return nullptr; }
+        // complete before any (possibly non-blocking) stream uses the buffer
+        if (!hip_ok(hipMemset(p, 0, kPartialBytes), "hipMemset(partials)") ||
+            !hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize")) {
+            (void)hipFree(p);
+            return nullptr;
+        }
         scratch[dev] = p;
     }
     return scratch[dev];

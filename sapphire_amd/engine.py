@@ -184,3 +184,48 @@ def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, rep
         "tok_per_s": round(steps / (best * 1e-3), 1), "first_tokens": [int(t) for t in toks[:8]],
         "weight_bytes_per_token": layer_bytes + int(m.lm_head.nbytes),
     }
+
+
+def bench_decode_batch(steps: int = 32, batch: int = 16, seed: int = 20260101, prefill: int = 1024, reps: int = 2,
+                       cfg=None, m=None, kv=None):
+    """Batched greedy decode of the Gemma-3-1B-shaped Q4_0 model: `batch` sequences, each with
+    its own KV cache prefilled to `prefill` of 2048 positions (the same N(0,1) contents in every
+    sequence's cache) and its own seeded start token. tokens/s = batch * steps / time, best of
+    `reps` runs after a warm-up (the graph capture)."""
+    cfg = cfg or smodel.GEMMA3_1B
+    if m is None:
+        m = smodel.synthetic_model(cfg, seed)
+    k, v = kv if kv is not None else m.kv_prefill(prefill)
+    dec = Decoder(m, batch=batch)
+    for b in range(batch):
+        dec.set_kv_seq(b, k, v)
+    rng = np.random.default_rng(seed)
+    toks0 = rng.integers(0, cfg.vocab, size=batch).astype(np.int32)
+    pos = np.full(batch, prefill, np.int32)
+    dec.generate_batch(toks0, pos, steps)            # graph capture + warm-up
+    best = None
+    for _ in range(reps):
+        toks, _, ms = dec.generate_batch(toks0, pos, steps)
+        best = ms if best is None else min(best, ms)
+    dec.close()
+    from . import synth
+    nq, nk = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+
+    def qb(m_, k_, dt):
+        return m_ * (k_ // 32) * synth.BLOCK_BYTES[dt]
+    layer_w = (qb(nq + 2 * nk, cfg.hidden, cfg.wdtype) + qb(cfg.hidden, nq, cfg.wdtype) +
+               qb(2 * cfg.ffn, cfg.hidden, cfg.wdtype) + qb(cfg.hidden, cfg.ffn, cfg.wdtype))
+    w_step = layer_w * cfg.n_layers + qb(cfg.vocab, cfg.hidden, cfg.lm_dtype)
+    # K and V rows read by one step of one sequence at the first decode position
+    win = cfg.sliding_window
+    rows = sum((prefill + 1) if l in cfg.global_layers else min(prefill + 1, win) for l in range(cfg.n_layers))
+    kv_step = batch * rows * cfg.n_kv_heads * cfg.head_dim * 4 * 2
+    ms_step = best / steps
+    return {
+        "model": "Gemma-3-1B-shaped, Q4_0 weights (random init), 26 layers, hidden 1152, FFN 6912, vocab 262144",
+        "batch": batch, "steps": steps, "kv_prefill": prefill, "ms_total": round(best, 3),
+        "ms_per_step": round(ms_step, 4), "tok_per_s": round(batch * steps / (best * 1e-3), 1),
+        "weight_bytes_per_step": w_step, "kv_bytes_per_step": kv_step,
+        "GB_per_s": round((w_step + kv_step) / (ms_step * 1e-3) / 1e9, 1),
+        "first_tokens": [int(t) for t in toks[0]],
+    }
