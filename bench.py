@@ -109,6 +109,35 @@ def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024)
     return out
 
 
+def lm_head_gemm(blocks, batch: int, seed: int, iters: int = 20):
+    """The batched decode's dominant kernel alone: Q4_0 262144 x 1152 times 16 vectors on the
+    matrix cores (two weight copies rotated, 2 x 189 MB > the 256 MB last-level cache)."""
+    from sapphire_amd import load, synth
+    from sapphire_amd.device import DeviceArray, QMatrix, Timer, check
+    L = load()
+    m, k = blocks.shape[0], blocks.shape[1] * 32
+    qs = [QMatrix(synth.Q4_0, blocks, layout=2) for _ in range(2)]
+    X = DeviceArray.from_numpy(synth.normal_f32((batch, k), seed, 77))
+    Y = DeviceArray.empty(batch * m)
+    ws = DeviceArray(L.sapphire_gemm_workspace_bytes(synth.Q4_0, m, k))
+    run = lambda i: check(L.sapphire_gemm_q_dev(synth.Q4_0, 2, qs[i % 2].ptr(), m, k, X.ptr, batch, Y.ptr,  # noqa: E731
+                                                ws.ptr, None))
+    for i in range(4):
+        run(i)
+    check(L.sapphire_synchronize())
+    t = Timer(None)
+    t.start()
+    for i in range(iters):
+        run(i)
+    us = t.stop() / iters * 1e3
+    algo = m * (k // 32) * synth.BLOCK_BYTES[synth.Q4_0] + 4 * batch * (k + m)
+    return {
+        "shape": f"{m}x{k} Q4_0, {batch} sequences", "us": round(us, 2),
+        "GB/s": round(algo / (us * 1e-6) / 1e9, 1), "frac_hbm_peak": round(algo / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "TFLOP/s": round(2.0 * batch * m * k / (us * 1e-6) / 1e12, 1), "algorithmic_bytes": algo,
+    }
+
+
 def decode_batch_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024, batch: int = 16):
     """Batched greedy decode of the Gemma-3-1B-shaped Q4_0 model, 16 sequences in lock step
     (projections as matrix-core GEMMs). CPU baseline: the reference engine (oracle/_ref) decodes
@@ -119,6 +148,7 @@ def decode_batch_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int =
     m = smodel.synthetic_model(smodel.GEMMA3_1B, seed)
     k, v = m.kv_prefill(prefill)
     out = bench_decode_batch(steps, batch=batch, seed=seed, prefill=prefill, m=m, kv=(k, v))
+    out["lm_head_gemm"] = lm_head_gemm(m.lm_head, batch, seed)
     if cpu:
         from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
         n = 3
