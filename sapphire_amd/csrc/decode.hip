@@ -399,9 +399,15 @@ __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float 
     }
 }
 
-__global__ void dec_embed_kernel(const uint16_t *__restrict__ embed, int hidden, float es, const int *__restrict__ tok,
-                                 float *__restrict__ resid) {
-    const size_t row = (size_t)(*tok) * hidden;
+// The token is device data (the previous step's argmax): it is clamped into the vocabulary
+// so that no value can address outside the table.
+__device__ __forceinline__ size_t embed_row(int tok, int vocab, int hidden) {
+    return (size_t)(tok >= 0 && tok < vocab ? tok : 0) * hidden;
+}
+
+__global__ void dec_embed_kernel(const uint16_t *__restrict__ embed, int hidden, int vocab, float es,
+                                 const int *__restrict__ tok, float *__restrict__ resid) {
+    const size_t row = embed_row(*tok, vocab, hidden);
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x) {
         const float v = __uint_as_float((uint32_t)embed[row + i] << 16);
         resid[i] = es != 1.0f ? __fmul_rn(v, es) : v;
@@ -420,9 +426,9 @@ __global__ void dec_advance_kernel(const int *__restrict__ tok, int *__restrict_
 
 // ---- batched decode: embedding, greedy token and position of a batch of sequences ----
 
-__global__ void dec_embed_batch_kernel(const uint16_t *__restrict__ embed, int hidden, float es,
+__global__ void dec_embed_batch_kernel(const uint16_t *__restrict__ embed, int hidden, int vocab, float es,
                                        const int *__restrict__ tok, float *__restrict__ resid) {
-    const size_t row = (size_t)tok[blockIdx.y] * hidden;
+    const size_t row = embed_row(tok[blockIdx.y], vocab, hidden);
     float *out = resid + (size_t)blockIdx.y * hidden;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x) {
         const float v = __uint_as_float((uint32_t)embed[row + i] << 16);
@@ -472,8 +478,10 @@ __global__ __launch_bounds__(kThreads) void dec_argmax_part_kernel(const float *
     }
 }
 
-// grid (batch), one wave: tokens[b] = best of the sequence's partials
-__global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int nparts, int *__restrict__ tokens) {
+// grid (batch), one wave: tokens[b] = best of the sequence's partials; 0 when no logit is
+// above -inf (all NaN), as sample_greedy (utils.c:145-156) starts at index 0
+__global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int nparts, int n,
+                                         int *__restrict__ tokens) {
     const float *p = part + (size_t)blockIdx.x * nparts * 2;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
@@ -483,7 +491,7 @@ __global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int npa
         if (better(v, i, bv, bi)) { bv = v; bi = i; }
     }
     wave_best(bv, bi);
-    if (threadIdx.x == 0) tokens[blockIdx.x] = bi;
+    if (threadIdx.x == 0) tokens[blockIdx.x] = bi >= 0 && bi < n ? bi : 0;
 }
 
 __global__ void dec_advance_batch_kernel(const int *__restrict__ tok, int *__restrict__ pos, int *__restrict__ step,
@@ -567,9 +575,10 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
 }
 
-int dec_embed(const uint16_t *embed, int hidden, float es, const int *d_token, float *resid, hipStream_t s) {
+int dec_embed(const uint16_t *embed, int hidden, int vocab, float es, const int *d_token, float *resid,
+              hipStream_t s) {
     hipLaunchKernelGGL(dec_embed_kernel, dim3((hidden + kThreads - 1) / kThreads), dim3(kThreads), 0, s, embed, hidden,
-                       es, d_token, resid);
+                       vocab, es, d_token, resid);
     return hip_ok(hipGetLastError(), "embed launch") ? 0 : -1;
 }
 
@@ -578,10 +587,10 @@ int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, hipStream
     return hip_ok(hipGetLastError(), "advance launch") ? 0 : -1;
 }
 
-int dec_embed_batch(const uint16_t *embed, int hidden, float es, const int *d_tokens, int batch, float *resid,
-                    hipStream_t s) {
+int dec_embed_batch(const uint16_t *embed, int hidden, int vocab, float es, const int *d_tokens, int batch,
+                    float *resid, hipStream_t s) {
     hipLaunchKernelGGL(dec_embed_batch_kernel, dim3((hidden + kThreads - 1) / kThreads, batch), dim3(kThreads), 0, s,
-                       embed, hidden, es, d_tokens, resid);
+                       embed, hidden, vocab, es, d_tokens, resid);
     return hip_ok(hipGetLastError(), "batched embed launch") ? 0 : -1;
 }
 
@@ -593,7 +602,7 @@ size_t argmax_batch_part_floats(int n, int batch) {
 int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_tokens, hipStream_t s) {
     hipLaunchKernelGGL(dec_argmax_part_kernel, dim3(kArgmaxParts, batch), dim3(kThreads), 0, s, logits, n, part);
     if (!hip_ok(hipGetLastError(), "argmax launch")) return -1;
-    hipLaunchKernelGGL(dec_argmax_finish_kernel, dim3(batch), dim3(kWave), 0, s, part, kArgmaxParts, d_tokens);
+    hipLaunchKernelGGL(dec_argmax_finish_kernel, dim3(batch), dim3(kWave), 0, s, part, kArgmaxParts, n, d_tokens);
     return hip_ok(hipGetLastError(), "argmax finish launch") ? 0 : -1;
 }
 

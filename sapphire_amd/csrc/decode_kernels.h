@@ -59,15 +59,17 @@ struct AttnArgs {
 size_t attn_part_floats(int nh, int hd);
 int dec_attention(const AttnArgs &a, float *out, hipStream_t s);
 
-// resid[i] = bf16 row of *d_token * es (transformer.c:347-365)
-int dec_embed(const uint16_t *embed, int hidden, float es, const int *d_token, float *resid, hipStream_t s);
+// resid[i] = bf16 row of *d_token * es (transformer.c:347-365); a token outside [0, vocab)
+// reads row 0
+int dec_embed(const uint16_t *embed, int hidden, int vocab, float es, const int *d_token, float *resid,
+              hipStream_t s);
 // log[*d_step] = *d_token; ++*d_step; ++*d_pos
 int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, hipStream_t s);
 
 // ---- batched decode (a batch of sequences in lock step) ----
 // resid[b][i] = bf16 row of tokens[b] * es
-int dec_embed_batch(const uint16_t *embed, int hidden, float es, const int *d_tokens, int batch, float *resid,
-                    hipStream_t s);
+int dec_embed_batch(const uint16_t *embed, int hidden, int vocab, float es, const int *d_tokens, int batch,
+                    float *resid, hipStream_t s);
 // tokens[b] = first index of the maximum of logits[b][0..n) (utils.c:145-156); part holds
 // argmax_batch_part_floats(n, batch) floats
 size_t argmax_batch_part_floats(int n, int batch);

@@ -202,7 +202,7 @@ int enqueue_step(sapphire_decoder *d) {
     const float es = sqrtf((float)H);
     const float scale = 1.0f / sqrtf(c.query_pre_attn_scalar > 0.f ? c.query_pre_attn_scalar : (float)hd);
     const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
-    if (dec_embed(d->embed, H, es, d->state, d->resid[0], s) != 0) return -1;
+    if (dec_embed(d->embed, H, c.vocab, es, d->state, d->resid[0], s) != 0) return -1;
     int cur = 0;
     const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
     for (int l = 0; l < c.n_layers; ++l) {
@@ -285,7 +285,7 @@ int enqueue_step_batch(sapphire_decoder *d) {
     const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
     const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
     const int nsd = gemm_splits(c.ffn);
-    if (dec_embed_batch(d->embed, H, es, d->state, B, d->resid[0], s) != 0) return -1;
+    if (dec_embed_batch(d->embed, H, c.vocab, es, d->state, B, d->resid[0], s) != 0) return -1;
     int cur = 0;
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer &L = d->layers[l];

@@ -309,7 +309,8 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
         SoftPart t = wp[0];
         for (int w = 1; w < (int)(blockDim.x / kWave); ++w) t = soft_merge(t, wp[w]);
         tot = t;
-        if (blockIdx.x == 0 && argmax) *argmax = t.i;
+        // no logit above -inf (all NaN): index 0, as sample_greedy (utils.c:145-156) starts there
+        if (blockIdx.x == 0 && argmax) *argmax = t.i >= 0 && t.i < n ? t.i : 0;
     }
     __syncthreads();
     if (!probs) return;

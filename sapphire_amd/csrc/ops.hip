@@ -144,7 +144,8 @@ __global__ __launch_bounds__(kSmBlock) void softmax_finish(const float *__restri
         if (threadIdx.x == 0) {
             s_gmax = m.v;
             s_inv = 1.0f / s;
-            if (blockIdx.x == 0 && argmax_out) *argmax_out = m.i;
+            // no logit above -inf (all NaN): index 0, as sample_greedy (utils.c:145-156)
+            if (blockIdx.x == 0 && argmax_out) *argmax_out = m.i >= 0 && m.i < n ? m.i : 0;
         }
     }
     __syncthreads();

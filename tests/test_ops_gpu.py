@@ -107,3 +107,26 @@ def test_softmax_all_equal(hip, oracle):
     assert int(arg.numpy()[0]) == 0
     ok, err = close(probs.numpy(), oracle.softmax(x), rel=1e-3, abs_=1e-9)
     assert ok, err
+
+
+@pytest.mark.parametrize("fill", [np.nan, -np.inf], ids=["nan", "neg_inf"])
+def test_argmax_without_a_finite_logit(hip, oracle, fill):
+    """No logit above -inf: the greedy token is 0, as sample_greedy (utils.c:145-156) starts
+    there, never an index outside [0, n) (a decode step embeds that token next). Covers the
+    standalone softmax/argmax and the LM-head GEMV's fused epilogue."""
+    from sapphire_amd.device import DeviceArray, QMatrix, check
+    n = 20000
+    x = np.full(n, fill, np.float32)
+    arg = DeviceArray.empty(1, np.int32)
+    arg.upload(np.array([-7], np.int32))
+    check(hip.sapphire_softmax_argmax_dev(dev(x).ptr, n, None, arg.ptr, None))
+    assert int(arg.numpy()[0]) == 0
+    assert oracle.argmax(x) == 0
+    # the fused epilogue: a NaN activation makes every logit NaN
+    W = synth.quant_matrix(synth.Q8_0, n, 640, seed=9, tensor_id=1)
+    qm = QMatrix(synth.Q8_0, W, layout=2)
+    xv = np.full(640, fill, np.float32)
+    logits = DeviceArray.empty(n)
+    arg.upload(np.array([-7], np.int32))
+    check(hip.sapphire_gemv_softmax_dev(synth.Q8_0, 2, qm.ptr(), n, 640, dev(xv).ptr, logits.ptr, None, arg.ptr, None))
+    assert 0 <= int(arg.numpy()[0]) < n
