@@ -72,6 +72,17 @@ int sapphire_decoder_get_kv(sapphire_decoder_t *dec, float *k, float *v);
 int sapphire_decoder_generate(sapphire_decoder_t *dec, int token, int pos, int steps, int *tokens_out,
                               float *logits_out, float *elapsed_ms);
 
+/* The form of a one-sequence step. groups > 0: the layers run as one persistent cooperative
+ * kernel of `groups` workgroups (all co-resident) whose stages exchange epoch-tagged vectors
+ * instead of waiting for kernel boundaries; this is the default (128 workgroups, or the value
+ * of the SAPPHIRE_DECODE_WORKGROUPS environment variable at create time) where the shapes and
+ * the device allow it. groups == 0: six fused launches per layer in a HIP graph. Both forms
+ * compute the same step. Returns -1 (and keeps the current form) when `groups` cannot run
+ * these shapes on this device, and for a batched decoder. */
+int sapphire_decoder_set_workgroups(sapphire_decoder_t *dec, int groups);
+/* The current form: workgroups of the persistent step, 0 for the multi-launch step. */
+int sapphire_decoder_workgroups(const sapphire_decoder_t *dec);
+
 /* ---- batched decode ----
  * `batch` (2..16) independent sequences decoded in lock step, each with its own KV cache,
  * position and greedy token: one step runs every projection as one matrix-core GEMM over

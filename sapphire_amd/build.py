@@ -4,6 +4,7 @@
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -14,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libsapphire_hip.so")
 SOURCES = ["runtime.cpp", "tensor.cpp", "dispatch.cpp", "decoder.cpp", "gemv.hip", "gemv_mfma.hip", "gemm_mfma.hip",
-           "ops.hip", "decode.hip"]
+           "ops.hip", "decode.hip",
+           "decode_persist.hip"]
 ARCH = os.environ.get("SAPPHIRE_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [
@@ -34,10 +36,12 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compiles every source (in parallel, `jobs` at a time; 0 = one per CPU up to 8) and links."""
     cc = hipcc()
+    jobs = jobs or max(1, min(8, os.cpu_count() or 1))
     with tempfile.TemporaryDirectory(prefix="sapphire_build_") as tmp:
-        objs = []
+        cmds, objs = [], []
         for src in SOURCES:
             path = os.path.join(CSRC, src)
             if not os.path.exists(path):
@@ -49,8 +53,11 @@ def build(verbose: bool = False) -> str:
                 cmd.insert(2, "hip")
             if verbose:
                 print(" ".join(cmd), flush=True)
-            subprocess.run(cmd, check=True)
+            cmds.append(cmd)
             objs.append(obj)
+        with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+            for f in [pool.submit(subprocess.run, c, check=True) for c in cmds]:
+                f.result()
         tmp_out = OUT + ".tmp"
         cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_out, *objs, "-lpthread"]
         if verbose:

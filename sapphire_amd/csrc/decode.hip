@@ -15,60 +15,11 @@
 // so a Q4_0 lane issues one 16-byte quant load per block and reads its 32 x values from LDS.
 // Row sums are wave-wide shuffle reductions. These GEMVs are small (<= 2 MiB of weights):
 // their cost is latency, hence the fusion of the vector work around them.
-#include <cmath>
-
-#include "decode_kernels.h"
-#include "devmath.h"
-#include "qdot.h"
+#include "decode_device.h"
 
 namespace sapphire {
 
 namespace {
-
-using namespace devmath;
-using namespace qdot;
-
-constexpr int kWave = 64;
-constexpr int kThreads = 256;
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
-// Sum of squares of v[0..n) (LDS) in the reference order of sum_sq_avx2
-// (normalization.c:12-32): eight sequential FMA lanes over elements l, l+8, ..., then
-// ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)) and a sequential fused tail. Threads 0..7 run the
-// lanes, loading eight elements ahead of their FMA chain; the result is returned to every
-// thread (the call synchronises the workgroup).
-__device__ float lds_sum_sq(const float *v, int n, float *sh) {
-    const int t = threadIdx.x;
-    if (t < 8) {
-        float s = 0.f;
-        const int full = n & ~7;
-        int i = t;
-        for (; i + 56 < full; i += 64) {
-            float w[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) w[u] = v[i + 8 * u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) s = __builtin_fmaf(w[u], w[u], s);
-        }
-        for (; i < full; i += 8) s = __builtin_fmaf(v[i], v[i], s);
-        sh[t] = s;
-    }
-    __syncthreads();
-    if (t == 0) {
-        const float a0 = sh[0] + sh[4], a1 = sh[1] + sh[5], a2 = sh[2] + sh[6], a3 = sh[3] + sh[7];
-        float s = (a0 + a1) + (a2 + a3);
-        for (int i = n & ~7; i < n; ++i) s = __builtin_fmaf(v[i], v[i], s);
-        sh[8] = s;
-    }
-    __syncthreads();
-    return sh[8];
-}
 
 // xs[0..K) = x(in) (see GemvIn); every thread of the workgroup takes part. dl is LDS
 // scratch of K floats for the delta vector.
@@ -92,37 +43,6 @@ __device__ void stage_input(const GemvIn &in, int K, float *xs, float *dl, float
             xs[i] = __fmul_rn(__fmul_rn(xs[i], r), __fadd_rn(1.0f, in.w_norm[i]));
     }
     __syncthreads();
-}
-
-template <int DT> struct QB;
-template <> struct QB<DT_Q4_0> { static constexpr int BYTES = 16, WORDS = 4; };
-template <> struct QB<DT_Q8_0> { static constexpr int BYTES = 32, WORDS = 8; };
-
-// The quants and scale of this lane's block of `row` (zeros for a lane off the matrix),
-// loaded before the input vector is staged so their latency overlaps the prologue.
-template <int DT>
-struct LaneBlock {
-    uint32_t q[QB<DT>::WORDS];
-    float s;
-};
-
-template <int DT>
-__device__ __forceinline__ void load_lane_block(const QMat &w, int row, int blk, int nb, bool on, LaneBlock<DT> &b) {
-    const bool ok = on && row < w.M;
-    const size_t bi = ok ? (size_t)row * nb + blk : 0;
-    const u32x4 *qp = reinterpret_cast<const u32x4 *>(w.q + bi * QB<DT>::BYTES);
-#pragma unroll
-    for (int i = 0; i < QB<DT>::WORDS / 4; ++i) {
-        const u32x4 t = __builtin_nontemporal_load(qp + i);
-        b.q[4 * i + 0] = t.x; b.q[4 * i + 1] = t.y; b.q[4 * i + 2] = t.z; b.q[4 * i + 3] = t.w;
-    }
-    b.s = ok ? w.s[bi] : 0.f;
-}
-
-template <int DT>
-__device__ __forceinline__ float block_value(const LaneBlock<DT> &b, const float (&xv)[32], float xsum) {
-    if constexpr (DT == DT_Q4_0) return b.s * dot_q4(b.q, xv, xsum);
-    else return b.s * dot_q8(b.q, xv, xsum);
 }
 
 // One wave-step per wave: rps rows of w0 (and of w1 for the GeGLU form).
@@ -170,61 +90,6 @@ __global__ __launch_bounds__(kThreads) void dec_prologue_kernel(GemvIn in, int K
 }
 
 // ---- attention ----
-
-// Sums of squares of nv consecutive vectors of length hd in LDS, each in the reference
-// order of sum_sq_avx2 (eight sequential lanes, then the fixed tree and a sequential
-// tail); eight threads per vector, loading eight elements ahead. Result in ss[v].
-__device__ void vectors_sum_sq(const float *base, int nv, int hd, float *part8, float *ss) {
-    const int t = threadIdx.x;
-    if (t < 8 * nv) {
-        const int v = t / 8, l = t - 8 * v;
-        const float *p = base + (size_t)v * hd;
-        const int full = hd & ~7;
-        float s = 0.f;
-        int i = l;
-        for (; i + 56 < full; i += 64) {
-            float w[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) w[u] = p[i + 8 * u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) s = __builtin_fmaf(w[u], w[u], s);
-        }
-        for (; i < full; i += 8) s = __builtin_fmaf(p[i], p[i], s);
-        part8[t] = s;
-    }
-    __syncthreads();
-    if (t < nv) {
-        const float *s8 = part8 + 8 * t;
-        const float a0 = s8[0] + s8[4], a1 = s8[1] + s8[5], a2 = s8[2] + s8[6], a3 = s8[3] + s8[7];
-        float s = (a0 + a1) + (a2 + a3);
-        const float *p = base + (size_t)t * hd;
-        for (int i = hd & ~7; i < hd; ++i) s = __builtin_fmaf(p[i], p[i], s);
-        ss[t] = s;
-    }
-    __syncthreads();
-}
-
-// dst[v] = rope(rmsnorm_delta(src[v], g)) for nv head vectors held in LDS (attention.c:
-// 221-309; rope_apply_fast rope.c:99-117 with the fused forms of the reference build).
-__device__ void norm_rope_heads(const float *src, int nv, int hd, const float *__restrict__ g,
-                                const float *__restrict__ cs, const float *__restrict__ sn, float eps, float *dst,
-                                float *part8, float *ss) {
-    vectors_sum_sq(src, nv, hd, part8, ss);
-    if (threadIdx.x < nv) ss[threadIdx.x] = rms_inv_of(ss[threadIdx.x], hd, eps);
-    __syncthreads();
-    const int half = hd / 2;
-    for (int idx = threadIdx.x; idx < nv * half; idx += blockDim.x) {
-        const int v = idx / half, i = idx - v * half;
-        const float r = ss[v];
-        const float *p = src + (size_t)v * hd;
-        const float x0 = __fmul_rn(__fmul_rn(p[i], r), __fadd_rn(1.0f, g[i]));
-        const float x1 = __fmul_rn(__fmul_rn(p[i + half], r), __fadd_rn(1.0f, g[i + half]));
-        const float c = cs[i], s = sn[i];
-        dst[v * hd + i] = __builtin_fmaf(x0, c, -__fmul_rn(x1, s));
-        dst[v * hd + i + half] = __builtin_fmaf(x1, c, __fmul_rn(x0, s));
-    }
-    __syncthreads();
-}
 
 // Workgroup b takes positions [t0, t1) of the layer's attention range; each wave walks
 // every fourth of them with a running (max, sum, weighted V) per head; the waves are then
@@ -399,12 +264,6 @@ __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float 
     }
 }
 
-// The token is device data (the previous step's argmax): it is clamped into the vocabulary
-// so that no value can address outside the table.
-__device__ __forceinline__ size_t embed_row(int tok, int vocab, int hidden) {
-    return (size_t)(tok >= 0 && tok < vocab ? tok : 0) * hidden;
-}
-
 __global__ void dec_embed_kernel(const uint16_t *__restrict__ embed, int hidden, int vocab, float es,
                                  const int *__restrict__ tok, float *__restrict__ resid) {
     const size_t row = embed_row(*tok, vocab, hidden);
@@ -415,12 +274,13 @@ __global__ void dec_embed_kernel(const uint16_t *__restrict__ embed, int hidden,
 }
 
 __global__ void dec_advance_kernel(const int *__restrict__ tok, int *__restrict__ pos, int *__restrict__ step,
-                                   int *__restrict__ log) {
+                                   int *__restrict__ log, uint32_t *__restrict__ seq) {
     if (threadIdx.x == 0 && blockIdx.x == 0) {
         const int s = *step;
         log[s] = *tok;
         *step = s + 1;
         *pos = *pos + 1;
+        if (seq) *seq = *seq + 1u;
     }
 }
 
@@ -582,8 +442,8 @@ int dec_embed(const uint16_t *embed, int hidden, int vocab, float es, const int 
     return hip_ok(hipGetLastError(), "embed launch") ? 0 : -1;
 }
 
-int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, hipStream_t s) {
-    hipLaunchKernelGGL(dec_advance_kernel, dim3(1), dim3(64), 0, s, d_token, d_pos, d_step, log);
+int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, uint32_t *d_seq, hipStream_t s) {
+    hipLaunchKernelGGL(dec_advance_kernel, dim3(1), dim3(64), 0, s, d_token, d_pos, d_step, log, d_seq);
     return hip_ok(hipGetLastError(), "advance launch") ? 0 : -1;
 }
 

@@ -1,0 +1,189 @@
+// decode_device.h - device helpers shared by the decode kernels (decode.hip) and the
+// persistent decode kernel (decode_persist.hip). Not installed.
+#pragma once
+
+#include <cmath>
+
+#include "decode_kernels.h"
+#include "devmath.h"
+#include "qdot.h"
+
+namespace sapphire {
+namespace {
+
+using namespace devmath;
+using namespace qdot;
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// DPP move of v (dpp_ctrl CTRL, every row and bank enabled).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each row of 16 lanes, left in every lane of the row: quad_perm [1,0,3,2] and
+// [2,3,0,1], then row_half_mirror and row_mirror. Each step adds a lane to its partner in
+// the other half, so every lane of the row ends with the same bits (fp addition commutes).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    return v;
+}
+
+// Maximum over each row of 16 lanes, left in every lane of the row (as row16_sum).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return v;
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over the 64 lanes of a wave as a wave-uniform value: row sums by DPP, then the four
+// rows added in a fixed order.
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+    v = row16_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+// Sum of squares of v[0..n) (LDS) in the reference order of sum_sq_avx2
+// (normalization.c:12-32): eight sequential FMA lanes over elements l, l+8, ..., then
+// ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)) and a sequential fused tail. Threads 0..7 run the
+// lanes, loading eight elements ahead of their FMA chain; the result is returned to every
+// thread (the call synchronises the workgroup).
+__device__ __forceinline__ float lds_sum_sq(const float *v, int n, float *sh) {
+    const int t = threadIdx.x;
+    if (t < 8) {
+        float s = 0.f;
+        const int full = n & ~7;
+        int i = t;
+        for (; i + 56 < full; i += 64) {
+            float w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = v[i + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s = __builtin_fmaf(w[u], w[u], s);
+        }
+        for (; i < full; i += 8) s = __builtin_fmaf(v[i], v[i], s);
+        sh[t] = s;
+    }
+    __syncthreads();
+    if (t == 0) {
+        const float a0 = sh[0] + sh[4], a1 = sh[1] + sh[5], a2 = sh[2] + sh[6], a3 = sh[3] + sh[7];
+        float s = (a0 + a1) + (a2 + a3);
+        for (int i = n & ~7; i < n; ++i) s = __builtin_fmaf(v[i], v[i], s);
+        sh[8] = s;
+    }
+    __syncthreads();
+    return sh[8];
+}
+
+template <int DT> struct QB;
+template <> struct QB<DT_Q4_0> { static constexpr int BYTES = 16, WORDS = 4; };
+template <> struct QB<DT_Q8_0> { static constexpr int BYTES = 32, WORDS = 8; };
+
+// The quants and scale of this lane's block of `row` (zeros for a lane off the matrix),
+// loaded before the input vector is staged so their latency overlaps the prologue.
+template <int DT>
+struct LaneBlock {
+    uint32_t q[QB<DT>::WORDS];
+    float s;
+};
+
+template <int DT>
+__device__ __forceinline__ void load_lane_block(const QMat &w, int row, int blk, int nb, bool on, LaneBlock<DT> &b) {
+    const bool ok = on && row < w.M;
+    const size_t bi = ok ? (size_t)row * nb + blk : 0;
+    const u32x4 *qp = reinterpret_cast<const u32x4 *>(w.q + bi * QB<DT>::BYTES);
+#pragma unroll
+    for (int i = 0; i < QB<DT>::WORDS / 4; ++i) {
+        const u32x4 t = __builtin_nontemporal_load(qp + i);
+        b.q[4 * i + 0] = t.x; b.q[4 * i + 1] = t.y; b.q[4 * i + 2] = t.z; b.q[4 * i + 3] = t.w;
+    }
+    b.s = ok ? w.s[bi] : 0.f;
+}
+
+template <int DT>
+__device__ __forceinline__ float block_value(const LaneBlock<DT> &b, const float (&xv)[32], float xsum) {
+    if constexpr (DT == DT_Q4_0) return b.s * dot_q4(b.q, xv, xsum);
+    else return b.s * dot_q8(b.q, xv, xsum);
+}
+
+// Sums of squares of nv consecutive vectors of length hd in LDS, each in the reference
+// order of sum_sq_avx2 (eight sequential lanes, then the fixed tree and a sequential
+// tail); eight threads per vector, loading eight elements ahead. Result in ss[v].
+__device__ __forceinline__ void vectors_sum_sq(const float *base, int nv, int hd, float *part8, float *ss) {
+    const int t = threadIdx.x;
+    if (t < 8 * nv) {
+        const int v = t / 8, l = t - 8 * v;
+        const float *p = base + (size_t)v * hd;
+        const int full = hd & ~7;
+        float s = 0.f;
+        int i = l;
+        for (; i + 56 < full; i += 64) {
+            float w[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[u] = p[i + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s = __builtin_fmaf(w[u], w[u], s);
+        }
+        for (; i < full; i += 8) s = __builtin_fmaf(p[i], p[i], s);
+        part8[t] = s;
+    }
+    __syncthreads();
+    if (t < nv) {
+        const float *s8 = part8 + 8 * t;
+        const float a0 = s8[0] + s8[4], a1 = s8[1] + s8[5], a2 = s8[2] + s8[6], a3 = s8[3] + s8[7];
+        float s = (a0 + a1) + (a2 + a3);
+        const float *p = base + (size_t)t * hd;
+        for (int i = hd & ~7; i < hd; ++i) s = __builtin_fmaf(p[i], p[i], s);
+        ss[t] = s;
+    }
+    __syncthreads();
+}
+
+// dst[v] = rope(rmsnorm_delta(src[v], g)) for nv head vectors held in LDS (attention.c:
+// 221-309; rope_apply_fast rope.c:99-117 with the fused forms of the reference build).
+__device__ __forceinline__ void norm_rope_heads(const float *src, int nv, int hd, const float *__restrict__ g,
+                                                const float *__restrict__ cs, const float *__restrict__ sn, float eps,
+                                                float *dst, float *part8, float *ss) {
+    vectors_sum_sq(src, nv, hd, part8, ss);
+    if (threadIdx.x < nv) ss[threadIdx.x] = rms_inv_of(ss[threadIdx.x], hd, eps);
+    __syncthreads();
+    const int half = hd / 2;
+    for (int idx = threadIdx.x; idx < nv * half; idx += blockDim.x) {
+        const int v = idx / half, i = idx - v * half;
+        const float r = ss[v];
+        const float *p = src + (size_t)v * hd;
+        const float x0 = __fmul_rn(__fmul_rn(p[i], r), __fadd_rn(1.0f, g[i]));
+        const float x1 = __fmul_rn(__fmul_rn(p[i + half], r), __fadd_rn(1.0f, g[i + half]));
+        const float c = cs[i], s = sn[i];
+        dst[v * hd + i] = __builtin_fmaf(x0, c, -__fmul_rn(x1, s));
+        dst[v * hd + i + half] = __builtin_fmaf(x1, c, __fmul_rn(x0, s));
+    }
+    __syncthreads();
+}
+
+// The token is device data (the previous step's argmax): it is clamped into the vocabulary
+// so that no value can address outside the table.
+__device__ __forceinline__ size_t embed_row(int tok, int vocab, int hidden) {
+    return (size_t)(tok >= 0 && tok < vocab ? tok : 0) * hidden;
+}
+
+}  // namespace
+}  // namespace sapphire

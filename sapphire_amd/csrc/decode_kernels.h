@@ -63,8 +63,52 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s);
 // reads row 0
 int dec_embed(const uint16_t *embed, int hidden, int vocab, float es, const int *d_token, float *resid,
               hipStream_t s);
-// log[*d_step] = *d_token; ++*d_step; ++*d_pos
-int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, hipStream_t s);
+// log[*d_step] = *d_token; ++*d_step; ++*d_pos; ++*d_seq when d_seq is set
+int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, uint32_t *d_seq, hipStream_t s);
+
+// ---- the layers of a step as one persistent kernel (decode_persist.hip) ----
+
+// One layer's weights and caches, in device memory (an array of n_layers).
+struct PLayer {
+    QMat qkv, o, gate, up, down;
+    const float *n_attn, *n_attn_post, *n_ffn, *n_ffn_post, *qn, *kn;
+    const float *cos_t, *sin_t;      // RoPE tables of the layer (global or local base)
+    float *kc, *vc;                  // [nkv][max_ctx][hd]
+    int window;                      // sliding window, 0 for a global layer
+};
+
+// Exchanged vectors are fp32 arrays in device memory; flags[G] holds the last stage epoch each
+// workgroup has completed (see decode_persist.hip).
+struct PersistArgs {
+    const PLayer *layers = nullptr;
+    int n_layers = 0;
+    const uint16_t *embed = nullptr;  // [vocab][H] bf16
+    int vocab = 0;
+    float es = 1.f;                   // embedding scale sqrt(H)
+    const float *norm_final = nullptr;
+    int H = 0, nh = 0, nkv = 0, hd = 0, ffn = 0, max_ctx = 0;
+    float scale = 1.f, eps = 1e-6f;
+    const int *state = nullptr;       // [0] token, [1] position
+    const uint32_t *seq = nullptr;    // step counter that makes the epochs unique
+    float *t_qkv = nullptr, *t_part = nullptr, *t_attn = nullptr, *t_o = nullptr, *t_g = nullptr,
+          *t_dn = nullptr;
+    uint32_t *flags = nullptr;
+    float *xfin = nullptr;            // [H] final-norm output (the LM-head input)
+    int *err = nullptr;               // incremented by a workgroup whose wait timed out
+    int spin_limit = 0;
+};
+constexpr int kPersistMaxGroups = 256;
+// 4-byte words of the exchange buffers for a model shape, contiguous in this order: the fp32
+// vectors qkv, partials for kPersistMaxGroups workgroups, attention output, o, g, down, then
+// the kPersistMaxGroups uint32 epoch flags.
+size_t persist_words(int H, int nh, int nkv, int hd, int ffn);
+// Whether `groups` workgroups can run the persistent step for these shapes on the current
+// device (co-residency included); sets the error message when not.
+bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int ffn);
+// Cooperative launch of the persistent step (capturable into a HIP graph).
+int dec_persist(int dt, const PersistArgs &a, int groups, hipStream_t s);
+// Epoch stride of one step: 8 stages per layer plus the final one.
+__host__ __device__ inline uint32_t persist_epochs_per_step(int n_layers) { return 8u * (uint32_t)(n_layers + 1); }
 
 // ---- batched decode (a batch of sequences in lock step) ----
 // resid[b][i] = bf16 row of tokens[b] * es

@@ -1,0 +1,640 @@
+// decode_persist.hip - the layers of one Gemma-3 decode step as one persistent kernel.
+//
+// The multi-launch step (decode.hip) separates its stages by kernel boundaries; each of its
+// ~110 launches per token costs a launch and a cold start of its memory loads. Here one
+// cooperative grid of G workgroups (all co-resident) runs every layer, and the stages are
+// separated by data instead:
+//
+// * Exchanged vectors are fp32 arrays stored and loaded with agent-scope atomics, which are
+//   coherent across the L2 caches of the eight XCDs.
+// * A workgroup ends a stage by waiting for its stores' acknowledgements and then publishing
+//   the stage's epoch in its own flag word. A consumer's first wave polls one flag per
+//   workgroup until all have reached the epoch it needs, then every thread reads its inputs
+//   once. Only one wave per workgroup polls, so waiting adds little memory traffic. A
+//   workgroup's weight and KV-cache loads for its next stage are issued before that wait, so
+//   their latency hides behind it.
+// * Every workgroup keeps its own copy of the residual stream in LDS. It is updated by the same
+//   instructions from the same inputs, so the copies are bit-identical.
+//
+// Stages of layer l, epoch e = seq * 8 * (n_layers + 1) + 8 * l + stage (seq counts steps):
+//   1 QKV GEMV       input: previous layer's down output (post-FFN norm + residual), pre-norm
+//   2 attention      input: q, k, v; QK-norm, RoPE, KV write; partial over a slice of positions
+//   3 combine        input: every workgroup's partial for this workgroup's attention elements
+//   4 o-proj GEMV    input: attention output
+//   5 gate/up GEMV   input: o (post-attention norm + residual, pre-FFN norm); epilogue gelu*up
+//   6 down GEMV      input: g
+// After the last layer the final finalize + norm run; workgroup 0 writes the LM-head input.
+// The op order is that of inference_forward_batch (inference.c:616-651) with the stages of
+// attention.c:311-375 and transformer.c:96-283, as in decode.hip.
+//
+// Every wait is bounded. A wait that exceeds spin_limit polls increments *err and ends its
+// workgroup; every other workgroup then times out at its next wait. So the kernel always ends,
+// and the host reports the failure.
+#include "decode_device.h"
+
+namespace sapphire {
+
+namespace {
+
+constexpr int kLpr = 16;                          // lanes per GEMV row
+constexpr int kRpw = kWave / kLpr;                // rows per wave-step
+constexpr int kSlots = 4;                         // (wave-step, block) slots per lane in one GEMV stage
+constexpr int kCombMax = 4096;                    // gathered partial words per workgroup in the combine
+constexpr int kVecRegs = kDecMaxK / kThreads;     // vector elements per thread
+
+__device__ __forceinline__ void put_shared(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_shared(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NH, int DPL>
+struct alignas(16) PersistLds {
+    float resid[kDecMaxK];                       // the residual stream
+    float xs[kDecMaxK];                          // input of the current GEMV
+    float dl[kDecMaxK];                          // gathered delta vector
+    float raw[kAttnMaxQ + 2 * kAttnMaxKV];       // q | k | v as projected
+    float qk[kAttnMaxQ + kAttnMaxKV];            // q | k after QK-norm and RoPE
+    float part8[8 * 16];
+    float ss[16];
+    float wm[kThreads / kWave][NH], wsum[kThreads / kWave][NH];
+    float wo[kThreads / kWave][NH][kWave * DPL];
+    float wx[kThreads / kWave][NH];              // wave merge weights
+    float wmax[NH], wtot[NH];
+    float comb[kCombMax];
+    float sh[16];
+    int flag;
+};
+
+// The end of a stage: every wave waits for the acknowledgements of its exchange stores (they
+// are then visible at device scope), then thread 0 publishes the stage's epoch in the
+// workgroup's flag.
+__device__ __forceinline__ void signal(uint32_t *flags, uint32_t ep) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(flags + blockIdx.x, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every workgroup's flag has reached epoch ep (epochs only grow within a step
+// sequence): wave 0 polls one flag per workgroup and lane. Returns false (and counts the
+// failure in *err) when a flag is still behind after spin_limit polls. Synchronises the
+// workgroup; the result is the same in every thread.
+__device__ __forceinline__ bool wait_all(const uint32_t *flags, uint32_t ep, int spin_limit, int *err, int *bail) {
+    if (threadIdx.x < kWave) {
+        const int G = gridDim.x;
+        for (int spins = 0;; ++spins) {
+            bool ok = true;
+            for (int i = threadIdx.x; i < G; i += kWave)
+                ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= ep;
+            if (__all(ok)) break;
+            if (spins >= spin_limit) {
+                if (threadIdx.x == 0) *bail = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+    const bool ok = *bail == 0;
+    if (!ok && threadIdx.x == 0) atomicAdd(err, 1);
+    return ok;
+}
+
+// dst[j] = *src(j) for j < n (device-scope loads, all issued before any is used); thread t
+// takes j = t + 256 e. Synchronises the workgroup.
+template <int MAXE, class Src>
+__device__ __forceinline__ void load_shared(Src src, int n, float *dst) {
+    float v[MAXE];
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+        const int j = threadIdx.x + e * kThreads;
+        v[e] = j < n ? get_shared(src(j)) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+        const int j = threadIdx.x + e * kThreads;
+        if (j < n) dst[j] = v[e];
+    }
+    __syncthreads();
+}
+
+struct Contig {
+    const float *p;
+    __device__ const float *operator()(int j) const { return p + j; }
+};
+
+// Elements t + 256 e of a K-long weight vector in registers (loaded before a wait).
+struct VecRegs {
+    float v[kVecRegs];
+    __device__ __forceinline__ void load(const float *__restrict__ p, int K) {
+#pragma unroll
+        for (int e = 0; e < kVecRegs; ++e) {
+            const int i = threadIdx.x + e * kThreads;
+            v[e] = i < K ? p[i] : 0.f;
+        }
+    }
+};
+
+// Sum of squares of v[0..K) (LDS) over the workgroup: per-thread FMA chains of at most
+// K / 256 elements, DPP row sums, then the four waves in a fixed order. The reference sums
+// in eight sequential lanes (normalization.c:12-32); this order is a tree (within the decode
+// tolerance) and takes a few hundred cycles instead of a K/8-long dependent chain. Every
+// thread gets the same value; the call synchronises the workgroup.
+__device__ __forceinline__ float par_sum_sq(const float *v, int K, float *sh) {
+    float acc = 0.f;
+    for (int i = threadIdx.x; i < K; i += kThreads) acc = __builtin_fmaf(v[i], v[i], acc);
+    acc = wave_sum_uniform(acc);
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+// resid += rmsnorm_delta(dl, w) (attention.c:358-366, transformer.c:231-239)
+__device__ __forceinline__ void add_norm_delta(float *resid, const float *dl, const VecRegs &w, int K, float eps,
+                                               float *sh) {
+    const float r = rms_inv_of(par_sum_sq(dl, K, sh), K, eps);
+#pragma unroll
+    for (int e = 0; e < kVecRegs; ++e) {
+        const int i = threadIdx.x + e * kThreads;
+        if (i < K) resid[i] = __fadd_rn(resid[i], __fmul_rn(__fmul_rn(dl[i], r), __fadd_rn(1.0f, w.v[e])));
+    }
+    __syncthreads();
+}
+
+// xs = rmsnorm_delta(resid, w) (normalization.c:104-117)
+__device__ __forceinline__ void norm_to(float *xs, const float *resid, const VecRegs &w, int K, float eps,
+                                        float *sh) {
+    const float r = rms_inv_of(par_sum_sq(resid, K, sh), K, eps);
+#pragma unroll
+    for (int e = 0; e < kVecRegs; ++e) {
+        const int i = threadIdx.x + e * kThreads;
+        if (i < K) xs[i] = __fmul_rn(__fmul_rn(resid[i], r), __fadd_rn(1.0f, w.v[e]));
+    }
+    __syncthreads();
+}
+
+// The rows of one GEMV stage owned by this workgroup. A wave-step is 4 rows, 16 lanes each;
+// lane q of a row takes blocks q, q + 16, ... (bpl = ceil(K / 512) of them), and the row's
+// lanes are summed by DPP. The S = ceil(M / 4) wave-steps are split into contiguous ranges of
+// ceil(S / G) per workgroup; wave w takes every fourth step of its workgroup's range. A lane
+// holds kSlots (step, block) slots, slot = step * bpl + block (steps per wave x bpl <= kSlots,
+// checked by the host). load() issues the weight loads; finish() forms the rows.
+template <int DT, bool GEGLU>
+struct GemvStage {
+    LaneBlock<DT> b0[kSlots], b1[kSlots];
+    int M, nb, bpl, q, rin, s0, s1;
+
+    __device__ __forceinline__ void load(const QMat &w0, const QMat &w1) {
+        M = w0.M;
+        nb = w0.K / kBlock;
+        bpl = (nb + kLpr - 1) / kLpr;
+        const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+        q = lane & (kLpr - 1);
+        rin = lane / kLpr;
+        const int S = (M + kRpw - 1) / kRpw, per = (S + (int)gridDim.x - 1) / (int)gridDim.x;
+        s0 = min(S, (int)blockIdx.x * per);
+        s1 = min(S, s0 + per);
+#pragma unroll
+        for (int slot = 0; slot < kSlots; ++slot) {
+            const int k = slot / bpl, j = slot - k * bpl;
+            const int st = s0 + wid + 4 * k;
+            if (st < s1) {
+                const int blk = q + kLpr * j;
+                load_lane_block<DT>(w0, st * kRpw + rin, blk, nb, blk < nb, b0[slot]);
+                if constexpr (GEGLU) load_lane_block<DT>(w1, st * kRpw + rin, blk, nb, blk < nb, b1[slot]);
+            }
+        }
+    }
+
+    // y[row] = W0[row] . xs, or gelu(W0[row] . xs) * (W1[row] . xs) for the GeGLU form. The
+    // stage's signal() follows (its barrier also ends the reads of xs).
+    __device__ __forceinline__ void finish(const float *xs, float *y) {
+        const int wid = threadIdx.x / kWave;
+        float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+        for (int slot = 0; slot < kSlots; ++slot) {
+            const int k = slot / bpl, j = slot - k * bpl;
+            const int st = s0 + wid + 4 * k;
+            if (st < s1) {
+                const int blk = q + kLpr * j;
+                const bool on = blk < nb;
+                float xv[32];
+                const float4 *xp = reinterpret_cast<const float4 *>(xs + blk * kBlock);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float4 v = on ? xp[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    xv[4 * i] = v.x;
+                    xv[4 * i + 1] = v.y;
+                    xv[4 * i + 2] = v.z;
+                    xv[4 * i + 3] = v.w;
+                }
+                float xt[16];   // sum of the block's x as a tree (not a 32-long chain)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) xt[i] = xv[2 * i] + xv[2 * i + 1];
+#pragma unroll
+                for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+                    for (int i = 0; i < w; ++i) xt[i] = xt[2 * i] + xt[2 * i + 1];
+                const float xsum = xt[0];
+                p0 += block_value<DT>(b0[slot], xv, xsum);
+                if constexpr (GEGLU) p1 += block_value<DT>(b1[slot], xv, xsum);
+                if (j == bpl - 1) {   // the step's last block: sum the row's lanes and store
+                    p0 = row16_sum(p0);
+                    if constexpr (GEGLU) p1 = row16_sum(p1);
+                    const int row = st * kRpw + rin;
+                    if (q == 0 && row < M) put_shared(y + row, GEGLU ? __fmul_rn(gelu_ref(p0), p1) : p0);
+                    p0 = 0.f;
+                    p1 = 0.f;
+                }
+            }
+            // one slot's 32 x values live at a time
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
+// Stage 2: QK-norm, RoPE and the KV write of the token, then this workgroup's partial
+// (o, max in log2 units, sum per head) over its slice of the layer's positions:
+// dec_attn_part_kernel with one slice per workgroup. The gammas, RoPE rows and the first K/V rows of the slice are
+// loaded before the wait for q, k, v; scores are summed by DPP into wave-uniform values.
+template <int DPL, int NH>
+__device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L, int pos, uint32_t ep_in,
+                                           PersistLds<NH, DPL> &s) {
+    const int hd = a.hd, half = hd / 2;
+    constexpr int nkv = 1;
+    const int seq = pos + 1;
+    const int start = (L.window > 0 && seq > L.window) ? seq - L.window : 0;
+    const int len = seq - start, G = gridDim.x;
+    const int chunk = (len + G - 1) / G;
+    const int t0 = min(seq, start + (int)blockIdx.x * chunk), t1 = min(seq, t0 + chunk);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    constexpr int PF = 4;
+    constexpr int NW = kThreads / kWave;
+    float kr[PF][DPL], vr[PF][DPL];   // one K/V head: its rows are [max_ctx][hd]
+    auto load_batch = [&](int tb) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const int t = tb + j * NW;
+            const bool ok = t < t1 && t != pos;
+            const size_t off = ok ? (size_t)t * hd : 0;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                kr[j][d] = ok ? L.kc[off + lane * DPL + d] : 0.f;
+                vr[j][d] = ok ? L.vc[off + lane * DPL + d] : 0.f;
+            }
+        }
+    };
+    if (t0 + wid < t1) load_batch(t0 + wid);   // in flight during the wait for q, k, v
+
+    // rotation pairs (vector v, index i < half) of the q heads then the k heads: their
+    // gammas and RoPE row entries (rope.c:99-117; q/k norms attention.c:221-226)
+    constexpr int MAXP = (NH + 1) * kWave * DPL / 2 / kThreads + 1;
+    const int npairs = (NH + nkv) * half;
+    float g0[MAXP], g1[MAXP], cs[MAXP], sn[MAXP];
+#pragma unroll
+    for (int e = 0; e < MAXP; ++e) {
+        const int p = threadIdx.x + e * kThreads;
+        const bool ok = p < npairs;
+        const int v = ok ? p / half : 0, i = ok ? p - v * half : 0;
+        const float *gam = v < NH ? L.qn : L.kn;
+        g0[e] = ok ? gam[i] : 0.f;
+        g1[e] = ok ? gam[i + half] : 0.f;
+        cs[e] = ok ? L.cos_t[(size_t)pos * hd + i] : 0.f;
+        sn[e] = ok ? L.sin_t[(size_t)pos * hd + i] : 0.f;
+    }
+
+    if (!wait_all(a.flags, ep_in, a.spin_limit, a.err, &s.flag)) return false;
+    load_shared<(kAttnMaxQ + 2 * kAttnMaxKV) / kThreads>(Contig{a.t_qkv}, (NH + 2 * nkv) * hd, s.raw);
+    // rmsnorm_delta of every q and k head vector, then the half-split rotation
+    {   // sum of squares of each head vector: 16-lane row v takes vector v (tree order)
+        const int v = threadIdx.x / 16, q16 = threadIdx.x & 15;
+        if (v < NH + nkv) {
+            float acc = 0.f;
+            for (int i = q16; i < hd; i += 16) acc = __builtin_fmaf(s.raw[v * hd + i], s.raw[v * hd + i], acc);
+            acc = row16_sum(acc);
+            if (q16 == 0) s.ss[v] = rms_inv_of(acc, hd, a.eps);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int e = 0; e < MAXP; ++e) {
+        const int p = threadIdx.x + e * kThreads;
+        if (p < npairs) {
+            const int v = p / half, i = p - v * half;
+            const float r = s.ss[v];
+            const float *src = s.raw + (size_t)v * hd;
+            const float x0 = __fmul_rn(__fmul_rn(src[i], r), __fadd_rn(1.0f, g0[e]));
+            const float x1 = __fmul_rn(__fmul_rn(src[i + half], r), __fadd_rn(1.0f, g1[e]));
+            s.qk[v * hd + i] = __builtin_fmaf(x0, cs[e], -__fmul_rn(x1, sn[e]));
+            s.qk[v * hd + i + half] = __builtin_fmaf(x1, cs[e], __fmul_rn(x0, sn[e]));
+        }
+    }
+    __syncthreads();
+    const float *ks = s.qk + NH * hd;
+    const float *vnew = s.raw + (NH + nkv) * hd;
+    if (t0 <= pos && pos < t1)   // kv_cache_write_token: [head][pos][dim]
+        for (int i = threadIdx.x; i < nkv * hd; i += kThreads) {
+            const int h = i / hd, d = i - h * hd;
+            const size_t off = ((size_t)h * a.max_ctx + pos) * hd + d;
+            L.kc[off] = ks[i];
+            L.vc[off] = vnew[i];
+        }
+
+    // scores in log2 units, so that every softmax weight is one exp2 (v_exp_f32)
+    const float sl2 = __fmul_rn(a.scale, 1.44269504088896341f);
+    float qr[NH][DPL];
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) qr[h][d] = s.qk[h * hd + lane * DPL + d];
+    float m[NH], sm[NH], o[NH][DPL];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        m[h] = -INFINITY;
+        sm[h] = 0.f;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
+    }
+    for (int tb = t0 + wid; tb < t1; tb += PF * NW) {
+        if (tb != t0 + wid) load_batch(tb);
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const int t = tb + j * NW;
+            if (t >= t1) break;
+            if (t == pos) {
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) {
+                    kr[j][d] = ks[lane * DPL + d];
+                    vr[j][d] = vnew[lane * DPL + d];
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                float dp = 0.f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) dp = __builtin_fmaf(qr[h][d], kr[j][d], dp);
+                const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
+                const float mn = fmaxf(m[h], score);
+                const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
+                const float p = __builtin_amdgcn_exp2f(score - mn);
+                sm[h] = __builtin_fmaf(sm[h], c, p);
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) o[h][d] = __builtin_fmaf(o[h][d], c, p * vr[j][d]);
+                m[h] = mn;
+            }
+        }
+    }
+    // merge the four waves and store the slice's partial: the (wave, head) weights
+    // exp2(m_w - M) are formed once, then every element is a weighted sum
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        if (lane == 0) {
+            s.wm[wid][h] = m[h];
+            s.wsum[wid][h] = sm[h];
+        }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) s.wo[wid][h][lane * DPL + d] = o[h][d];
+    }
+    __syncthreads();
+    if (threadIdx.x < NH) {
+        const int h = threadIdx.x;
+        float M = -INFINITY;
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, s.wm[w][h]);
+        float S = 0.f;
+        for (int w = 0; w < NW; ++w) {
+            const float e = s.wm[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s.wm[w][h] - M);
+            s.wx[w][h] = e;
+            S = __builtin_fmaf(s.wsum[w][h], e, S);
+        }
+        s.wmax[h] = M;
+        s.wtot[h] = S;
+    }
+    __syncthreads();
+    float *out = a.t_part + (size_t)blockIdx.x * NH * (hd + 2);
+    for (int idx = threadIdx.x; idx < NH * hd; idx += kThreads) {
+        const int h = idx / hd, d = idx - h * hd;
+        float O = 0.f;
+        for (int w = 0; w < NW; ++w) O = __builtin_fmaf(s.wo[w][h][d], s.wx[w][h], O);
+        put_shared(out + h * (hd + 2) + d, O);
+        if (d == 0) {
+            put_shared(out + h * (hd + 2) + hd, s.wmax[h]);
+            put_shared(out + h * (hd + 2) + hd + 1, s.wtot[h]);
+        }
+    }
+    return true;
+}
+
+// Stage 3: attention elements [e0, e1) of this workgroup, E = ceil(NH*hd / G) each:
+// out = sum_b e_b o_b / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) over every workgroup's
+// partial b (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes.
+template <int NH, int DPL>
+__device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t ep_in, PersistLds<NH, DPL> &s) {
+    const int hd = a.hd, nq = NH * hd, G = gridDim.x;
+    const int E = (nq + G - 1) / G;
+    const int e0 = min(nq, (int)blockIdx.x * E), e1 = min(nq, e0 + E);
+    if (!wait_all(a.flags, ep_in, a.spin_limit, a.err, &s.flag)) return false;
+    if (e0 >= e1) return true;
+    const int h_lo = e0 / hd, h_hi = (e1 - 1) / hd;   // E <= hd: at most two heads
+    const int per = E + 4;                            // E values, then (m, s) of h_lo and h_hi
+    const float *part = a.t_part;
+    auto src = [=](int j) -> const float * {
+        const int b = j / per, k = j - b * per;
+        size_t off;
+        if (k < E) {
+            const int el = min(e0 + k, e1 - 1);
+            off = ((size_t)b * NH + el / hd) * (hd + 2) + el % hd;
+        } else {
+            const int hh = (k - E) < 2 ? h_lo : h_hi;
+            off = ((size_t)b * NH + hh) * (hd + 2) + hd + ((k - E) & 1);
+        }
+        return part + off;
+    };
+    load_shared<kCombMax / kThreads>(src, G * per, s.comb);
+    // 16-lane row r takes elements k = r, r + 16, ...; lane q of the row takes partials
+    // b = q, q + 16, ...; max, weights and sums are reduced over the row by DPP
+    const int q = threadIdx.x & 15;
+    for (int k = threadIdx.x / 16; k < e1 - e0; k += kThreads / 16) {
+        const int el = e0 + k, hk = el / hd == h_lo ? 0 : 2;
+        float M = -INFINITY;
+        for (int b = q; b < G; b += 16) M = fmaxf(M, s.comb[b * per + E + hk]);
+        M = row16_max(M);
+        float S = 0.f, O = 0.f;
+        for (int b = q; b < G; b += 16) {
+            const float mb = s.comb[b * per + E + hk];
+            const float e = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
+            S = __builtin_fmaf(s.comb[b * per + E + hk + 1], e, S);
+            O = __builtin_fmaf(s.comb[b * per + k], e, O);
+        }
+        S = row16_sum(S);
+        O = row16_sum(O);
+        if (q == 0) put_shared(a.t_attn + el, O * (1.0f / S));
+    }
+    return true;
+}
+
+template <int DT, int DPL, int NH>
+__global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
+    __shared__ PersistLds<NH, DPL> s;
+    // a wait of an earlier step of this generate call timed out: its results are void, and
+    // every later step ends at once instead of timing out again
+    if (*a.err != 0) return;
+    if (threadIdx.x == 0) s.flag = 0;
+    const int H = a.H, nq = NH * a.hd;
+    const int tok = a.state[0], pos = a.state[1];
+    const uint32_t base = *a.seq * persist_epochs_per_step(a.n_layers);
+    {   // sapphire_embed_lookup (transformer.c:347-365)
+        const size_t row = embed_row(tok, a.vocab, H);
+        for (int i = threadIdx.x; i < H; i += kThreads) {
+            const float v = __uint_as_float((uint32_t)a.embed[row + i] << 16);
+            s.resid[i] = a.es != 1.0f ? __fmul_rn(v, a.es) : v;
+        }
+    }
+    __syncthreads();
+    for (int l = 0; l < a.n_layers; ++l) {
+        const PLayer &L = a.layers[l];
+        const uint32_t ep = base + 8u * (uint32_t)l;
+        {   // 1: previous layer's finalize, pre-attention norm, QKV
+            GemvStage<DT, false> g;
+            g.load(L.qkv, L.qkv);
+            VecRegs wn;
+            wn.load(L.n_attn, H);
+            if (l > 0) {
+                VecRegs wd;
+                wd.load(a.layers[l - 1].n_ffn_post, H);
+                if (!wait_all(a.flags, ep - 2, a.spin_limit, a.err, &s.flag)) return;
+                load_shared<kVecRegs>(Contig{a.t_dn}, H, s.dl);
+                add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
+            }
+            norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
+            g.finish(s.xs, a.t_qkv);
+            signal(a.flags, ep + 1);
+        }
+        if (!attn_stage<DPL, NH>(a, L, pos, ep + 1, s)) return;
+        signal(a.flags, ep + 2);
+        if (!combine_stage<NH, DPL>(a, ep + 2, s)) return;
+        signal(a.flags, ep + 3);
+        {   // 4: o-proj
+            GemvStage<DT, false> g;
+            g.load(L.o, L.o);
+            if (!wait_all(a.flags, ep + 3, a.spin_limit, a.err, &s.flag)) return;
+            load_shared<kVecRegs>(Contig{a.t_attn}, nq, s.xs);
+            g.finish(s.xs, a.t_o);
+            signal(a.flags, ep + 4);
+        }
+        {   // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU
+            GemvStage<DT, true> g;
+            g.load(L.gate, L.up);
+            VecRegs wd, wn;
+            wd.load(L.n_attn_post, H);
+            wn.load(L.n_ffn, H);
+            if (!wait_all(a.flags, ep + 4, a.spin_limit, a.err, &s.flag)) return;
+            load_shared<kVecRegs>(Contig{a.t_o}, H, s.dl);
+            add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
+            norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
+            g.finish(s.xs, a.t_g);
+            signal(a.flags, ep + 5);
+        }
+        {   // 6: down
+            GemvStage<DT, false> g;
+            g.load(L.down, L.down);
+            if (!wait_all(a.flags, ep + 5, a.spin_limit, a.err, &s.flag)) return;
+            load_shared<kVecRegs>(Contig{a.t_g}, a.ffn, s.xs);
+            g.finish(s.xs, a.t_dn);
+            signal(a.flags, ep + 6);
+        }
+    }
+    // last finalize + final norm (transformer.c:400-406)
+    VecRegs wd, wn;
+    wd.load(a.layers[a.n_layers - 1].n_ffn_post, H);
+    wn.load(a.norm_final, H);
+    const uint32_t ep_last = base + 8u * (uint32_t)(a.n_layers - 1) + 6u;
+    if (!wait_all(a.flags, ep_last, a.spin_limit, a.err, &s.flag)) return;
+    load_shared<kVecRegs>(Contig{a.t_dn}, H, s.dl);
+    add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
+    norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < H; i += kThreads) a.xfin[i] = s.xs[i];
+}
+
+using PersistKernel = void (*)(PersistArgs);
+
+template <int DT>
+PersistKernel pick(int dpl, int nh) {
+#define SPH_PK(DPLV, NHV) \
+    if (dpl == DPLV && nh == NHV) return dec_persist_kernel<DT, DPLV, NHV>;
+    SPH_PK(1, 4) SPH_PK(2, 4) SPH_PK(4, 4) SPH_PK(1, 8) SPH_PK(2, 8) SPH_PK(4, 8)
+#undef SPH_PK
+    return nullptr;
+}
+
+PersistKernel kernel_for(int dt, int nh, int hd) {
+    if (hd % kWave) return nullptr;
+    const int dpl = hd / kWave;
+    return dt == DT_Q4_0 ? pick<DT_Q4_0>(dpl, nh) : dt == DT_Q8_0 ? pick<DT_Q8_0>(dpl, nh) : nullptr;
+}
+
+// (wave-step, block) slots per lane of an M x K GEMV stage over `groups` workgroups.
+int slots_per_lane(int M, int K, int groups) {
+    const int S = (M + kRpw - 1) / kRpw, per = (S + groups - 1) / groups;
+    const int bpl = (K / kBlock + kLpr - 1) / kLpr;
+    return (per + 3) / 4 * bpl;
+}
+
+}  // namespace
+
+size_t persist_words(int H, int nh, int nkv, int hd, int ffn) {
+    return (size_t)(nh + 2 * nkv) * hd + (size_t)kPersistMaxGroups * nh * (hd + 2) + (size_t)nh * hd + H + ffn + H +
+           kPersistMaxGroups;
+}
+
+bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int ffn) {
+    const PersistKernel k = kernel_for(dt, nh, hd);
+    const int nq = nh * hd;
+    if (!k || nkv != 1 || nq > kAttnMaxQ || hd > kAttnMaxKV) {
+        set_error("persistent decode: %d heads of dim %d / %d KV heads not instantiated (one KV head)", nh, hd, nkv);
+        return false;
+    }
+    if (groups < nh || groups > kPersistMaxGroups) {
+        set_error("persistent decode: %d workgroups (needs %d..%d)", groups, nh, kPersistMaxGroups);
+        return false;
+    }
+    if (H % kBlock || nq % kBlock || ffn % kBlock || H > kDecMaxK || nq > kDecMaxK || ffn > kDecMaxK) {
+        set_error("persistent decode: GEMV inputs must be multiples of 32 and at most %d", kDecMaxK);
+        return false;
+    }
+    const int worst = std::max({slots_per_lane(nq + 2 * nkv * hd, H, groups), slots_per_lane(H, nq, groups),
+                                slots_per_lane(ffn, H, groups), slots_per_lane(H, ffn, groups)});
+    const int E = (nq + groups - 1) / groups;
+    if (worst > kSlots || groups * (E + 4) > kCombMax) {
+        set_error("persistent decode: %d workgroups are too few for these shapes", groups);
+        return false;
+    }
+    int dev = 0, cus = 0, occ = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice") ||
+        !hip_ok(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count") ||
+        !hip_ok(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, kThreads, 0), "occupancy"))
+        return false;
+    if (occ * cus < groups) {
+        set_error("persistent decode: %d workgroups cannot be co-resident (%d per CU x %d CUs)", groups, occ, cus);
+        return false;
+    }
+    return true;
+}
+
+int dec_persist(int dt, const PersistArgs &a, int groups, hipStream_t s) {
+    const PersistKernel k = kernel_for(dt, a.nh, a.hd);
+    if (!k) {
+        set_error("persistent decode: shape not instantiated");
+        return -1;
+    }
+    PersistArgs args = a;
+    void *params[] = {&args};
+    return hip_ok(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k), dim3(groups), dim3(kThreads), params,
+                                             0, s),
+                  "persistent decode launch")
+               ? 0
+               : -1;
+}
+
+}  // namespace sapphire

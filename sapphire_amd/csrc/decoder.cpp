@@ -6,7 +6,9 @@
 // replayed: embedding of the token in device memory, 18 x (QKV GEMV, attention, o-proj,
 // gate/up GEMV, down GEMV), final norm, LM head with its argmax epilogue writing the next
 // token, and a one-thread kernel that logs the token and advances the position. The host
-// only launches the graph; nothing crosses PCIe between steps.
+// only launches the graph; nothing crosses PCIe between steps. By default the layers of the
+// step run as one persistent cooperative kernel (decode_persist.hip) instead of six launches
+// per layer; sapphire_decoder_set_workgroups selects either form.
 //
 // A batched decoder (sapphire_decoder_create_batch) runs 2..16 sequences in lock step, each
 // with its own KV cache and position. Its projections are TILED matrices multiplied on the
@@ -17,6 +19,7 @@
 // argmax and the advance.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -44,7 +47,9 @@ struct sapphire_decoder {
     sapphire_decoder_config_t cfg{};
     int device = 0;
     hipStream_t stream = nullptr;
-    std::vector<void *> allocs;
+    std::vector<void *> allocs;  // the arena's chunks
+    char *arena_cur = nullptr;
+    size_t arena_left = 0;
     std::vector<Layer> layers;
     const uint16_t *embed = nullptr;
     const float *norm_final = nullptr;
@@ -66,14 +71,39 @@ struct sapphire_decoder {
     float *dout = nullptr;       // their sum [B][hidden]
     float *amax_part = nullptr;  // argmax partials
     void *gws = nullptr;         // GEMM workspace
+    // persistent step (one sequence): workgroups (0: the multi-launch step), the layer
+    // descriptors in device memory, the tagged exchange buffers, the epoch counter, the
+    // wait-timeout counter and the steps run since the epochs were last reset
+    int groups = 0;
+    PLayer *players = nullptr;
+    float *tbuf = nullptr;       // exchange vectors, then the epoch flags
+    size_t tbuf_words = 0;
+    uint32_t *seq = nullptr;
+    int *perr = nullptr;
+    uint64_t persist_steps = 0;
 };
 
 namespace {
 
+// Device buffers are carved from large chunks (256-byte aligned pieces): a few big
+// allocations instead of one per weight matrix and buffer.
+constexpr size_t kArenaChunk = size_t(256) << 20;
+
 bool dev_alloc(sapphire_decoder *d, void **p, size_t bytes, const char *what) {
     *p = nullptr;
-    if (!hip_ok(hipMalloc(p, bytes ? bytes : 1), what)) return false;
-    d->allocs.push_back(*p);
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes == 0) bytes = 256;
+    if (bytes > d->arena_left) {
+        const size_t chunk = std::max(bytes, kArenaChunk);
+        void *c = nullptr;
+        if (!hip_ok(hipMalloc(&c, chunk), what)) return false;
+        d->allocs.push_back(c);
+        d->arena_cur = static_cast<char *>(c);
+        d->arena_left = chunk;
+    }
+    *p = d->arena_cur;
+    d->arena_cur += bytes;
+    d->arena_left -= bytes;
     return true;
 }
 
@@ -194,6 +224,26 @@ bool layer_is_global(const sapphire_decoder_config_t &c, int l) {   // attention
     return ((l + 1) % 6) == 0;
 }
 
+// A persistent-step wait longer than this many polls (about a second) is a failure.
+constexpr int kPersistSpinLimit = 1 << 19;
+
+// LM head on d->xfin with the greedy token into d->state[0], then the advance.
+int enqueue_lm_head(sapphire_decoder *d) {
+    const auto &c = d->cfg;
+    hipStream_t s = d->stream;
+    const int H = c.hidden;
+    if (d->lm_layout == LAYOUT_TILED) {
+        if (launch_gemv_tiled_softmax(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, nullptr, d->state,
+                                      d->lm_scratch, s) != 0)
+            return -1;
+    } else {
+        if (launch_gemv_q(c.lm_dtype, LAYOUT_PACKED, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
+        if (launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
+            return -1;
+    }
+    return dec_advance(d->state, d->state + 1, d->state + 2, d->log, d->groups > 0 ? d->seq : nullptr, s);
+}
+
 // One decode step, enqueued on d->stream (recorded into the graph).
 int enqueue_step(sapphire_decoder *d) {
     const auto &c = d->cfg;
@@ -202,6 +252,38 @@ int enqueue_step(sapphire_decoder *d) {
     const float es = sqrtf((float)H);
     const float scale = 1.0f / sqrtf(c.query_pre_attn_scalar > 0.f ? c.query_pre_attn_scalar : (float)hd);
     const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
+    if (d->groups > 0) {
+        PersistArgs pa;
+        pa.layers = d->players;
+        pa.n_layers = c.n_layers;
+        pa.embed = d->embed;
+        pa.vocab = c.vocab;
+        pa.es = es;
+        pa.norm_final = d->norm_final;
+        pa.H = H;
+        pa.nh = c.n_heads;
+        pa.nkv = c.n_kv_heads;
+        pa.hd = hd;
+        pa.ffn = c.ffn;
+        pa.max_ctx = c.max_ctx;
+        pa.scale = scale;
+        pa.eps = c.eps;
+        pa.state = d->state;
+        pa.seq = d->seq;
+        const size_t nqkv = (size_t)(c.n_heads + 2 * c.n_kv_heads) * hd;
+        pa.t_qkv = d->tbuf;
+        pa.t_part = pa.t_qkv + nqkv;
+        pa.t_attn = pa.t_part + (size_t)kPersistMaxGroups * c.n_heads * (hd + 2);
+        pa.t_o = pa.t_attn + (size_t)c.n_heads * hd;
+        pa.t_g = pa.t_o + H;
+        pa.t_dn = pa.t_g + c.ffn;
+        pa.flags = reinterpret_cast<uint32_t *>(pa.t_dn + H);
+        pa.xfin = d->xfin;
+        pa.err = d->perr;
+        pa.spin_limit = kPersistSpinLimit;
+        if (dec_persist(c.wdtype, pa, d->groups, s) != 0) return -1;
+        return enqueue_lm_head(d);
+    }
     if (dec_embed(d->embed, H, c.vocab, es, d->state, d->resid[0], s) != 0) return -1;
     int cur = 0;
     const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
@@ -262,16 +344,7 @@ int enqueue_step(sapphire_decoder *d) {
     fin.w_norm = d->norm_final;
     fin.eps = c.eps;
     if (dec_prologue_only(fin, H, d->xfin, s) != 0) return -1;
-    if (d->lm_layout == LAYOUT_TILED) {
-        if (launch_gemv_tiled_softmax(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, nullptr, d->state,
-                                      d->lm_scratch, s) != 0)
-            return -1;
-    } else {
-        if (launch_gemv_q(c.lm_dtype, LAYOUT_PACKED, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
-        if (launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
-            return -1;
-    }
-    return dec_advance(d->state, d->state + 1, d->state + 2, d->log, s);
+    return enqueue_lm_head(d);
 }
 
 // One step of the batched decoder, enqueued on d->stream (recorded into the graph).
@@ -448,6 +521,8 @@ bool valid_batch_config(const sapphire_decoder_config_t &c, int batch) {
     return true;
 }
 
+bool setup_persistent(sapphire_decoder *d);
+
 sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const sapphire_decoder_weights_t *w,
                                    int batch) {
     if (!cfg || !w) {
@@ -577,9 +652,54 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
             !dev_alloc(d, &d->gws, wsb, "gemm workspace"))
             return fail();
     }
+    if (B == 1 && !setup_persistent(d)) return fail();
     // the zero fills above run on the null stream; the decoder's stream does not wait for it
     if (!hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize")) return fail();
     return d;
+}
+
+// Workgroups of the persistent step unless SAPPHIRE_DECODE_WORKGROUPS says otherwise.
+constexpr int kDefaultGroups = 128;
+
+// Device resources of the persistent step (one sequence) and its default workgroup count:
+// kDefaultGroups when the shapes and the device allow it, else 0 (the multi-launch step).
+bool setup_persistent(sapphire_decoder *d) {
+    const auto &c = d->cfg;
+    const int hd = c.head_dim, win = c.sliding_window > 0 ? c.sliding_window : 1024;
+    const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
+    std::vector<PLayer> pl((size_t)c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer &L = d->layers[l];
+        PLayer &P = pl[l];
+        P.qkv = L.qkv;
+        P.o = L.o;
+        P.gate = L.gate;
+        P.up = L.up;
+        P.down = L.down;
+        P.n_attn = L.n_attn;
+        P.n_attn_post = L.n_attn_post;
+        P.n_ffn = L.n_ffn;
+        P.n_ffn_post = L.n_ffn_post;
+        P.qn = L.qn;
+        P.kn = L.kn;
+        P.cos_t = L.global ? d->cos_g : d->cos_l;
+        P.sin_t = L.global ? d->sin_g : d->sin_l;
+        P.kc = d->kc + (size_t)l * layer_kv;
+        P.vc = d->vc + (size_t)l * layer_kv;
+        P.window = L.global ? 0 : win;
+    }
+    d->tbuf_words = persist_words(c.hidden, c.n_heads, c.n_kv_heads, hd, c.ffn);
+    if (!dev_alloc_t(d, &d->players, pl.size(), "layer descriptors") ||
+        !hip_ok(hipMemcpy(d->players, pl.data(), sizeof(PLayer) * pl.size(), hipMemcpyHostToDevice), "descriptors") ||
+        !dev_alloc_t(d, &d->tbuf, d->tbuf_words, "exchange buffers") ||
+        !hip_ok(hipMemset(d->tbuf, 0, d->tbuf_words * sizeof(float)), "exchange zero") ||
+        !dev_alloc_t(d, &d->seq, 1, "epoch counter") || !hip_ok(hipMemset(d->seq, 0, sizeof(uint32_t)), "epoch zero") ||
+        !dev_alloc_t(d, &d->perr, 1, "timeout counter") || !hip_ok(hipMemset(d->perr, 0, sizeof(int)), "timeout zero"))
+        return false;
+    int g = kDefaultGroups;
+    if (const char *e = getenv("SAPPHIRE_DECODE_WORKGROUPS")) g = atoi(e);
+    d->groups = g > 0 && persist_supported(c.wdtype, g, c.hidden, c.n_heads, c.n_kv_heads, hd, c.ffn) ? g : 0;
+    return true;
 }
 
 size_t seq_kv_floats(const sapphire_decoder_config_t &c) {
@@ -687,6 +807,17 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         }
     }
     SPH_CHECK(hipMemcpy(d->state, st.data(), sizeof(int) * st.size(), hipMemcpyHostToDevice));
+    if (d->groups > 0) {
+        // epochs must stay below 2^32: start them over (and clear every flag) before they would wrap
+        const uint64_t per = persist_epochs_per_step(c.n_layers);
+        if ((d->persist_steps + (uint64_t)steps + 1) * per > 0xFFFFFFFFull) {
+            SPH_CHECK(hipMemsetAsync(d->tbuf, 0, d->tbuf_words * sizeof(float), d->stream));
+            SPH_CHECK(hipMemsetAsync(d->seq, 0, sizeof(uint32_t), d->stream));
+            d->persist_steps = 0;
+        }
+        SPH_CHECK(hipMemsetAsync(d->perr, 0, sizeof(int), d->stream));
+        d->persist_steps += (uint64_t)steps;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (elapsed_ms) {
         SPH_CHECK(hipEventCreate(&e0));
@@ -707,9 +838,43 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         (void)hipEventDestroy(e0);
         (void)hipEventDestroy(e1);
     }
+    if (d->groups > 0) {
+        int timeouts = 0;
+        SPH_CHECK(hipMemcpy(&timeouts, d->perr, sizeof(int), hipMemcpyDeviceToHost));
+        if (timeouts) {
+            set_error("sapphire_decoder_generate: %d persistent-step waits timed out; results are invalid", timeouts);
+            return -1;
+        }
+    }
     SPH_CHECK(hipMemcpy(tokens_out, d->log, sizeof(int) * (size_t)steps * B, hipMemcpyDeviceToHost));
     return 0;
 }
+
+int sapphire_decoder_set_workgroups(sapphire_decoder_t *d, int groups) {
+    if (!d || groups < 0) {
+        set_error("sapphire_decoder_set_workgroups: bad arguments");
+        return -1;
+    }
+    if (groups > 0) {
+        const auto &c = d->cfg;
+        if (d->batch != 1) {
+            set_error("sapphire_decoder_set_workgroups: the persistent step decodes one sequence");
+            return -1;
+        }
+        SPH_CHECK(hipSetDevice(d->device));
+        if (!persist_supported(c.wdtype, groups, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn)) return -1;
+    }
+    if (groups == d->groups) return 0;
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    d->exec = nullptr;
+    d->graph = nullptr;
+    d->groups = groups;
+    return 0;
+}
+
+int sapphire_decoder_workgroups(const sapphire_decoder_t *d) { return d ? d->groups : -1; }
 
 int sapphire_decoder_generate(sapphire_decoder_t *d, int token, int pos, int steps, int *tokens_out, float *logits_out,
                               float *elapsed_ms) {

@@ -52,6 +52,10 @@ def _protos(L):
     for n in ("sapphire_decoder_set_kv_seq", "sapphire_decoder_get_kv_seq"):
         getattr(L, n).restype = C.c_int
         getattr(L, n).argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+    L.sapphire_decoder_set_workgroups.restype = C.c_int
+    L.sapphire_decoder_set_workgroups.argtypes = [C.c_void_p, C.c_int]
+    L.sapphire_decoder_workgroups.restype = C.c_int
+    L.sapphire_decoder_workgroups.argtypes = [C.c_void_p]
     L.sapphire_decoder_generate_batch.restype = C.c_int
     L.sapphire_decoder_generate_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                                                   C.c_void_p, C.POINTER(C.c_float)]
@@ -123,6 +127,14 @@ class Decoder:
                     "get_kv_seq")
         return k, v
 
+    @property
+    def workgroups(self) -> int:
+        """Workgroups of the persistent step; 0 = the multi-launch step."""
+        return int(self.lib.sapphire_decoder_workgroups(self.ptr))
+
+    def set_workgroups(self, groups: int) -> None:
+        self._check(self.lib.sapphire_decoder_set_workgroups(self.ptr, int(groups)), "set_workgroups")
+
     def generate_batch(self, tokens, pos, steps: int, keep_logits: bool = False):
         """(tokens[steps, batch], logits[steps, batch, vocab] or None, device milliseconds)."""
         tk = np.ascontiguousarray(tokens, np.int32)
@@ -159,15 +171,20 @@ class Decoder:
             pass
 
 
-def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, reps: int = 3, m=None, kv=None):
+def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, reps: int = 3, m=None, kv=None,
+                 groups=None):
     """Greedy decode of the Gemma-3-270M-shaped Q4_0 model (KV prefilled to `prefill` of
     2048 positions): tokens/s over `steps` steps, best of `reps` runs after a warm-up.
-    `m` / `kv` reuse an already generated model and prefilled caches."""
+    `m` / `kv` reuse an already generated model and prefilled caches. `groups`: workgroups of
+    the persistent step (0: the multi-launch step; None: the decoder's default)."""
     cfg = smodel.GEMMA3_270M
     if m is None:
         m = smodel.synthetic_model(cfg, seed)
     k, v = kv if kv is not None else m.kv_prefill(prefill)
     dec = Decoder(m)
+    if groups is not None:
+        dec.set_workgroups(groups)
+    groups = dec.workgroups
     tok = smodel.start_token(cfg, seed)
     dec.set_kv(k, v)
     dec.generate(tok, prefill, steps)                 # graph capture + warm-up
@@ -183,6 +200,7 @@ def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, rep
         "steps": steps, "kv_prefill": prefill, "ms_total": round(best, 3), "ms_per_token": round(best / steps, 4),
         "tok_per_s": round(steps / (best * 1e-3), 1), "first_tokens": [int(t) for t in toks[:8]],
         "weight_bytes_per_token": layer_bytes + int(m.lm_head.nbytes),
+        "step_form": f"persistent, {groups} workgroups" if groups else "multi-launch graph",
     }
 
 

@@ -36,18 +36,32 @@ MID = smodel.DecodeConfig(n_layers=6, hidden=256, n_heads=4, n_kv_heads=1, head_
 TINY_Q8 = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "wdtype": synth.Q8_0, "lm_dtype": synth.Q8_0})
 
 
-@pytest.mark.parametrize("cfg,seed,prefill,steps", [
-    (smodel.TINY, 31, 40, 16),        # window 24 < positions: local layers slide
-    (TINY_Q8, 32, 10, 12),            # Q8_0 weights, positions inside the window
-    (MID, 33, 40, 24),                # head_dim 128, crosses the 48-position window while decoding
-], ids=["tiny", "tiny_q8", "mid_window"])
-def test_decode_matches_oracle(oracle, cfg, seed, prefill, steps):
+# groups: workgroups of the persistent step (None: the decoder's default), 0: the multi-launch step
+@pytest.mark.parametrize("cfg,seed,prefill,steps,groups", [
+    (smodel.TINY, 31, 40, 16, None),      # window 24 < positions: local layers slide
+    (smodel.TINY, 31, 40, 16, 0),
+    (smodel.TINY, 31, 40, 16, 16),        # fewer workgroups than positions: several per slice
+    (smodel.TINY, 31, 40, 16, 256),       # more workgroups than positions: empty slices
+    (TINY_Q8, 32, 10, 12, None),          # Q8_0 weights, positions inside the window
+    (TINY_Q8, 32, 10, 12, 0),
+    (MID, 33, 40, 24, None),              # head_dim 128, crosses the 48-position window while decoding
+    (MID, 33, 40, 24, 0),
+    (MID, 33, 40, 24, 96),
+], ids=["tiny", "tiny_graph", "tiny_g16", "tiny_g256", "tiny_q8", "tiny_q8_graph", "mid_window", "mid_window_graph",
+        "mid_window_g96"])
+def test_decode_matches_oracle(oracle, cfg, seed, prefill, steps, groups):
     from sapphire_amd.engine import Decoder
-    print(f"decode cfg={cfg.n_layers}x{cfg.hidden} seed={seed} prefill={prefill} steps={steps}", flush=True)
+    print(f"decode cfg={cfg.n_layers}x{cfg.hidden} seed={seed} prefill={prefill} steps={steps} groups={groups}",
+          flush=True)
     m = smodel.synthetic_model(cfg, seed)
     k, v = m.kv_prefill(prefill)
     tok = smodel.start_token(cfg, seed)
     dec = Decoder(m)
+    if groups is None:
+        assert dec.workgroups > 0, "the persistent step is the default"
+    else:
+        dec.set_workgroups(groups)
+        assert dec.workgroups == groups
     dec.set_kv(k, v)
     got_toks, got_logits, _ = dec.generate(tok, prefill, steps, keep_logits=True)
     gk, gv = dec.get_kv()
@@ -65,7 +79,8 @@ def test_decode_matches_oracle(oracle, cfg, seed, prefill, steps):
 
 def test_decode_gemma3_270m_64_steps(oracle):
     """The Gemma-3-270M-shaped Q4_0 model, KV prefilled to 1024 of 2048 positions, 64
-    greedy steps: identical tokens, logits within 2e-3 on every step."""
+    greedy steps: identical tokens, logits within 2e-3 on every step, for the persistent step
+    at 128 (the default), 64 and 256 workgroups and for the multi-launch step."""
     from sapphire_amd.engine import Decoder
     cfg, seed, prefill, steps = smodel.GEMMA3_270M, 20260101, 1024, 64
     print("decode gemma3-270m 64 steps", flush=True)
@@ -73,13 +88,59 @@ def test_decode_gemma3_270m_64_steps(oracle):
     k, v = m.kv_prefill(prefill)
     tok = smodel.start_token(cfg, seed)
     dec = Decoder(m)
-    dec.set_kv(k, v)
-    got_toks, got_logits, _ = dec.generate(tok, prefill, steps, keep_logits=True)
+    assert dec.workgroups == 128
+    runs = {}
+    for groups in (128, 64, 256, 0):
+        dec.set_workgroups(groups)
+        dec.set_kv(k, v)
+        runs[groups] = dec.generate(tok, prefill, steps, keep_logits=True)[:2]
+        print(f"gpu done: groups={groups}", flush=True)
     dec.close()
-    print("gpu done; oracle", flush=True)
     ref_toks, ref_logits = oracle_decode(oracle, m, k, v, tok, prefill, steps, nthreads=16, keep_logits=True)
-    n = _compare(ref_toks, ref_logits, got_toks, got_logits)
-    assert n == steps, f"near-tie at step {n}: tokens agree on steps 0..{n - 1}"
+    for groups, (got_toks, got_logits) in runs.items():
+        n = _compare(ref_toks, ref_logits, got_toks, got_logits)
+        assert n == steps, f"groups={groups}: near-tie at step {n}: tokens agree on steps 0..{n - 1}"
+
+
+def test_decode_workgroups_validation():
+    """sapphire_decoder_set_workgroups keeps the current form when the count cannot run."""
+    from sapphire_amd.engine import Decoder
+    m = smodel.synthetic_model(smodel.TINY, 35)
+    dec = Decoder(m)
+    try:
+        g0 = dec.workgroups
+        for bad in (-1, 2, 257):          # negative, fewer than the query heads, above the maximum
+            with pytest.raises(RuntimeError):
+                dec.set_workgroups(bad)
+            assert dec.workgroups == g0
+    finally:
+        dec.close()
+    bdec = Decoder(m, batch=2)
+    try:
+        assert bdec.workgroups == 0
+        with pytest.raises(RuntimeError):
+            bdec.set_workgroups(64)
+    finally:
+        bdec.close()
+
+
+def test_decode_persistent_epochs_across_calls(oracle):
+    """Many short generate calls on one decoder: every call's steps get fresh epochs, so no stage
+    reads a vector left by an earlier step; each call matches the oracle from the same state."""
+    from sapphire_amd.engine import Decoder
+    cfg = smodel.TINY
+    m = smodel.synthetic_model(cfg, 36)
+    k, v = m.kv_prefill(30)
+    tok = smodel.start_token(cfg, 36)
+    ref_toks, _ = oracle_decode(oracle, m, k.copy(), v.copy(), tok, 30, 3, nthreads=4)
+    dec = Decoder(m)
+    try:
+        for _ in range(20):
+            dec.set_kv(k, v)
+            got, _, _ = dec.generate(tok, 30, 3)
+            assert list(got) == list(ref_toks)
+    finally:
+        dec.close()
 
 
 def test_decode_repeatable(oracle):
