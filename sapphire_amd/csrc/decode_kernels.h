@@ -77,8 +77,8 @@ struct PLayer {
     int window;                      // sliding window, 0 for a global layer
 };
 
-// Exchanged vectors are fp32 arrays in device memory; flags[G] holds the last stage epoch each
-// workgroup has completed (see decode_persist.hip).
+// Exchanged vectors are 64-bit words: fp32 value in the low half, the producing stage's
+// epoch in the high half (see decode_persist.hip).
 struct PersistArgs {
     const PLayer *layers = nullptr;
     int n_layers = 0;
@@ -90,17 +90,15 @@ struct PersistArgs {
     float scale = 1.f, eps = 1e-6f;
     const int *state = nullptr;       // [0] token, [1] position
     const uint32_t *seq = nullptr;    // step counter that makes the epochs unique
-    float *t_qkv = nullptr, *t_part = nullptr, *t_attn = nullptr, *t_o = nullptr, *t_g = nullptr,
-          *t_dn = nullptr;
-    uint32_t *flags = nullptr;
+    uint64_t *t_qkv = nullptr, *t_part = nullptr, *t_attn = nullptr, *t_o = nullptr, *t_g = nullptr,
+             *t_dn = nullptr;
     float *xfin = nullptr;            // [H] final-norm output (the LM-head input)
     int *err = nullptr;               // incremented by a workgroup whose wait timed out
     int spin_limit = 0;
 };
 constexpr int kPersistMaxGroups = 256;
-// 4-byte words of the exchange buffers for a model shape, contiguous in this order: the fp32
-// vectors qkv, partials for kPersistMaxGroups workgroups, attention output, o, g, down, then
-// the kPersistMaxGroups uint32 epoch flags.
+// 64-bit words of the tagged exchange buffers for a model shape (all six, contiguous in this
+// order: qkv, partials for kPersistMaxGroups workgroups, attention output, o, g, down).
 size_t persist_words(int H, int nh, int nkv, int hd, int ffn);
 // Whether `groups` workgroups can run the persistent step for these shapes on the current
 // device (co-residency included); sets the error message when not.

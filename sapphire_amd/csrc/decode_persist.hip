@@ -5,14 +5,13 @@
 // cooperative grid of G workgroups (all co-resident) runs every layer, and the stages are
 // separated by data instead:
 //
-// * Exchanged vectors are fp32 arrays stored and loaded with agent-scope atomics, which are
-//   coherent across the L2 caches of the eight XCDs.
-// * A workgroup ends a stage by waiting for its stores' acknowledgements and then publishing
-//   the stage's epoch in its own flag word. A consumer's first wave polls one flag per
-//   workgroup until all have reached the epoch it needs, then every thread reads its inputs
-//   once. Only one wave per workgroup polls, so waiting adds little memory traffic. A
-//   workgroup's weight and KV-cache loads for its next stage are issued before that wait, so
-//   their latency hides behind it.
+// * Every exchanged vector element is one 64-bit word: the fp32 value in the low half and the
+//   epoch of the stage that produced it in the high half. Words are stored and loaded with
+//   agent-scope atomics, which are coherent across the L2 caches of the eight XCDs.
+// * A consumer polls exactly the words it needs until every tag equals the producer's epoch:
+//   the poll is the data load, and no store acknowledgement is waited for. A workgroup's weight
+//   and KV-cache loads for its next stage are issued before that wait, so their latency hides
+//   behind it.
 // * Every workgroup keeps its own copy of the residual stream in LDS. It is updated by the same
 //   instructions from the same inputs, so the copies are bit-identical.
 //
@@ -42,12 +41,13 @@ constexpr int kSlots = 4;                         // (wave-step, block) slots pe
 constexpr int kCombMax = 4096;                    // gathered partial words per workgroup in the combine
 constexpr int kVecRegs = kDecMaxK / kThreads;     // vector elements per thread
 
-__device__ __forceinline__ void put_shared(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void put_tagged(uint64_t *p, float v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float get_shared(const float *p) {
+__device__ __forceinline__ uint64_t get_tagged(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ bool tag_is(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 
 template <int NH, int DPL>
 struct alignas(16) PersistLds {
@@ -67,61 +67,49 @@ struct alignas(16) PersistLds {
     int flag;
 };
 
-// The end of a stage: every wave waits for the acknowledgements of its exchange stores (they
-// are then visible at device scope), then thread 0 publishes the stage's epoch in the
-// workgroup's flag.
-__device__ __forceinline__ void signal(uint32_t *flags, uint32_t ep) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(flags + blockIdx.x, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Waits until every workgroup's flag has reached epoch ep (epochs only grow within a step
-// sequence): wave 0 polls one flag per workgroup and lane. Returns false (and counts the
-// failure in *err) when a flag is still behind after spin_limit polls. Synchronises the
-// workgroup; the result is the same in every thread.
-__device__ __forceinline__ bool wait_all(const uint32_t *flags, uint32_t ep, int spin_limit, int *err, int *bail) {
-    if (threadIdx.x < kWave) {
-        const int G = gridDim.x;
-        for (int spins = 0;; ++spins) {
-            bool ok = true;
-            for (int i = threadIdx.x; i < G; i += kWave)
-                ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= ep;
-            if (__all(ok)) break;
-            if (spins >= spin_limit) {
-                if (threadIdx.x == 0) *bail = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+// dst[j] = value of word *src(j) for j < n, once its tag equals `tag`; thread t takes
+// j = t + 256 e. All loads are issued first, then only stale words are polled again. Returns
+// false when a word is still stale after spin_limit polls (and counts the failure in *err).
+// Synchronises the workgroup; the result is the same in every thread.
+template <int MAXE, class Src>
+__device__ __forceinline__ bool gather(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
+                                       int *flag) {
+    uint64_t w[MAXE];
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+        const int j = threadIdx.x + e * kThreads;
+        w[e] = j < n ? get_tagged(src(j)) : (uint64_t)tag << 32;
+    }
+    for (int spins = 0;; ++spins) {
+        bool ready = true;
+#pragma unroll
+        for (int e = 0; e < MAXE; ++e) ready = ready && tag_is(w[e], tag);
+        if (ready) break;
+        if (spins >= spin_limit) {
+            *flag = 1;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int e = 0; e < MAXE; ++e) {
+            const int j = threadIdx.x + e * kThreads;
+            if (j < n && !tag_is(w[e], tag)) w[e] = get_tagged(src(j));
         }
     }
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+        const int j = threadIdx.x + e * kThreads;
+        if (j < n) dst[j] = __uint_as_float((uint32_t)w[e]);
+    }
     __syncthreads();
-    const bool ok = *bail == 0;
+    const bool ok = *flag == 0;
     if (!ok && threadIdx.x == 0) atomicAdd(err, 1);
     return ok;
 }
 
-// dst[j] = *src(j) for j < n (device-scope loads, all issued before any is used); thread t
-// takes j = t + 256 e. Synchronises the workgroup.
-template <int MAXE, class Src>
-__device__ __forceinline__ void load_shared(Src src, int n, float *dst) {
-    float v[MAXE];
-#pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-        const int j = threadIdx.x + e * kThreads;
-        v[e] = j < n ? get_shared(src(j)) : 0.f;
-    }
-#pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-        const int j = threadIdx.x + e * kThreads;
-        if (j < n) dst[j] = v[e];
-    }
-    __syncthreads();
-}
-
 struct Contig {
-    const float *p;
-    __device__ const float *operator()(int j) const { return p + j; }
+    const uint64_t *p;
+    __device__ const uint64_t *operator()(int j) const { return p + j; }
 };
 
 // Elements t + 256 e of a K-long weight vector in registers (loaded before a wait).
@@ -207,9 +195,9 @@ struct GemvStage {
         }
     }
 
-    // y[row] = W0[row] . xs, or gelu(W0[row] . xs) * (W1[row] . xs) for the GeGLU form. The
-    // stage's signal() follows (its barrier also ends the reads of xs).
-    __device__ __forceinline__ void finish(const float *xs, float *y) {
+    // y[row] (tagged) = W0[row] . xs, or gelu(W0[row] . xs) * (W1[row] . xs) for the GeGLU form.
+    // Ends with a workgroup barrier, after which xs may be overwritten.
+    __device__ __forceinline__ void finish(const float *xs, uint64_t *y, uint32_t tag) {
         const int wid = threadIdx.x / kWave;
         float p0 = 0.f, p1 = 0.f;
 #pragma unroll
@@ -243,7 +231,7 @@ struct GemvStage {
                     p0 = row16_sum(p0);
                     if constexpr (GEGLU) p1 = row16_sum(p1);
                     const int row = st * kRpw + rin;
-                    if (q == 0 && row < M) put_shared(y + row, GEGLU ? __fmul_rn(gelu_ref(p0), p1) : p0);
+                    if (q == 0 && row < M) put_tagged(y + row, GEGLU ? __fmul_rn(gelu_ref(p0), p1) : p0, tag);
                     p0 = 0.f;
                     p1 = 0.f;
                 }
@@ -251,6 +239,7 @@ struct GemvStage {
             // one slot's 32 x values live at a time
             __builtin_amdgcn_sched_barrier(0);
         }
+        __syncthreads();
     }
 };
 
@@ -259,8 +248,8 @@ struct GemvStage {
 // dec_attn_part_kernel with one slice per workgroup. The gammas, RoPE rows and the first K/V rows of the slice are
 // loaded before the wait for q, k, v; scores are summed by DPP into wave-uniform values.
 template <int DPL, int NH>
-__device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L, int pos, uint32_t ep_in,
-                                           PersistLds<NH, DPL> &s) {
+__device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L, int pos, uint32_t tag_in,
+                                           uint32_t tag_out, PersistLds<NH, DPL> &s) {
     const int hd = a.hd, half = hd / 2;
     constexpr int nkv = 1;
     const int seq = pos + 1;
@@ -304,8 +293,9 @@ __device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L
         sn[e] = ok ? L.sin_t[(size_t)pos * hd + i] : 0.f;
     }
 
-    if (!wait_all(a.flags, ep_in, a.spin_limit, a.err, &s.flag)) return false;
-    load_shared<(kAttnMaxQ + 2 * kAttnMaxKV) / kThreads>(Contig{a.t_qkv}, (NH + 2 * nkv) * hd, s.raw);
+    if (!gather<(kAttnMaxQ + 2 * kAttnMaxKV) / kThreads>(Contig{a.t_qkv}, (NH + 2 * nkv) * hd, tag_in, s.raw,
+                                                          a.spin_limit, a.err, &s.flag))
+        return false;
     // rmsnorm_delta of every q and k head vector, then the half-split rotation
     {   // sum of squares of each head vector: 16-lane row v takes vector v (tree order)
         const int v = threadIdx.x / 16, q16 = threadIdx.x & 15;
@@ -411,15 +401,15 @@ __device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L
         s.wtot[h] = S;
     }
     __syncthreads();
-    float *out = a.t_part + (size_t)blockIdx.x * NH * (hd + 2);
+    uint64_t *out = a.t_part + (size_t)blockIdx.x * NH * (hd + 2);
     for (int idx = threadIdx.x; idx < NH * hd; idx += kThreads) {
         const int h = idx / hd, d = idx - h * hd;
         float O = 0.f;
         for (int w = 0; w < NW; ++w) O = __builtin_fmaf(s.wo[w][h][d], s.wx[w][h], O);
-        put_shared(out + h * (hd + 2) + d, O);
+        put_tagged(out + h * (hd + 2) + d, O, tag_out);
         if (d == 0) {
-            put_shared(out + h * (hd + 2) + hd, s.wmax[h]);
-            put_shared(out + h * (hd + 2) + hd + 1, s.wtot[h]);
+            put_tagged(out + h * (hd + 2) + hd, s.wmax[h], tag_out);
+            put_tagged(out + h * (hd + 2) + hd + 1, s.wtot[h], tag_out);
         }
     }
     return true;
@@ -429,16 +419,16 @@ __device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L
 // out = sum_b e_b o_b / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) over every workgroup's
 // partial b (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes.
 template <int NH, int DPL>
-__device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t ep_in, PersistLds<NH, DPL> &s) {
+__device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag_in, uint32_t tag_out,
+                                              PersistLds<NH, DPL> &s) {
     const int hd = a.hd, nq = NH * hd, G = gridDim.x;
     const int E = (nq + G - 1) / G;
     const int e0 = min(nq, (int)blockIdx.x * E), e1 = min(nq, e0 + E);
-    if (!wait_all(a.flags, ep_in, a.spin_limit, a.err, &s.flag)) return false;
     if (e0 >= e1) return true;
     const int h_lo = e0 / hd, h_hi = (e1 - 1) / hd;   // E <= hd: at most two heads
     const int per = E + 4;                            // E values, then (m, s) of h_lo and h_hi
-    const float *part = a.t_part;
-    auto src = [=](int j) -> const float * {
+    const uint64_t *part = a.t_part;
+    auto src = [=](int j) -> const uint64_t * {
         const int b = j / per, k = j - b * per;
         size_t off;
         if (k < E) {
@@ -450,7 +440,7 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t ep_
         }
         return part + off;
     };
-    load_shared<kCombMax / kThreads>(src, G * per, s.comb);
+    if (!gather<kCombMax / kThreads>(src, G * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag)) return false;
     // 16-lane row r takes elements k = r, r + 16, ...; lane q of the row takes partials
     // b = q, q + 16, ...; max, weights and sums are reduced over the row by DPP
     const int q = threadIdx.x & 15;
@@ -468,8 +458,9 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t ep_
         }
         S = row16_sum(S);
         O = row16_sum(O);
-        if (q == 0) put_shared(a.t_attn + el, O * (1.0f / S));
+        if (q == 0) put_tagged(a.t_attn + el, O * (1.0f / S), tag_out);
     }
+    __syncthreads();
     return true;
 }
 
@@ -502,25 +493,19 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             if (l > 0) {
                 VecRegs wd;
                 wd.load(a.layers[l - 1].n_ffn_post, H);
-                if (!wait_all(a.flags, ep - 2, a.spin_limit, a.err, &s.flag)) return;
-                load_shared<kVecRegs>(Contig{a.t_dn}, H, s.dl);
+                if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag)) return;
                 add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
             }
             norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
-            g.finish(s.xs, a.t_qkv);
-            signal(a.flags, ep + 1);
+            g.finish(s.xs, a.t_qkv, ep + 1);
         }
-        if (!attn_stage<DPL, NH>(a, L, pos, ep + 1, s)) return;
-        signal(a.flags, ep + 2);
-        if (!combine_stage<NH, DPL>(a, ep + 2, s)) return;
-        signal(a.flags, ep + 3);
+        if (!attn_stage<DPL, NH>(a, L, pos, ep + 1, ep + 2, s)) return;
+        if (!combine_stage<NH, DPL>(a, ep + 2, ep + 3, s)) return;
         {   // 4: o-proj
             GemvStage<DT, false> g;
             g.load(L.o, L.o);
-            if (!wait_all(a.flags, ep + 3, a.spin_limit, a.err, &s.flag)) return;
-            load_shared<kVecRegs>(Contig{a.t_attn}, nq, s.xs);
-            g.finish(s.xs, a.t_o);
-            signal(a.flags, ep + 4);
+            if (!gather<kVecRegs>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
+            g.finish(s.xs, a.t_o, ep + 4);
         }
         {   // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU
             GemvStage<DT, true> g;
@@ -528,20 +513,16 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             VecRegs wd, wn;
             wd.load(L.n_attn_post, H);
             wn.load(L.n_ffn, H);
-            if (!wait_all(a.flags, ep + 4, a.spin_limit, a.err, &s.flag)) return;
-            load_shared<kVecRegs>(Contig{a.t_o}, H, s.dl);
+            if (!gather<kVecRegs>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag)) return;
             add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
             norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
-            g.finish(s.xs, a.t_g);
-            signal(a.flags, ep + 5);
+            g.finish(s.xs, a.t_g, ep + 5);
         }
         {   // 6: down
             GemvStage<DT, false> g;
             g.load(L.down, L.down);
-            if (!wait_all(a.flags, ep + 5, a.spin_limit, a.err, &s.flag)) return;
-            load_shared<kVecRegs>(Contig{a.t_g}, a.ffn, s.xs);
-            g.finish(s.xs, a.t_dn);
-            signal(a.flags, ep + 6);
+            if (!gather<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag)) return;
+            g.finish(s.xs, a.t_dn, ep + 6);
         }
     }
     // last finalize + final norm (transformer.c:400-406)
@@ -549,8 +530,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     wd.load(a.layers[a.n_layers - 1].n_ffn_post, H);
     wn.load(a.norm_final, H);
     const uint32_t ep_last = base + 8u * (uint32_t)(a.n_layers - 1) + 6u;
-    if (!wait_all(a.flags, ep_last, a.spin_limit, a.err, &s.flag)) return;
-    load_shared<kVecRegs>(Contig{a.t_dn}, H, s.dl);
+    if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag)) return;
     add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
     norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
     if (blockIdx.x == 0)
@@ -584,8 +564,7 @@ int slots_per_lane(int M, int K, int groups) {
 }  // namespace
 
 size_t persist_words(int H, int nh, int nkv, int hd, int ffn) {
-    return (size_t)(nh + 2 * nkv) * hd + (size_t)kPersistMaxGroups * nh * (hd + 2) + (size_t)nh * hd + H + ffn + H +
-           kPersistMaxGroups;
+    return (size_t)(nh + 2 * nkv) * hd + (size_t)kPersistMaxGroups * nh * (hd + 2) + (size_t)nh * hd + H + ffn + H;
 }
 
 bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int ffn) {

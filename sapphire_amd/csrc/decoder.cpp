@@ -76,7 +76,7 @@ struct sapphire_decoder {
     // wait-timeout counter and the steps run since the epochs were last reset
     int groups = 0;
     PLayer *players = nullptr;
-    float *tbuf = nullptr;       // exchange vectors, then the epoch flags
+    uint64_t *tbuf = nullptr;    // tagged exchange vectors
     size_t tbuf_words = 0;
     uint32_t *seq = nullptr;
     int *perr = nullptr;
@@ -277,7 +277,6 @@ int enqueue_step(sapphire_decoder *d) {
         pa.t_o = pa.t_attn + (size_t)c.n_heads * hd;
         pa.t_g = pa.t_o + H;
         pa.t_dn = pa.t_g + c.ffn;
-        pa.flags = reinterpret_cast<uint32_t *>(pa.t_dn + H);
         pa.xfin = d->xfin;
         pa.err = d->perr;
         pa.spin_limit = kPersistSpinLimit;
@@ -692,7 +691,7 @@ bool setup_persistent(sapphire_decoder *d) {
     if (!dev_alloc_t(d, &d->players, pl.size(), "layer descriptors") ||
         !hip_ok(hipMemcpy(d->players, pl.data(), sizeof(PLayer) * pl.size(), hipMemcpyHostToDevice), "descriptors") ||
         !dev_alloc_t(d, &d->tbuf, d->tbuf_words, "exchange buffers") ||
-        !hip_ok(hipMemset(d->tbuf, 0, d->tbuf_words * sizeof(float)), "exchange zero") ||
+        !hip_ok(hipMemset(d->tbuf, 0, d->tbuf_words * sizeof(uint64_t)), "exchange zero") ||
         !dev_alloc_t(d, &d->seq, 1, "epoch counter") || !hip_ok(hipMemset(d->seq, 0, sizeof(uint32_t)), "epoch zero") ||
         !dev_alloc_t(d, &d->perr, 1, "timeout counter") || !hip_ok(hipMemset(d->perr, 0, sizeof(int)), "timeout zero"))
         return false;
@@ -808,10 +807,10 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
     }
     SPH_CHECK(hipMemcpy(d->state, st.data(), sizeof(int) * st.size(), hipMemcpyHostToDevice));
     if (d->groups > 0) {
-        // epochs must stay below 2^32: start them over (and clear every flag) before they would wrap
+        // epochs must stay below 2^32: start them over (and clear every tag) before they would wrap
         const uint64_t per = persist_epochs_per_step(c.n_layers);
         if ((d->persist_steps + (uint64_t)steps + 1) * per > 0xFFFFFFFFull) {
-            SPH_CHECK(hipMemsetAsync(d->tbuf, 0, d->tbuf_words * sizeof(float), d->stream));
+            SPH_CHECK(hipMemsetAsync(d->tbuf, 0, d->tbuf_words * sizeof(uint64_t), d->stream));
             SPH_CHECK(hipMemsetAsync(d->seq, 0, sizeof(uint32_t), d->stream));
             d->persist_steps = 0;
         }
