@@ -123,6 +123,78 @@ float oracle_q8_0_row(const void *w_row, const float *x, int block_count, int bl
 }
 
 /* ------------------------------------------------------------------------- */
+/* F32 / BF16 rows (the dtypes the reference loader produces).                  */
+/* ------------------------------------------------------------------------- */
+
+/* A scalar chain acc += w[j] * x[j], j = j0 .. j1-1, as the reference build compiles it: BF16
+ * terms are fused (one FMA each); F32 loops are vectorised four wide, so the first
+ * 4 * floor(n / 4) products are rounded before their in-order additions and the last n % 4
+ * terms are fused. Both forms are pinned against the compiled reference (tests/test_oracle_pin.py). */
+static float f_elem(int dtype, const void *w, int j);
+static float scalar_chain(int dtype, const void *w, const float *x, int j0, int j1, float acc) {
+    const int vec_end = dtype == ORC_F32 ? j0 + (j1 - j0) / 4 * 4 : j0;
+    int j = j0;
+    for (; j < vec_end; ++j) acc = acc + f_elem(dtype, w, j) * x[j];
+    for (; j < j1; ++j) acc = fmaf(f_elem(dtype, w, j), x[j], acc);
+    return acc;
+}
+
+/* element j of an F32 row, or of a BF16 row widened by a 16-bit shift (bf16_avx.c:30-33,
+ * :77-79) */
+static float f_elem(int dtype, const void *w, int j) {
+    if (dtype == ORC_F32) return ((const float *)w)[j];
+    uint32_t b = (uint32_t)((const uint16_t *)w)[j] << 16;
+    float f;
+    memcpy(&f, &b, sizeof f);
+    return f;
+}
+
+/* quantized_gemv_{bf16,f32}_avx2: bf16_avx.c:57-113, f32_avx.c:43-90. Chunks of 32: element
+ * j + 8k + l goes to accumulator k, lane l (FMA); the remainder is one scalar_chain; the
+ * lanes reduce as (a0 + a1) + (a2 + a3), then t0 + ... + t7 + remainder left to right. */
+float oracle_f_row(int dtype, const void *w_row, const float *x, int cols) {
+    if (!w_row || !x) return 0.0f;
+    float acc[4][8];
+    memset(acc, 0, sizeof acc);
+    int j = 0;
+    for (; j + 32 <= cols; j += 32)
+        for (int k = 0; k < 4; ++k)
+            for (int l = 0; l < 8; ++l) acc[k][l] = fmaf(f_elem(dtype, w_row, j + 8 * k + l), x[j + 8 * k + l], acc[k][l]);
+    const float rem = scalar_chain(dtype, w_row, x, j, cols, 0.0f);
+    float t[8];
+    for (int l = 0; l < 8; ++l) t[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+    return t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6] + t[7] + rem;
+}
+
+/* kernel_gemv without a context for F32 / BF16: gemv_f32 / gemv_bf16, dispatch.c:60-85, one
+ * scalar_chain per row. */
+float oracle_f_row_scalar(int dtype, const void *w_row, const float *x, int cols) {
+    return scalar_chain(dtype, w_row, x, 0, cols, 0.0f);
+}
+
+/* kernel_gemm_{bf16,f32}_avx2 (bf16_avx.c:115-159, f32_avx.c): per sequence one accumulator
+ * of eight lanes over chunks of 8, t0 + ... + t7 left to right, then the remainder added as a
+ * scalar_chain. Y[b * ldy + r]. */
+int oracle_gemm_f(int dtype, const void *W, int M, int K, const float *X, int batch, float *Y, int ldy) {
+    if (!W || !X || !Y || M <= 0 || K <= 0 || batch <= 0 || (dtype != ORC_F32 && dtype != ORC_BF16)) return -1;
+    const size_t es = dtype == ORC_F32 ? 4 : 2;
+    for (int r = 0; r < M; ++r) {
+        const void *w = (const unsigned char *)W + (size_t)r * K * es;
+        for (int b = 0; b < batch; ++b) {
+            const float *x = X + (size_t)b * K;
+            float acc[8] = { 0 };
+            int j = 0;
+            for (; j + 8 <= K; j += 8)
+                for (int l = 0; l < 8; ++l) acc[l] = fmaf(f_elem(dtype, w, j + l), x[j + l], acc[l]);
+            float sum = acc[0] + acc[1] + acc[2] + acc[3] + acc[4] + acc[5] + acc[6] + acc[7];
+            sum = scalar_chain(dtype, w, x, j, K, sum);
+            Y[(size_t)b * ldy + r] = sum;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
 /* Pooled GEMV: pool.c:270-362. Rows are independent (y[r] = kernel(row r),     */
 /* pool.c:112-140); the partition (chunk = ceil(rows/threads), pool.c:326-329)  */
 /* changes only which thread computes a row, never its value.                  */
@@ -138,8 +210,11 @@ typedef struct {
 static void gemv_rows(const gemv_task *t) {
     for (int r = t->r0; r < t->r1; ++r) {
         const void *row = t->W + (size_t)r * t->stride;
-        t->y[r] = (t->dtype == ORC_Q4_0) ? oracle_q4_0_row(row, t->x, t->nb, 32)
-                                         : oracle_q8_0_row(row, t->x, t->nb, 32);
+        if (t->dtype == ORC_F32 || t->dtype == ORC_BF16)   /* count = cols, pool.c:116-121 */
+            t->y[r] = oracle_f_row(t->dtype, row, t->x, t->K);
+        else
+            t->y[r] = (t->dtype == ORC_Q4_0) ? oracle_q4_0_row(row, t->x, t->nb, 32)
+                                             : oracle_q8_0_row(row, t->x, t->nb, 32);
     }
 }
 
@@ -147,9 +222,10 @@ static void *gemv_thread(void *arg) { gemv_rows((const gemv_task *)arg); return 
 
 int oracle_gemv(int dtype, const void *W, int M, int K, const float *x, float *y, int nthreads) {
     if (!W || !x || !y || M <= 0 || K <= 0) return -1;                    /* dispatch.c:102-124 */
-    if (dtype != ORC_Q4_0 && dtype != ORC_Q8_0) return -1;
+    if (dtype != ORC_Q4_0 && dtype != ORC_Q8_0 && dtype != ORC_F32 && dtype != ORC_BF16) return -1;
     int nb = (K + 31) / 32;                                               /* pool.c:285 */
-    size_t stride = (size_t)nb * (dtype == ORC_Q4_0 ? 20 : 36);           /* pool.c:297,301 */
+    size_t stride = dtype == ORC_F32 ? (size_t)K * 4 : dtype == ORC_BF16 ? (size_t)K * 2   /* pool.c:303-312 */
+                                     : (size_t)nb * (dtype == ORC_Q4_0 ? 20 : 36);        /* pool.c:297,301 */
     if (nthreads <= 1) {
         gemv_task t = { dtype, K, nb, 0, M, stride, (const unsigned char *)W, x, y };
         gemv_rows(&t);

@@ -32,8 +32,15 @@ void  oracle_dequant(int dtype, const void *blocks, int nblocks, float *out /* 3
 float oracle_q4_0_row(const void *w_row, const float *x, int block_count, int block_size);
 float oracle_q8_0_row(const void *w_row, const float *x, int block_count, int block_size);
 
+/* ---- F32 / BF16 rows (src/kernels/f32_avx.c, bf16_avx.c, dispatch.c:60-85) ---- */
+float oracle_f_row(int dtype, const void *w_row, const float *x, int cols);          /* pooled kernel */
+float oracle_f_row_scalar(int dtype, const void *w_row, const float *x, int cols);   /* no context */
+/* batched form: Y[b * ldy + r] = W[r] . X[b] (kernel_gemm_{f32,bf16}_avx2) */
+int   oracle_gemm_f(int dtype, const void *W, int M, int K, const float *X, int batch, float *Y, int ldy);
+
 /* ---- pooled GEMV (src/kernels/pool.c:270-362 + dispatch.c:101-156) ----
- * y[M] = W[M x K] . x[K]; W is the reference AoS block array, row stride ceil(K/32)*B_blk.
+ * y[M] = W[M x K] . x[K]; W is the reference AoS block array, row stride ceil(K/32)*B_blk,
+ * or an F32 / BF16 matrix with row stride K elements.
  * nthreads <= 1 runs on the calling thread. Returns 0, or -1 on bad arguments. */
 int   oracle_gemv(int dtype, const void *W, int M, int K, const float *x, float *y, int nthreads);
 

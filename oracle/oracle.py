@@ -84,6 +84,11 @@ class Oracle:
         L.oracle_vec_dot.argtypes = [vp, vp, i]
         L.oracle_decode_step.restype = i
         L.oracle_decode_step.argtypes = [C.POINTER(ModelStruct), i, i, vp]
+        for n in ("oracle_f_row", "oracle_f_row_scalar"):
+            getattr(L, n).restype = f
+            getattr(L, n).argtypes = [i, vp, vp, i]
+        L.oracle_gemm_f.restype = i
+        L.oracle_gemm_f.argtypes = [i, vp, i, i, vp, i, vp, i]
 
     # -- numpy conveniences --------------------------------------------------
     def gemv(self, dtype, blocks, x, nthreads=1):
@@ -97,6 +102,22 @@ class Oracle:
     def row(self, dtype, blocks_row, x):
         fn = self.lib.oracle_q4_0_row if dtype == 3 else self.lib.oracle_q8_0_row
         return np.float32(fn(_p(np.ascontiguousarray(blocks_row)), _p(x), blocks_row.shape[0], 32))
+
+    def gemv_scalar(self, dtype, w, x):
+        """F32 / BF16 rows as kernel_gemv computes them without a context (dispatch.c:60-85)."""
+        w = np.ascontiguousarray(w)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        return np.array([self.lib.oracle_f_row_scalar(dtype, _p(w[r]), _p(x), w.shape[1]) for r in range(w.shape[0])],
+                        np.float32)
+
+    def gemm_f(self, dtype, w, X):
+        """Y[b] = W . X[b] for F32 / BF16 W, the batched kernels' order (kernel_gemm_*_avx2)."""
+        w = np.ascontiguousarray(w)
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        m, k = w.shape
+        Y = np.empty((X.shape[0], m), np.float32)
+        assert self.lib.oracle_gemm_f(dtype, _p(w), m, k, _p(X), X.shape[0], _p(Y), m) == 0
+        return Y
 
     def dequant(self, dtype, blocks):
         flat = np.ascontiguousarray(blocks).reshape(-1)
@@ -170,6 +191,8 @@ class Reference:
         L.tensor_release.argtypes = [vp]
         L.kernel_gemv.restype = i
         L.kernel_gemv.argtypes = [vp, vp, vp, vp]
+        L.kernel_gemv_batch.restype = i
+        L.kernel_gemv_batch.argtypes = [vp, vp, vp, vp, i]
         for n in ("rmsnorm", "rmsnorm_delta"):
             getattr(L, n).restype = i
             getattr(L, n).argtypes = [vp, vp, vp, f, i]
@@ -215,6 +238,29 @@ class Reference:
         self.lib.tensor_release(t)
         assert rc == 0
         return y
+
+    def gemv_noctx(self, dtype, w, x):
+        """kernel_gemv with a NULL context (the F32 / BF16 fallback, dispatch.c:131-142)."""
+        m = w.shape[0]
+        shape = (C.c_int * 2)(m, x.shape[0])
+        t = self.lib.tensor_create_view(dtype, 2, shape, _p(w))
+        y = np.empty(m, np.float32)
+        rc = self.lib.kernel_gemv(None, _p(y), t, _p(x))
+        self.lib.tensor_release(t)
+        assert rc == 0
+        return y
+
+    def gemv_batch(self, dtype, w, X, nthreads=1):
+        """kernel_gemv_batch: the pooled batched kernels for F32 / BF16 (dispatch.c:234-266)."""
+        m = w.shape[0]
+        X = np.ascontiguousarray(X, np.float32)
+        shape = (C.c_int * 2)(m, X.shape[1])
+        t = self.lib.tensor_create_view(dtype, 2, shape, _p(w))
+        Y = np.empty((X.shape[0], m), np.float32)
+        rc = self.lib.kernel_gemv_batch(self.ctx(nthreads), _p(Y), t, _p(X), X.shape[0])
+        self.lib.tensor_release(t)
+        assert rc == 0
+        return Y
 
     def row(self, dtype, blocks_row, x, aligned=False):
         name = "quantized_gemv_q4_0_" if dtype == 3 else "quantized_gemv_q8_0_"

@@ -11,6 +11,7 @@ Fixtures:
   known_answers.json  the reference's own known-answer cases: test_dispatch.c:6-29 and
                       the sum(y) of bench_sapphire_end_to_end.c:76-110,166-173
   gemv.npz            seeded Q4_0/Q8_0 pooled kernel_gemv at small shapes (dispatch.c:101)
+  gemv_f.npz          seeded F32/BF16 GEMVs: pooled, without a context, and batched
   primitives.npz      rmsnorm(_delta), rope tables + rotation, gelu, geglu, softcap,
                       softmax, sample_greedy, vec_dot
   decode_tiny.json    greedy decode of a 3-layer Gemma-3-shaped model (tokens + logits
@@ -91,6 +92,7 @@ def e2e_matrices(rows, bpr):
 
 E2E_CONFIGS = [(64, 2), (128, 4), (256, 8), (1024, 16), (8192, 32)]
 GEMV_SHAPES = [(64, 256), (33, 96), (17, 640), (5, 2048), (3, 32), (9, 1152)]
+GEMV_F_SHAPES = [(17, 640), (5, 100), (3, 7), (9, 1152), (4, 33)]
 
 
 def main():
@@ -140,6 +142,23 @@ def main():
             g[key + "_x"] = xv
             g[key + "_y"] = y1
     np.savez_compressed(os.path.join(HERE, "gemv.npz"), **g)
+
+    # ---- seeded F32 / BF16 GEMVs: pooled kernel_gemv, kernel_gemv without a context, and
+    # the batched kernel_gemv_batch (three sequences) ----
+    gf = {}
+    for dt, name in ((0, "F32"), (1, "BF16")):
+        for (m, k) in GEMV_F_SHAPES:
+            Wm = synth.normal_f32((m, k), 1235, m * 31 + k) if dt == 0 else synth.bf16_normal((m, k), 1235, m * 31 + k)
+            xv = synth.normal_f32(k, 1235, 7 + k)
+            Xb = synth.normal_f32((3, k), 1235, 9 + k)
+            key = f"{name}_{m}x{k}"
+            gf[key + "_w"] = Wm
+            gf[key + "_x"] = xv
+            gf[key + "_X"] = Xb
+            gf[key + "_y"] = ref.gemv(dt, Wm, xv, nthreads=3)
+            gf[key + "_ynoctx"] = ref.gemv_noctx(dt, Wm, xv)
+            gf[key + "_Y"] = ref.gemv_batch(dt, Wm, Xb, nthreads=2)
+    np.savez_compressed(os.path.join(HERE, "gemv_f.npz"), **gf)
 
     # ---- primitives ----
     pr = {}

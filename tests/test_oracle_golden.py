@@ -95,6 +95,25 @@ def test_gemv_fixture(oracle, key):
         assert np.array_equal(bits(y), bits(g[key + "_y"]))
 
 
+def gemv_f_cases():
+    g = load_npz("gemv_f.npz")
+    return sorted({k.rsplit("_", 1)[0] for k in g.files})
+
+
+@pytest.mark.parametrize("key", gemv_f_cases())
+def test_gemv_f_fixture(oracle, key):
+    """F32 / BF16 rows: the pooled kernel (bf16_avx.c:57-113, f32_avx.c), kernel_gemv without a
+    context (dispatch.c:60-85) and the batched kernel (kernel_gemm_*_avx2), against the
+    compiled reference's outputs bit for bit."""
+    g = load_npz("gemv_f.npz")
+    dt = 0 if key.startswith("F32") else 1
+    w, x, X = g[key + "_w"], g[key + "_x"], g[key + "_X"]
+    for nt in (1, 3):
+        assert np.array_equal(bits(oracle.gemv(dt, w, x, nthreads=nt)), bits(g[key + "_y"]))
+    assert np.array_equal(bits(oracle.gemv_scalar(dt, w, x)), bits(g[key + "_ynoctx"]))
+    assert np.array_equal(bits(oracle.gemm_f(dt, w, X)), bits(g[key + "_Y"]))
+
+
 @pytest.mark.parametrize("dim", [640, 256, 1152, 7, 1001])
 def test_rmsnorm_fixture(oracle, dim):
     pr = load_npz("primitives.npz")

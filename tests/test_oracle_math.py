@@ -72,6 +72,27 @@ def test_gemv_float64_brute_force(oracle, dtype):
     assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-7)
 
 
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f32", "bf16"])
+def test_f_gemv_float64_and_exact(oracle, dtype):
+    """F32 / BF16 rows: all three forms within 1e-5 of the float64 dot product, and bit-exact
+    when every product and partial sum is exact (small-integer weights times x = j / 4)."""
+    m, k = 37, 1001
+    w = synth.normal_f32((m, k), 5, 1) if dtype == 0 else synth.bf16_normal((m, k), 5, 1)
+    wf = w.astype(np.float64) if dtype == 0 else (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    x = synth.normal_f32(k, 5, 2)
+    want = wf @ x.astype(np.float64)
+    scale = np.abs(wf) @ np.abs(x.astype(np.float64))
+    X = np.stack([x, 2 * x])
+    for got in (oracle.gemv(dtype, w, x), oracle.gemv_scalar(dtype, w, x), oracle.gemm_f(dtype, w, X)[0]):
+        assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * scale + 1e-7)
+    iw = np.random.default_rng(6).integers(-8, 9, (m, k)).astype(np.float32)
+    w2 = iw if dtype == 0 else (iw.view(np.uint32) >> 16).astype(np.uint16)   # small integers are exact in bf16
+    x2 = (np.random.default_rng(7).integers(-64, 65, k) / 4.0).astype(np.float32)
+    exact = (iw.astype(np.float64) @ x2.astype(np.float64)).astype(np.float32)
+    for got in (oracle.gemv(dtype, w2, x2), oracle.gemv_scalar(dtype, w2, x2), oracle.gemm_f(dtype, w2, x2[None])[0]):
+        assert np.array_equal(bits(got), bits(exact))
+
+
 @pytest.mark.parametrize("dtype", [Q4, Q8])
 def test_gemv_invariants(oracle, dtype):
     m, k = 97, 640

@@ -64,6 +64,29 @@ def test_lm_head_gemv(oracle, ref, dtype):
     assert np.array_equal(bits(ref.gemv(dtype, W, x, nthreads=8)), bits(oracle.gemv(dtype, W, x, nthreads=8)))
 
 
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f32", "bf16"])
+@pytest.mark.parametrize("k", [1, 3, 4, 5, 7, 8, 9, 31, 32, 33, 63, 65, 255, 640, 1152, 2051])
+def test_f_gemv_variants(oracle, ref, dtype, k):
+    """F32 / BF16 GEMVs in all three reference forms: the pooled row kernel (4 x 8 accumulators
+    over chunks of 32 plus a scalar remainder), the context-free loop and the batched kernel.
+    The scalar chains differ by dtype in the compiled reference (BF16 terms fused, F32 products
+    rounded first except the last n % 4): these K cover every remainder length."""
+    m = 6
+    w = synth.normal_f32((m, k), 80, k) if dtype == 0 else synth.bf16_normal((m, k), 80, k)
+    x = synth.normal_f32(k, 80, k + 1)
+    X = synth.normal_f32((3, k), 80, k + 2)
+    assert np.array_equal(bits(ref.gemv(dtype, w, x, nthreads=3)), bits(oracle.gemv(dtype, w, x, nthreads=2)))
+    assert np.array_equal(bits(ref.gemv_noctx(dtype, w, x)), bits(oracle.gemv_scalar(dtype, w, x)))
+    assert np.array_equal(bits(ref.gemv_batch(dtype, w, X, nthreads=2)), bits(oracle.gemm_f(dtype, w, X)))
+
+
+def test_bf16_lm_head_gemv(oracle, ref):
+    """The weight-tied LM head of the real model (transformer.c:407): BF16 262144 x 640."""
+    w = synth.bf16_normal((262144, 640), 81, 1)
+    x = synth.normal_f32(640, 81, 2)
+    assert np.array_equal(bits(ref.gemv(1, w, x, nthreads=8)), bits(oracle.gemv(1, w, x, nthreads=8)))
+
+
 def test_primitives_random(oracle, ref):
     import ctypes as C
     L = ref.lib
