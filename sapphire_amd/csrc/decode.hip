@@ -93,7 +93,9 @@ __global__ __launch_bounds__(kThreads) void dec_prologue_kernel(GemvIn in, int K
 
 // Workgroup b takes positions [t0, t1) of the layer's attention range; each wave walks
 // every fourth of them with a running (max, sum, weighted V) per head; the waves are then
-// merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL).
+// merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL). Scores are
+// summed by DPP into wave-uniform values and the weights are powers of two of log2-scaled
+// scores (one exp2 each).
 template <int DPL, int NH>
 __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     {   // sequence blockIdx.y of a batch
@@ -111,6 +113,8 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     __shared__ float ss[16];
     __shared__ float wm[kThreads / kWave][NH], wsum[kThreads / kWave][NH];
     __shared__ float wo[kThreads / kWave][NH][kWave * DPL];
+    __shared__ float wx[kThreads / kWave][NH];   // wave merge weights
+    __shared__ float wmax[NH], wtot[NH];
     const int hd = a.hd, nkv = a.nkv;
     const int pos = *a.d_pos, seq = pos + 1;
     const int start = (a.window > 0 && seq > a.window) ? seq - a.window : 0;
@@ -119,13 +123,14 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     const int t0 = start + blockIdx.x * chunk, t1 = min(seq, t0 + chunk);
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int group = NH / nkv;
-    // The wave's positions t0 + wid + 4j, PF at a time: every K/V row of a batch is loaded
-    // before its first score is formed. Rows come from the cache; the row of the current
-    // position is taken from this kernel's own K (after RoPE) and V.
+    // The wave's positions t0 + wid + 4j, PF at a time. The rows of the next batch are loaded
+    // while the current one is used (two register sets). Rows come from the cache; the row of
+    // the current position is taken from this kernel's own K (after RoPE) and V.
     constexpr int PF = 4;
     constexpr int NW = kThreads / kWave;
     float kr[PF][2][DPL], vr[PF][2][DPL];   // up to two K/V heads per row
-    auto load_batch = [&](int tb) {
+    float nk[PF][2][DPL], nv[PF][2][DPL];   // the next batch
+    auto load_batch = [&](int tb, float(&K)[PF][2][DPL], float(&V)[PF][2][DPL]) {
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
             const int t = tb + j * NW;
@@ -135,13 +140,13 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
                 const size_t off = ok ? ((size_t)hk * a.max_ctx + t) * hd : 0;
 #pragma unroll
                 for (int d = 0; d < DPL; ++d) {
-                    kr[j][hk][d] = ok ? a.kc[off + lane * DPL + d] : 0.f;
-                    vr[j][hk][d] = ok ? a.vc[off + lane * DPL + d] : 0.f;
+                    K[j][hk][d] = ok ? a.kc[off + lane * DPL + d] : 0.f;
+                    V[j][hk][d] = ok ? a.vc[off + lane * DPL + d] : 0.f;
                 }
             }
         }
     };
-    if (t0 + wid < t1) load_batch(t0 + wid);   // in flight during the prologue
+    if (t0 + wid < t1) load_batch(t0 + wid, kr, vr);   // in flight during the prologue
 
     for (int i = threadIdx.x; i < (NH + 2 * nkv) * hd; i += blockDim.x) raw[i] = a.qkv[i];
     __syncthreads();
@@ -157,6 +162,9 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
             a.vc[off] = vnew[i];
         }
 
+    // scores in log2 units, so that every softmax weight is one exp2 (v_exp_f32); the
+    // partial's maximum is stored in these units
+    const float sl2 = __fmul_rn(a.scale, 1.44269504088896341f);
     float m[NH], s[NH], o[NH][DPL];
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -166,7 +174,8 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
     for (int tb = t0 + wid; tb < t1; tb += PF * NW) {
-        if (tb != t0 + wid) load_batch(tb);
+        const int tn = tb + PF * NW;
+        if (tn < t1) load_batch(tn, nk, nv);
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
             const int t = tb + j * NW;
@@ -187,10 +196,10 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 #pragma unroll
                 for (int d = 0; d < DPL; ++d)
                     dp = __builtin_fmaf(qs[h * hd + lane * DPL + d], hk == 0 ? kr[j][0][d] : kr[j][1][d], dp);
-                const float score = __fmul_rn(wave_sum(dp), a.scale);
+                const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
                 const float mn = fmaxf(m[h], score);
-                const float c = m[h] == -INFINITY ? 0.f : expf(m[h] - mn);
-                const float p = expf(score - mn);
+                const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
+                const float p = __builtin_amdgcn_exp2f(score - mn);
                 s[h] = __builtin_fmaf(s[h], c, p);
 #pragma unroll
                 for (int d = 0; d < DPL; ++d)
@@ -198,8 +207,19 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
                 m[h] = mn;
             }
         }
+        if (tn < t1) {
+#pragma unroll
+            for (int j = 0; j < PF; ++j)
+#pragma unroll
+                for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+                    for (int d = 0; d < DPL; ++d) {
+                        kr[j][hk][d] = nk[j][hk][d];
+                        vr[j][hk][d] = nv[j][hk][d];
+                    }
+        }
     }
-    // merge the four waves
+    // merge the four waves: the (wave, head) weights exp2(m_w - M) are formed once
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         if (lane == 0) {
@@ -210,29 +230,36 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
         for (int d = 0; d < DPL; ++d) wo[wid][h][lane * DPL + d] = o[h][d];
     }
     __syncthreads();
+    if (threadIdx.x < NH) {
+        const int h = threadIdx.x;
+        float M = -INFINITY;
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w][h]);
+        float S = 0.f;
+        for (int w = 0; w < NW; ++w) {
+            const float e = wm[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][h] - M);
+            wx[w][h] = e;
+            S = __builtin_fmaf(wsum[w][h], e, S);
+        }
+        wmax[h] = M;
+        wtot[h] = S;
+    }
+    __syncthreads();
     float *out = a.part + (size_t)blockIdx.x * NH * (hd + 2);
     for (int idx = threadIdx.x; idx < NH * hd; idx += blockDim.x) {
         const int h = idx / hd, d = idx - h * hd;
-        float M = -INFINITY;
-        for (int w = 0; w < kThreads / kWave; ++w) M = fmaxf(M, wm[w][h]);
-        float S = 0.f, O = 0.f;
-        for (int w = 0; w < kThreads / kWave; ++w) {
-            if (wm[w][h] == -INFINITY) continue;
-            const float e = expf(wm[w][h] - M);
-            S = __builtin_fmaf(wsum[w][h], e, S);
-            O = __builtin_fmaf(wo[w][h][d], e, O);
-        }
+        float O = 0.f;
+        for (int w = 0; w < NW; ++w) O = __builtin_fmaf(wo[w][h][d], wx[w][h], O);
         out[h * (hd + 2) + d] = O;
         if (d == 0) {
-            out[h * (hd + 2) + hd] = M;
-            out[h * (hd + 2) + hd + 1] = S;
+            out[h * (hd + 2) + hd] = wmax[h];
+            out[h * (hd + 2) + hd + 1] = wtot[h];
         }
     }
 }
 
-// out[h*hd + d] = sum_b e_b o_b[d] / sum_b e_b s_b with e_b = exp(m_b - max_b m_b): the
-// softmax-weighted sum of values of attention.c:140-158 over all slices. One workgroup per
-// head, one thread per dim.
+// out[h*hd + d] = sum_b e_b o_b[d] / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) (the
+// partials' maxima are in log2 units): the softmax-weighted sum of values of
+// attention.c:140-158 over all slices. One workgroup per head, one thread per dim.
 template <int NS>
 __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float *__restrict__ part, int nh, int hd,
                                                                     float *__restrict__ out, size_t out_stride) {
@@ -249,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float 
         float M = mb;
 #pragma unroll
         for (int off = kWave / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
-        const float e = mb == -INFINITY ? 0.f : expf(mb - M);
+        const float e = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
         if (t < NS) es[t] = e;
         const float tot = wave_sum(e * sb);
         if (t == 0) S = tot;
