@@ -245,7 +245,9 @@ def main() -> int:
 
     # each kernel alone, back to back on the bench stream (HIP events on that stream); the
     # Q8_0 GEMV is the dominant kernel of the step and gives roofline.achieved
-    def time_alone(fn, iters=20):
+    def time_alone(fn, iters=20, warm=3):
+        for i in range(warm):
+            fn(i)
         tt = Timer(stream)
         tt.start()
         for i in range(iters):
@@ -258,6 +260,24 @@ def main() -> int:
     q8sm_ms = time_alone(lambda i: check(L.sapphire_gemv_softmax_dev(
         synth.Q8_0, LAY, q8[i % n_sets].ptr(), M_LM, K_LM, dx.ptr, logits.ptr, probs.ptr, arg.ptr, stream)))
     sm_ms = time_alone(lambda i: check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream)))
+
+    # The same LM head held as BF16 / F32 rows (a weight-tied embedding), on the element
+    # types' own GEMV kernel; two copies of each rotate so the weights come from HBM.
+    f_lines = {}
+    for name, dt, es in (("gemv_bf16_lm_head", synth.BF16, 2), ("gemv_f32_lm_head", synth.F32, 4)):
+        tile = synth.normal_f32((M_LM // 64, K_LM), seed, 40 + dt, 0.0, 0.05)
+        if dt == synth.BF16:
+            tile = (tile.view(np.uint32) >> 16).astype(np.uint16)
+        tile = np.ascontiguousarray(np.tile(tile, (64, 1)))
+        mats = [DeviceArray.from_numpy(tile) for _ in range(n_sets)]
+        del tile
+        f_ms = time_alone(lambda i: check(L.sapphire_gemv_f_dev(dt, mats[i % n_sets].ptr, M_LM, K_LM, dx.ptr,
+                                                                 logits.ptr, stream)))
+        fb = M_LM * K_LM * es + 4 * K_LM + 4 * M_LM
+        f_lines[name] = {"us": round(f_ms * 1e3, 2), "GB/s": round(fb / (f_ms * 1e-3) / 1e9, 1),
+                         "frac_peak": round(fb / (f_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        for m_ in mats:
+            m_.free()
 
     b8, b4 = gemv_bytes(synth.Q8_0, M_LM, K_LM), gemv_bytes(synth.Q4_0, M_LM, K_LM)
     b_sm = 2 * 4 * M_LM
@@ -302,6 +322,7 @@ def main() -> int:
                                   "frac_peak": round(b4 / (q4_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
             "gemv_q8_0_lm_head_with_softmax_epilogue": {"us": round(q8sm_ms * 1e3, 2)},
             "softmax_argmax_262144_standalone": {"us": round(sm_ms * 1e3, 2)},
+            **f_lines,
         },
         "decode": decode,
         "decode_batch16_gemma3_1b": decode_batch,

@@ -6,6 +6,7 @@
 
 #include "decode_kernels.h"
 #include "devmath.h"
+#include "lanes.h"
 #include "qdot.h"
 
 namespace sapphire {
@@ -13,6 +14,7 @@ namespace {
 
 using namespace devmath;
 using namespace qdot;
+using namespace lanes;
 
 constexpr int kWave = 64;
 constexpr int kThreads = 256;
@@ -21,32 +23,6 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
-// DPP move of v (dpp_ctrl CTRL, every row and bank enabled).
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over each row of 16 lanes, left in every lane of the row: quad_perm [1,0,3,2] and
-// [2,3,0,1], then row_half_mirror and row_mirror. Each step adds a lane to its partner in
-// the other half, so every lane of the row ends with the same bits (fp addition commutes).
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp_mov<0xB1>(v);
-    v += dpp_mov<0x4E>(v);
-    v += dpp_mov<0x141>(v);
-    v += dpp_mov<0x140>(v);
-    return v;
-}
-
-// Maximum over each row of 16 lanes, left in every lane of the row (as row16_sum).
-__device__ __forceinline__ float row16_max(float v) {
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    v = fmaxf(v, dpp_mov<0x140>(v));
     return v;
 }
 

@@ -18,11 +18,16 @@
 //    the nb block partials go through a per-wave LDS transpose.
 //  * gemv_q_rows  (any K): one row per wave-step, lanes stride over the row's blocks,
 //    x read through L1, wave-wide reduction.
-//  * gemv_f       (F32/BF16 rows): float4 / 8xbf16 per lane, wave-wide reduction.
+//  * gemv_f16      (F32/BF16 rows, 16-byte aligned rows): 16 lanes per row, 4 rows per
+//    wave-step; lane q reads the 16-byte chunks q, q+16, ... of its row (4 fp32 or 8 bf16
+//    each), U chunks in flight, x from LDS; row sums by DPP.
+//  * gemv_f       (F32/BF16, any K or alignment): lanes stride over the elements of one
+//    row, wave-wide reduction.
 #include <algorithm>
 #include <cstdlib>
 
 #include "internal.h"
+#include "lanes.h"
 #include "qdot.h"
 
 namespace sapphire {
@@ -38,6 +43,7 @@ template <> struct QT<DT_Q4_0> { static constexpr int QB = 16, BB = 20, QD = 4; 
 template <> struct QT<DT_Q8_0> { static constexpr int QB = 32, BB = 36, QD = 8; };
 
 using namespace qdot;
+using namespace lanes;
 
 // Buffer descriptors over the quant and scale planes (gfx9-family word3 0x00020000).
 // A byte offset at or beyond num_records returns zeros without touching memory.
@@ -446,6 +452,69 @@ __global__ __launch_bounds__(256) void gemv_f(const void *__restrict__ w, const 
     }
 }
 
+// F32 / BF16 rows of 16-byte aligned length. x is staged once per workgroup in LDS,
+// zero-padded to xpad = a whole number of U-chunk rounds of 16 lanes; a chunk past the end
+// of its row (or a row past M) is loaded from an out-of-range buffer offset, which returns
+// zeros, and meets zero activations. Wave-steps of 4 rows are spread over all waves of the
+// grid. Each product is fused into one of two accumulators (even / odd element of the
+// chunk); the reference accumulates in its own lane order (bf16_avx.c:57-113,
+// f32_avx.c:43-90), so sums agree to fp32 rounding.
+template <int DT, int U>
+__global__ __launch_bounds__(256) void gemv_f16(const uint8_t *__restrict__ w, uint32_t w_bytes, uint32_t row_bytes,
+                                                const float *__restrict__ x, float *__restrict__ y, int M, int K,
+                                                int xpad) {
+    constexpr int E = DT == DT_F32 ? 4 : 8;   // elements per 16-byte chunk
+    extern __shared__ float xs[];
+    for (int i = threadIdx.x; i < xpad; i += blockDim.x) xs[i] = i < K ? x[i] : 0.f;
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int q = lane & 15, g = lane >> 4;
+    const int nchunk = (int)(row_bytes / 16u);
+    const int rounds = xpad / (16 * E);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w_bytes);
+    const int nwaves = gridDim.x * (blockDim.x / kWave);
+    const int steps = (M + 3) / 4;
+    for (int st = blockIdx.x * (blockDim.x / kWave) + (int)(threadIdx.x / kWave); st < steps; st += nwaves) {
+        const int row = st * 4 + g;
+        const bool on = row < M;
+        const uint32_t rbase = (uint32_t)row * row_bytes;
+        float a0 = 0.f, a1 = 0.f;
+        for (int r = 0; r < rounds; r += U) {
+            u32x4 v[U];
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int c = (r + j) * 16 + q;
+                const uint32_t off = on && c < nchunk ? rbase + 16u * (uint32_t)c : kOffNone;
+                v[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kNT));
+            }
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const float *xp = xs + ((r + j) * 16 + q) * E;
+                if constexpr (DT == DT_F32) {
+                    const float4 xv = *reinterpret_cast<const float4 *>(xp);
+                    a0 = __builtin_fmaf(__uint_as_float(v[j].x), xv.x, a0);
+                    a1 = __builtin_fmaf(__uint_as_float(v[j].y), xv.y, a1);
+                    a0 = __builtin_fmaf(__uint_as_float(v[j].z), xv.z, a0);
+                    a1 = __builtin_fmaf(__uint_as_float(v[j].w), xv.w, a1);
+                } else {
+                    const float4 xl = *reinterpret_cast<const float4 *>(xp);
+                    const float4 xh = *reinterpret_cast<const float4 *>(xp + 4);
+                    a0 = __builtin_fmaf(__uint_as_float(v[j].x << 16), xl.x, a0);
+                    a1 = __builtin_fmaf(__uint_as_float(v[j].x & 0xFFFF0000u), xl.y, a1);
+                    a0 = __builtin_fmaf(__uint_as_float(v[j].y << 16), xl.z, a0);
+                    a1 = __builtin_fmaf(__uint_as_float(v[j].y & 0xFFFF0000u), xl.w, a1);
+                    a0 = __builtin_fmaf(__uint_as_float(v[j].z << 16), xh.x, a0);
+                    a1 = __builtin_fmaf(__uint_as_float(v[j].z & 0xFFFF0000u), xh.y, a1);
+                    a0 = __builtin_fmaf(__uint_as_float(v[j].w << 16), xh.z, a0);
+                    a1 = __builtin_fmaf(__uint_as_float(v[j].w & 0xFFFF0000u), xh.w, a1);
+                }
+            }
+        }
+        const float acc = row16_sum(a0 + a1);
+        if (on && q == 0) y[row] = acc;
+    }
+}
+
 template <int DT>
 __global__ void repack_kernel(const uint8_t *__restrict__ aos, uint8_t *__restrict__ qs, float *__restrict__ sc,
                               long nblocks) {
@@ -655,7 +724,74 @@ int launch_gemm_q(int dt, int layout, const void *w, int M, int K, const float *
     return hip_ok(hipGetLastError(), "gemm_q launch") ? 0 : -1;
 }
 
+namespace {
+
+constexpr int kF16MaxX = 16384;   // floats of x in LDS (64 KiB)
+
+template <int DT, int U>
+void launch_f16_u(const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes, const float *x, float *y, int M, int K,
+                  int xpad, hipStream_t st) {
+    const long steps = (M + 3) / 4;
+    const long blocks = std::max(1L, std::min((steps + 3) / 4, 8L * device_cus()));
+    hipLaunchKernelGGL((gemv_f16<DT, U>), dim3((unsigned)blocks), dim3(256), (size_t)xpad * sizeof(float), st, w,
+                       w_bytes, row_bytes, x, y, M, K, xpad);
+}
+
+template <int DT>
+void launch_f16(const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes, const float *x, float *y, int M, int K,
+                int rounds, int U, hipStream_t st) {
+    constexpr int E = DT == DT_F32 ? 4 : 8;
+    const int xpad = (rounds + U - 1) / U * U * 16 * E;
+    switch (U) {
+        case 1: launch_f16_u<DT, 1>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+        case 2: launch_f16_u<DT, 2>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+        case 3: launch_f16_u<DT, 3>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+        case 4: launch_f16_u<DT, 4>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+        case 5: launch_f16_u<DT, 5>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+        case 6: launch_f16_u<DT, 6>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+        case 7: launch_f16_u<DT, 7>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+        default: launch_f16_u<DT, 8>(w, w_bytes, row_bytes, x, y, M, K, xpad, st); break;
+    }
+}
+
+// Chunks in flight per lane for `rounds` rounds of 16 chunks: all of them up to 8, else the
+// depth in 4..8 that pads the fewest rounds (the deeper on a tie).
+int f16_depth(int rounds) {
+    if (rounds <= 8) return std::max(rounds, 1);
+    int best = 8, waste = (rounds + 7) / 8 * 8 - rounds;
+    for (int u = 7; u >= 4; --u) {
+        const int wst = (rounds + u - 1) / u * u - rounds;
+        if (wst < waste) best = u, waste = wst;
+    }
+    return best;
+}
+
+}  // namespace
+
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t st) {
+    if (M <= 0) return 0;
+    const size_t es = dt == DT_F32 ? 4 : 2;
+    const size_t row_bytes = (size_t)K * es;
+    const int E = (int)(16 / es);
+    const int rounds = (int)((row_bytes / 16 + 15) / 16);
+    const int U = f16_depth(rounds);
+    const long xpad = (long)(rounds + U - 1) / U * U * 16 * E;
+    if (K > 0 && row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 && xpad <= kF16MaxX) {
+        // 32-bit buffer offsets: launches of at most 2^32 - 2^20 bytes of rows each
+        const long rows_per = std::max(4L, (long)((((size_t)1 << 32) - ((size_t)1 << 20)) / row_bytes) & ~3L);
+        const uint8_t *wb = static_cast<const uint8_t *>(w);
+        for (long r0 = 0; r0 < M; r0 += rows_per) {
+            const int m = (int)std::min<long>(rows_per, M - r0);
+            const uint32_t wbytes = (uint32_t)((size_t)m * row_bytes);
+            if (dt == DT_F32)
+                launch_f16<DT_F32>(wb + (size_t)r0 * row_bytes, wbytes, (uint32_t)row_bytes, x, y + r0, m, K, rounds,
+                                   U, st);
+            else
+                launch_f16<DT_BF16>(wb + (size_t)r0 * row_bytes, wbytes, (uint32_t)row_bytes, x, y + r0, m, K,
+                                    rounds, U, st);
+        }
+        return hip_ok(hipGetLastError(), "gemv_f16 launch") ? 0 : -1;
+    }
     const int rpw = M >= 65536 ? 4 : 1;
     const dim3 g(grid_for((M + rpw - 1) / rpw, 4)), b(256);
     if (dt == DT_F32)

@@ -113,6 +113,12 @@ def gemv(qm: QMatrix, x: DeviceArray, y: DeviceArray, layout: int = 1, stream=No
     check(lib().sapphire_gemv_q_dev(qm.dtype, layout, qm.ptr(layout), qm.M, qm.K, x.ptr, y.ptr, stream), "gemv")
 
 
+def gemv_f(dtype: int, w: DeviceArray, M: int, K: int, x: DeviceArray, y: DeviceArray, offset: int = 0,
+           stream=None) -> None:
+    """y = W . x for a row-major F32 / BF16 matrix held at w.ptr + offset bytes."""
+    check(lib().sapphire_gemv_f_dev(dtype, w.ptr + offset, M, K, x.ptr, y.ptr, stream), "gemv_f")
+
+
 class Timer:
     """HIP-event timing on a given stream (None = null stream)."""
 
