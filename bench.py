@@ -16,6 +16,7 @@ read + 1 MiB written per softmax) / step time.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import re
@@ -84,10 +85,17 @@ def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024)
     one HIP graph per step), and the reference engine compiled from its sources (oracle/_ref)
     on this host's cores for a few steps of the same model as the CPU baseline."""
     from sapphire_amd import model as smodel
+    from sapphire_amd import synth
     from sapphire_amd.engine import bench_decode
     m = smodel.synthetic_model(smodel.GEMMA3_270M, seed)
     k, v = m.kv_prefill(prefill)
     out = bench_decode(steps, seed=seed, prefill=prefill, m=m, kv=(k, v))
+    # the same model with the reference's own LM head: the BF16 embedding table (tied)
+    tied_cfg = dataclasses.replace(m.cfg, lm_dtype=synth.BF16)
+    tied = dataclasses.replace(m, cfg=tied_cfg, lm_head=m.embed_bf16)
+    out["tied_bf16_lm_head"] = {kk: vv for kk, vv in bench_decode(steps, seed=seed, prefill=prefill, m=tied,
+                                                                    kv=(k, v)).items()
+                                if kk in ("ms_per_token", "tok_per_s", "weight_bytes_per_token", "first_tokens")}
     if cpu:
         from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
         tok = smodel.start_token(m.cfg, seed)

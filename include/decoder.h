@@ -35,7 +35,9 @@ typedef struct {
     float rope_local_base;          /* RoPE base of local layers (inference.c:485-491) */
     float eps;                      /* RMSNorm epsilon; the reference uses 1e-6 everywhere */
     int wdtype;                     /* DTYPE_Q4_0 (3) or DTYPE_Q8_0 (4): the seven projections */
-    int lm_dtype;                   /* DTYPE_Q4_0 or DTYPE_Q8_0: the LM head */
+    int lm_dtype;                   /* DTYPE_Q4_0 or DTYPE_Q8_0: a separate LM head; DTYPE_BF16 (1):
+                                     * the LM head is the embedding table (weight tying, as
+                                     * lm_head does, transformer.c:393-408); one sequence only */
 } sapphire_decoder_config_t;
 
 /* Host pointers, read once by sapphire_decoder_create. Projection arrays hold one pointer
@@ -49,7 +51,7 @@ typedef struct {
     const float *const *q_norm, *const *k_norm;
     const uint16_t *embed_bf16;     /* [vocab][hidden] bf16, scaled by sqrt(hidden) on lookup */
     const float *norm_final;        /* [hidden] */
-    const void *lm_head;            /* [vocab][hidden] blocks of lm_dtype */
+    const void *lm_head;            /* [vocab][hidden] blocks of lm_dtype; ignored for DTYPE_BF16 */
 } sapphire_decoder_weights_t;
 
 typedef struct sapphire_decoder sapphire_decoder_t;

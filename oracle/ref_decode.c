@@ -15,9 +15,9 @@
  *       with the global/local RoPE table choice           inference.c:629-632
  *     rmsnorm_delta(final) + kernel_gemv(lm_head)         transformer.c:393-408
  *     sample_greedy                                      utils.c:145-156
- * lm_head() itself always projects through embedding_weight (transformer.c:407);
- * the quantized LM head is therefore applied with the same two calls lm_head makes,
- * on a separate Q4_0/Q8_0 tensor view.
+ * lm_head() itself always projects through embedding_weight (transformer.c:407): a
+ * BF16 (tied) LM head calls it; a quantized LM head is applied with the same two calls
+ * lm_head makes, on a separate Q4_0/Q8_0 tensor view.
  */
 #define _POSIX_C_SOURCE 200809L
 #include <stdint.h>
@@ -143,8 +143,12 @@ int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, f
                                         glob ? s->rope_freqs_sin_global : s->rope_freqs_sin_local };
             sapphire_transformer_layer(s, l, pos, hidden, rope);
         }
-        rmsnorm_delta(norm, hidden, (const float *)tensor_data(model.norm_final_weight), 1e-6f, H);
-        if (kernel_gemv(s->gemv_ctx, logits, lm, norm) != 0) goto out;
+        if (c->lm_dtype == DTYPE_BF16) {
+            lm_head(s, hidden, logits);       /* tied: projects through embedding_weight */
+        } else {
+            rmsnorm_delta(norm, hidden, (const float *)tensor_data(model.norm_final_weight), 1e-6f, H);
+            if (kernel_gemv(s->gemv_ctx, logits, lm, norm) != 0) goto out;
+        }
         token = sample_greedy(logits, c->vocab);
         tokens_out[st] = token;
         if (logits_out) memcpy(logits_out + (size_t)st * c->vocab, logits, sizeof(float) * (size_t)c->vocab);

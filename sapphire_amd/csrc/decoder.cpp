@@ -232,7 +232,13 @@ int enqueue_lm_head(sapphire_decoder *d) {
     const auto &c = d->cfg;
     hipStream_t s = d->stream;
     const int H = c.hidden;
-    if (d->lm_layout == LAYOUT_TILED) {
+    if (c.lm_dtype == DT_BF16) {
+        // weight tying: the logits are the embedding table times the final norm
+        // (transformer.c:393-408 projects through embedding_weight)
+        if (launch_gemv_f(DT_BF16, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
+        if (launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
+            return -1;
+    } else if (d->lm_layout == LAYOUT_TILED) {
         if (launch_gemv_tiled_softmax(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, nullptr, d->state,
                                       d->lm_scratch, s) != 0)
             return -1;
@@ -463,8 +469,8 @@ bool valid_config(const sapphire_decoder_config_t &c) {
         set_error("decoder config: non-positive dimension");
         return false;
     }
-    if (!is_quant(c.wdtype) || !is_quant(c.lm_dtype)) {
-        set_error("decoder config: weights must be Q4_0 or Q8_0");
+    if (!is_quant(c.wdtype) || (!is_quant(c.lm_dtype) && c.lm_dtype != DT_BF16)) {
+        set_error("decoder config: projections must be Q4_0 or Q8_0, the LM head Q4_0, Q8_0 or BF16 (tied)");
         return false;
     }
     if (c.hidden % kBlock || (c.n_heads * c.head_dim) % kBlock || c.ffn % kBlock) {
@@ -585,7 +591,15 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
     d->embed = static_cast<const uint16_t *>(p);
     if (!(d->norm_final = upload_f32(d, w->norm_final, H, "norm_final"))) return fail();
     // LM head
-    {
+    if (c.lm_dtype == DT_BF16) {
+        if (B > 1) {
+            set_error("batched decoder: the LM head must be Q4_0 or Q8_0");
+            return fail();
+        }
+        d->lm = d->embed;
+        if (!dev_alloc(d, &d->lm_scratch, softmax_scratch_floats(c.vocab) * sizeof(float), "lm scratch"))
+            return fail();
+    } else {
         if (!w->lm_head) {
             set_error("decoder weights: lm_head is NULL");
             return fail();

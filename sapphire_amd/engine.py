@@ -177,9 +177,9 @@ def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, rep
     2048 positions): tokens/s over `steps` steps, best of `reps` runs after a warm-up.
     `m` / `kv` reuse an already generated model and prefilled caches. `groups`: workgroups of
     the persistent step (0: the multi-launch step; None: the decoder's default)."""
-    cfg = smodel.GEMMA3_270M
     if m is None:
-        m = smodel.synthetic_model(cfg, seed)
+        m = smodel.synthetic_model(smodel.GEMMA3_270M, seed)
+    cfg = m.cfg
     k, v = kv if kv is not None else m.kv_prefill(prefill)
     dec = Decoder(m)
     if groups is not None:
@@ -195,8 +195,11 @@ def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, rep
         best = ms if best is None else min(best, ms)
     dec.close()
     layer_bytes = sum(int(m.weights[n][0].nbytes) for n in smodel.PROJ) * cfg.n_layers
+    from . import synth
+    lm_names = {synth.Q4_0: "Q4_0", synth.Q8_0: "Q8_0", synth.BF16: "BF16 (the embedding table, tied)"}
     return {
-        "model": "Gemma-3-270M-shaped, Q4_0 weights (random init), 18 layers, hidden 640, vocab 262144",
+        "model": f"Gemma-3-270M-shaped, Q4_0 weights (random init), 18 layers, hidden 640, vocab 262144, "
+                 f"LM head {lm_names[cfg.lm_dtype]}",
         "steps": steps, "kv_prefill": prefill, "ms_total": round(best, 3), "ms_per_token": round(best / steps, 4),
         "tok_per_s": round(steps / (best * 1e-3), 1), "first_tokens": [int(t) for t in toks[:8]],
         "weight_bytes_per_token": layer_bytes + int(m.lm_head.nbytes),

@@ -92,7 +92,7 @@ class SyntheticModel:
     norms: dict = field(default_factory=dict)     # name -> [n_layers, len] f32
     embed_bf16: np.ndarray = None                 # [vocab, hidden] uint16
     norm_final: np.ndarray = None                 # [hidden] f32
-    lm_head: np.ndarray = None                    # [vocab, nb] blocks
+    lm_head: np.ndarray = None                    # [vocab, nb] blocks, or embed_bf16 (BF16, tied)
 
     def kv_prefill(self, n_pos: int, seed_offset: int = 0):
         """K/V caches [n_layers, n_kv, max_ctx, hd] with N(0,1) at positions < n_pos."""
@@ -122,7 +122,10 @@ def synthetic_model(cfg: DecodeConfig, seed: int) -> SyntheticModel:
     m.norms["k_norm"] = synth.normal_f32((cfg.n_layers, cfg.head_dim), seed, tid + 1, 1.0, 0.1)
     m.embed_bf16 = synth.bf16_normal((cfg.vocab, cfg.hidden), seed, tid + 2)
     m.norm_final = synth.normal_f32(cfg.hidden, seed, tid + 3, 1.0, 0.1)
-    m.lm_head = synth.quant_matrix(cfg.lm_dtype, cfg.vocab, cfg.hidden, seed, tid + 4)
+    if cfg.lm_dtype == synth.BF16:
+        m.lm_head = m.embed_bf16          # weight tying: lm_head projects through the embedding
+    else:
+        m.lm_head = synth.quant_matrix(cfg.lm_dtype, cfg.vocab, cfg.hidden, seed, tid + 4)
     return m
 
 

@@ -34,6 +34,8 @@ def _compare(ref_toks, ref_logits, got_toks, got_logits):
 MID = smodel.DecodeConfig(n_layers=6, hidden=256, n_heads=4, n_kv_heads=1, head_dim=128, ffn=512, vocab=8192,
                           max_ctx=160, sliding_window=48, global_layers=(5,))
 TINY_Q8 = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "wdtype": synth.Q8_0, "lm_dtype": synth.Q8_0})
+# the reference's own LM head: the BF16 embedding table (weight tying, transformer.c:393-408)
+TINY_TIED = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF16})
 
 
 # groups: workgroups of the persistent step (None: the decoder's default), 0: the multi-launch step
@@ -47,8 +49,10 @@ TINY_Q8 = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "wdtype": synth.Q8_0, "
     (MID, 33, 40, 24, None),              # head_dim 128, crosses the 48-position window while decoding
     (MID, 33, 40, 24, 0),
     (MID, 33, 40, 24, 96),
+    (TINY_TIED, 37, 40, 12, None),
+    (TINY_TIED, 37, 40, 12, 0),
 ], ids=["tiny", "tiny_graph", "tiny_g16", "tiny_g256", "tiny_q8", "tiny_q8_graph", "mid_window", "mid_window_graph",
-        "mid_window_g96"])
+        "mid_window_g96", "tiny_tied_bf16", "tiny_tied_bf16_graph"])
 def test_decode_matches_oracle(oracle, cfg, seed, prefill, steps, groups):
     from sapphire_amd.engine import Decoder
     print(f"decode cfg={cfg.n_layers}x{cfg.hidden} seed={seed} prefill={prefill} steps={steps} groups={groups}",
@@ -100,6 +104,30 @@ def test_decode_gemma3_270m_64_steps(oracle):
     for groups, (got_toks, got_logits) in runs.items():
         n = _compare(ref_toks, ref_logits, got_toks, got_logits)
         assert n == steps, f"groups={groups}: near-tie at step {n}: tokens agree on steps 0..{n - 1}"
+
+
+def test_decode_gemma3_270m_tied_bf16_lm_head(oracle):
+    """Gemma-3-270M shape with the reference's own LM head, the 335 MB BF16 embedding table
+    (weight tying): 16 greedy steps from KV 1024, persistent and multi-launch steps."""
+    from sapphire_amd.engine import Decoder
+    cfg = smodel.DecodeConfig(**{**smodel.GEMMA3_270M.__dict__, "lm_dtype": synth.BF16})
+    seed, prefill, steps = 20260102, 1024, 16
+    print("decode gemma3-270m tied bf16 lm head", flush=True)
+    m = smodel.synthetic_model(cfg, seed)
+    k, v = m.kv_prefill(prefill)
+    tok = smodel.start_token(cfg, seed)
+    dec = Decoder(m)
+    runs = {}
+    for groups in (128, 0):
+        dec.set_workgroups(groups)
+        dec.set_kv(k, v)
+        runs[groups] = dec.generate(tok, prefill, steps, keep_logits=True)[:2]
+        print(f"gpu done: groups={groups}", flush=True)
+    dec.close()
+    ref_toks, ref_logits = oracle_decode(oracle, m, k, v, tok, prefill, steps, nthreads=16, keep_logits=True)
+    for groups, (got_toks, got_logits) in runs.items():
+        n = _compare(ref_toks, ref_logits, got_toks, got_logits)
+        assert n == steps, f"groups={groups}: near-tie at step {n}"
 
 
 def test_decode_workgroups_validation():

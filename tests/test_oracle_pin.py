@@ -126,9 +126,13 @@ MID = smodel.DecodeConfig(n_layers=6, hidden=256, n_heads=4, n_kv_heads=1, head_
                           vocab=8192, max_ctx=160, sliding_window=48, global_layers=(5,))
 
 
+TINY_TIED = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF16})
+
+
 @pytest.mark.skipif(not ref_decode_available(), reason="oracle/_ref decode harness not built")
-@pytest.mark.parametrize("cfg,seed,prefill,steps", [(smodel.TINY, 5, 30, 12), (MID, 6, 100, 10)],
-                         ids=["tiny", "mid"])
+@pytest.mark.parametrize("cfg,seed,prefill,steps", [(smodel.TINY, 5, 30, 12), (MID, 6, 100, 10),
+                                                    (TINY_TIED, 7, 30, 8)],
+                         ids=["tiny", "mid", "tiny_tied_bf16_lm_head"])
 def test_decode_matches_reference(oracle, cfg, seed, prefill, steps):
     """Greedy decode through the reference's own session/layer functions against the
     oracle's decode step: tokens, logits and the updated KV cache bit for bit. The
