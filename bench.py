@@ -272,6 +272,7 @@ def main() -> int:
     # The same LM head held as BF16 / F32 rows (a weight-tied embedding), on the element
     # types' own GEMV kernel; two copies of each rotate so the weights come from HBM.
     f_lines = {}
+    qout = DeviceArray(gemv_bytes(synth.Q8_0, M_LM, K_LM))
     for name, dt, es in (("gemv_bf16_lm_head", synth.BF16, 2), ("gemv_f32_lm_head", synth.F32, 4)):
         tile = synth.normal_f32((M_LM // 64, K_LM), seed, 40 + dt, 0.0, 0.05)
         if dt == synth.BF16:
@@ -284,6 +285,14 @@ def main() -> int:
         fb = M_LM * K_LM * es + 4 * K_LM + 4 * M_LM
         f_lines[name] = {"us": round(f_ms * 1e3, 2), "GB/s": round(fb / (f_ms * 1e-3) / 1e9, 1),
                          "frac_peak": round(fb / (f_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        # the Q4_0 / Q8_0 producer over the same rows: bytes = source + blocks
+        for qdt in (synth.Q4_0, synth.Q8_0):
+            q_ms = time_alone(lambda i: check(L.sapphire_quantize_dev(qdt, dt, mats[i % n_sets].ptr, M_LM, K_LM,
+                                                                      qout.ptr, stream)))
+            qb = M_LM * K_LM * es + gemv_bytes(qdt, M_LM, K_LM) - 4 * K_LM - 4 * M_LM
+            f_lines[f"quantize_{'bf16' if dt == synth.BF16 else 'f32'}_to_{synth.DTYPE_NAME[qdt].lower()}"
+                    f"_lm_head"] = {"us": round(q_ms * 1e3, 2), "GB/s": round(qb / (q_ms * 1e-3) / 1e9, 1),
+                                    "frac_peak": round(qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         for m_ in mats:
             m_.free()
 

@@ -390,6 +390,82 @@ void oracle_bf16_to_f32(float *dst, const uint16_t *src, int n) {        /* util
 }
 
 /* ------------------------------------------------------------------------- */
+/* Quantizer (the producer of Q4_0 / Q8_0 blocks).                             */
+/* The reference has none: nothing in it creates quantized tensors            */
+/* (tensor.c:108-110, safetensors_reader.c:406-414); its block structs are    */
+/* ggml's. This restates ggml's published reference quantizer                 */
+/* (llama.cpp ggml-quants.c, quantize_row_q8_0_ref / quantize_row_q4_0_ref),  */
+/* adapted to the reference's block structs: an fp32 scale (kernels.h:29-38)  */
+/* and the reference's Q4_0 nibble order, element 2j in the low nibble of     */
+/* byte j and 2j+1 in the high nibble (q4_0_avx.c:61-66; ggml packs j and     */
+/* j+16). Every product and sum is rounded on its own (no contraction):       */
+/*   Q8_0: amax = max|x|; d = amax / 127; id = d ? 1/d : 0;                    */
+/*         q = roundf(x * id) (ties away from zero).                           */
+/*   Q4_0: max = the first x of largest |x| (+0 when all are zero);            */
+/*         d = max / -8; id = d ? 1/d : 0;                                     */
+/*         q = min(15, (int)(x * id + 8.5f)) (truncation: ties round up).      */
+/* Inputs must be finite. Elements past K in the last block are zeros.         */
+/* Parity pins: tests/test_oracle_quant.py (known answers, reconstruction     */
+/* bounds, idempotence on representable blocks, and the layout through the    */
+/* reference's own row kernels).                                              */
+/* ------------------------------------------------------------------------- */
+
+/* Integer codes of the rounded values. For blocks of normal scale these are ggml's
+ * conversions, min(15, (int)v) and (int)v; the guards only define the blocks ggml leaves
+ * undefined, whose scale is subnormal so that 1/d overflows: an infinite product saturates
+ * and a NaN one (0 * inf) gives the code of zero. */
+static int q8_code(float v) { return v != v ? 0 : v > 127.0f ? 127 : v < -127.0f ? -127 : (int)v; }
+static int q4_code(float v) { return v != v ? 8 : v > 15.0f ? 15 : v < 0.0f ? 0 : (int)v; }
+
+static void quantize_block(int dtype, const float *x, void *out) {
+    if (dtype == ORC_Q8_0) {
+        orc_q8_block *b = (orc_q8_block *)out;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        b->scale = d;
+        for (int i = 0; i < 32; ++i) b->q[i] = (uint8_t)(int8_t)q8_code(roundf(x[i] * id));
+    } else {
+        orc_q4_block *b = (orc_q4_block *)out;
+        float amax = 0.0f, max = 0.0f;
+        for (int i = 0; i < 32; ++i)
+            if (amax < fabsf(x[i])) {
+                amax = fabsf(x[i]);
+                max = x[i];
+            }
+        const float d = max / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        b->scale = d;
+        for (int j = 0; j < 16; ++j) {
+            const int q0 = q4_code(x[2 * j] * id + 8.5f), q1 = q4_code(x[2 * j + 1] * id + 8.5f);
+            b->q[j] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+int oracle_quantize(int dtype, int src_dtype, const void *src, int M, int K, void *blocks) {
+    if ((dtype != ORC_Q4_0 && dtype != ORC_Q8_0) || (src_dtype != ORC_F32 && src_dtype != ORC_BF16) || !src ||
+        !blocks || M <= 0 || K <= 0)
+        return -1;
+    const int nb = (K + 31) / 32;
+    const size_t bb = dtype == ORC_Q4_0 ? sizeof(orc_q4_block) : sizeof(orc_q8_block);
+    uint8_t *out = (uint8_t *)blocks;
+    float x[32];
+    for (int r = 0; r < M; ++r)
+        for (int j = 0; j < nb; ++j) {
+            for (int e = 0; e < 32; ++e) {
+                const int k = j * 32 + e;
+                if (k >= K) x[e] = 0.0f;
+                else if (src_dtype == ORC_F32) x[e] = ((const float *)src)[(size_t)r * K + k];
+                else oracle_bf16_to_f32(&x[e], (const uint16_t *)src + (size_t)r * K + k, 1);
+            }
+            quantize_block(dtype, x, out + ((size_t)r * nb + j) * bb);
+        }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
 /* Decode step.                                                                */
 /* ------------------------------------------------------------------------- */
 

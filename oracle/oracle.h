@@ -23,6 +23,9 @@ extern "C" {
 /* dtype codes: identical to tensor_dtype_t in the reference include/tensor.h:17-23 */
 enum { ORC_F32 = 0, ORC_BF16 = 1, ORC_F16 = 2, ORC_Q4_0 = 3, ORC_Q8_0 = 4 };
 
+/* ---- quantizer: F32 / BF16 rows [M][K] -> [M][ceil(K/32)] Q4_0 / Q8_0 blocks ---- */
+int   oracle_quantize(int dtype, int src_dtype, const void *src, int M, int K, void *blocks);
+
 /* ---- block formats and unpack (include/kernels.h:29-38) ---- */
 void  oracle_q4_0_unpack_ints(const void *blocks, int nblocks, int8_t *out /* 32*nblocks */);
 void  oracle_q8_0_unpack_ints(const void *blocks, int nblocks, int8_t *out /* 32*nblocks */);

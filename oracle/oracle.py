@@ -89,6 +89,7 @@ class Oracle:
             getattr(L, n).argtypes = [i, vp, vp, i]
         L.oracle_gemm_f.restype = i
         L.oracle_gemm_f.argtypes = [i, vp, i, i, vp, i, vp, i]
+        L.oracle_quantize.argtypes = [i, i, vp, i, i, vp]
 
     # -- numpy conveniences --------------------------------------------------
     def gemv(self, dtype, blocks, x, nthreads=1):
@@ -118,6 +119,15 @@ class Oracle:
         Y = np.empty((X.shape[0], m), np.float32)
         assert self.lib.oracle_gemm_f(dtype, _p(w), m, k, _p(X), X.shape[0], _p(Y), m) == 0
         return Y
+
+    def quantize(self, dtype, src_dtype, w):
+        """[M, K] F32 (float32) or BF16 (uint16 bits) rows -> [M, ceil(K/32)] blocks."""
+        from sapphire_amd import synth
+        w = np.ascontiguousarray(w)
+        m, k = w.shape
+        out = np.zeros((m, (k + 31) // 32), synth.block_dtype(dtype))
+        assert self.lib.oracle_quantize(dtype, src_dtype, _p(w), m, k, _p(out)) == 0
+        return out
 
     def dequant(self, dtype, blocks):
         flat = np.ascontiguousarray(blocks).reshape(-1)

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/kernels.h"
+#include "../../include/quantize.h"
 #include "internal.h"
 #include "tensor_impl.h"
 
@@ -311,6 +312,35 @@ int kernel_gemv(kernel_context_t *ctx, float *y, const tensor_t *A, const float 
             set_error("kernel_gemv unsupported dtype %d", (int)tensor_dtype(A));
             return -1;
     }
+}
+
+int kernel_quantize(kernel_context_t *ctx, void *blocks, tensor_dtype_t dtype, const tensor_t *src) {
+    if (!blocks || !src || !src->data) {
+        set_error("kernel_quantize null pointer");
+        return -1;
+    }
+    if (tensor_ndim(src) != 2 || (tensor_dtype(src) != DTYPE_F32 && tensor_dtype(src) != DTYPE_BF16) ||
+        (dtype != DTYPE_Q4_0 && dtype != DTYPE_Q8_0)) {
+        set_error("kernel_quantize: source must be a 2-D F32 or BF16 tensor, destination Q4_0 or Q8_0");
+        return -1;
+    }
+    const int M = tensor_shape(src)[0], K = tensor_shape(src)[1];
+    if (M <= 0 || K <= 0) {
+        set_error("kernel_quantize: non-positive shape");
+        return -1;
+    }
+    kernel_context_t *c = ctx ? ctx : default_ctx();
+    if (!c || !c->initialized) {
+        set_error("kernel context not initialized");
+        return -1;
+    }
+    const int sdt = tensor_dtype(src);
+    const size_t sb = (size_t)M * K * (sdt == DTYPE_F32 ? 4 : 2);
+    const size_t ob = q_aos_bytes(dtype, M, K);
+    return run_staged(c, {HostVec{src->data, nullptr, sb}}, {HostVec{nullptr, blocks, ob}},
+                      [&](std::vector<void *> &in, std::vector<void *> &out, hipStream_t s) {
+                          return launch_quantize(dtype, sdt, in[0], M, K, out[0], s);
+                      });
 }
 
 int kernel_gemm(kernel_context_t *ctx, float *Y, const tensor_t *A, const float *X, int batch_size, int out_stride) {

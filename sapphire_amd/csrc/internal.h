@@ -97,6 +97,8 @@ struct GemmOut {
 int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
                          void *ws, hipStream_t s);
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
+// F32 / BF16 rows [M][K] -> [M][ceil(K/32)] Q4_0 / Q8_0 blocks (AOS), quantize.hip
+int launch_quantize(int dst_dtype, int src_dtype, const void *src, int M, int K, void *blocks, hipStream_t s);
 
 int launch_rmsnorm(float *out, const float *in, const float *w, float eps, int dim, int batch, bool delta,
                    hipStream_t s);

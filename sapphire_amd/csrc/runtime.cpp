@@ -4,6 +4,7 @@
 #include <cstring>
 #include <mutex>
 
+#include "../../include/quantize.h"
 #include "../../include/sapphire_hip.h"
 #include "internal.h"
 
@@ -221,6 +222,10 @@ int sapphire_gemm_q_fused_dev(int dt, const void *w, int M, int K, int batch, co
     go.parts = out->parts;
     go.geglu = out->geglu != 0;
     return launch_gemm_tiled_ex(dt, w, M, K, batch, gi, go, ws, as_stream(stream));
+}
+
+int sapphire_quantize_dev(int dst_dtype, int src_dtype, const void *src, int M, int K, void *blocks, void *stream) {
+    return launch_quantize(dst_dtype, src_dtype, src, M, K, blocks, as_stream(stream));
 }
 
 int sapphire_gemv_f_dev(int dt, const void *w, int M, int K, const float *x, float *y, void *stream) {

@@ -113,6 +113,11 @@ def gemv(qm: QMatrix, x: DeviceArray, y: DeviceArray, layout: int = 1, stream=No
     check(lib().sapphire_gemv_q_dev(qm.dtype, layout, qm.ptr(layout), qm.M, qm.K, x.ptr, y.ptr, stream), "gemv")
 
 
+def quantize(dtype: int, src_dtype: int, src: DeviceArray, M: int, K: int, blocks: DeviceArray, stream=None) -> None:
+    """F32 / BF16 rows [M][K] on the device -> M * ceil(K/32) Q4_0 / Q8_0 blocks (AOS)."""
+    check(lib().sapphire_quantize_dev(dtype, src_dtype, src.ptr, M, K, blocks.ptr, stream), "quantize")
+
+
 def gemv_f(dtype: int, w: DeviceArray, M: int, K: int, x: DeviceArray, y: DeviceArray, offset: int = 0,
            stream=None) -> None:
     """y = W . x for a row-major F32 / BF16 matrix held at w.ptr + offset bytes."""
