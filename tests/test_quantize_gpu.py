@@ -120,3 +120,41 @@ def test_kernel_quantize_host_api(hip, oracle, dtype, src_dtype):
     finally:
         hip.tensor_release(A)
         hip.kernel_ctx_destroy(ctx)
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8], ids=["q4_0", "q8_0"])
+def test_quantize_checkpoint(hip, oracle, dtype, tmp_path):
+    """A BF16 safetensors checkpoint with Gemma-3 tensor names (two layers of the TINY
+    shape): the projections come back as the oracle's blocks, everything else unchanged."""
+    import torch
+    from safetensors.torch import save_file
+    from sapphire_amd import checkpoint
+    from sapphire_amd import model as smodel
+    print(f"quantize checkpoint dtype={dtype}", flush=True)
+    cfg = smodel.TINY
+    src = {}
+    tid = 0
+    for l in range(2):
+        for p in checkpoint.PROJECTIONS:
+            short = {"q_proj": "wq", "k_proj": "wk", "v_proj": "wv", "o_proj": "wo", "gate_proj": "wgate",
+                     "up_proj": "wup", "down_proj": "wdown"}[p.split(".")[1]]
+            m, k = smodel.proj_shape(cfg, short)
+            tid += 1
+            src[f"model.layers.{l}.{p}"] = torch.from_numpy(
+                synth.bf16_normal((m, k), 17, tid).view(np.int16)).view(torch.bfloat16)
+        src[f"model.layers.{l}.input_layernorm.weight"] = torch.from_numpy(synth.normal_f32(cfg.hidden, 17, 90 + l))
+    src["model.embed_tokens.weight"] = torch.from_numpy(
+        synth.bf16_normal((cfg.vocab, cfg.hidden), 17, 99).view(np.int16)).view(torch.bfloat16)
+    sp, dp = str(tmp_path / "src.safetensors"), str(tmp_path / "q.safetensors")
+    save_file(src, sp)
+    done = checkpoint.quantize_checkpoint(sp, dp, dtype)
+    assert len(done) == 14
+    tensors, quantized = checkpoint.load(dp)
+    assert set(quantized) == set(done) and set(tensors) == set(src) - set(done)
+    for name, (dt, blocks, k) in quantized.items():
+        w = src[name].view(torch.int16).numpy().view(np.uint16)
+        assert dt == dtype and k == w.shape[1]
+        assert blocks.tobytes() == oracle.quantize(dtype, BF16, w).tobytes(), name
+    for name, t in tensors.items():
+        assert torch.equal(t.view(torch.int16) if t.dtype == torch.bfloat16 else t,
+                           src[name].view(torch.int16) if src[name].dtype == torch.bfloat16 else src[name])
