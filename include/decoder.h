@@ -74,6 +74,16 @@ int sapphire_decoder_get_kv(sapphire_decoder_t *dec, float *k, float *v);
 int sapphire_decoder_generate(sapphire_decoder_t *dec, int token, int pos, int steps, int *tokens_out,
                               float *logits_out, float *elapsed_ms);
 
+/* Prefill: tokens[0..n) at positions pos..pos+n-1 of sequence `seq` (0 for a one-sequence
+ * decoder) run through every layer and leave their K/V rows in that sequence's cache, as
+ * inference_forward_batch does for a prompt without logits (inference.c:236-244, 616-651:
+ * every row of a chunk is written before its attention reads any, attention.c:292-309).
+ * Chunks of up to 16 tokens run their projections as one matrix-core GEMM. No logits; the
+ * next call is sapphire_decoder_generate with the prompt's last token at pos + n.
+ * Needs hidden, n_heads*head_dim and ffn multiples of 128 and hidden <= 1152 (-1
+ * otherwise). elapsed_ms, if not NULL, receives the device time. 0 / -1. */
+int sapphire_decoder_prefill(sapphire_decoder_t *dec, int seq, const int *tokens, int n, int pos,
+                             float *elapsed_ms);
 /* The form of a one-sequence step. groups > 0: the layers run as one persistent cooperative
  * kernel of `groups` workgroups (all co-resident) whose stages exchange epoch-tagged vectors
  * instead of waiting for kernel boundaries; this is the default (128 workgroups, or the value

@@ -354,6 +354,21 @@ def oracle_decode(orc: "Oracle", model, k_cache, v_cache, token, pos, steps, nth
     return tokens, logits
 
 
+def oracle_prefill(orc: "Oracle", model, k_cache, v_cache, tokens, pos, nthreads=1):
+    """The oracle's decode step over given tokens at positions pos.. (their logits unused):
+    the K/V rows a prompt leaves in the caches, updated in place. Returns the last logits."""
+    last = None
+    for i, t in enumerate(tokens):
+        _, last = oracle_decode_forced(orc, model, k_cache, v_cache, int(t), pos + i, nthreads)
+    return last
+
+
+def oracle_decode_forced(orc: "Oracle", model, k_cache, v_cache, token, pos, nthreads=1):
+    """One oracle decode step of `token` at `pos` -> (greedy token, logits)."""
+    toks, logits = oracle_decode(orc, model, k_cache, v_cache, token, pos, 1, nthreads=nthreads)
+    return int(toks[0]), logits[0]
+
+
 def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False):
     """Greedy decode through the compiled reference engine (oracle/_ref)."""
     cfg = model.cfg

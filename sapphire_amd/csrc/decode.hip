@@ -96,6 +96,29 @@ __global__ __launch_bounds__(kThreads) void dec_prologue_kernel(GemvIn in, int K
 // merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL). Scores are
 // summed by DPP into wave-uniform values and the weights are powers of two of log2-scaled
 // scores (one exp2 each).
+// K/V rows of a batch (sequence blockIdx.x): the same norm_rope_heads on the same inputs
+// as dec_attn_part_kernel, so the rows are bit-identical to the ones it writes.
+__global__ __launch_bounds__(kThreads) void dec_kv_write_kernel(AttnArgs a) {
+    const size_t b = blockIdx.x;
+    const float *qkv = a.qkv + b * a.qkv_stride;
+    float *kc = a.kc + b * a.kv_stride, *vc = a.vc + b * a.kv_stride;
+    const int pos = a.d_pos[b];
+    __shared__ float raw[kAttnMaxKV];
+    __shared__ float ks[kAttnMaxKV];
+    __shared__ float part8[8 * 16];
+    __shared__ float ss[16];
+    const int hd = a.hd, nkv = a.nkv, nq = a.nh * hd;
+    for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) raw[i] = qkv[nq + i];
+    __syncthreads();
+    norm_rope_heads(raw, nkv, hd, a.kn, a.cos_t + (size_t)pos * hd, a.sin_t + (size_t)pos * hd, a.eps, ks, part8, ss);
+    for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) {
+        const int h = i / hd, d = i - h * hd;
+        const size_t off = ((size_t)h * a.max_ctx + pos) * hd + d;
+        kc[off] = ks[i];
+        vc[off] = qkv[nq + nkv * hd + i];
+    }
+}
+
 template <int DPL, int NH>
 __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     {   // sequence blockIdx.y of a batch
@@ -154,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     norm_rope_heads(raw, NH, hd, a.qn, cs, sn, a.eps, qs, part8, ss);
     norm_rope_heads(raw + NH * hd, nkv, hd, a.kn, cs, sn, a.eps, ks, part8, ss);
     const float *vnew = raw + (NH + nkv) * hd;
-    if (blockIdx.x == 0)   // kv_cache_write_token: [head][pos][dim]
+    if (blockIdx.x == 0 && !a.kv_written)   // kv_cache_write_token: [head][pos][dim]
         for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) {
             const int h = i / hd, d = i - h * hd;
             const size_t off = ((size_t)h * a.max_ctx + pos) * hd + d;
@@ -460,6 +483,15 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
         hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplitBatch>, dim3(a.nh, a.batch), dim3(kThreads), 0, s,
                            a.part, a.nh, a.hd, out, a.out_stride);
     return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
+}
+
+int dec_kv_write(const AttnArgs &a, hipStream_t s) {
+    if (a.nkv * a.hd > kAttnMaxKV || a.batch <= 0) {
+        set_error("KV write: %d K/V heads of dim %d", a.nkv, a.hd);
+        return -1;
+    }
+    hipLaunchKernelGGL(dec_kv_write_kernel, dim3(a.batch), dim3(kThreads), 0, s, a);
+    return hip_ok(hipGetLastError(), "KV write launch") ? 0 : -1;
 }
 
 int dec_embed(const uint16_t *embed, int hidden, int vocab, float es, const int *d_token, float *resid,

@@ -52,12 +52,20 @@ struct AttnArgs {
     // + b*kv_stride, d_pos[b], and its own partials; out + b*out_stride
     int batch = 1;
     size_t qkv_stride = 0, kv_stride = 0, out_stride = 0;
+    // the K/V rows of every position already hold this batch's tokens (dec_kv_write ran):
+    // the attention kernel writes none (a prefill chunk of one sequence, whose tokens read
+    // each other's rows)
+    bool kv_written = false;
 };
 // QK-norm, RoPE, KV write and split attention partials, then their combination into
 // out[nh*hd] (attention.c:93-163, 271-309; kv_cache.c:252-278). part holds
 // attn_part_floats(nh, hd) floats per sequence.
 size_t attn_part_floats(int nh, int hd);
 int dec_attention(const AttnArgs &a, float *out, hipStream_t s);
+// The K/V rows of the batch only: K = rope(rmsnorm_delta(k, kn)) and V as projected, at
+// d_pos[b] (attention.c:292-309 writes every row of a batch before its attention runs).
+// Bit-identical to the rows dec_attention writes.
+int dec_kv_write(const AttnArgs &a, hipStream_t s);
 
 // resid[i] = bf16 row of *d_token * es (transformer.c:347-365); a token outside [0, vocab)
 // reads row 0

@@ -81,6 +81,15 @@ struct sapphire_decoder {
     uint32_t *seq = nullptr;
     int *perr = nullptr;
     uint64_t persist_steps = 0;
+    // prefill (chunks of up to kPrefillChunk tokens of one sequence through the batched
+    // GEMMs); pf_ok is false when the shapes do not fit the TILED GEMM
+    bool pf_ok = false;
+    float *pf_resid[2] = {nullptr, nullptr};
+    float *pf_qkv = nullptr, *pf_attn = nullptr, *pf_o = nullptr, *pf_g = nullptr;
+    float *pf_dparts = nullptr, *pf_dout = nullptr, *pf_part = nullptr;
+    int *pf_tok = nullptr;       // [kPrefillChunk] tokens, then [kPrefillChunk] positions
+    std::vector<hipGraph_t> pf_graph;          // per sequence: a full chunk's pass, captured once
+    std::vector<hipGraphExec_t> pf_exec;
 };
 
 namespace {
@@ -224,6 +233,16 @@ bool layer_is_global(const sapphire_decoder_config_t &c, int l) {   // attention
     return ((l + 1) % 6) == 0;
 }
 
+// Tokens of one prefill chunk: the batched GEMM's widest batch.
+constexpr int kPrefillChunk = 16;
+
+// Shapes the TILED matrix-core GEMM takes: every projection K a multiple of 128 and the
+// hidden size at most 36 blocks (the norms are formed inside one K chunk).
+bool tiled_shapes_ok(const sapphire_decoder_config_t &c) {
+    const int nq = c.n_heads * c.head_dim;
+    return c.hidden % 128 == 0 && nq % 128 == 0 && c.ffn % 128 == 0 && c.hidden <= 1152;
+}
+
 // A persistent-step wait longer than this many polls (about a second) is a failure.
 constexpr int kPersistSpinLimit = 1 << 19;
 
@@ -352,53 +371,69 @@ int enqueue_step(sapphire_decoder *d) {
     return enqueue_lm_head(d);
 }
 
-// One step of the batched decoder, enqueued on d->stream (recorded into the graph).
-int enqueue_step_batch(sapphire_decoder *d) {
+// One batched pass over the layers: r.B token vectors, either the sequences of a batched
+// decode step (each with its own cache and position) or a prefill chunk of one sequence (one
+// cache, kv_stride 0, positions pos..pos+B-1, all K/V rows written before attention reads
+// them, as attention.c:292-309 does for a batch). Leaves the last layer's down projection as
+// K-chunk partials in r.dparts and returns the index of r.resid holding the residual stream.
+struct BatchRun {
+    int B = 0;
+    const int *d_tokens = nullptr, *d_pos = nullptr;
+    float *kc = nullptr, *vc = nullptr;   // layer 0 of the first sequence's caches
+    size_t kv_stride = 0;                 // between sequences (0: one shared cache)
+    bool prefill = false;
+    float *resid[2] = {nullptr, nullptr};
+    float *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr, *dparts = nullptr, *dout = nullptr;
+    float *part = nullptr;
+    void *gws = nullptr;
+};
+
+int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
     const auto &c = d->cfg;
     hipStream_t s = d->stream;
-    const int B = d->batch, H = c.hidden, hd = c.head_dim;
+    const int B = r.B, H = c.hidden, hd = c.head_dim;
     const int nq = c.n_heads * hd, nqkv = nq + 2 * c.n_kv_heads * hd;
     const float es = sqrtf((float)H);
     const float scale = 1.0f / sqrtf(c.query_pre_attn_scalar > 0.f ? c.query_pre_attn_scalar : (float)hd);
     const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
     const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
     const int nsd = gemm_splits(c.ffn);
-    if (dec_embed_batch(d->embed, H, c.vocab, es, d->state, B, d->resid[0], s) != 0) return -1;
+    if (dec_embed_batch(d->embed, H, c.vocab, es, r.d_tokens, B, r.resid[0], s) != 0) return -1;
     int cur = 0;
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer &L = d->layers[l];
         // previous layer's finalize (transformer.c:231-239) + attention pre-norm (attention.c:316-325)
         GemmIn qi;
-        qi.x = d->resid[cur];
+        qi.x = r.resid[cur];
         qi.ldx = H;
         qi.w_norm = L.n_attn;
         qi.eps = c.eps;
         if (l > 0) {
             // the previous down projection's K-chunk partial sums, added once by a short kernel
             // (cheaper than every staging workgroup adding them)
-            if (launch_sum_parts(d->dparts, nsd, (size_t)B * H, B, H, d->dout, H, s) != 0) return -1;
-            qi.parts = d->dout;
+            if (launch_sum_parts(r.dparts, nsd, (size_t)B * H, B, H, r.dout, H, s) != 0) return -1;
+            qi.parts = r.dout;
             qi.nparts = 1;
             qi.ldp = H;
             qi.w_delta = d->layers[l - 1].n_ffn_post;
-            qi.resid_out = d->resid[1 - cur];
+            qi.resid_out = r.resid[1 - cur];
             qi.ldr = H;
             cur = 1 - cur;
         }
         GemmOut qo;
-        qo.y = d->qkv;
+        qo.y = r.qkv;
         qo.ldy = nqkv;
-        if (launch_gemm_tiled_ex(c.wdtype, L.t_qkv, nqkv, H, B, qi, qo, d->gws, s) != 0) return -1;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_qkv, nqkv, H, B, qi, qo, r.gws, s) != 0) return -1;
         AttnArgs at;
-        at.qkv = d->qkv;
+        at.qkv = r.qkv;
         at.qn = L.qn;
         at.kn = L.kn;
         at.cos_t = L.global ? d->cos_g : d->cos_l;
         at.sin_t = L.global ? d->sin_g : d->sin_l;
-        at.kc = d->kc + (size_t)l * layer_kv;
-        at.vc = d->vc + (size_t)l * layer_kv;
-        at.d_pos = d->state + B;
-        at.part = d->attn_part;
+        at.kc = r.kc + (size_t)l * layer_kv;
+        at.vc = r.vc + (size_t)l * layer_kv;
+        at.d_pos = r.d_pos;
+        at.part = r.part;
         at.nh = c.n_heads;
         at.nkv = c.n_kv_heads;
         at.hd = hd;
@@ -408,42 +443,74 @@ int enqueue_step_batch(sapphire_decoder *d) {
         at.eps = c.eps;
         at.batch = B;
         at.qkv_stride = (size_t)nqkv;
-        at.kv_stride = (size_t)c.n_layers * layer_kv;
+        at.kv_stride = r.kv_stride;
         at.out_stride = (size_t)nq;
-        if (dec_attention(at, d->attn, s) != 0) return -1;
+        if (r.prefill) {
+            if (dec_kv_write(at, s) != 0) return -1;
+            at.kv_written = true;
+        }
+        if (dec_attention(at, r.attn, s) != 0) return -1;
         GemmIn oi;
-        oi.x = d->attn;
+        oi.x = r.attn;
         oi.ldx = nq;
         GemmOut oo;
-        oo.y = d->o;
+        oo.y = r.o;
         oo.ldy = H;
-        if (launch_gemm_tiled_ex(c.wdtype, L.t_o, H, nq, B, oi, oo, d->gws, s) != 0) return -1;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_o, H, nq, B, oi, oo, r.gws, s) != 0) return -1;
         // post-attention norm + residual (attention.c:356-366), FFN pre-norm (transformer.c:119-121),
         // gate/up projections with the GeGLU (transformer.c:126-157)
         GemmIn fi;
-        fi.x = d->resid[cur];
+        fi.x = r.resid[cur];
         fi.ldx = H;
-        fi.parts = d->o;
+        fi.parts = r.o;
         fi.nparts = 1;
         fi.ldp = H;
         fi.w_delta = L.n_attn_post;
-        fi.resid_out = d->resid[1 - cur];
+        fi.resid_out = r.resid[1 - cur];
         fi.ldr = H;
         fi.w_norm = L.n_ffn;
         fi.eps = c.eps;
         cur = 1 - cur;
         GemmOut fo;
-        fo.y = d->g;
+        fo.y = r.g;
         fo.ldy = c.ffn;
         fo.geglu = true;
-        if (launch_gemm_tiled_ex(c.wdtype, L.t_gu, 2 * c.ffn, H, B, fi, fo, d->gws, s) != 0) return -1;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_gu, 2 * c.ffn, H, B, fi, fo, r.gws, s) != 0) return -1;
         GemmIn di;
-        di.x = d->g;
+        di.x = r.g;
         di.ldx = c.ffn;
         GemmOut dout;
-        dout.parts = d->dparts;
-        if (launch_gemm_tiled_ex(c.wdtype, L.t_down, H, c.ffn, B, di, dout, d->gws, s) != 0) return -1;
+        dout.parts = r.dparts;
+        if (launch_gemm_tiled_ex(c.wdtype, L.t_down, H, c.ffn, B, di, dout, r.gws, s) != 0) return -1;
     }
+    return cur;
+}
+
+// One step of the batched decoder, enqueued on d->stream (recorded into the graph).
+int enqueue_step_batch(sapphire_decoder *d) {
+    const auto &c = d->cfg;
+    hipStream_t s = d->stream;
+    const int B = d->batch, H = c.hidden;
+    const int nsd = gemm_splits(c.ffn);
+    BatchRun r;
+    r.B = B;
+    r.d_tokens = d->state;
+    r.d_pos = d->state + B;
+    r.kc = d->kc;
+    r.vc = d->vc;
+    r.kv_stride = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim;
+    r.resid[0] = d->resid[0];
+    r.resid[1] = d->resid[1];
+    r.qkv = d->qkv;
+    r.attn = d->attn;
+    r.o = d->o;
+    r.g = d->g;
+    r.dparts = d->dparts;
+    r.dout = d->dout;
+    r.part = d->attn_part;
+    r.gws = d->gws;
+    const int cur = enqueue_layers_batch(d, r);
+    if (cur < 0) return -1;
     // last finalize + final norm (transformer.c:400-406), LM head, greedy tokens
     if (launch_sum_parts(d->dparts, nsd, (size_t)B * H, B, H, d->dout, H, s) != 0) return -1;
     GemmIn li;
@@ -498,6 +565,10 @@ void sapphire_decoder_destroy(sapphire_decoder_t *d) {
     if (d->stream) (void)hipStreamSynchronize(d->stream);
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
     if (d->graph) (void)hipGraphDestroy(d->graph);
+    for (hipGraphExec_t e : d->pf_exec)
+        if (e) (void)hipGraphExecDestroy(e);
+    for (hipGraph_t g : d->pf_graph)
+        if (g) (void)hipGraphDestroy(g);
     for (void *p : d->allocs) (void)hipFree(p);
     if (d->stream) (void)hipStreamDestroy(d->stream);
     delete d;
@@ -545,6 +616,7 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
     if (!d) return nullptr;
     d->cfg = *cfg;
     d->batch = batch;
+    d->pf_ok = tiled_shapes_ok(*cfg);
     const int B = batch;
     const auto &c = d->cfg;
     auto fail = [&]() -> sapphire_decoder_t * {
@@ -571,7 +643,8 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
                 !upload_packed(d, c.wdtype, {{w->wup[l], c.ffn}}, H, &L.up, "wup") ||
                 !upload_packed(d, c.wdtype, {{w->wdown[l], H}}, c.ffn, &L.down, "wdown"))
                 return fail();
-        } else {
+        }
+        if (d->pf_ok) {   // TILED copies: the batched step and the prefill GEMMs
             if (!upload_tiled(d, c.wdtype, {{w->wq[l], nq}, {w->wk[l], nk}, {w->wv[l], nk}}, H, false, &L.t_qkv,
                               "wqkv") ||
                 !upload_tiled(d, c.wdtype, {{w->wo[l], H}}, nq, false, &L.t_o, "wo") ||
@@ -656,13 +729,28 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
         !dev_alloc_t(d, &d->attn_part, b * attn_part_floats(c.n_heads, hd), "attn partials") ||
         !dev_alloc_t(d, &d->state, 2 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log"))
         return fail();
-    if (B > 1) {
+    if (B > 1 || d->pf_ok) {
         const size_t wsb = std::max({gemm_workspace_bytes(H, c.ffn), gemm_workspace_bytes(H, nq),
                                      gemm_workspace_bytes(c.vocab, H)});
+        if (!dev_alloc(d, &d->gws, wsb, "gemm workspace")) return fail();
+    }
+    if (B > 1) {
         if (!dev_alloc_t(d, &d->dparts, (size_t)gemm_splits(c.ffn) * b * H, "down partials") ||
             !dev_alloc_t(d, &d->dout, b * H, "down output") ||
-            !dev_alloc_t(d, &d->amax_part, argmax_batch_part_floats(c.vocab, B), "argmax partials") ||
-            !dev_alloc(d, &d->gws, wsb, "gemm workspace"))
+            !dev_alloc_t(d, &d->amax_part, argmax_batch_part_floats(c.vocab, B), "argmax partials"))
+            return fail();
+    }
+    if (d->pf_ok) {
+        const size_t p = kPrefillChunk;
+        if (!dev_alloc_t(d, &d->pf_resid[0], p * H, "prefill resid") ||
+            !dev_alloc_t(d, &d->pf_resid[1], p * H, "prefill resid") ||
+            !dev_alloc_t(d, &d->pf_qkv, p * (nq + 2 * nk), "prefill qkv") ||
+            !dev_alloc_t(d, &d->pf_attn, p * nq, "prefill attn") || !dev_alloc_t(d, &d->pf_o, p * H, "prefill o") ||
+            !dev_alloc_t(d, &d->pf_g, p * c.ffn, "prefill g") ||
+            !dev_alloc_t(d, &d->pf_dparts, (size_t)gemm_splits(c.ffn) * p * H, "prefill partials") ||
+            !dev_alloc_t(d, &d->pf_dout, p * H, "prefill down") ||
+            !dev_alloc_t(d, &d->pf_part, p * attn_part_floats(c.n_heads, hd), "prefill attention partials") ||
+            !dev_alloc_t(d, &d->pf_tok, 2 * p, "prefill tokens"))
             return fail();
     }
     if (B == 1 && !setup_persistent(d)) return fail();
@@ -888,6 +976,93 @@ int sapphire_decoder_set_workgroups(sapphire_decoder_t *d, int groups) {
 }
 
 int sapphire_decoder_workgroups(const sapphire_decoder_t *d) { return d ? d->groups : -1; }
+
+int sapphire_decoder_prefill(sapphire_decoder_t *d, int seq, const int *tokens, int n, int pos, float *elapsed_ms) {
+    if (!d || !tokens || n <= 0 || seq < 0 || seq >= d->batch || pos < 0 || pos + n > d->cfg.max_ctx) {
+        set_error("sapphire_decoder_prefill: bad arguments (sequence %d, %d tokens at position %d)", seq, n, pos);
+        return -1;
+    }
+    if (!d->pf_ok) {
+        set_error("sapphire_decoder_prefill: needs hidden, n_heads*head_dim and ffn multiples of 128, hidden <= 1152");
+        return -1;
+    }
+    const auto &c = d->cfg;
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.vocab) {
+            set_error("sapphire_decoder_prefill: token %d (%d) outside the vocabulary", i, tokens[i]);
+            return -1;
+        }
+    SPH_CHECK(hipSetDevice(d->device));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    // per chunk: its tokens, then its positions (the host array outlives the stream's reads)
+    const int nchunks = (n + kPrefillChunk - 1) / kPrefillChunk;
+    std::vector<int> host((size_t)nchunks * 2 * kPrefillChunk, 0);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (elapsed_ms) {
+        SPH_CHECK(hipEventCreate(&e0));
+        SPH_CHECK(hipEventCreate(&e1));
+        SPH_CHECK(hipEventRecord(e0, d->stream));
+    }
+    const size_t seq_kv = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim;
+    for (int k = 0; k < nchunks; ++k) {
+        const int c0 = k * kPrefillChunk, m = std::min(kPrefillChunk, n - c0);
+        int *h = host.data() + (size_t)k * 2 * kPrefillChunk;
+        for (int i = 0; i < m; ++i) {
+            h[i] = tokens[c0 + i];
+            h[kPrefillChunk + i] = pos + c0 + i;
+        }
+        SPH_CHECK(hipMemcpyAsync(d->pf_tok, h, sizeof(int) * 2 * kPrefillChunk, hipMemcpyHostToDevice, d->stream));
+        BatchRun r;
+        const bool full = m == kPrefillChunk;
+        r.B = m;
+        r.d_tokens = d->pf_tok;
+        r.d_pos = d->pf_tok + kPrefillChunk;
+        r.kc = d->kc + (size_t)seq * seq_kv;
+        r.vc = d->vc + (size_t)seq * seq_kv;
+        r.kv_stride = 0;
+        r.prefill = true;
+        r.resid[0] = d->pf_resid[0];
+        r.resid[1] = d->pf_resid[1];
+        r.qkv = d->pf_qkv;
+        r.attn = d->pf_attn;
+        r.o = d->pf_o;
+        r.g = d->pf_g;
+        r.dparts = d->pf_dparts;
+        r.dout = d->pf_dout;
+        r.part = d->pf_part;
+        r.gws = d->gws;
+        if (!full) {   // the last, shorter chunk runs its launches directly
+            if (enqueue_layers_batch(d, r) < 0) return -1;
+            continue;
+        }
+        // a full chunk replays the sequence's captured pass (tokens and positions are device data)
+        if (d->pf_exec.empty()) {
+            d->pf_graph.assign((size_t)d->batch, nullptr);
+            d->pf_exec.assign((size_t)d->batch, nullptr);
+        }
+        if (!d->pf_exec[seq]) {
+            SPH_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+            const int rc = enqueue_layers_batch(d, r);
+            hipGraph_t g = nullptr;
+            const hipError_t e = hipStreamEndCapture(d->stream, &g);
+            if (rc < 0 || !hip_ok(e, "hipStreamEndCapture")) {
+                if (g) (void)hipGraphDestroy(g);
+                return -1;
+            }
+            d->pf_graph[seq] = g;
+            SPH_CHECK(hipGraphInstantiate(&d->pf_exec[seq], g, nullptr, nullptr, 0));
+        }
+        SPH_CHECK(hipGraphLaunch(d->pf_exec[seq], d->stream));
+    }
+    if (elapsed_ms) SPH_CHECK(hipEventRecord(e1, d->stream));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    if (elapsed_ms) {
+        SPH_CHECK(hipEventElapsedTime(elapsed_ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+    }
+    return 0;
+}
 
 int sapphire_decoder_generate(sapphire_decoder_t *d, int token, int pos, int steps, int *tokens_out, float *logits_out,
                               float *elapsed_ms) {

@@ -56,6 +56,8 @@ def _protos(L):
     L.sapphire_decoder_set_workgroups.argtypes = [C.c_void_p, C.c_int]
     L.sapphire_decoder_workgroups.restype = C.c_int
     L.sapphire_decoder_workgroups.argtypes = [C.c_void_p]
+    L.sapphire_decoder_prefill.restype = C.c_int
+    L.sapphire_decoder_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]
     L.sapphire_decoder_generate_batch.restype = C.c_int
     L.sapphire_decoder_generate_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                                                   C.c_void_p, C.POINTER(C.c_float)]
@@ -148,6 +150,15 @@ class Decoder:
                                                              logits.ctypes.data if logits is not None else None,
                                                              C.byref(ms)), "generate_batch")
         return toks, logits, float(ms.value)
+
+    def prefill(self, tokens, pos: int, seq: int = 0) -> float:
+        """Runs tokens at positions pos.. of sequence `seq` through the layers (their K/V rows
+        into the cache, no logits); returns the device milliseconds."""
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        ms = C.c_float(0.0)
+        self._check(self.lib.sapphire_decoder_prefill(self.ptr, int(seq), t.ctypes.data, int(t.shape[0]), int(pos),
+                                                      C.byref(ms)), "prefill")
+        return float(ms.value)
 
     def generate(self, token: int, pos: int, steps: int, keep_logits: bool = False):
         """(tokens[steps], logits[steps, vocab] or None, device milliseconds)."""

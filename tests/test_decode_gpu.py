@@ -189,3 +189,83 @@ def test_decode_repeatable(oracle):
             dec2.generate(5, m.cfg.max_ctx - 2, 8)      # positions past max_ctx are refused
         finally:
             dec2.close()
+
+
+# ---- prefill (sapphire_decoder_prefill) ----
+
+def _kv_close(got, ref, sl, what):
+    d = np.abs(got[:, :, sl] - ref[:, :, sl]).max() / max(np.abs(ref[:, :, sl]).max(), 1e-30)
+    assert d <= REL, f"{what} cache rows differ: {d:.2e}"
+
+
+@pytest.mark.parametrize("cfg,seed,kv0,n,steps", [
+    (smodel.TINY, 41, 0, 40, 8),       # chunks 16 + 16 + 8, local layers slide while prefilling
+    (MID, 42, 20, 37, 10),             # on top of 20 cached positions; chunks 16 + 16 + 5
+    (smodel.GEMMA3_270M, 43, 0, 100, 16),
+], ids=["tiny", "mid_on_cache", "gemma3_270m"])
+def test_prefill_matches_oracle(oracle, cfg, seed, kv0, n, steps):
+    """A prompt through sapphire_decoder_prefill, then greedy decode from its last token:
+    K/V rows and the decoded tokens and logits against the oracle running the same tokens
+    one decode step at a time (the reference's batched prefill computes the same thing:
+    every row of a chunk is written before attention reads it)."""
+    from oracle.oracle import oracle_prefill
+    from sapphire_amd.engine import Decoder
+    print(f"prefill cfg={cfg.n_layers}x{cfg.hidden} kv0={kv0} n={n} steps={steps}", flush=True)
+    m = smodel.synthetic_model(cfg, seed)
+    k, v = m.kv_prefill(kv0)
+    prompt = synth.rng(seed, 5).integers(0, cfg.vocab, n + 1).astype(np.int32)
+    dec = Decoder(m)
+    dec.set_kv(k, v)
+    dec.prefill(prompt[:n], kv0)
+    got_toks, got_logits, _ = dec.generate(int(prompt[n]), kv0 + n, steps, keep_logits=True)
+    gk, gv = dec.get_kv()
+    dec.close()
+    rk, rv = k.copy(), v.copy()
+    oracle_prefill(oracle, m, rk, rv, prompt[:n], kv0, nthreads=16)
+    pk, pv = rk.copy(), rv.copy()    # after the prompt
+    ref_toks, ref_logits = oracle_decode(oracle, m, rk, rv, int(prompt[n]), kv0 + n, steps, nthreads=16,
+                                         keep_logits=True)
+    assert np.array_equal(gk[:, :, :kv0], k[:, :, :kv0]) and np.array_equal(gv[:, :, :kv0], v[:, :, :kv0])
+    _kv_close(gk, pk, slice(kv0, kv0 + n), "K")
+    _kv_close(gv, pv, slice(kv0, kv0 + n), "V")
+    n_ok = _compare(ref_toks, ref_logits, got_toks, got_logits)
+    assert n_ok == steps, f"near-tie at step {n_ok}"
+
+
+def test_prefill_batched_decoder_sequence(oracle):
+    """Prefill of one sequence of a batched decoder fills that sequence's cache only."""
+    from oracle.oracle import oracle_prefill
+    from sapphire_amd.engine import Decoder
+    cfg, seed, n = smodel.TINY, 44, 20
+    print("prefill batched decoder", flush=True)
+    m = smodel.synthetic_model(cfg, seed)
+    prompt = synth.rng(seed, 6).integers(0, cfg.vocab, n).astype(np.int32)
+    dec = Decoder(m, batch=4)
+    shape = (cfg.n_layers, cfg.n_kv_heads, cfg.max_ctx, cfg.head_dim)
+    for b in range(4):
+        dec.set_kv_seq(b, np.zeros(shape, np.float32), np.zeros(shape, np.float32))
+    dec.prefill(prompt, 0, seq=2)
+    caches = [dec.get_kv_seq(b) for b in range(4)]
+    dec.close()
+    rk, rv = np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+    oracle_prefill(oracle, m, rk, rv, prompt, 0, nthreads=4)
+    for b in (0, 1, 3):
+        assert not caches[b][0].any() and not caches[b][1].any()
+    _kv_close(caches[2][0], rk, slice(0, n), "K")
+    _kv_close(caches[2][1], rv, slice(0, n), "V")
+    assert not caches[2][0][:, :, n:].any()
+
+
+def test_prefill_argument_checks():
+    from sapphire_amd.engine import Decoder
+    m = smodel.synthetic_model(smodel.TINY, 45)
+    dec = Decoder(m)
+    try:
+        with pytest.raises(RuntimeError):
+            dec.prefill([1, 2, 3], smodel.TINY.max_ctx - 2)        # past max_ctx
+        with pytest.raises(RuntimeError):
+            dec.prefill([1, smodel.TINY.vocab], 0)                 # outside the vocabulary
+        with pytest.raises(RuntimeError):
+            dec.prefill([1, 2], 0, seq=1)                          # one-sequence decoder
+    finally:
+        dec.close()
