@@ -280,6 +280,23 @@ def main() -> int:
 
     # The same LM head held as BF16 / F32 rows (a weight-tied embedding), on the element
     # types' own GEMV kernel; two copies of each rotate so the weights come from HBM.
+    # the small GEMVs of one decode layer (Gemma-3-270M MLP shapes), PACKED layout: per call
+    # time of 200 back-to-back launches on the bench stream (weights stay in the 256 MB MALL,
+    # so these are launch- and latency-bound, not HBM-bound)
+    small = {}
+    for name, dt, shapes in (("gemv_q8_0_2048x640", synth.Q8_0, [(2048, 640)]),
+                             ("gemv_q4_0_pair_2048x640_640x2048", synth.Q4_0, [(2048, 640), (640, 2048)])):
+        mats = [(QMatrix(dt, synth.quant_matrix(dt, m_, k_, seed, 50 + m_), layout=1), m_, k_) for m_, k_ in shapes]
+        xs = [DeviceArray.from_numpy(synth.normal_f32(k_, seed, 60 + k_)) for _, _, k_ in mats]
+        ys = [DeviceArray.empty(m_) for _, m_, _ in mats]
+
+        def call(i, mats=mats, xs=xs, ys=ys, dt=dt):
+            for (qm, m_, k_), xx, yy in zip(mats, xs, ys):
+                check(L.sapphire_gemv_q_dev(dt, 1, qm.ptr(), m_, k_, xx.ptr, yy.ptr, stream))
+        s_ms = time_alone(call, iters=200, warm=10)
+        sb = sum(gemv_bytes(dt, m_, k_) for _, m_, k_ in mats)
+        small[name] = {"us_per_call": round(s_ms * 1e3, 2), "GB/s": round(sb / (s_ms * 1e-3) / 1e9, 1),
+                       "bytes": sb}
     f_lines = {}
     qout = DeviceArray(gemv_bytes(synth.Q8_0, M_LM, K_LM))
     for name, dt, es in (("gemv_bf16_lm_head", synth.BF16, 2), ("gemv_f32_lm_head", synth.F32, 4)):
@@ -349,6 +366,7 @@ def main() -> int:
             "gemv_q8_0_lm_head_with_softmax_epilogue": {"us": round(q8sm_ms * 1e3, 2)},
             "softmax_argmax_262144_standalone": {"us": round(sm_ms * 1e3, 2)},
             **f_lines,
+            **small,
         },
         "decode": decode,
         "decode_batch16_gemma3_1b": decode_batch,
