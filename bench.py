@@ -311,6 +311,19 @@ def main() -> int:
         fb = M_LM * K_LM * es + 4 * K_LM + 4 * M_LM
         f_lines[name] = {"us": round(f_ms * 1e3, 2), "GB/s": round(fb / (f_ms * 1e-3) / 1e9, 1),
                          "frac_peak": round(fb / (f_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if dt == synth.BF16:
+            # the batched form (16 vectors) on the matrix cores: weights read once
+            xb = DeviceArray.from_numpy(synth.normal_f32((16, K_LM), seed, 45))
+            yb = DeviceArray.empty(16 * M_LM)
+            g_ms = time_alone(lambda i: check(L.sapphire_gemm_bf16_dev(mats[i % n_sets].ptr, M_LM, K_LM, xb.ptr, K_LM,
+                                                                       16, yb.ptr, M_LM, stream)))
+            gb = M_LM * K_LM * 2 + 16 * 4 * (K_LM + M_LM)
+            f_lines["gemm_bf16_lm_head_16_vectors"] = {
+                "us": round(g_ms * 1e3, 2), "GB/s": round(gb / (g_ms * 1e-3) / 1e9, 1),
+                "frac_peak": round(gb / (g_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "TFLOP/s": round(2 * 16 * M_LM * K_LM / (g_ms * 1e-3) / 1e12, 1)}
+            xb.free()
+            yb.free()
         # the Q4_0 / Q8_0 producer over the same rows: bytes = source + blocks
         for qdt in (synth.Q4_0, synth.Q8_0):
             q_ms = time_alone(lambda i: check(L.sapphire_quantize_dev(qdt, dt, mats[i % n_sets].ptr, M_LM, K_LM,

@@ -85,6 +85,12 @@ int sapphire_gemv_q_dev(int dtype, int layout, const void *w, int M, int K,
                         const float *x, float *y, void *stream);
 /* y[M] = W[M,K] . x[K] for F32 or BF16 row-major W (f32_avx.c:44-83, bf16_avx.c:55-108). */
 int sapphire_gemv_f_dev(int dtype, const void *w, int M, int K, const float *x, float *y, void *stream);
+/* Y[b][r] = W[r,:] . X[b][:] for BF16 row-major W and `batch` fp32 vectors (rows of X with
+ * stride ldx, rows of Y with stride ldy), on the matrix cores in passes of 16 vectors: the
+ * batched form kernel_gemm_bf16_avx2 computes (bf16_avx.c:115-159). Needs K % 8 == 0, W
+ * 16-byte aligned and M*K*2 below 4 GiB. */
+int sapphire_gemm_bf16_dev(const void *w, int M, int K, const float *x, int ldx, int batch, float *y, int ldy,
+                           void *stream);
 
 /* Y[b][M] = W[M,K] . X[b][K] for b < batch: the batched GEMV of kernel_gemm /
  * kernel_gemv_batch (dispatch.c:87-99, 234-266) for Q4_0/Q8_0, which the reference

@@ -60,6 +60,7 @@ def load_library(path: str):
     P("sapphire_gemv_q_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp])
     P("sapphire_gemv_f_dev", i32, [i32, vp, i32, i32, vp, vp, vp])
     P("sapphire_quantize_dev", i32, [i32, i32, vp, i32, i32, vp, vp])
+    P("sapphire_gemm_bf16_dev", i32, [vp, i32, i32, vp, i32, i32, vp, i32, vp])
     P("kernel_quantize", i32, [vp, vp, i32, vp])
     P("sapphire_softmax_argmax_dev", i32, [vp, i32, vp, vp, vp])
     P("sapphire_gemv_softmax_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp, vp, vp])

@@ -157,6 +157,8 @@ int gemv_exec(kernel_context_t *c, const tensor_t *A, const float *X, float *Y, 
         else
             rc = batch == 1 ? launch_gemv_q(dt, layout, w, M, Kp, dx, dy, c->stream)
                             : launch_gemm_q(dt, layout, w, M, Kp, dx, dy, batch, c->stream);
+    } else if (dt == DT_BF16 && batch > 1 && gemm_bf16_supported(w, M, K)) {
+        rc = launch_gemm_bf16(w, M, K, dx, K, batch, dy, M, c->stream);   // weights read once per 16
     } else {
         rc = 0;
         for (int b = 0; b < batch && rc == 0; ++b)

@@ -97,6 +97,11 @@ struct GemmOut {
 int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
                          void *ws, hipStream_t s);
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
+// BF16 W [M][K] times up to any number of fp32 vectors X[b][ldx] -> Y[b][ldy] on the matrix
+// cores (gemm_bf16.hip); supported: K % 8 == 0, W 16-byte aligned, below 4 GiB
+bool gemm_bf16_supported(const void *w, int M, int K);
+int launch_gemm_bf16(const void *w, int M, int K, const float *x, int ldx, int batch, float *y, int ldy,
+                     hipStream_t s);
 // F32 / BF16 rows [M][K] -> [M][ceil(K/32)] Q4_0 / Q8_0 blocks (AOS), quantize.hip
 int launch_quantize(int dst_dtype, int src_dtype, const void *src, int M, int K, void *blocks, hipStream_t s);
 

@@ -228,6 +228,11 @@ int sapphire_quantize_dev(int dst_dtype, int src_dtype, const void *src, int M, 
     return launch_quantize(dst_dtype, src_dtype, src, M, K, blocks, as_stream(stream));
 }
 
+int sapphire_gemm_bf16_dev(const void *w, int M, int K, const float *x, int ldx, int batch, float *y, int ldy,
+                           void *stream) {
+    return launch_gemm_bf16(w, M, K, x, ldx, batch, y, ldy, as_stream(stream));
+}
+
 int sapphire_gemv_f_dev(int dt, const void *w, int M, int K, const float *x, float *y, void *stream) {
     if ((dt != DT_F32 && dt != DT_BF16) || !w || !x || !y || M <= 0 || K <= 0) {
         set_error("bad F32/BF16 GEMV arguments");

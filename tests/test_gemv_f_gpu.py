@@ -156,3 +156,57 @@ def test_kernel_gemv_f_tensor_api(hip, oracle, dtype, ctx_kind):
         hip.tensor_release(A)
         if ctx is not None:
             hip.kernel_ctx_destroy(ctx)
+
+
+# ---- the batched BF16 form on the matrix cores (sapphire_gemm_bf16_dev) ----
+
+def run_gemm_bf16(W, X, ldx=None, ldy=None):
+    from sapphire_amd.device import DeviceArray, check, lib
+    m, k = W.shape
+    b = X.shape[0]
+    ldx = ldx or k
+    ldy = ldy or m
+    Xp = np.zeros((b, ldx), np.float32)
+    Xp[:, :k] = X
+    dw, dx = DeviceArray.from_numpy(W), DeviceArray.from_numpy(Xp)
+    dy = DeviceArray.empty(b * ldy)
+    dy.zero()
+    check(lib().sapphire_gemm_bf16_dev(dw.ptr, m, k, dx.ptr, ldx, b, dy.ptr, ldy, None), "gemm_bf16")
+    return dy.numpy().reshape(b, ldy)[:, :m]
+
+
+@pytest.mark.parametrize("shape,batch", [((262144, 640), 16), ((2048, 640), 3), ((1000, 1152), 16), ((640, 2048), 7),
+                                         ((33, 40), 5), ((16, 8), 1), ((4096, 256), 17), ((96, 6912), 16)],
+                         ids=["lm_head_b16", "2048x640_b3", "ragged_m_b16", "640x2048_b7", "k40_b5", "16x8_b1",
+                              "b17_two_passes", "k6912_b16"])
+def test_gemm_bf16_matches_oracle(hip, oracle, shape, batch):
+    m, k = shape
+    print(f"gemm_bf16 shape={shape} batch={batch}", flush=True)
+    W = weights(BF16, m, k, 31)
+    X = synth.normal_f32((batch, k), 32, batch)
+    ref = oracle.gemm_f(BF16, W, X)
+    got = run_gemm_bf16(W, X)
+    ok, err = close(got, ref)
+    assert ok, f"max abs err {err}"
+
+
+def test_gemm_bf16_strides_and_exact(hip, oracle):
+    """Row strides of X and Y wider than K and M; small integers give the oracle's bits."""
+    m, k, batch = 300, 96, 9
+    print("gemm_bf16 strides / exact", flush=True)
+    g = np.random.default_rng(5)
+    Wf = g.integers(-3, 4, size=(m, k)).astype(np.float32)
+    W = (Wf.view(np.uint32) >> 16).astype(np.uint16)
+    X = g.integers(-4, 5, size=(batch, k)).astype(np.float32)
+    ref = oracle.gemm_f(BF16, W, X)
+    got = run_gemm_bf16(W, X, ldx=k + 13, ldy=m + 7)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_gemm_bf16_rejects(hip):
+    from sapphire_amd.device import DeviceArray, lib
+    w, x, y = DeviceArray(4096), DeviceArray(4096), DeviceArray(4096)
+    L = lib()
+    assert L.sapphire_gemm_bf16_dev(w.ptr, 16, 12, x.ptr, 12, 2, y.ptr, 16, None) == -1     # K % 8
+    assert L.sapphire_gemm_bf16_dev(w.ptr + 2, 16, 16, x.ptr, 16, 2, y.ptr, 16, None) == -1  # alignment
+    assert L.sapphire_gemm_bf16_dev(w.ptr, 16, 16, x.ptr, 8, 2, y.ptr, 16, None) == -1       # ldx < K
