@@ -166,6 +166,12 @@ def decode_batch_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int =
     k, v = m.kv_prefill(prefill)
     out = bench_decode_batch(steps, batch=batch, seed=seed, prefill=prefill, m=m, kv=(k, v))
     out["lm_head_gemm"] = lm_head_gemm(m.lm_head, batch, seed)
+    # the same model with the reference's own LM head: the BF16 embedding table (tied)
+    from sapphire_amd import synth
+    tied = dataclasses.replace(m, cfg=dataclasses.replace(m.cfg, lm_dtype=synth.BF16), lm_head=m.embed_bf16)
+    out["tied_bf16_lm_head"] = {kk: vv for kk, vv in bench_decode_batch(steps, batch=batch, seed=seed,
+                                                                          prefill=prefill, m=tied, kv=(k, v)).items()
+                                if kk in ("ms_per_step", "tok_per_s", "weight_bytes_per_step")}
     if cpu:
         from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
         n = 3

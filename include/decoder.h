@@ -37,7 +37,7 @@ typedef struct {
     int wdtype;                     /* DTYPE_Q4_0 (3) or DTYPE_Q8_0 (4): the seven projections */
     int lm_dtype;                   /* DTYPE_Q4_0 or DTYPE_Q8_0: a separate LM head; DTYPE_BF16 (1):
                                      * the LM head is the embedding table (weight tying, as
-                                     * lm_head does, transformer.c:393-408); one sequence only */
+                                     * lm_head does, transformer.c:393-408) */
 } sapphire_decoder_config_t;
 
 /* Host pointers, read once by sapphire_decoder_create. Projection arrays hold one pointer

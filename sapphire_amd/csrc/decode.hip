@@ -81,7 +81,15 @@ __global__ __launch_bounds__(kThreads) void dec_gemv_kernel(QMat w0, QMat w1, Ge
     }
 }
 
-__global__ __launch_bounds__(kThreads) void dec_prologue_kernel(GemvIn in, int K, float *__restrict__ out) {
+// Sequence blockIdx.y of a batch: its vectors at + blockIdx.y * stride.
+__global__ __launch_bounds__(kThreads) void dec_prologue_kernel(GemvIn in, int K, float *__restrict__ out,
+                                                                size_t stride) {
+    {
+        const size_t o = blockIdx.y * stride;
+        in.resid_in += o;
+        if (in.delta) in.delta += o;
+        out += o;
+    }
     __shared__ float xs[kDecMaxK];
     __shared__ float dl[kDecMaxK];
     __shared__ float sh[16];
@@ -91,11 +99,6 @@ __global__ __launch_bounds__(kThreads) void dec_prologue_kernel(GemvIn in, int K
 
 // ---- attention ----
 
-// Workgroup b takes positions [t0, t1) of the layer's attention range; each wave walks
-// every fourth of them with a running (max, sum, weighted V) per head; the waves are then
-// merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL). Scores are
-// summed by DPP into wave-uniform values and the weights are powers of two of log2-scaled
-// scores (one exp2 each).
 // K/V rows of a batch (sequence blockIdx.x): the same norm_rope_heads on the same inputs
 // as dec_attn_part_kernel, so the rows are bit-identical to the ones it writes.
 __global__ __launch_bounds__(kThreads) void dec_kv_write_kernel(AttnArgs a) {
@@ -119,6 +122,11 @@ __global__ __launch_bounds__(kThreads) void dec_kv_write_kernel(AttnArgs a) {
     }
 }
 
+// Workgroup b takes positions [t0, t1) of the layer's attention range; each wave walks
+// every fourth of them with a running (max, sum, weighted V) per head; the waves are then
+// merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL). Scores are
+// summed by DPP into wave-uniform values and the weights are powers of two of log2-scaled
+// scores (one exp2 each).
 template <int DPL, int NH>
 __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     {   // sequence blockIdx.y of a batch
@@ -445,12 +453,21 @@ int dec_geglu(int dt, const QMat &wg, const QMat &wu, const GemvIn &in, float *g
                          : launch_gemv_kernel<DT_Q8_0, true>(wg, wu, in, g, s);
 }
 
+int dec_prologue_batch(const GemvIn &in, int K, int batch, size_t stride, float *out, hipStream_t s) {
+    if (K > kDecMaxK || batch <= 0 || in.resid_out) {
+        set_error("batched prologue: %d floats (at most %d), %d sequences, no residual output", K, kDecMaxK, batch);
+        return -1;
+    }
+    hipLaunchKernelGGL(dec_prologue_kernel, dim3(1, batch), dim3(kThreads), 0, s, in, K, out, stride);
+    return hip_ok(hipGetLastError(), "dec_prologue launch") ? 0 : -1;
+}
+
 int dec_prologue_only(const GemvIn &in, int K, float *out, hipStream_t s) {
     if (K > kDecMaxK) {
         set_error("vector of %d floats exceeds %d", K, kDecMaxK);
         return -1;
     }
-    hipLaunchKernelGGL(dec_prologue_kernel, dim3(1), dim3(kThreads), 0, s, in, K, out);
+    hipLaunchKernelGGL(dec_prologue_kernel, dim3(1), dim3(kThreads), 0, s, in, K, out, (size_t)0);
     return hip_ok(hipGetLastError(), "dec_prologue launch") ? 0 : -1;
 }
 

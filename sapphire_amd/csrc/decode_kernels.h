@@ -37,6 +37,9 @@ int dec_gemv(int dt, const QMat &w, const GemvIn &in, float *y, hipStream_t s);
 int dec_geglu(int dt, const QMat &wg, const QMat &wu, const GemvIn &in, float *g, hipStream_t s);
 // out = x(in) for K elements (one workgroup): the final norm before the LM head
 int dec_prologue_only(const GemvIn &in, int K, float *out, hipStream_t s);
+// the same for `batch` sequences whose vectors (resid_in, delta, out) are `stride` floats apart;
+// resid_out must be unset
+int dec_prologue_batch(const GemvIn &in, int K, int batch, size_t stride, float *out, hipStream_t s);
 
 struct AttnArgs {
     const float *qkv = nullptr;      // [nh*hd | nkv*hd | nkv*hd]: q, k, v projections

@@ -513,6 +513,19 @@ int enqueue_step_batch(sapphire_decoder *d) {
     if (cur < 0) return -1;
     // last finalize + final norm (transformer.c:400-406), LM head, greedy tokens
     if (launch_sum_parts(d->dparts, nsd, (size_t)B * H, B, H, d->dout, H, s) != 0) return -1;
+    if (c.lm_dtype == DT_BF16) {
+        // weight tying: the embedding table times the final norms, on the matrix cores
+        GemvIn fin;
+        fin.resid_in = d->resid[cur];
+        fin.delta = d->dout;
+        fin.w_delta = d->layers[c.n_layers - 1].n_ffn_post;
+        fin.w_norm = d->norm_final;
+        fin.eps = c.eps;
+        if (dec_prologue_batch(fin, H, B, (size_t)H, d->xfin, s) != 0) return -1;
+        if (launch_gemm_bf16(d->lm, c.vocab, H, d->xfin, H, B, d->logits, c.vocab, s) != 0) return -1;
+        if (dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s) != 0) return -1;
+        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
+    }
     GemmIn li;
     li.x = d->resid[cur];
     li.ldx = H;
@@ -608,8 +621,8 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
     if (batch == 1 ? !valid_config(*cfg) : !valid_batch_config(*cfg, batch)) return nullptr;
     if (batch > 1 && (cfg->n_layers <= 0 || cfg->hidden <= 0 || cfg->n_heads <= 0 || cfg->n_kv_heads <= 0 ||
                       cfg->head_dim <= 0 || cfg->ffn <= 0 || cfg->vocab <= 0 || cfg->max_ctx <= 0 ||
-                      !is_quant(cfg->wdtype) || !is_quant(cfg->lm_dtype))) {
-        set_error("decoder config: non-positive dimension or weights not Q4_0/Q8_0");
+                      !is_quant(cfg->wdtype) || (!is_quant(cfg->lm_dtype) && cfg->lm_dtype != DT_BF16))) {
+        set_error("decoder config: non-positive dimension, projections not Q4_0/Q8_0 or LM head not Q4_0/Q8_0/BF16");
         return nullptr;
     }
     sapphire_decoder *d = new (std::nothrow) sapphire_decoder();
@@ -665,8 +678,8 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
     if (!(d->norm_final = upload_f32(d, w->norm_final, H, "norm_final"))) return fail();
     // LM head
     if (c.lm_dtype == DT_BF16) {
-        if (B > 1) {
-            set_error("batched decoder: the LM head must be Q4_0 or Q8_0");
+        if (B > 1 && !gemm_bf16_supported(d->embed, c.vocab, H)) {
+            set_error("batched decoder: a BF16 LM head needs hidden % 8 == 0 and a table below 4 GiB");
             return fail();
         }
         d->lm = d->embed;
@@ -724,7 +737,7 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
     if (!dev_alloc_t(d, &d->resid[0], b * H, "resid") || !dev_alloc_t(d, &d->resid[1], b * H, "resid") ||
         !dev_alloc_t(d, &d->qkv, b * (nq + 2 * nk), "qkv") || !dev_alloc_t(d, &d->attn, b * nq, "attn") ||
         !dev_alloc_t(d, &d->o, b * H, "o") || !dev_alloc_t(d, &d->g, b * c.ffn, "g") ||
-        !dev_alloc_t(d, &d->ffn_out, H, "ffn_out") || !dev_alloc_t(d, &d->xfin, H, "xfin") ||
+        !dev_alloc_t(d, &d->ffn_out, H, "ffn_out") || !dev_alloc_t(d, &d->xfin, b * H, "xfin") ||
         !dev_alloc_t(d, &d->logits, b * c.vocab, "logits") ||
         !dev_alloc_t(d, &d->attn_part, b * attn_part_floats(c.n_heads, hd), "attn partials") ||
         !dev_alloc_t(d, &d->state, 2 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log"))

@@ -224,9 +224,9 @@ def bench_decode_batch(steps: int = 32, batch: int = 16, seed: int = 20260101, p
     its own KV cache prefilled to `prefill` of 2048 positions (the same N(0,1) contents in every
     sequence's cache) and its own seeded start token. tokens/s = batch * steps / time, best of
     `reps` runs after a warm-up (the graph capture)."""
-    cfg = cfg or smodel.GEMMA3_1B
     if m is None:
-        m = smodel.synthetic_model(cfg, seed)
+        m = smodel.synthetic_model(cfg or smodel.GEMMA3_1B, seed)
+    cfg = m.cfg
     k, v = kv if kv is not None else m.kv_prefill(prefill)
     dec = Decoder(m, batch=batch)
     for b in range(batch):
@@ -244,7 +244,7 @@ def bench_decode_batch(steps: int = 32, batch: int = 16, seed: int = 20260101, p
     nq, nk = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
 
     def qb(m_, k_, dt):
-        return m_ * (k_ // 32) * synth.BLOCK_BYTES[dt]
+        return m_ * k_ * 2 if dt == synth.BF16 else m_ * (k_ // 32) * synth.BLOCK_BYTES[dt]
     layer_w = (qb(nq + 2 * nk, cfg.hidden, cfg.wdtype) + qb(cfg.hidden, nq, cfg.wdtype) +
                qb(2 * cfg.ffn, cfg.hidden, cfg.wdtype) + qb(cfg.hidden, cfg.ffn, cfg.wdtype))
     w_step = layer_w * cfg.n_layers + qb(cfg.vocab, cfg.hidden, cfg.lm_dtype)
@@ -254,7 +254,8 @@ def bench_decode_batch(steps: int = 32, batch: int = 16, seed: int = 20260101, p
     kv_step = batch * rows * cfg.n_kv_heads * cfg.head_dim * 4 * 2
     ms_step = best / steps
     return {
-        "model": "Gemma-3-1B-shaped, Q4_0 weights (random init), 26 layers, hidden 1152, FFN 6912, vocab 262144",
+        "model": "Gemma-3-1B-shaped, Q4_0 weights (random init), 26 layers, hidden 1152, FFN 6912, vocab 262144"
+                 + (", LM head = the BF16 embedding table (tied)" if cfg.lm_dtype == synth.BF16 else ""),
         "batch": batch, "steps": steps, "kv_prefill": prefill, "ms_total": round(best, 3),
         "ms_per_step": round(ms_step, 4), "tok_per_s": round(batch * steps / (best * 1e-3), 1),
         "weight_bytes_per_step": w_step, "kv_bytes_per_step": kv_step,

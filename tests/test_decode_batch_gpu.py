@@ -48,6 +48,8 @@ def _run(oracle, cfg, seed, batch, prefills, steps, nthreads=4, check_kv=True):
 
 
 TINY_Q8 = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "wdtype": synth.Q8_0, "lm_dtype": synth.Q8_0})
+# the reference's own LM head: the BF16 embedding table (weight tying, transformer.c:393-408)
+TINY_TIED = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF16})
 
 
 @pytest.mark.parametrize("cfg,seed,batch,prefills,steps", [
@@ -55,7 +57,8 @@ TINY_Q8 = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "wdtype": synth.Q8_0, "
     (TINY_Q8, 52, 3, [8, 30, 60], 10),                       # Q8_0 weights
     (smodel.TINY, 53, 16, [5 + 4 * b for b in range(16)], 8),  # a full batch of 16
     (MID, 54, 5, [40, 44, 20, 47, 1], 16),                   # head_dim 128, 48-position window
-], ids=["tiny_b4", "tiny_q8_b3", "tiny_b16", "mid_b5"])
+    (TINY_TIED, 56, 6, [12, 33, 4, 50, 27, 9], 10),         # tied BF16 LM head on the matrix cores
+], ids=["tiny_b4", "tiny_q8_b3", "tiny_b16", "mid_b5", "tiny_tied_bf16_b6"])
 def test_decode_batch_matches_oracle(oracle, cfg, seed, batch, prefills, steps):
     print(f"batched decode cfg={cfg.n_layers}x{cfg.hidden} batch={batch} steps={steps}", flush=True)
     _run(oracle, cfg, seed, batch, prefills, steps)
@@ -66,6 +69,13 @@ def test_decode_batch_gemma3_1b(oracle):
     four sequences prefilled to different lengths around 1024 of 2048 positions, 4 steps."""
     print("batched decode gemma3-1b", flush=True)
     _run(oracle, smodel.GEMMA3_1B, 20260101, 4, [1024, 1000, 1031, 515], 4, nthreads=16, check_kv=False)
+
+
+def test_decode_batch_gemma3_1b_tied_bf16_lm_head(oracle):
+    """The Gemma-3-1B shape with the tied BF16 LM head (604 MB table), four sequences, 4 steps."""
+    print("batched decode gemma3-1b tied bf16 lm head", flush=True)
+    cfg = smodel.DecodeConfig(**{**smodel.GEMMA3_1B.__dict__, "lm_dtype": synth.BF16})
+    _run(oracle, cfg, 20260103, 4, [1024, 700, 1031, 300], 4, nthreads=16, check_kv=False)
 
 
 def test_decode_batch_repeatable_and_rejects(oracle):
