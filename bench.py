@@ -98,7 +98,9 @@ def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024)
     pf_ms = min(dec.prefill(prompt, 0) for _ in range(3))
     dec.close()
     out["prefill"] = {"tokens": prefill, "ms": round(pf_ms, 3), "tok_per_s": round(prefill / (pf_ms * 1e-3), 1),
-                      "form": "chunks of 16 tokens, projections as matrix-core GEMMs"}
+                      "form": "chunks of 16 tokens, projections as matrix-core GEMMs",
+                      "reference": "quantized prompt batches are rejected by the reference's pool (pool.c:318-321); "
+                                   "its prompt rate is its one-token decode rate (cpu_baseline.tok_per_s)"}
     # the same model with the reference's own LM head: the BF16 embedding table (tied)
     tied_cfg = dataclasses.replace(m.cfg, lm_dtype=synth.BF16)
     tied = dataclasses.replace(m, cfg=tied_cfg, lm_head=m.embed_bf16)
