@@ -179,13 +179,18 @@ struct SoftPart {
     int i;
 };
 
+// e^d as one v_exp_f32 of d * log2(e): the running sums only normalise the probabilities,
+// which are formed with expf (1-ulp-class differences in the sum, far inside the softmax
+// tolerance)
+__device__ __forceinline__ float exp_fast(float d) { return __builtin_amdgcn_exp2f(d * 1.44269504088896341f); }
+
 __device__ __forceinline__ void soft_push(SoftPart &p, float v, int row) {
     if (v > p.m) {                      // strict: an equal later value keeps the earlier index
-        p.s = (p.m == -INFINITY ? 0.f : p.s * expf(p.m - v)) + 1.f;
+        p.s = (p.m == -INFINITY ? 0.f : p.s * exp_fast(p.m - v)) + 1.f;
         p.m = v;
         p.i = row;
     } else {
-        p.s += expf(v - p.m);
+        p.s += exp_fast(v - p.m);
     }
 }
 
@@ -193,7 +198,7 @@ __device__ __forceinline__ SoftPart soft_merge(SoftPart a, SoftPart b) {
     const float m = fmaxf(a.m, b.m);
     SoftPart r;
     r.m = m;
-    r.s = (a.m == -INFINITY ? 0.f : a.s * expf(a.m - m)) + (b.m == -INFINITY ? 0.f : b.s * expf(b.m - m));
+    r.s = (a.m == -INFINITY ? 0.f : a.s * exp_fast(a.m - m)) + (b.m == -INFINITY ? 0.f : b.s * exp_fast(b.m - m));
     r.i = (b.m > a.m || (b.m == a.m && b.i < a.i)) ? b.i : a.i;
     return r;
 }
@@ -299,6 +304,16 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
     __shared__ SoftPart wp[4];
     __shared__ SoftPart tot;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    // the first pass's logits are loaded before the partials are folded (independent loads)
+    constexpr int U = 8;
+    const int begin = blockIdx.x * chunk, end = min(n, begin + chunk);
+    float4 v0[U];
+    if (probs && aligned)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = begin + 4 * threadIdx.x + 4 * u * blockDim.x;
+            v0[u] = i + 3 < end ? *reinterpret_cast<const float4 *>(logits + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     SoftPart b{-INFINITY, 0.f, 0x7fffffff};
     for (int i = threadIdx.x; i < nparts; i += blockDim.x) b = soft_merge(b, part[i]);
 #pragma unroll
@@ -315,19 +330,18 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
     __syncthreads();
     if (!probs) return;
     const float m = tot.m, inv = 1.0f / tot.s;
-    const int begin = blockIdx.x * chunk, end = min(n, begin + chunk);
     if (!aligned) {
         for (int i = begin + threadIdx.x; i < end; i += blockDim.x) probs[i] = expf(logits[i] - m) * inv;
         return;
     }
     // eight 16-byte loads in flight per thread, then their exps and stores
-    constexpr int U = 8;
     for (int i0 = begin + 4 * threadIdx.x; i0 < end; i0 += 4 * U * blockDim.x) {
         float4 v[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int i = i0 + 4 * u * blockDim.x;
-            v[u] = i + 3 < end ? *reinterpret_cast<const float4 *>(logits + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[u] = i0 == begin + 4 * (int)threadIdx.x ? v0[u]
+                   : (i + 3 < end ? *reinterpret_cast<const float4 *>(logits + i) : make_float4(0.f, 0.f, 0.f, 0.f));
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
