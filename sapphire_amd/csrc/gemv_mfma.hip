@@ -294,6 +294,8 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
     }
 }
 
+constexpr int kFinishVec = 1;   // float4 logits per thread and pass of softmax_finish_parts
+
 // Every block folds the nparts partials (256 threads, then the block), block 0 writes the
 // greedy token, and each block turns its chunk of logits into probabilities:
 // probs[i] = exp(logits[i] - max) / sum (utils.c:43-58).
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
     __shared__ SoftPart tot;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     // the first pass's logits are loaded before the partials are folded (independent loads)
-    constexpr int U = 8;
+    constexpr int U = kFinishVec;
     const int begin = blockIdx.x * chunk, end = min(n, begin + chunk);
     float4 v0[U];
     if (probs && aligned)
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
         for (int i = begin + threadIdx.x; i < end; i += blockDim.x) probs[i] = expf(logits[i] - m) * inv;
         return;
     }
-    // eight 16-byte loads in flight per thread, then their exps and stores
+    // kFinishVec 16-byte loads in flight per thread, then their exps and stores
     for (int i0 = begin + 4 * threadIdx.x; i0 < end; i0 += 4 * U * blockDim.x) {
         float4 v[U];
 #pragma unroll
@@ -517,9 +519,11 @@ int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *
                               int *argmax, void *scratch, hipStream_t st) {
     SoftPart *part = static_cast<SoftPart *>(scratch);
     if (launch_tiled(dt, w, M, K, x, logits, part, st) != 0) return -1;
-    // 8192 logits per block (one pass of eight float4 per thread); chunks are multiples of
-    // 4 floats so the float4 accesses stay aligned
-    const int blocks = probs ? std::max(1, (M + 8191) / 8192) : 1;
+    // 4 * kFinishVec * 256 logits per block (one pass of kFinishVec float4 per thread), so the
+    // 262144-entry vocabulary spreads over 256 blocks; chunks are multiples of 4 floats so the
+    // float4 accesses stay aligned
+    constexpr int per_block = 4 * kFinishVec * 256;
+    const int blocks = probs ? std::max(1, (M + per_block - 1) / per_block) : 1;
     const int chunk = ((M + blocks - 1) / blocks + 3) & ~3;
     const int aligned = ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(probs)) & 15u) == 0;
     hipLaunchKernelGGL(softmax_finish_parts, dim3(blocks), dim3(256), 0, st, logits, M, chunk, part,
