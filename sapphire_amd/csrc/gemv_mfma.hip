@@ -316,8 +316,15 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
             const int i = begin + 4 * threadIdx.x + 4 * u * blockDim.x;
             v0[u] = i + 3 < end ? *reinterpret_cast<const float4 *>(logits + i) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    SoftPart b{-INFINITY, 0.f, 0x7fffffff};
-    for (int i = threadIdx.x; i < nparts; i += blockDim.x) b = soft_merge(b, part[i]);
+    // two partials per thread and trip, both loads issued before either is merged (the fold's
+    // order changes only the rounding of the sum: ties keep the lower index whatever the order)
+    const SoftPart none{-INFINITY, 0.f, 0x7fffffff};
+    SoftPart b = none;
+    for (int i = threadIdx.x; i < nparts; i += 2 * blockDim.x) {
+        const SoftPart p0 = part[i];
+        const SoftPart p1 = i + (int)blockDim.x < nparts ? part[i + blockDim.x] : none;
+        b = soft_merge(b, soft_merge(p0, p1));
+    }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) b = soft_merge(b, soft_shfl_xor(b, off));
     if (lane == 0) wp[wid] = b;
