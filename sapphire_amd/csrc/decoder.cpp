@@ -679,7 +679,7 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
     // LM head
     if (c.lm_dtype == DT_BF16) {
         if (B > 1 && !gemm_bf16_supported(d->embed, c.vocab, H)) {
-            set_error("batched decoder: a BF16 LM head needs hidden % 8 == 0 and a table below 4 GiB");
+            set_error("batched decoder: a BF16 LM head needs hidden %% 8 == 0 and a table below 4 GiB");
             return fail();
         }
         d->lm = d->embed;
