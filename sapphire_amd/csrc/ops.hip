@@ -95,6 +95,23 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Each thread visits elements i = i0 + u * stride (u < kSmVec) of [.., end) per trip. The loads
+// go through an index clamped to end - 1 (in bounds, branch-free), so a trip's kSmVec loads are
+// issued together; f sees the in-range ones in ascending order, as a plain strided loop would.
+constexpr int kSmVec = 4;
+
+template <typename T, typename F>
+__device__ __forceinline__ void strided_visit(const T *__restrict__ a, int first, int end, int stride, F f) {
+    for (int i0 = first; i0 < end; i0 += kSmVec * stride) {
+        T v[kSmVec];
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u) v[u] = a[min(i0 + u * stride, end - 1)];
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u)
+            if (i0 + u * stride < end) f(v[u], i0 + u * stride);
+    }
+}
+
 // Pass 1: each block reduces a contiguous chunk to (max, first argmax, sum exp(x - max)).
 __global__ __launch_bounds__(kSmBlock) void softmax_partials(const float *__restrict__ x, int n, int chunk,
                                                              float *__restrict__ pmax, float *__restrict__ psum,
@@ -105,7 +122,7 @@ __global__ __launch_bounds__(kSmBlock) void softmax_partials(const float *__rest
     const int begin = blockIdx.x * chunk;
     const int end = min(n, begin + chunk);
     MaxArg m{-INFINITY, 0x7fffffff};
-    for (int i = begin + threadIdx.x; i < end; i += kSmBlock) m = better(m, MaxArg{x[i], i});
+    strided_visit(x, begin + (int)threadIdx.x, end, kSmBlock, [&](float v, int i) { m = better(m, MaxArg{v, i}); });
     m = wave_maxarg(m);
     if (lane == 0) smax[wid] = m;
     __syncthreads();
@@ -113,7 +130,7 @@ __global__ __launch_bounds__(kSmBlock) void softmax_partials(const float *__rest
     for (int k = 1; k < kSmBlock / kWave; ++k) bm = better(bm, smax[k]);
     float s = 0.f;
     if (bm.v > -INFINITY)
-        for (int i = begin + threadIdx.x; i < end; i += kSmBlock) s += expf(x[i] - bm.v);
+        strided_visit(x, begin + (int)threadIdx.x, end, kSmBlock, [&](float v, int) { s += expf(v - bm.v); });
     s = wave_sum(s);
     if (lane == 0) ssum[wid] = s;
     __syncthreads();
@@ -126,20 +143,42 @@ __global__ __launch_bounds__(kSmBlock) void softmax_partials(const float *__rest
     }
 }
 
-// Pass 2: every block folds the partials (cheap, kSmParts values) and normalises its chunk.
+// Pass 2: every block folds the partials (cheap, kSmParts values) and normalises its chunk. The
+// chunk's first kSmVec values per thread are loaded before the fold (independent loads).
 __global__ __launch_bounds__(kSmBlock) void softmax_finish(const float *__restrict__ x, int n, int chunk, int parts,
                                                            const float *__restrict__ pmax,
                                                            const float *__restrict__ psum,
                                                            const int *__restrict__ parg, float *__restrict__ probs,
                                                            int *__restrict__ argmax_out) {
     __shared__ float s_gmax, s_inv;
+    const int begin = blockIdx.x * chunk;
+    const int end = min(n, begin + chunk);
+    const int first = begin + (int)threadIdx.x;
+    float v0[kSmVec];
+    if (probs && first < end)
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u) v0[u] = x[min(first + u * kSmBlock, end - 1)];
+    static_assert(kSmParts <= kWave * kSmVec, "one trip of wave 0 covers the partials");
     if (threadIdx.x < kWave) {
+        // lane l holds partials l + 64u (clamped loads, all issued together)
+        float pm[kSmVec], ps[kSmVec];
+        int pa[kSmVec];
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u) {
+            const int p = min((int)threadIdx.x + u * kWave, parts - 1);
+            pm[u] = pmax[p];
+            ps[u] = psum[p];
+            pa[u] = parg[p];
+        }
         MaxArg m{-INFINITY, 0x7fffffff};
-        for (int p = threadIdx.x; p < parts; p += kWave) m = better(m, MaxArg{pmax[p], parg[p]});
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u)
+            if ((int)threadIdx.x + u * kWave < parts) m = better(m, MaxArg{pm[u], pa[u]});
         m = wave_maxarg(m);
         float s = 0.f;
-        for (int p = threadIdx.x; p < parts; p += kWave)
-            if (pmax[p] > -INFINITY) s += psum[p] * expf(pmax[p] - m.v);
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u)
+            if ((int)threadIdx.x + u * kWave < parts && pm[u] > -INFINITY) s += ps[u] * expf(pm[u] - m.v);
         s = wave_sum(s);
         if (threadIdx.x == 0) {
             s_gmax = m.v;
@@ -151,9 +190,14 @@ __global__ __launch_bounds__(kSmBlock) void softmax_finish(const float *__restri
     __syncthreads();
     if (!probs) return;
     const float gm = s_gmax, inv = s_inv;
-    const int begin = blockIdx.x * chunk;
-    const int end = min(n, begin + chunk);
-    for (int i = begin + threadIdx.x; i < end; i += kSmBlock) probs[i] = expf(x[i] - gm) * inv;
+    for (int i0 = first; i0 < end; i0 += kSmVec * kSmBlock) {
+        float v[kSmVec];
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u) v[u] = i0 == first ? v0[u] : x[min(i0 + u * kSmBlock, end - 1)];
+#pragma unroll
+        for (int u = 0; u < kSmVec; ++u)
+            if (i0 + u * kSmBlock < end) probs[i0 + u * kSmBlock] = expf(v[u] - gm) * inv;
+    }
 }
 
 
