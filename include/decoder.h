@@ -10,7 +10,7 @@
  * trip behind every GEMV. This engine is the MI355X-native form of the same step: weights,
  * activations, the KV cache and the sampled token stay in HBM, and one step is a captured
  * HIP graph of fused kernels. The host engine keeps its model loader and session and hands
- * the weights over once.
+ * the weights over once (sapphire_decoder_create below).
  *
  * Not a reference interface: the reference has no device engine. Semantics follow the
  * functions cited above; weights are the reference's Q4_0 / Q8_0 block arrays

@@ -1,7 +1,7 @@
 /*
  * oracle.c - CPU restatement of Sapphire's quantized decode hot path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product). See oracle.h.
+ * TEST INFRASTRUCTURE ONLY (the parity reference, never the product). See oracle.h.
  *
  * Arithmetic-order notes. The reference is built by gcc with -O3 -mavx2 -mfma and
  * GNU C's default -ffp-contract=fast, so a few scalar expressions in the reference

@@ -1,7 +1,7 @@
 /*
  * oracle.h - CPU restatement of Sapphire's quantized decode hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker the HIP path is compared
+ * TEST INFRASTRUCTURE ONLY. This library is the parity reference the HIP path is compared
  * against; it is never linked into, loaded by, or called from the product library
  * (sapphire_amd/). Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may load it.

@@ -1,4 +1,4 @@
-"""ctypes bindings for the CPU checkers.
+"""ctypes bindings for the CPU parity oracle.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()`` and by
 bench.py's cpu_baseline leg, never by the product package.

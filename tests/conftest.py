@@ -36,7 +36,7 @@ def hip():
 
 
 def close(gpu, ref, rel=1e-3, abs_=1e-4):
-    """The north-star tolerance for fp32 outputs: |gpu-ref| <= abs + rel*|ref|."""
+    """The parity tolerance for fp32 outputs: |gpu-ref| <= abs + rel*|ref|."""
     import numpy as np
     gpu = np.asarray(gpu, np.float64)
     ref = np.asarray(ref, np.float64)

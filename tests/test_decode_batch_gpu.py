@@ -3,7 +3,7 @@ projection one matrix-core GEMM over the batch) against the oracle's decode step
 sequence on its own. The reference decodes one sequence per inference_forward call
 (inference.c:612-651), so that is the expected result of every sequence.
 
-Bar (north star): per sequence and step, logits within 2e-3 relative and identical greedy
+Parity bar: per sequence and step, logits within 2e-3 relative and identical greedy
 tokens, except after a near-tie (top-2 gap inside the tolerance), as in test_decode_gpu.
 """
 import numpy as np

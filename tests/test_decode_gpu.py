@@ -1,7 +1,7 @@
 """Device-resident greedy decode (include/decoder.h) against the oracle's decode step, which
 is bit-exact with the compiled reference engine (tests/test_oracle_pin.py).
 
-Bar (north star): logits within 2e-3 relative (max |gpu - ref| over a step / max |ref|)
+Parity bar: logits within 2e-3 relative (max |gpu - ref| over a step / max |ref|)
 and identical greedy tokens. A token may differ only where the oracle's top-2 logit gap
 is inside that tolerance (a near-tie); the sequences are then compared up to that step.
 """

@@ -3,7 +3,7 @@ against the oracle.
 
 The reference has no quantized batched kernel (pool.c:318-321 rejects it), so the
 expected output of sequence b is the oracle's kernel_gemv of that sequence's vector
-(dispatch.c:101-156). Tolerance: |gpu - ref| <= 1e-4 + 1e-3*|ref| (north star); the
+(dispatch.c:101-156). Tolerance: |gpu - ref| <= 1e-4 + 1e-3*|ref| (the parity bar); the
 exactly representable case is compared bit for bit.
 """
 import ctypes as C

@@ -1,6 +1,6 @@
 """GEMV parity on the GPU against the oracle (which is bit-exact with the reference).
 
-Tolerance for float outputs: |gpu - ref| <= 1e-4 + 1e-3*|ref| (north star). Integer
+Tolerance for float outputs: |gpu - ref| <= 1e-4 + 1e-3*|ref| (the parity bar). Integer
 unpack and dequantised weights are compared bit for bit; so are GEMVs whose every
 product and partial sum is exact in fp32 (power-of-two scales, small-integer x).
 """

@@ -2,7 +2,7 @@
 
 Bit-exact: RMSNorm / RMSNorm-delta (same sum-of-squares order and correctly rounded
 sqrt/divide), RoPE (same fused forms), residual add, argmax, vec_dot. Within the
-north-star tolerance (1e-3 rel / 1e-4 abs): GELU*up and softmax, which use the device
+parity tolerance (1e-3 rel / 1e-4 abs): GELU*up and softmax, which use the device
 expf/tanhf.
 """
 import numpy as np
