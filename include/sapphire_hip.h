@@ -144,8 +144,10 @@ int sapphire_gemm_q_fused_dev(int dtype, const void *w_tiled, int M, int K, int 
 
 /* ---- LM-head epilogue ----
  * probs = softmax(logits) (utils.c:18-59) written to probs (may equal logits) and the
- * greedy token (utils.c:145-156: first index of the maximum) written to *argmax_dev.
- * probs may be NULL to compute only the argmax. */
+ * greedy token (utils.c:145-156: the first index of the maximum; 0 when logits[0] is NaN)
+ * written to *argmax_dev. probs may be NULL to compute only the argmax. The partials use a
+ * small per-device buffer (allocated on the device's first call): calls that overlap on one
+ * device must be ordered on one stream. */
 int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *argmax_dev, void *stream);
 
 /* The LM head with its epilogue fused: logits = W . x as sapphire_gemv_q_dev, then probs

@@ -396,10 +396,11 @@ __global__ __launch_bounds__(kThreads) void dec_argmax_part_kernel(const float *
     }
 }
 
-// grid (batch), one wave: tokens[b] = best of the sequence's partials; 0 when no logit is
-// above -inf (all NaN), as sample_greedy (utils.c:145-156) starts at index 0
+// grid (batch), one wave: tokens[b] = best of the sequence's partials; 0 when logits[b][0] is
+// NaN or no logit is above -inf, as sample_greedy (utils.c:145-156) starts at index 0 and
+// only a greater logit replaces it
 __global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int nparts, int n,
-                                         int *__restrict__ tokens) {
+                                         const float *__restrict__ logits, int *__restrict__ tokens) {
     const float *p = part + (size_t)blockIdx.x * nparts * 2;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
@@ -409,7 +410,8 @@ __global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int npa
         if (better(v, i, bv, bi)) { bv = v; bi = i; }
     }
     wave_best(bv, bi);
-    if (threadIdx.x == 0) tokens[blockIdx.x] = bi >= 0 && bi < n ? bi : 0;
+    if (threadIdx.x == 0)
+        tokens[blockIdx.x] = (bi >= 0 && bi < n && !isnan(logits[(size_t)blockIdx.x * n])) ? bi : 0;
 }
 
 __global__ void dec_advance_batch_kernel(const int *__restrict__ tok, int *__restrict__ pos, int *__restrict__ step,
@@ -538,7 +540,8 @@ size_t argmax_batch_part_floats(int n, int batch) {
 int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_tokens, hipStream_t s) {
     hipLaunchKernelGGL(dec_argmax_part_kernel, dim3(kArgmaxParts, batch), dim3(kThreads), 0, s, logits, n, part);
     if (!hip_ok(hipGetLastError(), "argmax launch")) return -1;
-    hipLaunchKernelGGL(dec_argmax_finish_kernel, dim3(batch), dim3(kWave), 0, s, part, kArgmaxParts, n, d_tokens);
+    hipLaunchKernelGGL(dec_argmax_finish_kernel, dim3(batch), dim3(kWave), 0, s, part, kArgmaxParts, n, logits,
+                       d_tokens);
     return hip_ok(hipGetLastError(), "argmax finish launch") ? 0 : -1;
 }
 

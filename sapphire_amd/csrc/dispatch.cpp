@@ -479,15 +479,10 @@ void softmax(float *scores, int n) {
     kernel_context_t *c = default_ctx();
     if (!c) return;
     const size_t b = sizeof(float) * (size_t)n;
-    static float *scratch = nullptr;
     (void)run_staged(c, {HostVec{scores, nullptr, b}}, {HostVec{nullptr, scores, b}},
                      [&](std::vector<void *> &i, std::vector<void *> &o, hipStream_t s) {
-                         if (!scratch) {
-                             void *p = nullptr;
-                             if (!hip_ok(hipMalloc(&p, softmax_scratch_floats(n) * sizeof(float)), "hipMalloc"))
-                                 return -1;
-                             scratch = static_cast<float *>(p);
-                         }
+                         float *scratch = softmax_partials_scratch();   // the current device's
+                         if (!scratch) return -1;
                          return launch_softmax_argmax(static_cast<float *>(i[0]), n, static_cast<float *>(o[0]),
                                                       nullptr, scratch, s);
                      });

@@ -25,6 +25,7 @@
 
 #include "devmath.h"
 #include "internal.h"
+#include "nonfinite.h"
 
 namespace sapphire {
 
@@ -199,6 +200,32 @@ constexpr int kStageH8 = (kBatchMax * kRawLd * 4 + 15) / 16 > kChunkBlocks * 2 *
                              ? (kBatchMax * kRawLd * 4 + 15) / 16
                              : kChunkBlocks * 2 * kWave;
 
+// Positions of the non-finite activations of a K chunk (at most kChunkBlocks blocks): per
+// sequence a bit mask of the +inf and of the -inf elements of every block, and one bit per
+// sequence that holds a NaN.
+struct NfChunk {
+    uint32_t inf[kBatchMax][2][kChunkBlocks];
+    uint32_t nan;
+};
+
+// Row `row`'s share of the non-finite activations of sequence seq in this chunk (blocks
+// b0 .. b0+nbl-1 of rows of nb blocks): NaN if one is NaN, else the fold of fl(w * +-inf)
+// over the recorded positions (nonfinite.h).
+template <int DT>
+__device__ float chunk_fold(const NfChunk &c, const uint8_t *__restrict__ wq, const uint8_t *__restrict__ wsc,
+                            int nb, int b0, int nbl, int row, int seq) {
+    if ((c.nan >> seq) & 1u) return __builtin_nanf("");
+    float a = 0.f;
+    for (int bl = 0; bl < nbl; ++bl)
+        for (int sg = 0; sg < 2; ++sg)
+            for (uint32_t m = c.inf[seq][sg][bl]; m != 0; m &= m - 1) {
+                const int k = (b0 + bl) * kBlock + __builtin_ctz(m);
+                const float w = nonfinite::weight_at<DT, LAYOUT_TILED>(wq, wsc, nb, row, k);
+                a = __fadd_rn(a, __fmul_rn(w, sg ? -INFINITY : INFINITY));
+            }
+    return a;
+}
+
 // grid.x: workgroups over the tiles (grid-stride), grid.y: K chunks of `cb` blocks.
 // Four waves per SIMD (two workgroups per CU): at most 128 VGPRs.
 template <int DT>
@@ -210,7 +237,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     __shared__ float xsc[kBatchMax];
     __shared__ float npart[kBatchMax][8];
     __shared__ float rinv[kBatchMax];
+    __shared__ NfChunk nfc;
+    __shared__ int wnf[kWaves];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    if (tid == 0) nfc.nan = 0;
     const int nb = K / kBlock, G = nb / kGroupBlocks;
     const int b0 = blockIdx.y * cb, b1 = min(nb, b0 + cb);
 
@@ -231,6 +261,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     BConst bk = {0x000F000Fu, 0x00F000F0u, 0x64086408u, 0x64806480u};
     asm volatile("" : "+v"(bk.lo_mask), "+v"(bk.hi_mask), "+v"(bk.lo_bits), "+v"(bk.hi_bits));
     // ---- stage the chunk: input transform, range scale per sequence, hi/lo operands ----
+    bool any_nf;                                       // a NaN / inf activation in this chunk
     {
         const int seq = tid & (kBatchMax - 1), q = tid / kBatchMax;   // q: 0..31
         const int pairs = (b1 - b0) * 4;
@@ -324,17 +355,66 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             }
         }
         float mx = 0.f;
+        bool bad = false;
 #pragma unroll
         for (int i = 0; i < kStagePairs; ++i)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[i][e]));
+            for (int e = 0; e < 8; ++e) {
+                mx = fmaxf(mx, fabsf(v[i][e]));
+                bad |= nonfinite::is_nf(v[i][e]);
+            }
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const bool wbad = __any(bad) != 0;
         if (lane < kBatchMax) wmax[wid][lane] = mx;
+        if (lane == 0) wnf[wid] = wbad;
         __syncthreads();                               // also ends every read of raw
         mx = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wmax[w][seq]);
+        any_nf = false;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) any_nf |= wnf[w] != 0;
+        if (any_nf) {
+            // NaN / inf activations (workgroup-uniform, rare): record where they are, zero them,
+            // and take the range maxima again over the rest. Pairs p = 4 bl .. 4 bl + 3 of block
+            // bl sit in the lanes 16 (p & 3) + seq of one wave.
+            __syncthreads();                           // every wave has read wmax
+            mx = 0.f;
+#pragma unroll
+            for (int i = 0; i < kStagePairs; ++i) {
+                const int p = q + i * (kThreads / kBatchMax);
+                uint32_t pinf = 0, ninf = 0;
+                bool nan = false;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float t = v[i][e];
+                    nan |= t != t;
+                    pinf |= (t == INFINITY ? 1u : 0u) << e;
+                    ninf |= (t == -INFINITY ? 1u : 0u) << e;
+                    v[i][e] = nonfinite::is_nf(t) ? 0.f : t;
+                    mx = fmaxf(mx, fabsf(v[i][e]));
+                }
+                if (nan && p < pairs && seq < batch) atomicOr(&nfc.nan, 1u << seq);
+                pinf <<= 8 * (p & 3);
+                ninf <<= 8 * (p & 3);
+                pinf |= __shfl_xor(pinf, 16, kWave);
+                ninf |= __shfl_xor(ninf, 16, kWave);
+                pinf |= __shfl_xor(pinf, 32, kWave);
+                ninf |= __shfl_xor(ninf, 32, kWave);
+                if ((p & 3) == 0 && p < pairs) {
+                    nfc.inf[seq][0][p >> 2] = pinf;
+                    nfc.inf[seq][1][p >> 2] = ninf;
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            if (lane < kBatchMax) wmax[wid][lane] = mx;
+            __syncthreads();
+            mx = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wmax[w][seq]);
+        }
         // e: the chunk's largest |x| * 2^-e in [2^14, 2^15) (finite in fp16, lo term normal)
         int e = 0;
         if (mx > 0.f) {
@@ -412,7 +492,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                         // lanes n < 8 hold gate rows 8t'+n, lanes n + 8 the matching up rows
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const float val = acc[r] * sc[r];
+                            float val = acc[r] * sc[r];
+                            if (any_nf && 4 * m + r < batch)
+                                val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, ct * kTileRows + n, 4 * m + r);
                             const float up = __shfl_xor(val, 8, kWave);
                             const int j = ct * 8 + n;
                             if (n < 8 && 4 * m + r < batch && 2 * j < M)
@@ -423,7 +505,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                         if (row < M)
 #pragma unroll
                             for (int r = 0; r < 4; ++r)
-                                if (4 * m + r < batch) dst[(size_t)(4 * m + r) * ldd + row] = acc[r] * sc[r];
+                                if (4 * m + r < batch) {
+                                    float val = acc[r] * sc[r];
+                                    if (any_nf) val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, row, 4 * m + r);
+                                    dst[(size_t)(4 * m + r) * ldd + row] = val;
+                                }
                     }
                     acc = f4{0.f, 0.f, 0.f, 0.f};
                     cg = 0;

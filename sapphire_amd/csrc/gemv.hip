@@ -28,6 +28,7 @@
 
 #include "internal.h"
 #include "lanes.h"
+#include "nonfinite.h"
 #include "qdot.h"
 
 namespace sapphire {
@@ -139,6 +140,17 @@ __global__ __launch_bounds__(256) void gemv_q_cols(const uint8_t *__restrict__ w
     float xs = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) xs += xv[i];
+    // a NaN or infinite activation makes xs non-finite (so does an overflowing sum, for which
+    // the fold below is 0): zero them for the block dots and add their fold to every row
+    const bool nf = __any(nonfinite::is_nf(xs));
+    if (nf) {
+        xs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            xv[i] = nonfinite::is_nf(xv[i]) ? 0.f : xv[i];
+            xs += xv[i];
+        }
+    }
 
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(w, q_bytes);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(w + sc_off, s_bytes);
@@ -171,219 +183,8 @@ __global__ __launch_bounds__(256) void gemv_q_cols(const uint8_t *__restrict__ w
             float acc = 0.f;
             for (int b = 0; b < nb; ++b) acc += rp[b];
             const int row = row0 + lane;
-            if (row < rend) y[row] = acc;
+            if (row < rend) y[row] = nf ? acc + nonfinite::fold<DT, LAYOUT>(w, w + sc_off, nb, row, x) : acc;
         }
-    }
-}
-
-// ---------------------------------------------------------------------------------
-// Integer-dot GEMV for long matrices (the LM head and other large M).
-//
-// x is converted once per workgroup into block floating point: for each 32-element
-// block, X_i = rint(x_i * 2^sh) with sh chosen so that |X_i| < 2^22 (the largest
-// element keeps 21-22 significant bits, as fp32 would keep 24), split into signed
-// digits: six 4-bit digits for Q4_0 (X = sum_k D_k 16^k) and three 8-bit digits for
-// Q8_0 (X = sum_k D_k 256^k). Then per 8 weights
-//   Q4_0: q ^ 0x88888888 turns every nibble into the signed value nib - 8, and six
-//         v_dot8c_i32_i4 accumulate sum (nib-8)*D_k exactly;
-//   Q8_0: the raw int8 quants feed three v_dot4c_i32_i8 per 4 weights.
-// Digit sums are combined exactly in int32 and once in fp32, then scaled by 2^-sh.
-// Block scales are applied by the lane that finishes a row, which fetches the row's
-// nb scales with 16-byte loads.
-// ---------------------------------------------------------------------------------
-constexpr int kDigitWords = 24;   // per block: Q4_0 6 planes x 4 words, Q8_0 3 planes x 8 words
-
-template <int DT>
-__device__ void prep_x_digits(const float *__restrict__ x, int K, uint32_t *lds_u, uint32_t *lds_dig,
-                              float *lds_xsc) {
-    const int t = threadIdx.x, T = blockDim.x;
-    for (int base = 0; base < K; base += T) {          // uniform trip count: shuffles see all lanes
-        const int e = base + t;
-        const bool valid = e < K;
-        const float v = valid ? x[e] : 0.0f;
-        int m = (int)((__float_as_uint(v) >> 23) & 0xFFu);   // biased exponent; |v| < 2^(m-126)
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) m = max(m, __shfl_xor(m, off, 64));   // 32-lane groups = blocks
-        const int sh = 148 - m;                           // max|x_b| * 2^sh < 2^22
-        const int X = (int)rintf(ldexpf(v, sh));
-        uint32_t U;
-        if constexpr (DT == DT_Q4_0) U = ((uint32_t)X + 0x888888u) ^ 0x888888u;   // nibbles = signed digits
-        else U = ((uint32_t)X + 0x808080u) ^ 0x808080u;                           // bytes = signed digits
-        if (valid) {
-            lds_u[e] = U;
-            if ((e & 31) == 0) lds_xsc[e >> 5] = ldexpf(1.0f, -sh);
-        }
-    }
-    __syncthreads();
-    const int nb = K >> 5;
-    for (int d = t; d < nb * kDigitWords; d += T) {
-        const int b = d / kDigitWords, r = d - b * kDigitWords;
-        uint32_t wd = 0;
-        if constexpr (DT == DT_Q4_0) {
-            const int k = r >> 2, g = r & 3;              // plane k, elements 8g..8g+7
-            const uint32_t *u = lds_u + b * 32 + 8 * g;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) wd |= ((u[i] >> (4 * k)) & 0xFu) << (4 * i);
-        } else {
-            const int k = r >> 3, g = r & 7;              // plane k, elements 4g..4g+3
-            const uint32_t *u = lds_u + b * 32 + 4 * g;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wd |= ((u[i] >> (8 * k)) & 0xFFu) << (8 * i);
-        }
-        lds_dig[d] = wd;
-    }
-    __syncthreads();
-}
-
-// sum_e int(e) * X(e) over one block as fp32 (exact integer sums, one final rounding).
-template <int DT>
-__device__ __forceinline__ float block_dot_int(const uint32_t (&q)[QT<DT>::QD], const uint32_t (&dig)[kDigitWords]) {
-    if constexpr (DT == DT_Q4_0) {
-        int acc[6] = {0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const int qq = (int)(q[d] ^ 0x88888888u);
-#pragma unroll
-            for (int k = 0; k < 6; ++k) acc[k] = __builtin_amdgcn_sdot8(qq, (int)dig[4 * k + d], acc[k], false);
-        }
-        // |acc_k| <= 32*8*8 = 2048, so A and B are exact in int32 and in fp32.
-        const int A = acc[0] + acc[1] * 16 + acc[2] * 256;
-        const int B = acc[3] + acc[4] * 16 + acc[5] * 256;
-        return __builtin_fmaf((float)B, 4096.0f, (float)A);
-    } else {
-        int acc[3] = {0, 0, 0};
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-#pragma unroll
-            for (int k = 0; k < 3; ++k) acc[k] = __builtin_amdgcn_sdot4((int)q[d], (int)dig[8 * k + d], acc[k], false);
-        }
-        // |acc_k| <= 32*128*128 = 2^19; A = acc0 + 256*acc1 is exact in int32 and fp32.
-        const int A = acc[0] + acc[1] * 256;
-        return __builtin_fmaf((float)acc[2], 65536.0f, (float)A);
-    }
-}
-
-// Register double buffer of one iteration (S wave-steps) of the integer-dot kernel.
-template <int DT, int NB, int S>
-struct IntStage {
-    uint32_t q[S][QT<DT>::QD];
-    float s[S];       // AOS: per-lane block scale
-    float rs[NB];     // PACKED: the reducing lane's row scales
-};
-
-// Wave-step st of an iteration starting at row0 covers rows row0 + st*SSTRIDE + [0, RPS).
-template <int DT, int LAYOUT, int NB, int S, int SSTRIDE>
-__device__ __forceinline__ void int_issue(IntStage<DT, NB, S> &g, __amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rs,
-                                          int row0, int rend, int r_in, int blk, bool lane_on, int lane) {
-    constexpr int RPS = kWave / NB;
-    const int row_l = row0 + r_in;
-    const uint32_t bi0 = (uint32_t)row_l * NB + (uint32_t)blk;
-#pragma unroll
-    for (int st = 0; st < S; ++st) {
-        const bool ok = lane_on && row_l + st * SSTRIDE < rend;
-        if constexpr (LAYOUT == LAYOUT_PACKED) {
-            const uint32_t oq = ok ? (bi0 + st * SSTRIDE * NB) * QT<DT>::QB : kOffNone;
-#pragma unroll
-            for (int i = 0; i < QT<DT>::QD / 4; ++i) {
-                const u32x4 t = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq + 16u * i, 0, kNT));
-                g.q[st][4 * i + 0] = t.x; g.q[st][4 * i + 1] = t.y; g.q[st][4 * i + 2] = t.z; g.q[st][4 * i + 3] = t.w;
-            }
-        } else {
-            load_block_buf<DT, LAYOUT>(rq, rs, bi0 + st * SSTRIDE * NB, ok, g.q[st], g.s[st]);
-        }
-    }
-    if constexpr (LAYOUT == LAYOUT_PACKED) {
-        const int my_row = row0 + (lane / RPS) * SSTRIDE + lane % RPS;
-        const uint32_t os = (lane < S * RPS && my_row < rend) ? (uint32_t)my_row * NB * 4u : kOffNone;
-#pragma unroll
-        for (int i = 0; i < NB / 4; ++i) {
-            const u32x4 t = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, os + 16u * i, 0, kNT));
-            g.rs[4 * i + 0] = __uint_as_float(t.x); g.rs[4 * i + 1] = __uint_as_float(t.y);
-            g.rs[4 * i + 2] = __uint_as_float(t.z); g.rs[4 * i + 3] = __uint_as_float(t.w);
-        }
-    }
-}
-
-template <int DT, int LAYOUT, int NB, int S, int SSTRIDE>
-__device__ __forceinline__ void int_consume(const IntStage<DT, NB, S> &g, const uint32_t (&dig)[kDigitWords], float xsc,
-                                            float *redw, float *__restrict__ y, int row0, int rend, int lane) {
-    constexpr int RPS = kWave / NB;
-    float part[S];
-#pragma unroll
-    for (int st = 0; st < S; ++st) {
-        const float d = block_dot_int<DT>(g.q[st], dig) * xsc;
-        if constexpr (LAYOUT == LAYOUT_PACKED) part[st] = d;
-        else part[st] = g.s[st] * d;
-    }
-    wave_lds_sync();
-#pragma unroll
-    for (int st = 0; st < S; ++st) redw[st * kWave + lane] = part[st];
-    wave_lds_sync();
-    const int my_row = row0 + (lane / RPS) * SSTRIDE + lane % RPS;
-    if (lane < S * RPS && my_row < rend) {
-        const int st = lane / RPS;
-        const int r = lane - st * RPS;
-        const float *rp = &redw[st * kWave + r * NB];
-        float acc = 0.f;
-        if constexpr (LAYOUT == LAYOUT_PACKED) {
-#pragma unroll
-            for (int b = 0; b < NB; ++b) acc = __builtin_fmaf(g.rs[b], rp[b], acc);
-        } else {
-#pragma unroll
-            for (int b = 0; b < NB; ++b) acc += rp[b];
-        }
-        y[my_row] = acc;
-    }
-}
-
-// Each workgroup owns the contiguous rows [blockIdx*rows_per_block, +rows_per_block).
-// One iteration of the workgroup covers WAVES*S wave-steps of consecutive rows; wave w
-// takes wave-steps w, w+WAVES, ..., so each load instruction of the four waves reads
-// one contiguous span. Loads of iteration i+1 are in flight while iteration i is
-// reduced; the first iteration's loads are issued before the x conversion.
-template <int DT, int LAYOUT, int NB, int S>
-__global__ __launch_bounds__(256) void gemv_q_int(const uint8_t *__restrict__ w, size_t sc_off, uint32_t q_bytes,
-                                                  uint32_t s_bytes, const float *__restrict__ x,
-                                                  float *__restrict__ y, int M, int rows_per_block) {
-    constexpr int RPS = kWave / NB;                // rows per wave-step
-    constexpr int K = NB * kBlock;
-    constexpr int WAVES = 4;
-    constexpr int SSTRIDE = WAVES * RPS;           // rows between a wave's consecutive wave-steps
-    constexpr int STEP = WAVES * S * RPS;          // rows per workgroup iteration
-    __shared__ uint32_t lds_u[K];
-    __shared__ uint32_t lds_dig[NB * kDigitWords];
-    __shared__ float lds_xsc[NB];
-    __shared__ float red[WAVES][S * kWave];
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wid = threadIdx.x / kWave;
-    const int r_in = lane / NB;
-    const int blk = lane - r_in * NB;
-    const bool lane_on = r_in < RPS;
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(w, q_bytes);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(w + sc_off, s_bytes);
-    const int bbeg = blockIdx.x * rows_per_block;
-    const int rend = min(M, bbeg + rows_per_block);
-    float *redw = red[wid];
-
-    IntStage<DT, NB, S> A, B;
-    int row0 = bbeg + wid * RPS;
-    int_issue<DT, LAYOUT, NB, S, SSTRIDE>(A, rq, rs, row0, rend, r_in, blk, lane_on, lane);
-
-    prep_x_digits<DT>(x, K, lds_u, lds_dig, lds_xsc);
-    uint32_t dig[kDigitWords];
-#pragma unroll
-    for (int i = 0; i < kDigitWords; ++i) dig[i] = lds_dig[blk * kDigitWords + i];
-    const float xsc = lds_xsc[blk];
-
-    while (row0 < rend) {
-        int_issue<DT, LAYOUT, NB, S, SSTRIDE>(B, rq, rs, row0 + STEP, rend, r_in, blk, lane_on, lane);
-        int_consume<DT, LAYOUT, NB, S, SSTRIDE>(A, dig, xsc, redw, y, row0, rend, lane);
-        row0 += STEP;
-        if (row0 >= rend) break;
-        int_issue<DT, LAYOUT, NB, S, SSTRIDE>(A, rq, rs, row0 + STEP, rend, r_in, blk, lane_on, lane);
-        int_consume<DT, LAYOUT, NB, S, SSTRIDE>(B, dig, xsc, redw, y, row0, rend, lane);
-        row0 += STEP;
     }
 }
 
@@ -407,6 +208,7 @@ __global__ __launch_bounds__(256) void gemv_q_rows(const uint8_t *__restrict__ w
         for (int b = 0; b < batch; ++b) {
             const float *x = X + (size_t)b * K;
             float acc = 0.f;
+            bool nfl = false;
             for (int blk = lane; blk < nb; blk += kWave) {
                 uint32_t q[QT<DT>::QD];
                 float s;
@@ -421,10 +223,21 @@ __global__ __launch_bounds__(256) void gemv_q_rows(const uint8_t *__restrict__ w
                 float xs = 0.f;
 #pragma unroll
                 for (int i = 0; i < 32; ++i) xs += xv[i];
+                if (nonfinite::is_nf(xs)) {   // NaN / inf activations: zeroed here, folded in below
+                    nfl = true;
+                    xs = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        xv[i] = nonfinite::is_nf(xv[i]) ? 0.f : xv[i];
+                        xs += xv[i];
+                    }
+                }
                 acc = __builtin_fmaf(s, block_dot<DT>(q, xv, xs), acc);
             }
             acc = wave_sum(acc);
-            if (lane == 0) Y[(size_t)b * M + row] = acc;
+            const bool nf = __any(nfl);
+            if (lane == 0)
+                Y[(size_t)b * M + row] = nf ? acc + nonfinite::fold<DT, LAYOUT>(w, w + sc_off, nb, (int)row, x) : acc;
         }
     }
 }
@@ -578,32 +391,6 @@ void launch_cols(const uint8_t *w, size_t sc_off, int M, int nb, int rps, const 
                        st, w, sc_off, q_bytes, (uint32_t)(nblk * 4), x, y, M, nb, rps, rows_per_wave);
 }
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
-template <int DT, int LAYOUT, int NB, int S>
-void launch_int(const uint8_t *w, size_t sc_off, int M, const float *x, float *y, hipStream_t st, int waves_per_cu) {
-    constexpr int RPS = kWave / NB;
-    constexpr int STEP = 4 * S * RPS;                                   // rows per workgroup iteration
-    const long iters = (M + STEP - 1) / STEP;
-    const long want = std::max(1L, std::min((long)device_cus() * waves_per_cu / 4, iters));
-    const long iters_per_block = (iters + want - 1) / want;
-    const long blocks = (iters + iters_per_block - 1) / iters_per_block;
-    const int rows_per_block = (int)(iters_per_block * STEP);
-    const size_t nblk = (size_t)M * NB;
-    const uint32_t q_bytes = (uint32_t)(nblk * (LAYOUT == LAYOUT_PACKED ? QT<DT>::QB : QT<DT>::BB));
-    hipLaunchKernelGGL((gemv_q_int<DT, LAYOUT, NB, S>), dim3((unsigned)blocks), dim3(256), 0, st, w, sc_off, q_bytes,
-                       (uint32_t)(nblk * 4), x, y, M, rows_per_block);
-}
-
-template <int DT, int LAYOUT, int NB>
-bool try_int(const uint8_t *w, size_t sc_off, int M, const float *x, float *y, hipStream_t st) {
-    launch_int<DT, LAYOUT, NB, 8>(w, sc_off, M, x, y, st, 8);
-    return true;
-}
-
 template <int DT, int LAYOUT>
 int gemv_q_typed(const uint8_t *w, size_t sc_off, int M, int nb, const float *x, float *y, hipStream_t st) {
     if ((size_t)M * (size_t)nb * QT<DT>::BB >= (size_t(1) << 32) - 256) {
@@ -613,15 +400,7 @@ int gemv_q_typed(const uint8_t *w, size_t sc_off, int M, int nb, const float *x,
     const int rps = nb <= kWave ? kWave / nb : 0;
     if (rps > 0 && nb * rps * 4 >= kWave * 3) {   // >= 75% of lanes busy
         const long steps = (M + rps - 1) / rps;
-        // The integer-dot kernel is opt-in (SAPPHIRE_GEMV_INT=1): on gfx950 v_dot8c/v_dot4c
-        // issue at about a third of the rate of simple VALU ops, so it does not beat the
-        // fp32 convert+FMA kernel at the LM-head shape.
-        static const bool use_int = env_int("SAPPHIRE_GEMV_INT", 0) != 0;
-        const bool big = use_int && steps >= 8L * 8 * device_cus();
-        if (big && nb == 20) try_int<DT, LAYOUT, 20>(w, sc_off, M, x, y, st);
-        else if (big && nb == 32) try_int<DT, LAYOUT, 32>(w, sc_off, M, x, y, st);
-        else if (big && nb == 64) try_int<DT, LAYOUT, 64>(w, sc_off, M, x, y, st);
-        else if (steps >= 8L * 16 * device_cus())
+        if (steps >= 8L * 16 * device_cus())
             launch_cols<DT, LAYOUT, 8>(w, sc_off, M, nb, rps, x, y, st, 16);
         else if (steps >= 2L * 16 * device_cus())
             launch_cols<DT, LAYOUT, 2>(w, sc_off, M, nb, rps, x, y, st, 16);

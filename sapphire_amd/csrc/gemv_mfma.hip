@@ -34,6 +34,7 @@
 #include <algorithm>
 
 #include "internal.h"
+#include "nonfinite.h"
 
 namespace sapphire {
 
@@ -86,9 +87,11 @@ __device__ __forceinline__ float row16_scatter(const float (&a)[4], int n) {
 // group, digit d = n % 4) for the k-slots of lane group m = l / 16: elements 8m..8m+7 of
 // block 4g + j, in the order the A operand holds them (natural for Q8_0; even then odd
 // elements for Q4_0, whose A bytes are the low nibbles, then the high nibbles).
+// NaN and infinite activations are zeroed here (nf is set): the row results get their fold
+// added when they are stored.
 template <int DT>
 __device__ __forceinline__ void lane_digits(const float *__restrict__ x, int g, int lane, uint32_t &w0,
-                                            uint32_t &w1, float &p) {
+                                            uint32_t &w1, float &p, bool &nf) {
     const int n = lane & 15, m = lane >> 4;
     const int j = n >> 2, d = n & 3;
     const float4 *xp = reinterpret_cast<const float4 *>(x + (4 * g + j) * 32 + 8 * m);
@@ -96,7 +99,11 @@ __device__ __forceinline__ void lane_digits(const float *__restrict__ x, int g, 
     float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
     int mexp = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) mexp = max(mexp, (int)((__float_as_uint(v[i]) >> 23) & 0xFFu));
+    for (int i = 0; i < 8; ++i) {
+        nf |= nonfinite::is_nf(v[i]);
+        v[i] = nonfinite::is_nf(v[i]) ? 0.f : v[i];
+        mexp = max(mexp, (int)((__float_as_uint(v[i]) >> 23) & 0xFFu));
+    }
     // the block's 32 elements are held by lanes n, n+16, n+32, n+48
     mexp = max(mexp, __shfl_xor(mexp, 16, kWave));
     mexp = max(mexp, __shfl_xor(mexp, 32, kWave));
@@ -184,9 +191,11 @@ struct SoftPart {
 // tolerance)
 __device__ __forceinline__ float exp_fast(float d) { return __builtin_amdgcn_exp2f(d * 1.44269504088896341f); }
 
+// A +inf logit contributes exp(inf - inf) = NaN to the sum, as in utils.c:43-46, so every
+// probability of such a vector is NaN there and here.
 __device__ __forceinline__ void soft_push(SoftPart &p, float v, int row) {
     if (v > p.m) {                      // strict: an equal later value keeps the earlier index
-        p.s = (p.m == -INFINITY ? 0.f : p.s * exp_fast(p.m - v)) + 1.f;
+        p.s = (p.m == -INFINITY ? 0.f : p.s * exp_fast(p.m - v)) + exp_fast(v - v);
         p.m = v;
         p.i = row;
     } else {
@@ -207,15 +216,25 @@ __device__ __forceinline__ SoftPart soft_shfl_xor(SoftPart p, int mask) {
     return SoftPart{__shfl_xor(p.m, mask, kWave), __shfl_xor(p.s, mask, kWave), __shfl_xor(p.i, mask, kWave)};
 }
 
+// What tile_store needs for activations with NaN / inf elements (nf, wave-uniform): the
+// weight planes, the blocks per row and x itself, for the fold of its non-finite elements.
+struct NfCtx {
+    const uint8_t *wq, *wsc;
+    int nb;
+    const float *x;
+    bool nf;
+};
+
 // The 16 columns of each row summed across the row group; lane 16m + 4r stores row
 // 4m + r and, with SM, folds it into its softmax partial.
-template <bool SM>
+template <int DT, bool SM>
 __device__ __forceinline__ void tile_store(const float (&acc)[4], float *__restrict__ y, int M, int t, int lane,
-                                           SoftPart &sp) {
+                                           SoftPart &sp, const NfCtx &nc) {
     const int n = lane & 15;
-    const float v = row16_scatter(acc, n);
+    float v = row16_scatter(acc, n);
     const int row = t * kTileRows + 4 * (lane >> 4) + ((n >> 2) & 3);
     if ((n & 3) == 0 && row < M) {
+        if (nc.nf) v += nonfinite::fold<DT, LAYOUT_TILED>(nc.wq, nc.wsc, nc.nb, row, nc.x);
         y[row] = v;
         if constexpr (SM) soft_push(sp, v, row);
     }
@@ -245,12 +264,15 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
 
     float p[NG];
     long bop[NG];
+    bool nfl = false;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
         uint32_t w0, w1;
-        lane_digits<DT>(x, g, lane, w0, w1, p[g]);
+        lane_digits<DT>(x, g, lane, w0, w1, p[g], nfl);
         bop[g] = (long)(((unsigned long)w1 << 32) | w0);
     }
+    // the wave's lanes cover all of x
+    const NfCtx nc{wq, wsc, NG * kGroupBlocks, x, __any(nfl) != 0};
 
     float acc[4];
     SoftPart sp{-INFINITY, 0.f, 0x7fffffff};
@@ -259,12 +281,12 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
         while (t < ntiles) {
             if (t + nwaves < ntiles) tile_issue<DT, NG>(RB, rq, rs, t + nwaves, lane);
             tile_mfma<DT, NG>(RA, bop, p, lane, acc);
-            tile_store<SM>(acc, y, M, t, lane, sp);
+            tile_store<DT, SM>(acc, y, M, t, lane, sp, nc);
             t += nwaves;
             if (t >= ntiles) break;
             if (t + nwaves < ntiles) tile_issue<DT, NG>(RA, rq, rs, t + nwaves, lane);
             tile_mfma<DT, NG>(RB, bop, p, lane, acc);
-            tile_store<SM>(acc, y, M, t, lane, sp);
+            tile_store<DT, SM>(acc, y, M, t, lane, sp, nc);
             t += nwaves;
         }
     } else {
@@ -272,7 +294,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
             tile_mfma<DT, NG>(RA, bop, p, lane, acc);
             const int tn = t + nwaves;
             if (tn < ntiles) tile_issue<DT, NG>(RA, rq, rs, tn, lane);
-            tile_store<SM>(acc, y, M, t, lane, sp);
+            tile_store<DT, SM>(acc, y, M, t, lane, sp, nc);
             t = tn;
         }
     }
@@ -333,8 +355,9 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
         SoftPart t = wp[0];
         for (int w = 1; w < (int)(blockDim.x / kWave); ++w) t = soft_merge(t, wp[w]);
         tot = t;
-        // no logit above -inf (all NaN): index 0, as sample_greedy (utils.c:145-156) starts there
-        if (blockIdx.x == 0 && argmax) *argmax = t.i >= 0 && t.i < n ? t.i : 0;
+        // sample_greedy (utils.c:145-156) starts at index 0 and only a greater logit replaces
+        // it: 0 when logits[0] is NaN or no logit is above -inf, else the first maximum
+        if (blockIdx.x == 0 && argmax) *argmax = (t.i >= 0 && t.i < n && !isnan(logits[0])) ? t.i : 0;
     }
     __syncthreads();
     if (!probs) return;

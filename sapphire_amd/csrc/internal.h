@@ -113,6 +113,10 @@ int launch_gelu_mul(float *gate, const float *up, int n, hipStream_t s);
 int launch_softmax_argmax(const float *logits, int n, float *probs, int *argmax, float *scratch,
                           hipStream_t s);
 size_t softmax_scratch_floats(int n);
+// The current device's buffer for launch_softmax_argmax's partials (allocated once per device,
+// kept until the process ends; calls that overlap on one device must share a stream). NULL on
+// error.
+float *softmax_partials_scratch();
 enum : int { UOP_GELU = 0, UOP_SILU = 1, UOP_RELU = 2, UOP_SCALE = 3, UOP_SOFTCAP = 4 };
 int launch_unary(float *x, int n, int op, float a, hipStream_t s);
 int launch_axpy(float *dst, const float *src, int n, float a, bool fused, hipStream_t s);

@@ -183,8 +183,9 @@ __global__ __launch_bounds__(kSmBlock) void softmax_finish(const float *__restri
         if (threadIdx.x == 0) {
             s_gmax = m.v;
             s_inv = 1.0f / s;
-            // no logit above -inf (all NaN): index 0, as sample_greedy (utils.c:145-156)
-            if (blockIdx.x == 0 && argmax_out) *argmax_out = m.i >= 0 && m.i < n ? m.i : 0;
+            // sample_greedy (utils.c:145-156) starts at index 0 and only a greater logit
+            // replaces it: 0 when x[0] is NaN or no logit is above -inf
+            if (blockIdx.x == 0 && argmax_out) *argmax_out = (m.i >= 0 && m.i < n && !isnan(x[0])) ? m.i : 0;
         }
     }
     __syncthreads();

@@ -277,6 +277,13 @@ float *standalone_part(void *scratch) { return reinterpret_cast<float *>(static_
 
 }  // namespace
 
+namespace sapphire {
+float *softmax_partials_scratch() {
+    void *s = partial_scratch();
+    return s ? standalone_part(s) : nullptr;
+}
+}  // namespace sapphire
+
 extern "C" {
 
 int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *argmax, void *stream) {

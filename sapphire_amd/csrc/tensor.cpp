@@ -114,9 +114,14 @@ float tensor_get_f32(const tensor_t *t, size_t idx) {
     return 0.0f;  // quantized element access is not provided (tensor.c:238-243)
 }
 
+// The reference reads a tensor's host data on every GEMV; here the device copy is marked stale
+// so the next GPU use uploads the new values. (Writes through tensor_data_mutable /
+// tensor_data_f32 bypass this: their callers invalidate with sapphire_tensor_invalidate.)
 int tensor_set_f32(tensor_t *t, size_t idx, float val) {
     if (!t || idx >= tensor_numel(t) || t->dtype != DTYPE_F32) return -1;
     static_cast<float *>(t->data)[idx] = val;
+    std::lock_guard<std::mutex> g(t->dev_mu);
+    t->dev_stale = t->dev != nullptr || t->dev_tiled != nullptr;
     return 0;
 }
 
@@ -159,8 +164,10 @@ int tensor_ref_count(const tensor_t *t) { return t ? t->ref_count : 0; }
 
 namespace sapphire {
 
-void tensor_drop_device(tensor_t *t) {
-    std::lock_guard<std::mutex> g(t->dev_mu);
+namespace {
+
+// Frees the device copies; the caller holds t->dev_mu.
+void drop_device_locked(tensor_t *t) {
     if (t->dev || t->dev_tiled) {
         int cur = 0;
         (void)hipGetDevice(&cur);
@@ -172,9 +179,8 @@ void tensor_drop_device(tensor_t *t) {
     t->dev = nullptr;
     t->dev_tiled = nullptr;
     t->dev_bytes = 0;
+    t->dev_stale = false;
 }
-
-namespace {
 
 // Uploads the AoS blocks of a quantized tensor and converts them to `lay` on the device.
 void *upload_quant(const tensor_t *t, int lay, hipStream_t s) {
@@ -195,9 +201,15 @@ void *upload_quant(const tensor_t *t, int lay, hipStream_t s) {
 
 }  // namespace
 
+void tensor_drop_device(tensor_t *t) {
+    std::lock_guard<std::mutex> g(t->dev_mu);
+    drop_device_locked(t);
+}
+
 const void *tensor_device_weights(const tensor_t *tc, int *layout, hipStream_t s) {
     tensor_t *t = const_cast<tensor_t *>(tc);
     std::lock_guard<std::mutex> g(t->dev_mu);
+    if (t->dev_stale) drop_device_locked(t);
     int dev = 0;
     if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
     if (t->dev && t->dev_device == dev) {

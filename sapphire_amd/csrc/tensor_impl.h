@@ -23,6 +23,8 @@ struct tensor_t {
     int dev_device = -1;
     // TILED copy for batched calls when the GEMV copy is PACKED (same device as dev)
     void *dev_tiled = nullptr;
+    // set by tensor_set_f32: the host data changed, the device copies are rebuilt on next use
+    bool dev_stale = false;
 };
 
 namespace sapphire {

@@ -184,14 +184,7 @@ def test_kernel_gemm_tensor_api(hip, oracle, dtype, shape, batch):
 
 # ---- the fused input / output transforms (sapphire_gemm_q_fused_dev) ----
 
-class _GemmIn(C.Structure):
-    _fields_ = [("x", C.c_void_p), ("ldx", C.c_int), ("parts", C.c_void_p), ("nparts", C.c_int), ("ldp", C.c_int),
-                ("part_stride", C.c_size_t), ("w_delta", C.c_void_p), ("resid_out", C.c_void_p), ("ldr", C.c_int),
-                ("w_norm", C.c_void_p), ("eps", C.c_float)]
-
-
-class _GemmOut(C.Structure):
-    _fields_ = [("y", C.c_void_p), ("ldy", C.c_int), ("parts", C.c_void_p), ("geglu", C.c_int)]
+from sapphire_amd._lib import GemmInput as _GemmIn, GemmOutput as _GemmOut  # noqa: E402
 
 
 def _fused(hip, qm, batch, gin, gout, ws=None):

@@ -119,14 +119,19 @@ def test_argmax_without_a_finite_logit(hip, oracle, fill):
     x = np.full(n, fill, np.float32)
     arg = DeviceArray.empty(1, np.int32)
     arg.upload(np.array([-7], np.int32))
-    check(hip.sapphire_softmax_argmax_dev(dev(x).ptr, n, None, arg.ptr, None))
+    dx = dev(x)                                   # held until the kernels have run
+    check(hip.sapphire_softmax_argmax_dev(dx.ptr, n, None, arg.ptr, None))
     assert int(arg.numpy()[0]) == 0
     assert oracle.argmax(x) == 0
-    # the fused epilogue: a NaN activation makes every logit NaN
+    # the fused epilogue: an activation vector of NaN (or -inf) makes every logit NaN (NaN
+    # products, or +-inf terms of both signs), and the token is sample_greedy's 0
     W = synth.quant_matrix(synth.Q8_0, n, 640, seed=9, tensor_id=1)
     qm = QMatrix(synth.Q8_0, W, layout=2)
     xv = np.full(640, fill, np.float32)
+    dxv = dev(xv)
     logits = DeviceArray.empty(n)
     arg.upload(np.array([-7], np.int32))
-    check(hip.sapphire_gemv_softmax_dev(synth.Q8_0, 2, qm.ptr(), n, 640, dev(xv).ptr, logits.ptr, None, arg.ptr, None))
-    assert 0 <= int(arg.numpy()[0]) < n
+    check(hip.sapphire_gemv_softmax_dev(synth.Q8_0, 2, qm.ptr(), n, 640, dxv.ptr, logits.ptr, None, arg.ptr, None))
+    ref = oracle.gemv(synth.Q8_0, W, xv, nthreads=8)
+    assert np.isnan(ref).all() and np.isnan(logits.numpy()).all()
+    assert int(arg.numpy()[0]) == oracle.argmax(ref) == 0

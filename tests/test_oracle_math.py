@@ -245,3 +245,53 @@ def test_decode_step_float64(oracle):
         assert err < 2e-4, f"step {s}: relative error {err}"
         t = int(np.argmax(want))
         assert t == toks[s]
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8])
+def test_gemv_non_finite_activations_are_the_ieee_fold(oracle, dtype):
+    """With NaN / infinite activations every row's fp32 accumulation ends in the IEEE sum of
+    the non-finite terms fl(w * x) alone (finite terms cannot change NaN or +-inf): NaN for a
+    NaN activation, for w = 0 under an infinity (0 * inf) or for infinities of both signs,
+    else the infinity. numpy's float32 arithmetic computes that sum independently."""
+    m, k = 64, 640
+    W = synth.quant_matrix(dtype, m, k, 9, 9)
+    deq = oracle.dequant(dtype, W).reshape(m, k)
+    deq32 = deq.astype(np.float32)
+    for pos in ([(5, np.inf)], [(5, np.inf), (600, -np.inf)], [(70, -np.inf), (72, -np.inf)], [(300, np.nan)]):
+        x = synth.normal_f32(k, 9, 2)
+        for p, v in pos:
+            x[p] = v
+        if dtype == Q8:                                   # a zero weight under the first one
+            W2 = W.copy()
+            W2[0, pos[0][0] // 32]["q"][pos[0][0] % 32] = 0
+        else:
+            W2 = W.copy()
+            byte = int(W2[0, pos[0][0] // 32]["q"][(pos[0][0] % 32) >> 1])
+            e = pos[0][0] % 32
+            W2[0, pos[0][0] // 32]["q"][e >> 1] = (byte & 0x0F) | 0x80 if e & 1 else (byte & 0xF0) | 0x08
+        d2 = deq32.copy()
+        d2[0] = oracle.dequant(dtype, W2[0:1]).reshape(k)
+        nf = ~np.isfinite(x)
+        with np.errstate(invalid="ignore", over="ignore"):
+            want = np.zeros(m, np.float32)
+            for p in np.flatnonzero(nf):
+                want = want + d2[:, p] * x[p]
+        got = oracle.gemv(dtype, W2, x)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(got[~np.isnan(want)], want[~np.isnan(want)])
+        assert not np.isfinite(got).any() and np.isnan(got[0])
+
+
+def test_softmax_and_greedy_of_non_finite_logits(oracle):
+    """utils.c:18-59 and 145-156 with special values: a +inf or NaN logit makes every
+    probability NaN (exp(inf - inf) or NaN enters the sum); the greedy token is the first
+    +inf, and 0 whenever logits[0] is NaN (nothing compares greater than the NaN it starts
+    from); all -inf logits give index 0."""
+    x = synth.normal_f32(1000, 10, 1)
+    a = x.copy(); a[17] = np.inf; a[400] = np.inf
+    assert np.isnan(oracle.softmax(a)).all() and oracle.argmax(a) == 17
+    b = x.copy(); b[5] = np.nan
+    assert np.isnan(oracle.softmax(b)).all() and oracle.argmax(b) == int(np.argmax(np.where(np.isnan(b), -np.inf, b)))
+    c = x.copy(); c[0] = np.nan
+    assert oracle.argmax(c) == 0
+    assert oracle.argmax(np.full(50, -np.inf, np.float32)) == 0

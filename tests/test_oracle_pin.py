@@ -46,6 +46,21 @@ def test_row_kernels(oracle, ref, dtype, nb):
 
 
 @pytest.mark.parametrize("dtype", [Q4, Q8], ids=["q4_0", "q8_0"])
+def test_gemv_non_finite(oracle, ref, dtype):
+    """NaN and infinite activations (one NaN; +inf and -inf in different blocks; a run of
+    infinities in one block): the same NaN pattern and the same infinities as the reference."""
+    m, k = 96, 640
+    W = synth.quant_matrix(dtype, m, k, 79, 1)
+    for marks in ([(11, np.nan)], [(5, np.inf), (600, -np.inf)], [(64, np.inf), (66, np.inf), (70, -np.inf)]):
+        x = synth.normal_f32(k, 79, 2)
+        for p, v in marks:
+            x[p] = v
+        want = oracle.gemv(dtype, W, x, nthreads=4)
+        for nt in (1, 8):
+            assert np.array_equal(bits(ref.gemv(dtype, W, x, nthreads=nt)), bits(want))
+
+
+@pytest.mark.parametrize("dtype", [Q4, Q8], ids=["q4_0", "q8_0"])
 @pytest.mark.parametrize("shape", [(2048, 640), (640, 2048), (1024, 640), (256, 640), (640, 1024),
                                    (333, 1152), (96, 6912)], ids=lambda s: f"{s[0]}x{s[1]}")
 def test_pooled_gemv(oracle, ref, dtype, shape):

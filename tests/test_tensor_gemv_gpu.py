@@ -111,3 +111,39 @@ def test_ctx_create_destroy_repeated(hip):
         c = hip.kernel_ctx_create(0, 1024)
         assert c and hip.kernel_ctx_init(c) == 0
         hip.kernel_ctx_destroy(c)
+
+
+def test_weights_changed_after_a_gemv(hip, ctx, oracle):
+    """The reference reads a weight tensor's host data on every call. tensor_set_f32 after a
+    GEMV therefore changes the next GEMV's result (the device copy is rebuilt), and a write
+    through the raw data pointer does once sapphire_tensor_invalidate has been called."""
+    from sapphire_amd import synth
+    A = matrix(hip, 4, 8, range(32))
+    x = np.ones(8, np.float32)
+    y = np.zeros(4, np.float32)
+    assert hip.kernel_gemv(ctx, f32p(y), A, f32p(x)) == 0
+    assert np.array_equal(y, np.arange(32, dtype=np.float32).reshape(4, 8).sum(1))
+    assert hip.tensor_set_f32(A, 9, 100.0) == 0
+    assert hip.kernel_gemv(ctx, f32p(y), A, f32p(x)) == 0
+    want = np.arange(32, dtype=np.float32).reshape(4, 8)
+    want[1, 1] = 100.0
+    assert np.array_equal(y, want.sum(1))
+    hip.tensor_release(A)
+    # a quantized view whose blocks the caller rewrites in place
+    for dtype in (synth.Q4_0, synth.Q8_0):
+        W = synth.quant_matrix(dtype, 64, 640, 5, dtype)
+        xq = synth.normal_f32(640, 5, 1)
+        A = hip.tensor_create_view(dtype, 2, (C.c_int * 2)(64, 640), W.ctypes.data)
+        yq = np.zeros(64, np.float32)
+        assert hip.kernel_gemv(ctx, f32p(yq), A, f32p(xq)) == 0
+        assert close_to(yq, oracle.gemv(dtype, W, xq))
+        W["scale"] *= 2.0
+        assert hip.sapphire_tensor_invalidate(A) == 0
+        assert hip.kernel_gemv(ctx, f32p(yq), A, f32p(xq)) == 0
+        assert close_to(yq, oracle.gemv(dtype, W, xq))
+        hip.tensor_release(A)
+
+
+def close_to(got, ref):
+    from tests.conftest import close
+    return close(got, ref)[0]
