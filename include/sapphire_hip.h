@@ -159,6 +159,17 @@ int sapphire_softmax_argmax_dev(const float *logits, int n, float *probs, int *a
 int sapphire_gemv_softmax_dev(int dtype, int layout, const void *w, int M, int K, const float *x, float *logits,
                               float *probs, int *argmax_dev, void *stream);
 
+/* sapphire_gemv_softmax_dev for callers that cannot allocate device memory (code under HIP
+ * graph capture, fixed serving loops, hosts that forbid hipMalloc). No counterpart in the
+ * reference. Same arguments, results and kernels; the reduction partials live in a fixed
+ * 64 KiB array of the library's device code (one per GPU, kept until the process ends), so
+ * nothing is allocated or freed. The array's device address is looked up on a device's first
+ * call: make that call once before capturing. Sizes needing more partials than the array
+ * holds are rejected (-1) before any launch; the TILED layout needs K/128 in {5, 8, 9}. Calls
+ * that overlap on one GPU share the array and race: order them on one stream. */
+int sapphire_gemv_softmax_noalloc_dev(int dtype, int layout, const void *w, int M, int K, const float *x,
+                                      float *logits, float *probs, int *argmax_dev, void *stream);
+
 /* ---- device copies of tensor_t weights ----
  * The device-resident copy kernel_gemv keeps for a 2-D weight tensor (Q4_0/Q8_0 in the
  * PACKED layout, F32/BF16 as is), created on first use; *layout receives its layout.

@@ -76,6 +76,7 @@ def load_library(path: str):
     P("kernel_quantize", i32, [vp, vp, i32, vp])
     P("sapphire_softmax_argmax_dev", i32, [vp, i32, vp, vp, vp])
     P("sapphire_gemv_softmax_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp, vp, vp])
+    P("sapphire_gemv_softmax_noalloc_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp, vp, vp])
     P("sapphire_gemm_workspace_bytes", sz, [i32, i32, i32])
     P("sapphire_gemm_q_dev", i32, [i32, i32, vp, i32, i32, vp, i32, vp, vp, vp])
     P("sapphire_gemm_splits", i32, [i32])

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libsapphire_hip.so")
 SOURCES = ["runtime.cpp", "tensor.cpp", "dispatch.cpp", "decoder.cpp", "gemv.hip", "gemv_mfma.hip", "gemm_mfma.hip",
            "ops.hip", "decode.hip",
-           "decode_persist.hip", "quantize.hip", "gemm_bf16.hip"]
+           "decode_persist.hip", "quantize.hip", "gemm_bf16.hip", "noalloc.cpp"]
 ARCH = os.environ.get("SAPPHIRE_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [
