@@ -8,9 +8,9 @@
  * resident in HBM after the first call that reads them. Device-pointer and
  * stream-ordered forms of the same operations are declared in sapphire_hip.h.
  *
- * Scalar helpers float silu/relu/gelu/geglu(float) (reference activations.c:16-105)
- * are host arithmetic by nature and are not part of this library; the vector forms
- * that the engine calls on its buffers (gelu_inplace, sapphire_geglu, ...) are.
+ * The scalar activations silu/relu/gelu/geglu(float) are one value's host arithmetic (the
+ * reference's formula with its compiler's contraction, libm expf/tanhf); the vector forms the
+ * engine calls on its buffers (gelu_inplace, sapphire_geglu, ...) run on the GPU.
  */
 #ifndef SAPPHIRE_HIP_KERNELS_H
 #define SAPPHIRE_HIP_KERNELS_H
@@ -75,6 +75,23 @@ float quantized_gemv_q4_0_unaligned(const void *W_row, const float *x, int block
 float quantized_gemv_q8_0_aligned(const void *W_row, const float *x, int block_count, int block_size);
 float quantized_gemv_q8_0_unaligned(const void *W_row, const float *x, int block_count, int block_size);
 
+/* ---- F32 / BF16 rows: reference kernels.h:121-126 ----
+ * dot(W_row[0..cols), x[0..cols)) with cols = block_count when block_size == 1, else
+ * block_count * block_size (f32_avx.c:21-83, bf16_avx.c:21-108); 0.0f when a pointer is
+ * NULL or cols <= 0. The avx2 and scalar names compute the same dot on the GPU (one row); the
+ * reference's two differ only in fp32 summation order. */
+float quantized_gemv_bf16_avx2(const void *W_row, const float *x, int block_count, int block_size);
+float quantized_gemv_bf16_scalar(const void *W_row, const float *x, int block_count, int block_size);
+float quantized_gemv_f32_avx2(const void *W_row, const float *x, int block_count, int block_size);
+float quantized_gemv_f32_scalar(const void *W_row, const float *x, int block_count, int block_size);
+
+/* ---- one weight row times a batch: reference kernels.h:129-130 ----
+ * Y[b * out_stride] = w_row[0..d_model) . X[b * d_model ..] for b < batch_size
+ * (f32_avx.c:97-135, bf16_avx.c:110-150); nothing is written when an argument is NULL or a
+ * size is not positive. */
+void kernel_gemm_f32_avx2(const gemm_args_t *args);
+void kernel_gemm_bf16_avx2(const gemm_args_t *args);
+
 /* ---- tensor GEMV API: reference kernels.h:140-166, src/kernels/dispatch.c ---- */
 
 /* y[M] = A[M,K] . x[K]. A: 2-D tensor of dtype Q4_0, Q8_0, F32 or BF16 (rows = outputs).
@@ -103,6 +120,10 @@ int kernel_gemv_batch(kernel_context_t *ctx, float *Y, const tensor_t *A, const 
 int kernel_get_simd_lane_count(tensor_dtype_t dtype);
 
 /* ---- activations & normalization: reference kernels.h:173-207 ---- */
+float silu(float x);                                                  /* x / (1 + e^-x), activations.c:16-20 */
+float relu(float x);                                                  /* activations.c:37-39 */
+float gelu(float x);                       /* 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))), :64-76 */
+float geglu(float x, float y);                                        /* x * gelu(y), :103-105 */
 void gelu_inplace(float *x, int n);                                   /* activations.c:78-82 */
 int sapphire_geglu(float *output, const float *input, size_t size);  /* [x|y] -> x*gelu(y); -1 on bad args */
 void silu_inplace(float *x, int n);                                   /* activations.c:22-26 */

@@ -332,6 +332,31 @@ void oracle_gelu_mul(float *gate, const float *up, int n) {
     for (int i = 0; i < n; ++i) gate[i] *= up[i];                         /* :154-156 */
 }
 
+/* silu: activations.c:16-20 (a divide, then a product; nothing to contract). */
+float oracle_silu(float x) {
+    const float sigmoid = 1.0f / (1.0f + expf(-x));
+    return x * sigmoid;
+}
+
+/* geglu: activations.c:103-105. */
+float oracle_geglu(float x, float y) { return x * oracle_gelu(y); }
+
+/* apply_rope: rope.c:17-25 -> apply_positional_encoding (positional_encoding.c:76-104) with
+ * rope_encoding_strategy (:16-40). Pair j/2 of (x[j], x[j+1]), j + 1 < head_dim, rotates by
+ * theta = pos * powf(1/base, 2 (j/2) / head_dim); the reference build contracts the second
+ * product of each line onto the first one's result (pinned against the compiled reference). */
+void oracle_apply_rope(float *x, int pos, int head_dim, float base) {
+    if (!x) return;
+    for (int j = 0; j + 1 < head_dim; j += 2) {
+        const float inv_freq = powf(1.0f / base, 2.0f * (float)(j / 2) / (float)head_dim);
+        const float theta = (float)pos * inv_freq;
+        const float c = cosf(theta), s = sinf(theta);
+        const float xe = x[j], xo = x[j + 1];
+        x[j] = fmaf(-xo, s, xe * c);
+        x[j + 1] = fmaf(xo, c, xe * s);
+    }
+}
+
 /* ------------------------------------------------------------------------- */
 /* utils.c: softmax, argmax, vector ops.                                       */
 /* ------------------------------------------------------------------------- */

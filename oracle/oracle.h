@@ -54,6 +54,9 @@ int   oracle_rope_precompute_freqs(float *cos_t, float *sin_t, int d_k, int max_
 void  oracle_rope_apply_fast(float *x, int pos, int head_dim, const float *cos_t, const float *sin_t);
 float oracle_gelu(float x);
 void  oracle_gelu_mul(float *gate, const float *up, int n);   /* gate = gelu(gate) * up */
+float oracle_silu(float x);
+float oracle_geglu(float x, float y);                          /* x * gelu(y) */
+void  oracle_apply_rope(float *x, int pos, int head_dim, float base);   /* interleaved pairs */
 void  oracle_softmax(float *x, int n);
 int   oracle_sample_greedy(const float *logits, int n);
 void  oracle_vec_add(float *dst, const float *src, int n);

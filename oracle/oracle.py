@@ -76,12 +76,19 @@ class Oracle:
         L.oracle_rope_apply_fast.argtypes = [vp, i, i, vp, vp]
         L.oracle_gelu.restype = f
         L.oracle_gelu.argtypes = [f]
+        L.oracle_silu.restype = f
+        L.oracle_silu.argtypes = [f]
+        L.oracle_geglu.restype = f
+        L.oracle_geglu.argtypes = [f, f]
+        L.oracle_apply_rope.argtypes = [vp, i, i, f]
         L.oracle_gelu_mul.argtypes = [vp, vp, i]
         L.oracle_softmax.argtypes = [vp, i]
         L.oracle_sample_greedy.restype = i
         L.oracle_sample_greedy.argtypes = [vp, i]
         L.oracle_vec_dot.restype = f
         L.oracle_vec_dot.argtypes = [vp, vp, i]
+        L.oracle_vec_add.argtypes = [vp, vp, i]
+        L.oracle_bf16_to_f32.argtypes = [vp, vp, i]
         L.oracle_decode_step.restype = i
         L.oracle_decode_step.argtypes = [C.POINTER(ModelStruct), i, i, vp]
         for n in ("oracle_f_row", "oracle_f_row_scalar"):
@@ -163,6 +170,11 @@ class Oracle:
         self.lib.oracle_rope_apply_fast(_p(x), pos, x.shape[0], _p(cos_t), _p(sin_t))
         return x
 
+    def apply_rope(self, x, pos, base):
+        x = np.ascontiguousarray(x, np.float32).copy()
+        self.lib.oracle_apply_rope(_p(x), pos, x.shape[0], base)
+        return x
+
     def gelu_mul(self, gate, up):
         g = gate.copy()
         self.lib.oracle_gelu_mul(_p(g), _p(up), g.shape[0])
@@ -211,6 +223,13 @@ class Reference:
         L.rope_apply_fast.argtypes = [vp, i, i, vp, vp]
         L.gelu.restype = f
         L.gelu.argtypes = [f]
+        for n in ("silu", "relu"):
+            getattr(L, n).restype = f
+            getattr(L, n).argtypes = [f]
+        L.geglu.restype = f
+        L.geglu.argtypes = [f, f]
+        L.apply_rope.argtypes = [vp, i, i, f]
+        L.apply_rope_default.argtypes = [vp, i, i]
         L.gelu_inplace.argtypes = [vp, i]
         L.softmax.argtypes = [vp, i]
         L.sample_greedy.restype = i

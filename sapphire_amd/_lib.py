@@ -114,8 +114,20 @@ def load_library(path: str):
     P("kernel_ctx_destroy", None, [vp])
     P("kernel_parallel_for", i32, [vp, vp, vp, i32])
     for n in ("quantized_gemv_q4_0_aligned", "quantized_gemv_q4_0_unaligned",
-              "quantized_gemv_q8_0_aligned", "quantized_gemv_q8_0_unaligned"):
+              "quantized_gemv_q8_0_aligned", "quantized_gemv_q8_0_unaligned",
+              "quantized_gemv_bf16_avx2", "quantized_gemv_bf16_scalar",
+              "quantized_gemv_f32_avx2", "quantized_gemv_f32_scalar"):
         P(n, f32, [vp, vp, i32, i32])
+    P("kernel_gemm_f32_avx2", None, [vp])
+    P("kernel_gemm_bf16_avx2", None, [vp])
+    for n in ("silu", "relu", "gelu"):
+        P(n, f32, [f32])
+    P("geglu", f32, [f32, f32])
+    # rope.h
+    P("rope_precompute_freqs", i32, [vp, vp, i32, i32, f32])
+    P("rope_apply_fast", None, [vp, i32, i32, vp, vp])
+    P("apply_rope", None, [vp, i32, i32, f32])
+    P("apply_rope_default", None, [vp, i32, i32])
     P("kernel_gemv", i32, [vp, vp, vp, vp])
     P("kernel_gemm", i32, [vp, vp, vp, vp, i32, i32])
     P("kernel_gemv_tensor", i32, [vp, vp, vp, vp])

@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "../../include/decoder.h"
+#include "../../include/rope.h"
 #include "decode_kernels.h"
 #include "internal.h"
 
@@ -212,20 +213,12 @@ bool upload_tiled(sapphire_decoder *d, int dt, std::initializer_list<std::pair<c
     return true;
 }
 
-// rope_precompute_freqs (rope.c:41-63): half-split tables [max_ctx][hd] in fp32 with the
-// host libm, exactly as the reference computes them at session creation.
+// Half-split tables [max_ctx][hd] from rope_precompute_freqs (rope.c:41-63; host libm, as the
+// reference computes them at session creation).
 void rope_tables(int hd, int max_ctx, float base, std::vector<float> &c, std::vector<float> &s) {
     c.assign((size_t)max_ctx * hd, 0.f);
     s.assign((size_t)max_ctx * hd, 0.f);
-    const int half = hd / 2;
-    for (int pos = 0; pos < max_ctx; ++pos)
-        for (int m = 0; m < half; ++m) {
-            const float freq = 1.0f / powf(base, 2.0f * (float)m / (float)hd);
-            const float angle = (float)pos * freq;
-            const float cv = cosf(angle), sv = sinf(angle);
-            c[(size_t)pos * hd + m] = c[(size_t)pos * hd + m + half] = cv;
-            s[(size_t)pos * hd + m] = s[(size_t)pos * hd + m + half] = sv;
-        }
+    (void)rope_precompute_freqs(c.data(), s.data(), hd, max_ctx, base);
 }
 
 bool layer_is_global(const sapphire_decoder_config_t &c, int l) {   // attention.c:104-111

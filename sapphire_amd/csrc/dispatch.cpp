@@ -14,8 +14,11 @@
 #include <unistd.h>
 #include <vector>
 
+#include <cmath>
+
 #include "../../include/kernels.h"
 #include "../../include/quantize.h"
+#include "../../include/rope.h"
 #include "internal.h"
 #include "tensor_impl.h"
 
@@ -225,6 +228,51 @@ int norm_host(float *out, const float *in, const float *w, float eps, int dim, i
                       });
 }
 
+// One F32 / BF16 row of cols elements dotted with x (the row kernels of f32_avx.c / bf16_avx.c)
+// as a one-row GEMV.
+float f_row_dot(int dt, const void *W_row, const float *x, int block_count, int block_size) {
+    if (!W_row || !x) return 0.0f;
+    const long cols = block_size == 1 ? (long)block_count : (long)block_count * (long)block_size;
+    if (cols <= 0 || cols > (1L << 28)) return 0.0f;
+    kernel_context_t *c = default_ctx();
+    if (!c) return 0.0f;
+    const int K = (int)cols;
+    const size_t es = dt == DT_F32 ? 4 : 2;
+    float y = 0.0f;
+    const int rc = run_staged(c, {HostVec{W_row, nullptr, es * (size_t)K}, HostVec{x, nullptr, sizeof(float) * (size_t)K}},
+                              {HostVec{nullptr, &y, sizeof(float)}},
+                              [&](std::vector<void *> &i, std::vector<void *> &o, hipStream_t s) {
+                                  return launch_gemv_f(dt, i[0], 1, K, static_cast<float *>(i[1]),
+                                                       static_cast<float *>(o[0]), s);
+                              });
+    return rc == 0 ? y : 0.0f;
+}
+
+// One weight row times a batch (kernel_gemm_{f32,bf16}_avx2): Y[b * out_stride] = w . X[b].
+// Computed as the GEMV of the batch matrix X [batch][d_model] with w as the vector (the same
+// products; BF16 weights widen exactly to fp32 first).
+void gemm_row(int dt, const gemm_args_t *a) {
+    if (!a || !a->w_row || !a->X || !a->Y || a->batch_size <= 0 || a->d_model <= 0) return;
+    kernel_context_t *c = default_ctx();
+    if (!c) return;
+    const int B = a->batch_size, K = a->d_model;
+    const size_t es = dt == DT_F32 ? 4 : 2;
+    std::vector<float> y((size_t)B), wf((size_t)K);
+    const int rc = run_staged(
+        c, {HostVec{a->w_row, nullptr, es * (size_t)K}, HostVec{a->X, nullptr, sizeof(float) * (size_t)B * K}},
+        {HostVec{nullptr, y.data(), sizeof(float) * (size_t)B}, HostVec{nullptr, wf.data(), sizeof(float) * (size_t)K}},
+        [&](std::vector<void *> &i, std::vector<void *> &o, hipStream_t s) {
+            float *w = static_cast<float *>(i[0]);
+            if (dt == DT_BF16) {
+                w = static_cast<float *>(o[1]);
+                if (launch_bf16_to_f32(w, static_cast<uint16_t *>(i[0]), K, s) != 0) return -1;
+            }
+            return launch_gemv_f(DT_F32, i[1], B, K, w, static_cast<float *>(o[0]), s);
+        });
+    if (rc != 0) return;
+    for (int b = 0; b < B; ++b) a->Y[(size_t)b * (size_t)a->out_stride] = y[(size_t)b];
+}
+
 }  // namespace
 
 extern "C" {
@@ -290,6 +338,12 @@ float quantized_gemv_q4_0_aligned(const void *W, const float *x, int nb, int bs)
 float quantized_gemv_q4_0_unaligned(const void *W, const float *x, int nb, int bs) { return row_dot(DT_Q4_0, W, x, nb, bs); }
 float quantized_gemv_q8_0_aligned(const void *W, const float *x, int nb, int bs) { return row_dot(DT_Q8_0, W, x, nb, bs); }
 float quantized_gemv_q8_0_unaligned(const void *W, const float *x, int nb, int bs) { return row_dot(DT_Q8_0, W, x, nb, bs); }
+float quantized_gemv_bf16_avx2(const void *W, const float *x, int nb, int bs) { return f_row_dot(DT_BF16, W, x, nb, bs); }
+float quantized_gemv_bf16_scalar(const void *W, const float *x, int nb, int bs) { return f_row_dot(DT_BF16, W, x, nb, bs); }
+float quantized_gemv_f32_avx2(const void *W, const float *x, int nb, int bs) { return f_row_dot(DT_F32, W, x, nb, bs); }
+float quantized_gemv_f32_scalar(const void *W, const float *x, int nb, int bs) { return f_row_dot(DT_F32, W, x, nb, bs); }
+void kernel_gemm_f32_avx2(const gemm_args_t *args) { gemm_row(DT_F32, args); }
+void kernel_gemm_bf16_avx2(const gemm_args_t *args) { gemm_row(DT_BF16, args); }
 
 int kernel_gemv(kernel_context_t *ctx, float *y, const tensor_t *A, const float *x) {
     if (!y || !A || !x) {
@@ -439,6 +493,82 @@ int kernel_get_simd_lane_count(tensor_dtype_t dtype) {
 void gelu_inplace(float *x, int n) { (void)unary_host(x, n, UOP_GELU, 0.f); }
 void silu_inplace(float *x, int n) { (void)unary_host(x, n, UOP_SILU, 0.f); }
 void relu_inplace(float *x, int n) { (void)unary_host(x, n, UOP_RELU, 0.f); }
+
+// Scalar activations (activations.c:16-105): one value's host arithmetic with libm, written
+// with the fused multiply-add the reference build contracts x + 0.044715 x^3 into.
+float silu(float x) {
+    const float sigmoid = 1.0f / (1.0f + expf(-x));
+    return x * sigmoid;
+}
+float relu(float x) { return x > 0.0f ? x : 0.0f; }
+float gelu(float x) {
+    const float y = 0.7978845608f * fmaf((0.044715f * x) * x, x, x);
+    return 0.5f * x * (1.0f + tanhf(y));
+}
+float geglu(float x, float y) { return x * gelu(y); }
+
+// rope.c:41-63 on the host with libm, the same formula and rounding as the reference.
+int rope_precompute_freqs(float *freqs_cos, float *freqs_sin, int d_k, int max_context_len, float rope_base) {
+    if (!freqs_cos || !freqs_sin) return -1;
+    const int half = d_k / 2;
+    for (int pos = 0; pos < max_context_len; ++pos)
+        for (int m = 0; m < half; ++m) {
+            const float freq = 1.0f / powf(rope_base, 2.0f * (float)m / (float)d_k);
+            const float angle = (float)pos * freq;
+            const float cv = cosf(angle), sv = sinf(angle);
+            const size_t at = (size_t)pos * (size_t)d_k + (size_t)m;
+            freqs_cos[at] = freqs_cos[at + half] = cv;
+            freqs_sin[at] = freqs_sin[at + half] = sv;
+        }
+    return 0;
+}
+
+// rope.c:99-117: the half-split rotation of one head on the GPU, with table row pos.
+void rope_apply_fast(float *x, int pos, int head_dim, const float *freqs_cos, const float *freqs_sin) {
+    if (!x || !freqs_cos || !freqs_sin || head_dim < 2 || pos < 0) return;
+    kernel_context_t *c = default_ctx();
+    if (!c) return;
+    const int half = head_dim / 2;
+    const size_t row = (size_t)pos * (size_t)head_dim, xb = sizeof(float) * (size_t)head_dim;
+    (void)run_staged(c,
+                     {HostVec{x, nullptr, xb}, HostVec{freqs_cos + row, nullptr, sizeof(float) * (size_t)half},
+                      HostVec{freqs_sin + row, nullptr, sizeof(float) * (size_t)half}},
+                     {HostVec{nullptr, x, xb}},
+                     [&](std::vector<void *> &i, std::vector<void *> &o, hipStream_t s) {
+                         if (launch_rope(static_cast<float *>(i[0]), 1, head_dim, 0, static_cast<float *>(i[1]),
+                                         static_cast<float *>(i[2]), s) != 0)
+                             return -1;
+                         return hip_ok(hipMemcpyAsync(o[0], i[0], xb, hipMemcpyDeviceToDevice, s), "D2D") ? 0 : -1;
+                     });
+}
+
+// rope.c:17-25 with positional_encoding.c:16-40,76-104: pair p = (x[2p], x[2p+1]) for
+// 2p + 1 < head_dim is rotated by theta_p = pos * powf(1/base, 2p/head_dim). The angles are
+// host libm values, the rotation runs on the GPU.
+void apply_rope(float *x, int pos, int head_dim, float base) {
+    if (!x || head_dim < 2) return;
+    kernel_context_t *c = default_ctx();
+    if (!c) return;
+    const int np = head_dim / 2;
+    std::vector<float> cs((size_t)np), sn((size_t)np);
+    for (int p = 0; p < np; ++p) {
+        const float inv_freq = powf(1.0f / base, 2.0f * (float)p / (float)head_dim);
+        const float theta = (float)pos * inv_freq;
+        cs[(size_t)p] = cosf(theta);
+        sn[(size_t)p] = sinf(theta);
+    }
+    const size_t xb = sizeof(float) * (size_t)head_dim, tb = sizeof(float) * (size_t)np;
+    (void)run_staged(c, {HostVec{x, nullptr, xb}, HostVec{cs.data(), nullptr, tb}, HostVec{sn.data(), nullptr, tb}},
+                     {HostVec{nullptr, x, xb}},
+                     [&](std::vector<void *> &i, std::vector<void *> &o, hipStream_t s) {
+                         if (launch_rope_pairs(static_cast<float *>(i[0]), np, static_cast<float *>(i[1]),
+                                               static_cast<float *>(i[2]), s) != 0)
+                             return -1;
+                         return hip_ok(hipMemcpyAsync(o[0], i[0], xb, hipMemcpyDeviceToDevice, s), "D2D") ? 0 : -1;
+                     });
+}
+
+void apply_rope_default(float *x, int pos, int head_dim) { apply_rope(x, pos, head_dim, 1000000.0f); }
 
 void vec_scale(float *x, float s, int n) {
     if (s == 1.0f) return;  // utils.c:88

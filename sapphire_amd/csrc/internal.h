@@ -109,6 +109,9 @@ int launch_rmsnorm(float *out, const float *in, const float *w, float eps, int d
                    hipStream_t s);
 int launch_rope(float *x, int n_heads, int head_dim, int pos, const float *cos_t, const float *sin_t,
                 hipStream_t s);
+// Interleaved pairs: (x[2p], x[2p+1]) rotated by (cos_p[p], sin_p[p]) for p < npairs
+// (positional_encoding.c:95-99).
+int launch_rope_pairs(float *x, int npairs, const float *cos_p, const float *sin_p, hipStream_t s);
 int launch_gelu_mul(float *gate, const float *up, int n, hipStream_t s);
 int launch_softmax_argmax(const float *logits, int n, float *probs, int *argmax, float *scratch,
                           hipStream_t s);

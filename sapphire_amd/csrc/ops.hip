@@ -63,6 +63,18 @@ __global__ void rope_kernel(float *__restrict__ x, int n_heads, int head_dim, in
     xh[i + half] = __builtin_fmaf(x1, c, __fmul_rn(x0, s));
 }
 
+// (x[2p], x[2p+1]) -> (xe c - xo s, xe s + xo c) (positional_encoding.c:95-99), in the fused
+// forms of the reference build (the second product of each line fused onto the first).
+__global__ void rope_pairs_kernel(float *__restrict__ x, int npairs, const float *__restrict__ cos_p,
+                                  const float *__restrict__ sin_p) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npairs) return;
+    const float c = cos_p[p], s = sin_p[p];
+    const float xe = x[2 * p], xo = x[2 * p + 1];
+    x[2 * p] = __builtin_fmaf(-xo, s, __fmul_rn(xe, c));
+    x[2 * p + 1] = __builtin_fmaf(xo, c, __fmul_rn(xe, s));
+}
+
 __global__ void gelu_mul_kernel(float *__restrict__ gate, const float *__restrict__ up, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) gate[i] = __fmul_rn(gelu_ref(gate[i]), up[i]);
@@ -277,6 +289,11 @@ int launch_rope(float *x, int n_heads, int head_dim, int pos, const float *cos_t
     const int n = n_heads * (head_dim / 2);
     hipLaunchKernelGGL(rope_kernel, dim3((n + 255) / 256), dim3(256), 0, s, x, n_heads, head_dim, pos, cos_t, sin_t);
     return hip_ok(hipGetLastError(), "rope launch") ? 0 : -1;
+}
+
+int launch_rope_pairs(float *x, int npairs, const float *cos_p, const float *sin_p, hipStream_t s) {
+    hipLaunchKernelGGL(rope_pairs_kernel, dim3((npairs + 255) / 256), dim3(256), 0, s, x, npairs, cos_p, sin_p);
+    return hip_ok(hipGetLastError(), "rope_pairs launch") ? 0 : -1;
 }
 
 int launch_gelu_mul(float *gate, const float *up, int n, hipStream_t s) {

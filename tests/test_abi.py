@@ -48,12 +48,20 @@ def exported():
     return {line.split()[-1] for line in out.splitlines() if line.strip()}
 
 
+# rope.h declares the reference's strategy interface for the engine's own positional_encoding.c,
+# which keeps defining it (it is not on the decode path).
+ENGINE_SIDE = {"rope.h": {"apply_positional_encoding", "rope_encoding_strategy", "alibi_encoding_strategy"}}
+
+
 @pytest.mark.parametrize("header", HEADERS)
 def test_header_symbols_exported(exported, header):
     names = declared_functions(os.path.join(INCLUDE, header))
     assert names, f"no declarations parsed from {header}"
-    missing = sorted(n for n in names if n not in exported)
+    engine = ENGINE_SIDE.get(header, set())
+    assert engine <= names
+    missing = sorted(n for n in names - engine if n not in exported)
     assert not missing, f"{header}: declared but not exported: {missing}"
+    assert not (engine & exported), f"{header}: the engine's own functions must not be exported here"
 
 
 def test_reference_api_names_declared():

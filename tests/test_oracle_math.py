@@ -295,3 +295,25 @@ def test_softmax_and_greedy_of_non_finite_logits(oracle):
     c = x.copy(); c[0] = np.nan
     assert oracle.argmax(c) == 0
     assert oracle.argmax(np.full(50, -np.inf, np.float32)) == 0
+
+
+def test_silu_geglu_and_apply_rope_math(oracle):
+    """silu against float64 x / (1 + e^-x); geglu = x * gelu(y) exactly (one product);
+    apply_rope: identity at pos 0, each pair's norm kept, and the pair angles of
+    theta_p = pos * base^(-2p/d) in float64."""
+    x = synth.normal_f32(500, 82, 1) * 5
+    want = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    got = np.array([oracle.lib.oracle_silu(float(v)) for v in x])
+    assert np.allclose(got, want, rtol=4e-7, atol=1e-30)
+    y = synth.normal_f32(500, 82, 2)
+    for a, b in zip(x[:50].tolist(), y[:50].tolist()):
+        assert oracle.lib.oracle_geglu(a, b) == np.float32(np.float32(a) * np.float32(oracle.lib.oracle_gelu(b)))
+    v = synth.normal_f32(256, 82, 3)
+    assert np.array_equal(bits(oracle.apply_rope(v, 0, 1e4)), bits(v))
+    r = oracle.apply_rope(v, 913, 1e4).astype(np.float64)
+    v64 = v.astype(np.float64)
+    assert np.allclose(np.hypot(r[0::2], r[1::2]), np.hypot(v64[0::2], v64[1::2]), rtol=1e-5)
+    theta = 913 * (1.0 / 1e4) ** (2.0 * np.arange(128) / 256.0)
+    rot0 = v64[0::2] * np.cos(theta) - v64[1::2] * np.sin(theta)
+    rot1 = v64[0::2] * np.sin(theta) + v64[1::2] * np.cos(theta)
+    assert np.allclose(r[0::2], rot0, atol=2e-3) and np.allclose(r[1::2], rot1, atol=2e-3)

@@ -161,3 +161,27 @@ def test_decode_matches_reference(oracle, cfg, seed, prefill, steps):
     assert list(t_ref) == list(t_orc)
     assert np.array_equal(bits(l_ref), bits(l_orc))
     assert np.array_equal(bits(k1), bits(k2)) and np.array_equal(bits(v1), bits(v2))
+
+
+def test_scalar_activations_and_apply_rope(oracle, ref):
+    """silu / relu / gelu / geglu (activations.c:16-105) and apply_rope (rope.c:17-25 through
+    positional_encoding.c:16-104), bit for bit, including special values and odd head_dim."""
+    import ctypes as C
+    xs = np.concatenate([synth.normal_f32(2000, 80, 1) * 4,
+                         np.array([0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 90.0, -90.0, np.inf, -np.inf, np.nan],
+                                  np.float32)])
+    ys = synth.normal_f32(xs.size, 80, 2) * 3
+    L, O = ref.lib, oracle.lib
+    for x, y in zip(xs.tolist(), ys.tolist()):
+        for got, want in ((O.oracle_silu(x), L.silu(x)), (O.oracle_gelu(x), L.gelu(x)),
+                          (O.oracle_geglu(x, y), L.geglu(x, y))):
+            assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32), (x, y, got, want)
+    for hd, pos, base in ((256, 0, 1e4), (256, 1037, 1e6), (64, 5, 1e4), (7, 300, 1e4), (2, 2047, 1e6)):
+        x = synth.normal_f32(hd, 81, hd + pos)
+        want = x.copy()
+        L.apply_rope(want.ctypes.data, pos, hd, C.c_float(base))
+        assert np.array_equal(bits(oracle.apply_rope(x, pos, base)), bits(want))
+    x = synth.normal_f32(256, 81, 9)
+    want = x.copy()
+    L.apply_rope_default(want.ctypes.data, 77, 256)
+    assert np.array_equal(bits(oracle.apply_rope(x, 77, 1e6)), bits(want))
