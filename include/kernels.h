@@ -11,9 +11,11 @@
  * The scalar activations silu/relu/gelu/geglu(float) are one value's host arithmetic (the
  * reference's formula with its compiler's contraction, libm expf/tanhf); the vector forms the
  * engine calls on its buffers (gelu_inplace, sapphire_geglu, ...) run on the GPU.
+ *
+ * The include guard is the reference's own (KERNELS_H), like tensor.h's.
  */
-#ifndef SAPPHIRE_HIP_KERNELS_H
-#define SAPPHIRE_HIP_KERNELS_H
+#ifndef KERNELS_H
+#define KERNELS_H
 
 #include <stddef.h>
 #include <stdint.h>
@@ -162,4 +164,4 @@ const float *get_norm_weights(const tensor_t *weight, float *scratch, int n);
 #ifdef __cplusplus
 }
 #endif
-#endif /* SAPPHIRE_HIP_KERNELS_H */
+#endif /* KERNELS_H */

@@ -13,9 +13,12 @@
  *   tensor_create / tensor_create_view ....... include/tensor.h:60,208; tensor.c:81-152
  *   tensor_clone / tensor_transpose .......... include/tensor.h:64-77; tensor.c:163-204
  *   accessors ................................ include/tensor.h:85-202; tensor.c:210-390
+ *
+ * The include guard is the reference's own (TENSOR_H): an engine translation unit that also
+ * reaches the reference's tensor.h through a relative include sees one definition of the types.
  */
-#ifndef SAPPHIRE_HIP_TENSOR_H
-#define SAPPHIRE_HIP_TENSOR_H
+#ifndef TENSOR_H
+#define TENSOR_H
 
 #include <stddef.h>
 #include <stdint.h>
@@ -70,4 +73,4 @@ int tensor_ref_count(const tensor_t *t);
 #ifdef __cplusplus
 }
 #endif
-#endif /* SAPPHIRE_HIP_TENSOR_H */
+#endif /* TENSOR_H */

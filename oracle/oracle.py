@@ -388,17 +388,9 @@ def oracle_decode_forced(orc: "Oracle", model, k_cache, v_cache, token, pos, nth
     return int(toks[0]), logits[0]
 
 
-def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False):
-    """Greedy decode through the compiled reference engine (oracle/_ref)."""
+def _ref_structs(model):
+    """(RefCfg, RefWeights, arrays kept alive) of a synthetic model for ref_decode.c."""
     cfg = model.cfg
-    lib = C.CDLL(REF_DECODE_LIB)
-    lib.ref_decode_run.restype = C.c_int
-    lib.ref_decode_run.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p,
-                                   C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
-    try:
-        C.CDLL(REF_LIB).log_set_level(40)
-    except AttributeError:
-        pass
     rc = RefCfg(cfg.n_layers, cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn, cfg.vocab,
                 cfg.max_ctx, cfg.sliding_window, cfg.global_mask, cfg.query_pre_attn_scalar,
                 cfg.rope_theta, cfg.rope_local_base, cfg.wdtype, cfg.lm_dtype)
@@ -413,10 +405,90 @@ def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False):
     rw.embed_bf16 = model.embed_bf16.ctypes.data
     rw.norm_final = model.norm_final.ctypes.data
     rw.lm_head = model.lm_head.ctypes.data
+    return rc, rw, keep
+
+
+def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False):
+    """Greedy decode through the compiled reference engine (oracle/_ref)."""
+    cfg = model.cfg
+    lib = C.CDLL(REF_DECODE_LIB)
+    lib.ref_decode_run.restype = C.c_int
+    lib.ref_decode_run.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p,
+                                   C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    try:
+        C.CDLL(REF_LIB).log_set_level(40)
+    except AttributeError:
+        pass
+    rc, rw, _keep = _ref_structs(model)
     tokens = np.empty(steps, np.int32)
     logits = np.empty((steps, cfg.vocab), np.float32) if keep_logits else None
     r = lib.ref_decode_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data, int(token),
                            int(pos), int(steps), tokens.ctypes.data,
                            logits.ctypes.data if logits is not None else None)
     assert r == 0
+    return tokens, logits
+
+
+# ---------------------------------------------------------------------------
+# The reference's engine (inference.c, kv_cache.c, ... compiled from its sources) running its
+# layers through libsapphire_hip.so's transformer.h: `make -C oracle engine`.
+# ---------------------------------------------------------------------------
+ENGINE_HIP_LIB = os.path.join(HERE, "_ref", "libref_engine_hip.so")
+_ENGINE = None
+
+
+def engine_hip_available() -> bool:
+    return os.path.exists(ENGINE_HIP_LIB)
+
+
+def _engine():
+    global _ENGINE
+    if _ENGINE is None:
+        # RTLD_GLOBAL: the engine's kv_cache_get_keys / _values become visible to the library,
+        # as an executable's are
+        lib = C.CDLL(ENGINE_HIP_LIB, mode=C.RTLD_GLOBAL)
+        for n in ("ref_decode_run", "engine_forward_run"):
+            getattr(lib, n).restype = C.c_int
+        lib.ref_decode_run.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p,
+                                       C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        lib.engine_forward_run.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p,
+                                           C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        try:
+            lib.log_set_level.argtypes = [C.c_int]
+            lib.log_set_level(40)
+        except AttributeError:
+            pass
+        _ENGINE = lib
+    return _ENGINE
+
+
+def engine_layer_decode(model, k_cache, v_cache, token, pos, steps):
+    """ref_decode_run of the engine built on libsapphire_hip.so: per step sapphire_embed_lookup,
+    sapphire_transformer_layer for every layer, then lm_head (tied BF16 head) or the final norm
+    and kernel_gemv (quantized head); sample_greedy. The caches are updated in place.
+    Returns (tokens[steps], logits[steps, vocab])."""
+    lib = _engine()
+    rc, rw, _keep = _ref_structs(model)
+    tokens = np.empty(steps, np.int32)
+    logits = np.empty((steps, model.cfg.vocab), np.float32)
+    r = lib.ref_decode_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data, int(token), int(pos),
+                           int(steps), tokens.ctypes.data, logits.ctypes.data)
+    assert r == 0, "engine run failed"
+    return tokens, logits
+
+
+def engine_forward_decode(model, k_cache, v_cache, prompt, token, pos, steps):
+    """engine_forward_run of the engine built on libsapphire_hip.so: the prompt through
+    inference_forward_batch (chunks of 32), then inference_forward + sample_greedy per step
+    from `token` at pos + len(prompt). The caches are updated in place.
+    Returns (tokens[steps], logits[steps, vocab])."""
+    lib = _engine()
+    rc, rw, _keep = _ref_structs(model)
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    tokens = np.empty(steps, np.int32)
+    logits = np.empty((steps, model.cfg.vocab), np.float32)
+    r = lib.engine_forward_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data,
+                               prompt.ctypes.data if prompt.size else None, int(prompt.size), int(token), int(pos),
+                               int(steps), tokens.ctypes.data, logits.ctypes.data)
+    assert r == 0, "engine run failed"
     return tokens, logits

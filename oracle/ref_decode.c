@@ -1,12 +1,19 @@
 /*
- * ref_decode.c - drives the compiled reference engine through one configurable
- * Gemma-3-shaped decode loop, for pinning the oracle's decode step.
+ * ref_decode.c - drives an engine built from the reference's own sources through a
+ * configurable Gemma-3-shaped model (synthetic weights handed over as raw arrays).
  *
- * TEST INFRASTRUCTURE ONLY. Built by `make -C oracle ref` against the reference's own
- * headers and linked with oracle/_ref/libsapphire_ref.so (both compiled from the
- * reference sources); the output lives in oracle/_ref/ and is never shipped.
+ * TEST INFRASTRUCTURE ONLY, compiled twice from this one file:
+ *  - `make -C oracle ref`: with the reference's headers, linked with
+ *    oracle/_ref/libsapphire_ref.so (the whole reference engine) -> libref_decode.so, the
+ *    checker that pins the oracle's decode step;
+ *  - `make -C oracle engine`: with this repository's include/ first, linked with the
+ *    reference's engine sources that libsapphire_hip.so does not replace (inference.c,
+ *    kv_cache.c, the loaders, utils.c, log.c, ...) and with libsapphire_hip.so ->
+ *    libref_engine_hip.so: the reference's own session and forward loop running its layers
+ *    through the library's transformer.h, the thing the GPU tests compare with the oracle.
+ * Outputs live in oracle/_ref/ and are never shipped.
  *
- * Composition (reference public functions, in the reference's own order):
+ * ref_decode_run composes the reference's public functions in the reference's own order:
  *   inference_session_create(spec, max_ctx)            inference.c:499-584
  *   K/V prefill through kv_cache_get_keys/values         kv_cache.c:217-234
  *   per step:
@@ -18,6 +25,11 @@
  * lm_head() itself always projects through embedding_weight (transformer.c:407): a
  * BF16 (tied) LM head calls it; a quantized LM head is applied with the same two calls
  * lm_head makes, on a separate Q4_0/Q8_0 tensor view.
+ *
+ * engine_forward_run runs the reference's inference_forward_batch over a prompt in chunks of
+ * up to 32 tokens (as perform_inference does, inference.c:236-244), then inference_forward
+ * + sample_greedy per step (inference.c:250-297 at temperature 0): embed, layers and lm_head
+ * exactly as the engine calls them.
  */
 #define _POSIX_C_SOURCE 200809L
 #include <stdint.h>
@@ -65,35 +77,35 @@ static tensor_t *view1(int dtype, int n, const void *data) {
     return tensor_create_view((tensor_dtype_t)dtype, 1, shape, (void *)data);
 }
 
-/* Returns 0 on success. tokens_out[steps]; logits_out[steps*vocab] may be NULL;
- * k_cache/v_cache [n_layers][n_kv][max_ctx][hd] are read in and written back. */
-int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache,
-                   int start_token, int start_pos, int steps, int *tokens_out, float *logits_out) {
+/* The engine-side model: configuration, tensor views over the caller's arrays, spec. */
+typedef struct {
+    gemma3_270m_config_t cfg;
+    llm_model_t model;
+    tensor_t *lm;
+    model_spec_t spec;
+} built_t;
+
+static int build_model(const ref_cfg_t *c, const ref_weights_t *w, built_t *b) {
     int L = c->n_layers, H = c->hidden, hd = c->head_dim;
     int nq = c->n_heads * hd, nk = c->n_kv_heads * hd;
-
-    gemma3_270m_config_t cfg;
-    memset(&cfg, 0, sizeof cfg);
-    cfg.hidden_size = H;
-    cfg.intermediate_size = c->ffn;
-    cfg.num_attention_heads = c->n_heads;
-    cfg.num_key_value_heads = c->n_kv_heads;
-    cfg.num_hidden_layers = L;
-    cfg.head_dim = hd;
-    cfg.vocab_size = c->vocab;
-    cfg.query_pre_attn_scalar = c->query_pre_attn_scalar;
-    cfg.rope_theta = c->rope_theta;
-    cfg.rope_local_base_freq = c->rope_local_base;
-    cfg.sliding_window = c->sliding_window;
-    cfg.layer_types_mask = c->global_mask;
-    cfg.rms_norm_eps = 1e-6f;
-
-    llm_model_t model;
-    memset(&model, 0, sizeof model);
-    model.layers = calloc((size_t)L, sizeof(model_layer_weights_t));
-    if (!model.layers) return -1;
+    memset(b, 0, sizeof *b);
+    b->cfg.hidden_size = H;
+    b->cfg.intermediate_size = c->ffn;
+    b->cfg.num_attention_heads = c->n_heads;
+    b->cfg.num_key_value_heads = c->n_kv_heads;
+    b->cfg.num_hidden_layers = L;
+    b->cfg.head_dim = hd;
+    b->cfg.vocab_size = c->vocab;
+    b->cfg.query_pre_attn_scalar = c->query_pre_attn_scalar;
+    b->cfg.rope_theta = c->rope_theta;
+    b->cfg.rope_local_base_freq = c->rope_local_base;
+    b->cfg.sliding_window = c->sliding_window;
+    b->cfg.layer_types_mask = c->global_mask;
+    b->cfg.rms_norm_eps = 1e-6f;
+    b->model.layers = calloc((size_t)L, sizeof(model_layer_weights_t));
+    if (!b->model.layers) return -1;
     for (int l = 0; l < L; ++l) {
-        model_layer_weights_t *lw = &model.layers[l];
+        model_layer_weights_t *lw = &b->model.layers[l];
         lw->q_proj_weight = view2(c->wdtype, nq, H, (const char *)w->wq + (size_t)l * nq * row_bytes(c->wdtype, H));
         lw->k_proj_weight = view2(c->wdtype, nk, H, (const char *)w->wk + (size_t)l * nk * row_bytes(c->wdtype, H));
         lw->v_proj_weight = view2(c->wdtype, nk, H, (const char *)w->wv + (size_t)l * nk * row_bytes(c->wdtype, H));
@@ -108,29 +120,61 @@ int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, f
         lw->q_norm_weight = view1(DTYPE_F32, w->q_norm_len, w->q_norm + (size_t)l * w->q_norm_len);
         lw->k_norm_weight = view1(DTYPE_F32, w->k_norm_len, w->k_norm + (size_t)l * w->k_norm_len);
     }
-    model.embedding_weight = view2(DTYPE_BF16, c->vocab, H, w->embed_bf16);
-    model.norm_final_weight = view1(DTYPE_F32, H, w->norm_final);
-    tensor_t *lm = view2(c->lm_dtype, c->vocab, H, w->lm_head);
+    b->model.embedding_weight = view2(DTYPE_BF16, c->vocab, H, w->embed_bf16);
+    b->model.norm_final_weight = view1(DTYPE_F32, H, w->norm_final);
+    b->lm = view2(c->lm_dtype, c->vocab, H, w->lm_head);
+    b->spec.model_id = "gemma3-shaped-synthetic";
+    b->spec.llm_model = &b->model;
+    b->spec.variant_config = &b->cfg;
+    return 0;
+}
 
-    model_spec_t spec;
-    memset(&spec, 0, sizeof spec);
-    spec.model_id = "gemma3-shaped-synthetic";
-    spec.llm_model = &model;
-    spec.variant_config = &cfg;
+static void free_model(const ref_cfg_t *c, built_t *b) {
+    for (int l = 0; b->model.layers && l < c->n_layers; ++l) {
+        model_layer_weights_t *lw = &b->model.layers[l];
+        tensor_t *ts[] = { lw->q_proj_weight, lw->k_proj_weight, lw->v_proj_weight, lw->out_proj_weight,
+                           lw->gate_proj_weight, lw->up_proj_weight, lw->down_proj_weight,
+                           lw->norm_attn_weight, lw->norm_attn_post_weight, lw->norm_ffn_weight,
+                           lw->norm_ffn_post_weight, lw->q_norm_weight, lw->k_norm_weight };
+        for (size_t i = 0; i < sizeof ts / sizeof ts[0]; ++i) tensor_release(ts[i]);
+    }
+    free(b->model.layers);
+    tensor_release(b->model.embedding_weight);
+    tensor_release(b->model.norm_final_weight);
+    tensor_release(b->lm);
+}
 
+static void kv_in(inference_session_t *s, const ref_cfg_t *c, const float *k_cache, const float *v_cache) {
+    size_t per_layer = (size_t)c->n_kv_heads * c->max_ctx * c->head_dim;
+    for (int l = 0; l < c->n_layers; ++l) {
+        memcpy(tensor_data_mutable(kv_cache_get_keys(s->kv_cache, l)), k_cache + l * per_layer, per_layer * sizeof(float));
+        memcpy(tensor_data_mutable(kv_cache_get_values(s->kv_cache, l)), v_cache + l * per_layer, per_layer * sizeof(float));
+    }
+}
+
+static void kv_out(inference_session_t *s, const ref_cfg_t *c, float *k_cache, float *v_cache) {
+    size_t per_layer = (size_t)c->n_kv_heads * c->max_ctx * c->head_dim;
+    for (int l = 0; l < c->n_layers; ++l) {
+        memcpy(k_cache + l * per_layer, tensor_data(kv_cache_get_keys(s->kv_cache, l)), per_layer * sizeof(float));
+        memcpy(v_cache + l * per_layer, tensor_data(kv_cache_get_values(s->kv_cache, l)), per_layer * sizeof(float));
+    }
+}
+
+/* Returns 0 on success. tokens_out[steps]; logits_out[steps*vocab] may be NULL;
+ * k_cache/v_cache [n_layers][n_kv][max_ctx][hd] are read in and written back. */
+int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache,
+                   int start_token, int start_pos, int steps, int *tokens_out, float *logits_out) {
+    int L = c->n_layers, H = c->hidden;
+    built_t b;
+    if (build_model(c, w, &b) != 0) return -1;
     int rc = -1;
     float *norm = NULL, *logits = NULL;
-    inference_session_t *s = inference_session_create(&spec, c->max_ctx);
+    inference_session_t *s = inference_session_create(&b.spec, c->max_ctx);
     if (!s) goto out;
     if (posix_memalign((void **)&norm, 32, sizeof(float) * (size_t)((H + 7) & ~7)) != 0) goto out;
     logits = malloc(sizeof(float) * (size_t)c->vocab);
     if (!logits) goto out;
-
-    size_t per_layer = (size_t)c->n_kv_heads * c->max_ctx * hd;
-    for (int l = 0; l < L; ++l) {
-        memcpy(tensor_data_mutable(kv_cache_get_keys(s->kv_cache, l)), k_cache + l * per_layer, per_layer * sizeof(float));
-        memcpy(tensor_data_mutable(kv_cache_get_values(s->kv_cache, l)), v_cache + l * per_layer, per_layer * sizeof(float));
-    }
+    kv_in(s, c, k_cache, v_cache);
 
     int token = start_token;
     for (int st = 0; st < steps; ++st) {
@@ -141,38 +185,61 @@ int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, f
             int glob = s->layer_configs[l].config.attention.is_global;
             transformer_rope_t rope = { glob ? s->rope_freqs_cos_global : s->rope_freqs_cos_local,
                                         glob ? s->rope_freqs_sin_global : s->rope_freqs_sin_local };
-            sapphire_transformer_layer(s, l, pos, hidden, rope);
+            if (sapphire_transformer_layer(s, l, pos, hidden, rope) != 0) goto out;
         }
         if (c->lm_dtype == DTYPE_BF16) {
             lm_head(s, hidden, logits);       /* tied: projects through embedding_weight */
         } else {
-            rmsnorm_delta(norm, hidden, (const float *)tensor_data(model.norm_final_weight), 1e-6f, H);
-            if (kernel_gemv(s->gemv_ctx, logits, lm, norm) != 0) goto out;
+            rmsnorm_delta(norm, hidden, (const float *)tensor_data(b.model.norm_final_weight), 1e-6f, H);
+            if (kernel_gemv(s->gemv_ctx, logits, b.lm, norm) != 0) goto out;
         }
         token = sample_greedy(logits, c->vocab);
         tokens_out[st] = token;
         if (logits_out) memcpy(logits_out + (size_t)st * c->vocab, logits, sizeof(float) * (size_t)c->vocab);
     }
-    for (int l = 0; l < L; ++l) {
-        memcpy(k_cache + l * per_layer, tensor_data(kv_cache_get_keys(s->kv_cache, l)), per_layer * sizeof(float));
-        memcpy(v_cache + l * per_layer, tensor_data(kv_cache_get_values(s->kv_cache, l)), per_layer * sizeof(float));
-    }
+    kv_out(s, c, k_cache, v_cache);
     rc = 0;
 out:
     if (s) destroy_inference_session(s);
     free(norm);
     free(logits);
-    for (int l = 0; l < L; ++l) {
-        model_layer_weights_t *lw = &model.layers[l];
-        tensor_t *ts[] = { lw->q_proj_weight, lw->k_proj_weight, lw->v_proj_weight, lw->out_proj_weight,
-                           lw->gate_proj_weight, lw->up_proj_weight, lw->down_proj_weight,
-                           lw->norm_attn_weight, lw->norm_attn_post_weight, lw->norm_ffn_weight,
-                           lw->norm_ffn_post_weight, lw->q_norm_weight, lw->k_norm_weight };
-        for (size_t i = 0; i < sizeof ts / sizeof ts[0]; ++i) tensor_release(ts[i]);
+    free_model(c, &b);
+    return rc;
+}
+
+/* The engine's own loop (tied BF16 LM head, as lm_head computes it): prompt[n_prompt] at
+ * positions start_pos.. through inference_forward_batch in chunks of up to 32, then `steps`
+ * inference_forward + sample_greedy steps from start_token at start_pos + n_prompt.
+ * Returns 0; tokens_out[steps], logits_out[steps*vocab] (may be NULL); the caches are read in
+ * and written back. */
+int engine_forward_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache,
+                       const int *prompt, int n_prompt, int start_token, int start_pos, int steps, int *tokens_out,
+                       float *logits_out) {
+    built_t b;
+    if (build_model(c, w, &b) != 0) return -1;
+    int rc = -1;
+    float *logits = NULL;
+    inference_session_t *s = inference_session_create(&b.spec, c->max_ctx);
+    if (!s) goto out;
+    logits = malloc(sizeof(float) * (size_t)c->vocab);
+    if (!logits) goto out;
+    kv_in(s, c, k_cache, v_cache);
+    for (int p = 0; p < n_prompt; p += 32) {
+        int n = n_prompt - p > 32 ? 32 : n_prompt - p;
+        inference_forward_batch(s, prompt + p, start_pos + p, n, NULL);
     }
-    free(model.layers);
-    tensor_release(model.embedding_weight);
-    tensor_release(model.norm_final_weight);
-    tensor_release(lm);
+    int token = start_token;
+    for (int st = 0; st < steps; ++st) {
+        inference_forward(s, token, start_pos + n_prompt + st, logits);
+        token = sample_greedy(logits, c->vocab);
+        tokens_out[st] = token;
+        if (logits_out) memcpy(logits_out + (size_t)st * c->vocab, logits, sizeof(float) * (size_t)c->vocab);
+    }
+    kv_out(s, c, k_cache, v_cache);
+    rc = 0;
+out:
+    if (s) destroy_inference_session(s);
+    free(logits);
+    free_model(c, &b);
     return rc;
 }

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libsapphire_hip.so")
 SOURCES = ["runtime.cpp", "tensor.cpp", "dispatch.cpp", "decoder.cpp", "gemv.hip", "gemv_mfma.hip", "gemm_mfma.hip",
            "ops.hip", "decode.hip",
-           "decode_persist.hip", "quantize.hip", "gemm_bf16.hip", "noalloc.cpp"]
+           "decode_persist.hip", "quantize.hip", "gemm_bf16.hip", "noalloc.cpp", "transformer.cpp"]
 ARCH = os.environ.get("SAPPHIRE_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [
@@ -59,7 +59,10 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
             for f in [pool.submit(subprocess.run, c, check=True) for c in cmds]:
                 f.result()
         tmp_out = OUT + ".tmp"
-        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_out, *objs, "-lpthread"]
+        # -Bsymbolic-functions: the library's calls to its own exported API bind inside it, never to
+        # an engine's same-named functions loaded earlier
+        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-Bsymbolic-functions", "-o", tmp_out, *objs,
+               "-lpthread", "-ldl"]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)

@@ -6,6 +6,7 @@
 // weights are uploaded once and repacked into the PACKED (or, for the LM head, TILED)
 // layout, F32/BF16 uploaded as is; batched calls add a TILED copy. The copies are freed
 // with the tensor.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -19,6 +20,11 @@ static size_t shape_product(int ndim, const int *shape) {
     size_t p = 1;
     for (int i = 0; i < ndim; ++i) p *= (size_t)shape[i];
     return p;
+}
+
+static uint64_t next_serial() {
+    static std::atomic<uint64_t> counter{0};
+    return ++counter;
 }
 
 extern "C" {
@@ -65,6 +71,7 @@ tensor_t *tensor_create(int ndim, const int *shape, tensor_dtype_t dtype) {
     }
     t->ref_count = 1;
     t->is_external = 0;
+    t->serial = next_serial();
     return t;
 }
 
@@ -80,6 +87,7 @@ tensor_t *tensor_create_view(tensor_dtype_t dtype, int ndim, const int *shape, v
     t->is_external = 1;
     memcpy(t->shape, shape, sizeof(int) * (size_t)ndim);
     t->nbytes = shape_product(ndim, shape) * dtype_element_size(dtype);
+    t->serial = next_serial();
     return t;
 }
 
@@ -132,6 +140,7 @@ void tensor_ref_inc(tensor_t *t) {
 void tensor_release(tensor_t *t) {
     if (!t) return;
     if (--t->ref_count > 0) return;
+    transformer_tensor_released(t->serial);
     if (t->data && !t->is_external) free(t->data);
     tensor_drop_device(t);
     delete t;

@@ -25,6 +25,8 @@ struct tensor_t {
     void *dev_tiled = nullptr;
     // set by tensor_set_f32: the host data changed, the device copies are rebuilt on next use
     bool dev_stale = false;
+    // unique for the life of the process (never reused, unlike the tensor's address)
+    uint64_t serial = 0;
 };
 
 namespace sapphire {
@@ -34,4 +36,7 @@ const void *tensor_device_weights(const tensor_t *t, int *layout, hipStream_t s)
 // the GEMV copy when that is TILED, else a second copy made on first use.
 const void *tensor_device_tiled(const tensor_t *t, hipStream_t s);
 void tensor_drop_device(tensor_t *t);
+// Called by tensor_release before a tensor is freed: drops the device state of an engine
+// session whose KV cache held it (transformer.cpp).
+void transformer_tensor_released(uint64_t serial);
 }  // namespace sapphire

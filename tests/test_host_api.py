@@ -70,6 +70,56 @@ def test_reference_programs_link_against_the_library_alone():
         assert "libsapphire_hip.so" in needed and "libsapphire_ref" not in needed
 
 
+_LAYOUT_PROBE = r"""
+#include <stddef.h>
+#include <stdio.h>
+int main(void) {
+    printf("session %zu %zu %zu %zu %zu %zu %zu\n", sizeof(inference_session_t), offsetof(inference_session_t, kv_cache),
+           offsetof(inference_session_t, scratch_size), offsetof(inference_session_t, padded_d_ff),
+           offsetof(inference_session_t, rope_freqs_cos_global), offsetof(inference_session_t, gemv_ctx),
+           offsetof(inference_session_t, num_layers));
+    printf("spec %zu %zu %zu\n", sizeof(struct model_spec), offsetof(struct model_spec, llm_model),
+           offsetof(struct model_spec, variant_config));
+    printf("cfg %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(gemma3_270m_config_t),
+           offsetof(gemma3_270m_config_t, head_dim), offsetof(gemma3_270m_config_t, hidden_size),
+           offsetof(gemma3_270m_config_t, intermediate_size), offsetof(gemma3_270m_config_t, layer_types_mask),
+           offsetof(gemma3_270m_config_t, num_attention_heads), offsetof(gemma3_270m_config_t, num_hidden_layers),
+           offsetof(gemma3_270m_config_t, num_key_value_heads), offsetof(gemma3_270m_config_t, query_pre_attn_scalar),
+           offsetof(gemma3_270m_config_t, rope_local_base_freq), offsetof(gemma3_270m_config_t, sliding_window),
+           offsetof(gemma3_270m_config_t, vocab_size));
+    printf("model %zu %zu %zu %zu\n", sizeof(llm_model_t), offsetof(llm_model_t, norm_final_weight),
+           offsetof(llm_model_t, layers), sizeof(model_layer_weights_t));
+    printf("layer %zu %zu %zu %zu %zu\n", offsetof(model_layer_weights_t, q_proj_weight),
+           offsetof(model_layer_weights_t, q_norm_weight), offsetof(model_layer_weights_t, out_proj_weight),
+           offsetof(model_layer_weights_t, up_proj_weight), offsetof(model_layer_weights_t, down_proj_weight));
+    printf("bufs %zu %zu %zu ctx %zu %zu %zu\n", sizeof(layer_buffers_t), offsetof(layer_buffers_t, residual),
+           offsetof(layer_buffers_t, weight_scratch), sizeof(transformer_layer_ctx_t),
+           offsetof(transformer_layer_ctx_t, layer_idx), offsetof(transformer_layer_ctx_t, head_dim));
+    printf("rope %zu\n", sizeof(transformer_rope_t));
+    return 0;
+}
+"""
+
+
+@needs_reference
+def test_engine_struct_layouts_match_reference(tmp_path):
+    """The engine structs transformer.h's entry points read (csrc/engine_abi.h) have the
+    reference's sizes and field offsets (inference.h, model_spec.h, llm_model.h,
+    gemma3_270m_config.h, transformer.h), compiled by the same host compiler."""
+    ref = tmp_path / "ref.c"
+    ref.write_text('#include "inference.h"\n#include "gemma3_270m_config.h"\n#include "llm_model.h"\n'
+                   '#include "model_spec.h"\n#include "transformer.h"\n' + _LAYOUT_PROBE)
+    ours = tmp_path / "ours.cpp"
+    ours.write_text('#include "engine_abi.h"\n' + _LAYOUT_PROBE)
+    subprocess.run(["gcc", "-I", "/root/reference/include", "-I", "/root/reference", str(ref), "-o",
+                    str(tmp_path / "ref")], check=True)
+    subprocess.run(["g++", "-I", os.path.join(ROOT, "sapphire_amd", "csrc"), str(ours), "-o", str(tmp_path / "ours")],
+                   check=True)
+    a = subprocess.run([str(tmp_path / "ref")], capture_output=True, text=True, check=True).stdout
+    b = subprocess.run([str(tmp_path / "ours")], capture_output=True, text=True, check=True).stdout
+    assert a == b, f"reference:\n{a}\nlibrary:\n{b}"
+
+
 def test_scalar_activations_match_oracle(oracle):
     """silu / relu / gelu / geglu (activations.c:16-105) bit for bit with the oracle, which is
     pinned to the compiled reference; special values included."""
