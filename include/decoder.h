@@ -95,6 +95,15 @@ int sapphire_decoder_set_workgroups(sapphire_decoder_t *dec, int groups);
 /* The current form: workgroups of the persistent step, 0 for the multi-launch step. */
 int sapphire_decoder_workgroups(const sapphire_decoder_t *dec);
 
+/* How the following generate calls pick tokens (inference.c:262-266 and 297). temperature <= 0
+ * (the default): greedy, sample_greedy (utils.c:145-156). temperature > 0: each step scales
+ * its logits by 1.0f / temperature and draws as sample_temperature (utils.c:158-180), bit for
+ * bit, with draws[s * batch + b] in place of (float)rand() / RAND_MAX for step s of a call and
+ * sequence b; n_draws of them are copied here (at most max_ctx * batch), and a call may run at
+ * most n_draws / batch steps. logits_out still receives the unscaled logits. The vocabulary
+ * must be at most 2^21. NaN temperatures are rejected. 0 / -1. */
+int sapphire_decoder_set_sampling(sapphire_decoder_t *dec, float temperature, const float *draws, int n_draws);
+
 /* ---- batched decode ----
  * `batch` (2..16) independent sequences decoded in lock step, each with its own KV cache,
  * position and greedy token: one step runs every projection as one matrix-core GEMM over

@@ -170,6 +170,21 @@ int sapphire_gemv_softmax_dev(int dtype, int layout, const void *w, int M, int K
 int sapphire_gemv_softmax_noalloc_dev(int dtype, int layout, const void *w, int M, int K, const float *x,
                                       float *logits, float *probs, int *argmax_dev, void *stream);
 
+/* ---- the next token ----
+ * The next token of each of `batch` rows of logits (row b at logits + b * ld, ld >= n) as
+ * perform_inference draws it (inference.c:262-266 and 297): temperature <= 0 gives
+ * sample_greedy (utils.c:145-156); otherwise each row is scaled by 1.0f / temperature
+ * (vec_scale, utils.c:87-92) and sample_temperature (utils.c:158-180) draws its token with
+ * draws_dev[b] in place of (float)rand() / RAND_MAX. The result is the reference's token bit
+ * for bit (its float sums included). As there, a sampled row is overwritten with the weights
+ * expf((l / T - max) / T); a NaN or +inf among the scaled logits gives n - 1. tokens_dev[b]
+ * receives the token. workspace: sapphire_sample_workspace_bytes(n, batch) bytes of device
+ * memory (256-byte aligned, per-chunk sums and maps); calls sharing one must be ordered.
+ * 1 <= n <= 2^21. */
+size_t sapphire_sample_workspace_bytes(int n, int batch);
+int sapphire_sample_dev(float *logits, int n, int batch, int ld, float temperature, const float *draws_dev,
+                        int *tokens_dev, void *workspace, void *stream);
+
 /* ---- device copies of tensor_t weights ----
  * The device-resident copy kernel_gemv keeps for a 2-D weight tensor (Q4_0/Q8_0 in the
  * PACKED layout, F32/BF16 as is), created on first use; *layout receives its layout.

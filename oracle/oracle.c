@@ -11,7 +11,7 @@
  * _mm256_fmadd_ps intrinsic are marked "contracted", and each was pinned bitwise
  * against the compiled reference (tests/test_oracle_pin.py).
  *
- * Parity status of every function here is recorded in oracle/README.md.
+ * How each function is pinned is stated in tests/test_oracle_pin.py and tests/test_oracle_math.py.
  */
 #define _POSIX_C_SOURCE 200809L
 #include "oracle.h"
@@ -390,6 +390,41 @@ int oracle_sample_greedy(const float *logits, int n) {
     float bv = logits[0];
     for (int i = 1; i < n; ++i) if (logits[i] > bv) { bv = logits[i]; best = i; }
     return best;
+}
+
+/* sample_temperature: utils.c:158-180. The max is seeded with logits[0] (strict '>'), the
+ * weights expf((l - max) / T) overwrite the logits, their float sum runs left to right, and
+ * the walk returns the first i with r <= cumsum (cumsum += w_i / sum in float), n - 1 if
+ * none. r stands for (float)rand() / (float)RAND_MAX. */
+int oracle_sample_temperature(float *logits, int n, float temperature, float r) {
+    if (!logits || n <= 0) return -1;
+    if (temperature <= 0.0f) return oracle_sample_greedy(logits, n);
+    float mx = logits[0];
+    for (int i = 1; i < n; ++i) if (logits[i] > mx) mx = logits[i];
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        logits[i] = expf((logits[i] - mx) / temperature);
+        sum += logits[i];
+    }
+    float cum = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        cum += logits[i] / sum;
+        if (r <= cum) return i;
+    }
+    return n - 1;
+}
+
+/* perform_inference's draw (inference.c:262-266 and 297): the logits scaled by 1/T
+ * (vec_scale, utils.c:87-92, which skips a factor of exactly 1) when T > 0, then
+ * sample_temperature. */
+int oracle_sample(float *logits, int n, float temperature, float r) {
+    if (!logits || n <= 0) return -1;
+    if (temperature > 0.0f) {
+        const float inv = 1.0f / temperature;
+        if (inv != 1.0f)
+            for (int i = 0; i < n; ++i) logits[i] *= inv;
+    }
+    return oracle_sample_temperature(logits, n, temperature, r);
 }
 
 void oracle_vec_add(float *dst, const float *src, int n) {               /* utils.c:81-85 */

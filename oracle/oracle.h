@@ -59,6 +59,10 @@ float oracle_geglu(float x, float y);                          /* x * gelu(y) */
 void  oracle_apply_rope(float *x, int pos, int head_dim, float base);   /* interleaved pairs */
 void  oracle_softmax(float *x, int n);
 int   oracle_sample_greedy(const float *logits, int n);
+/* sample_temperature (utils.c:158-180; logits overwritten with the weights) with r in place
+ * of rand() / RAND_MAX, and perform_inference's draw: 1/T scaling, then sample_temperature */
+int   oracle_sample_temperature(float *logits, int n, float temperature, float r);
+int   oracle_sample(float *logits, int n, float temperature, float r);
 void  oracle_vec_add(float *dst, const float *src, int n);
 float oracle_vec_dot(const float *a, const float *b, int n);
 void  oracle_bf16_to_f32(float *dst, const uint16_t *src, int n);

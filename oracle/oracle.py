@@ -85,6 +85,9 @@ class Oracle:
         L.oracle_softmax.argtypes = [vp, i]
         L.oracle_sample_greedy.restype = i
         L.oracle_sample_greedy.argtypes = [vp, i]
+        for n in ("oracle_sample_temperature", "oracle_sample"):
+            getattr(L, n).restype = i
+            getattr(L, n).argtypes = [vp, i, f, f]
         L.oracle_vec_dot.restype = f
         L.oracle_vec_dot.argtypes = [vp, vp, i]
         L.oracle_vec_add.argtypes = [vp, vp, i]
@@ -188,6 +191,13 @@ class Oracle:
     def argmax(self, x):
         return self.lib.oracle_sample_greedy(_p(x), x.shape[0])
 
+    def sample(self, logits, temperature, r):
+        """perform_inference's draw of one row: (token, the row afterwards: the weights when
+        temperature > 0)."""
+        x = np.array(logits, np.float32, copy=True)
+        t = self.lib.oracle_sample(_p(x), x.shape[0], float(temperature), float(r))
+        return int(t), x
+
 
 class Reference:
     """The compiled reference engine (oracle/_ref), when it was built."""
@@ -234,6 +244,9 @@ class Reference:
         L.softmax.argtypes = [vp, i]
         L.sample_greedy.restype = i
         L.sample_greedy.argtypes = [vp, i]
+        L.sample_temperature.restype = i
+        L.sample_temperature.argtypes = [vp, i, f]
+        L.vec_scale.argtypes = [vp, f, i]
         L.vec_dot.restype = f
         L.vec_dot.argtypes = [vp, vp, i]
         # the reference logs through stderr; keep it quiet below WARN
@@ -328,8 +341,10 @@ def ref_decode_available() -> bool:
 _PROJ = ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
 
 
-def oracle_decode(orc: "Oracle", model, k_cache, v_cache, token, pos, steps, nthreads=1, keep_logits=False):
-    """Greedy decode with the oracle. k_cache/v_cache are updated in place.
+def oracle_decode(orc: "Oracle", model, k_cache, v_cache, token, pos, steps, nthreads=1, keep_logits=False,
+                  temperature=0.0, draws=None):
+    """Decode with the oracle: greedy, or with temperature > 0 perform_inference's draw with
+    draws[s] for step s. k_cache/v_cache are updated in place.
     Returns (tokens[steps], logits[steps, vocab] or last logits)."""
     cfg = model.cfg
     L = cfg.n_layers
@@ -369,6 +384,8 @@ def oracle_decode(orc: "Oracle", model, k_cache, v_cache, token, pos, steps, nth
         out = logits[s if keep_logits else 0]
         t = orc.lib.oracle_decode_step(C.byref(ms), int(token), int(pos + s), out.ctypes.data)
         assert t >= 0
+        if temperature > 0:
+            t = orc.sample(out, temperature, draws[s])[0]
         tokens[s] = token = t
     return tokens, logits
 

@@ -75,6 +75,8 @@ def load_library(path: str):
     P("sapphire_gemm_bf16_dev", i32, [vp, i32, i32, vp, i32, i32, vp, i32, vp])
     P("kernel_quantize", i32, [vp, vp, i32, vp])
     P("sapphire_softmax_argmax_dev", i32, [vp, i32, vp, vp, vp])
+    P("sapphire_sample_workspace_bytes", C.c_size_t, [i32, i32])
+    P("sapphire_sample_dev", i32, [vp, i32, i32, i32, C.c_float, vp, vp, vp, vp])
     P("sapphire_gemv_softmax_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp, vp, vp])
     P("sapphire_gemv_softmax_noalloc_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp, vp, vp])
     P("sapphire_gemm_workspace_bytes", sz, [i32, i32, i32])

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libsapphire_hip.so")
 SOURCES = ["runtime.cpp", "tensor.cpp", "dispatch.cpp", "decoder.cpp", "gemv.hip", "gemv_mfma.hip", "gemm_mfma.hip",
-           "ops.hip", "decode.hip",
+           "ops.hip", "sample.hip", "decode.hip",
            "decode_persist.hip", "quantize.hip", "gemm_bf16.hip", "noalloc.cpp", "transformer.cpp"]
 ARCH = os.environ.get("SAPPHIRE_OFFLOAD_ARCH", "gfx950")
 

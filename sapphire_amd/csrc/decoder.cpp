@@ -91,6 +91,13 @@ struct sapphire_decoder {
     int *pf_tok = nullptr;       // [kPrefillChunk] tokens, then [kPrefillChunk] positions
     std::vector<hipGraph_t> pf_graph;          // per sequence: a full chunk's pass, captured once
     std::vector<hipGraphExec_t> pf_exec;
+    // temperature sampling (temperature > 0): the draws of a generate call [max_ctx][B], the
+    // sampler's weights [B][vocab] and workspace
+    float temperature = 0.0f;
+    float *draws = nullptr;
+    int n_draws = 0;
+    float *smp_w = nullptr;
+    void *smp_ws = nullptr;
 };
 
 namespace {
@@ -239,26 +246,39 @@ bool tiled_shapes_ok(const sapphire_decoder_config_t &c) {
 // A persistent-step wait longer than this many polls (about a second) is a failure.
 constexpr int kPersistSpinLimit = 1 << 19;
 
-// LM head on d->xfin with the greedy token into d->state[0], then the advance.
+// The sampled tokens of the step's logits into tokens[B] (perform_inference's draw,
+// inference.c:262-266 and 297), the step's draws at d->draws[step * B].
+int enqueue_sample(sapphire_decoder *d, const int *d_step, hipStream_t s) {
+    const auto &c = d->cfg;
+    return launch_sample(d->logits, c.vocab, d->batch, c.vocab, d->temperature, d->smp_w, c.vocab, d->draws, d_step,
+                         d->state, d->smp_ws, s);
+}
+
+// LM head on d->xfin with the greedy (or sampled) token into d->state[0], then the advance.
 int enqueue_lm_head(sapphire_decoder *d) {
     const auto &c = d->cfg;
     hipStream_t s = d->stream;
     const int H = c.hidden;
+    const bool greedy = !(d->temperature > 0.0f);
     if (c.lm_dtype == DT_BF16) {
         // weight tying: the logits are the embedding table times the final norm
         // (transformer.c:393-408 projects through embedding_weight)
         if (launch_gemv_f(DT_BF16, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
-        if (launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
+        if (greedy &&
+            launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
             return -1;
     } else if (d->lm_layout == LAYOUT_TILED) {
-        if (launch_gemv_tiled_softmax(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, nullptr, d->state,
-                                      d->lm_scratch, s) != 0)
+        if ((greedy ? launch_gemv_tiled_softmax(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, nullptr, d->state,
+                                                d->lm_scratch, s)
+                    : launch_gemv_tiled(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, s)) != 0)
             return -1;
     } else {
         if (launch_gemv_q(c.lm_dtype, LAYOUT_PACKED, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
-        if (launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
+        if (greedy &&
+            launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
             return -1;
     }
+    if (!greedy && enqueue_sample(d, d->state + 2, s) != 0) return -1;
     return dec_advance(d->state, d->state + 1, d->state + 2, d->log, d->groups > 0 ? d->seq : nullptr, s);
 }
 
@@ -516,7 +536,9 @@ int enqueue_step_batch(sapphire_decoder *d) {
         fin.eps = c.eps;
         if (dec_prologue_batch(fin, H, B, (size_t)H, d->xfin, s) != 0) return -1;
         if (launch_gemm_bf16(d->lm, c.vocab, H, d->xfin, H, B, d->logits, c.vocab, s) != 0) return -1;
-        if (dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s) != 0) return -1;
+        if ((d->temperature > 0.0f ? enqueue_sample(d, d->state + 2 * B, s)
+                                   : dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s)) != 0)
+            return -1;
         return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
     }
     GemmIn li;
@@ -532,7 +554,9 @@ int enqueue_step_batch(sapphire_decoder *d) {
     lo.y = d->logits;
     lo.ldy = c.vocab;
     if (launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s) != 0) return -1;
-    if (dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s) != 0) return -1;
+    if ((d->temperature > 0.0f ? enqueue_sample(d, d->state + 2 * B, s)
+                               : dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s)) != 0)
+        return -1;
     return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
 }
 
@@ -889,6 +913,11 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
                       pos[b], pos[b] + steps - 1);
             return -1;
         }
+    if (d->temperature > 0.0f && (size_t)steps * B > (size_t)d->n_draws) {
+        set_error("sapphire_decoder_generate: %d steps of %d sequences need %d draws, %d were set", steps, B,
+                  steps * B, d->n_draws);
+        return -1;
+    }
     SPH_CHECK(hipSetDevice(d->device));
     if (!d->exec) {
         SPH_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
@@ -982,6 +1011,45 @@ int sapphire_decoder_set_workgroups(sapphire_decoder_t *d, int groups) {
 }
 
 int sapphire_decoder_workgroups(const sapphire_decoder_t *d) { return d ? d->groups : -1; }
+
+int sapphire_decoder_set_sampling(sapphire_decoder_t *d, float temperature, const float *draws, int n_draws) {
+    if (!d || temperature != temperature || (temperature > 0.0f && (!draws || n_draws <= 0))) {
+        set_error("sapphire_decoder_set_sampling: bad arguments");
+        return -1;
+    }
+    const auto &c = d->cfg;
+    const int B = d->batch;
+    SPH_CHECK(hipSetDevice(d->device));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    if (temperature > 0.0f) {
+        if (!sample_supported(c.vocab, B)) {
+            set_error("sapphire_decoder_set_sampling: vocabulary %d too large to sample", c.vocab);
+            return -1;
+        }
+        if ((size_t)n_draws > (size_t)c.max_ctx * B) {
+            set_error("sapphire_decoder_set_sampling: at most max_ctx * batch = %zu draws", (size_t)c.max_ctx * B);
+            return -1;
+        }
+        if (!d->smp_w && (!dev_alloc_t(d, &d->smp_w, (size_t)B * c.vocab, "sampling weights") ||
+                          !dev_alloc(d, &d->smp_ws, sample_workspace_bytes(c.vocab, B), "sampling workspace") ||
+                          !dev_alloc_t(d, &d->draws, (size_t)c.max_ctx * B, "draws"))) {
+            d->smp_w = nullptr;
+            return -1;
+        }
+        SPH_CHECK(hipMemcpy(d->draws, draws, sizeof(float) * n_draws, hipMemcpyHostToDevice));
+    }
+    const float t = temperature > 0.0f ? temperature : 0.0f;
+    d->n_draws = t > 0.0f ? n_draws : 0;
+    if (t != d->temperature) {
+        // the step's kernels (and the temperature in their arguments) change: capture again
+        if (d->exec) (void)hipGraphExecDestroy(d->exec);
+        if (d->graph) (void)hipGraphDestroy(d->graph);
+        d->exec = nullptr;
+        d->graph = nullptr;
+        d->temperature = t;
+    }
+    return 0;
+}
 
 int sapphire_decoder_prefill(sapphire_decoder_t *d, int seq, const int *tokens, int n, int pos, float *elapsed_ms) {
     if (!d || !tokens || n <= 0 || seq < 0 || seq >= d->batch || pos < 0 || pos + n > d->cfg.max_ctx) {

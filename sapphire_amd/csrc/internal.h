@@ -120,6 +120,16 @@ size_t softmax_scratch_floats(int n);
 // kept until the process ends; calls that overlap on one device must share a stream). NULL on
 // error.
 float *softmax_partials_scratch();
+// The next token of `batch` rows of logits (row b at logits + b * ld) as perform_inference
+// draws it (sample.hip): temperature <= 0 is sample_greedy; otherwise sample_temperature after
+// the 1/T scaling, bit for bit, with draws[step * batch + b] (step = *d_step, or 0 when d_step
+// is NULL) in place of rand() / RAND_MAX. The weights go to w (row b at w + b * ldw; w may be
+// the logits). ws: sample_workspace_bytes(n, batch) bytes, 256-byte aligned; calls sharing it
+// must be ordered. n at most 2^21.
+size_t sample_workspace_bytes(int n, int batch);
+bool sample_supported(int n, int batch);
+int launch_sample(const float *logits, int n, int batch, size_t ld, float temperature, float *w, size_t ldw,
+                  const float *draws, const int *d_step, int *tokens, void *ws, hipStream_t s);
 enum : int { UOP_GELU = 0, UOP_SILU = 1, UOP_RELU = 2, UOP_SCALE = 3, UOP_SOFTCAP = 4 };
 int launch_unary(float *x, int n, int op, float a, hipStream_t s);
 int launch_axpy(float *dst, const float *src, int n, float a, bool fused, hipStream_t s);

@@ -309,6 +309,23 @@ int sapphire_gemv_softmax_dev(int dt, int layout, const void *w, int M, int K, c
     return launch_gemv_tiled_softmax(dt, w, M, K, x, logits, probs, argmax, scratch, s);
 }
 
+size_t sapphire_sample_workspace_bytes(int n, int batch) {
+    return sample_supported(n, batch) ? sample_workspace_bytes(n, batch) : 0;
+}
+
+int sapphire_sample_dev(float *logits, int n, int batch, int ld, float temperature, const float *draws, int *tokens,
+                        void *workspace, void *stream) {
+    if (!logits || !tokens || !workspace || n <= 0 || batch <= 0 || ld < n ||
+        (!(temperature <= 0.0f) && !draws)) {
+        set_error("bad sampling arguments");
+        return -1;
+    }
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) { set_error("the sampling workspace must be 256-byte aligned"); return -1; }
+    if (!sample_supported(n, batch)) { set_error("sampling supports 1..2^21 logits per row, n=%d", n); return -1; }
+    return launch_sample(logits, n, batch, (size_t)ld, temperature, logits, (size_t)ld, draws, nullptr, tokens,
+                         workspace, as_stream(stream));
+}
+
 int sapphire_rmsnorm_delta_dev(float *out, const float *in, const float *w, float eps, int dim, int batch, void *s) {
     if (!out || !in || !w || dim <= 0 || batch <= 0 || eps < 0.f) { set_error("bad rmsnorm arguments"); return -1; }
     return launch_rmsnorm(out, in, w, eps, dim, batch, true, as_stream(s));

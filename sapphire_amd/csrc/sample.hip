@@ -1,0 +1,531 @@
+// sample.hip - the next token as perform_inference draws it (inference.c:262-266, 297), for a
+// batch of logit rows: temperature <= 0 is sample_greedy (utils.c:145-156); otherwise the
+// logits are scaled by 1/T (vec_scale, utils.c:87-92) and sample_temperature (utils.c:158-180)
+// draws: max seeded with logits[0] (strict >), w_i = expf((l_i - max) / T) in place, sum the
+// w_i left to right in float, then walk cumsum += w_i / sum (float) and return the first i with
+// r <= cumsum, n - 1 if there is none. r is the caller's draw in place of rand() / RAND_MAX.
+//
+// The token is the reference's bit for bit, so both float chains (the sum, and the running sum
+// the draw is compared with) are reproduced exactly, in parallel:
+// * while a chain v <- fl(v + x) (x >= 0) stays inside one binade [2^e, 2^(e+1)), whose
+//   spacing is u, it is integer arithmetic on M = v / u: fl(v + x) = (M + k) u with k = x / u
+//   rounded to nearest, and on a tie (x / u = f + 1/2) the even one of M + f and M + f + 1.
+//   Each element is the map M -> M + d[M & 1]; maps compose (associatively), so a chunk of
+//   kChunk elements is one pair (d0, d1) for a given binade. The binades a chain can occupy
+//   at a chunk's start are fixed to at most two by the exact prefix sum and the error bound
+//   of recursive summation (|fl-sum - sum| <= n 2^-24 sum for nonnegative terms);
+// * one workgroup per row walks the chunks with these maps and, in a chunk where the binade
+//   changes or the draw is reached, scans its runs' maps to find the run where that happens
+//   and adds that run's elements with real float adds (the reference's own operation).
+// The weights come from libm_expf, glibc's expf bit for bit.
+#include "internal.h"
+#include "libm_expf.h"
+
+#include <cmath>
+
+namespace sapphire {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+constexpr int kRun = 16;                        // consecutive elements per thread
+constexpr int kChunk = kThreads * kRun;         // elements per chunk
+constexpr int kMaxChunks = 512;                 // n <= 2^21 keeps the error bound below 1/4
+constexpr int kGallop = 32;                     // real adds tried before a chunk's run scan
+constexpr int kCap = 1 << 28;                   // saturation of map increments
+constexpr int kZero = -1000, kSub = -127;       // binade ids of 0 and of the subnormals
+
+struct ChunkStat {       // per row and chunk
+    float max;           // largest non-NaN scaled logit (+-inf included)
+    int arg;             // its first index, -1 if the chunk is all NaN
+    int nan;             // whether the chunk holds a NaN
+    int nan0;            // chunk 0 only: whether the row's first scaled logit is NaN
+    double wsum;         // sum of the chunk's weights (exact enough for the bounds)
+};
+struct ChunkMaps {       // per row and chunk: the chunk's map for up to two binades
+    int reg[2];
+    int d[2][2];
+};
+struct RowInfo {
+    float m;             // the reference's max (NaN when logits[0] is NaN)
+    int bad;             // a NaN weight (or an all -inf row): the token is n - 1
+    float sum;           // the float sum of the weights
+    int pad;
+};
+
+struct Reg {
+    int id, uexp, mlim;  // binade id, exponent of its spacing, 2^24 (2^23 subnormal, 1 for zero)
+};
+
+__device__ __forceinline__ Reg reg_zero() { return {kZero, 0, 1}; }
+__device__ __forceinline__ Reg reg_id(int id) {
+    if (id == kZero) return reg_zero();
+    if (id == kSub) return {kSub, -149, 1 << 23};
+    return {id, id - 23, 1 << 24};
+}
+__device__ __forceinline__ Reg reg_of(float v) {
+    if (v == 0.0f) return reg_zero();
+    if (v < 0x1p-126f) return reg_id(kSub);
+    return reg_id(ilogbf(v));
+}
+__device__ __forceinline__ Reg reg_of_bound(double x) {
+    if (!(x > 0.0)) return reg_zero();
+    if (x < 0x1p-126) return reg_id(kSub);
+    return reg_id(min(ilogb(x), 127));
+}
+__device__ __forceinline__ int m_of(float v, const Reg &R) {
+    return R.id == kZero ? 0 : (int)ldexp((double)v, -R.uexp);
+}
+__device__ __forceinline__ float val_of(int M, const Reg &R) {   // exact for M < R.mlim
+    return R.id == kZero ? 0.0f : (float)ldexp((double)M, R.uexp);
+}
+
+struct Map {
+    int d0, d1;
+};
+__device__ __forceinline__ Map map_id() { return {0, 0}; }
+// a then b
+__device__ __forceinline__ Map compose(Map a, Map b) {
+    const int e = a.d0 + ((a.d0 & 1) ? b.d1 : b.d0);
+    const int o = a.d1 + ((a.d1 & 1) ? b.d0 : b.d1);
+    return {min(e, kCap), min(o, kCap)};
+}
+__device__ __forceinline__ int apply(int M, Map m) { return M + min((M & 1) ? m.d1 : m.d0, kCap); }
+
+__device__ __forceinline__ Map elem_map(float x, const Reg &R) {
+    if (R.id == kZero) return x > 0.0f ? Map{kCap, kCap} : map_id();
+    const double q = ldexp((double)x, -R.uexp);   // exact
+    if (q >= 0x1p25) return {kCap, kCap};
+    const double f = floor(q), fr = q - f;
+    const int fi = (int)f;
+    if (fr > 0.5) return {fi + 1, fi + 1};
+    if (fr < 0.5) return {fi, fi};
+    return {fi + (fi & 1), fi + ((fi & 1) ^ 1)};
+}
+
+__device__ __forceinline__ float scaled(float l, float inv_t, int scale) { return scale ? __fmul_rn(l, inv_t) : l; }
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return bi < 0 || (i >= 0 && (v > bv || (v == bv && i < bi)));
+}
+
+// grid (chunks, batch): ChunkStat of each chunk of the (scaled) logits
+__global__ __launch_bounds__(kThreads) void smp_stats(const float *__restrict__ logits, int n, size_t ld,
+                                                      float inv_t, int scale, ChunkStat *__restrict__ stats) {
+    __shared__ float sv[kThreads / kWave];
+    __shared__ int si[kThreads / kWave], sn[kThreads / kWave];
+    const int nch = gridDim.x, c = blockIdx.x, b = blockIdx.y;
+    const float *x = logits + (size_t)b * ld;
+    const int i0 = c * kChunk + threadIdx.x * kRun;
+    float bv = -INFINITY;
+    int bi = -1, nan = 0;
+#pragma unroll
+    for (int k = 0; k < kRun; ++k) {
+        const int i = i0 + k;
+        if (i < n) {
+            const float s = scaled(x[i], inv_t, scale);
+            if (s != s) nan = 1;
+            else if (bi < 0 || s > bv) {
+                bv = s;
+                bi = i;
+            }
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, kWave);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+        nan |= __shfl_xor(nan, off, kWave);
+    }
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    if (lane == 0) {
+        sv[wid] = bv;
+        si[wid] = bi;
+        sn[wid] = nan;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / kWave; ++w) {
+            if (better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+            nan |= sn[w];
+        }
+        ChunkStat st;
+        st.max = bv;
+        st.arg = bi;
+        st.nan = nan;
+        st.nan0 = c == 0 ? (int)(scaled(x[0], inv_t, scale) != scaled(x[0], inv_t, scale)) : 0;
+        st.wsum = 0.0;
+        stats[(size_t)b * nch + c] = st;
+    }
+}
+
+// The reference's max and the row's status from the chunk statistics (all threads).
+__device__ void row_max(const ChunkStat *__restrict__ st, int nch, float *m_out, int *bad_out) {
+    __shared__ float sm[kThreads / kWave];
+    __shared__ int sb[kThreads / kWave];
+    float m = -INFINITY;
+    int nan = 0;
+    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
+        m = fmaxf(m, st[c].max);
+        nan |= st[c].nan;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, off, kWave));
+        nan |= __shfl_xor(nan, off, kWave);
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        sm[threadIdx.x / kWave] = m;
+        sb[threadIdx.x / kWave] = nan;
+    }
+    __syncthreads();
+    m = sm[0];
+    nan = sb[0];
+    for (int w = 1; w < (int)(blockDim.x / kWave); ++w) {
+        m = fmaxf(m, sm[w]);
+        nan |= sb[w];
+    }
+    __syncthreads();
+    if (st[0].nan0) m = __int_as_float(0x7fc00000);
+    *m_out = m;
+    // NaN anywhere, or max = +inf (inf - inf) or -inf (every weight NaN): the sum is NaN
+    *bad_out = nan || m != m || m == INFINITY || m == -INFINITY;
+}
+
+// grid (chunks, batch): w = expf((s - m) / T) written to w (may alias the logits), the
+// chunk's weight sum into its ChunkStat, the row's RowInfo (chunk 0)
+__global__ __launch_bounds__(kThreads) void smp_weights(const float *logits, int n, size_t ld, float inv_t,
+                                                        int scale, float t, float *w, size_t ldw,
+                                                        ChunkStat *__restrict__ stats, RowInfo *__restrict__ rows) {
+    __shared__ double sd[kThreads / kWave];
+    const int nch = gridDim.x, c = blockIdx.x, b = blockIdx.y;
+    ChunkStat *st = stats + (size_t)b * nch;
+    float m;
+    int bad;
+    row_max(st, nch, &m, &bad);
+    const float *x = logits + (size_t)b * ld;
+    float *wr = w + (size_t)b * ldw;
+    const int i0 = c * kChunk + threadIdx.x * kRun;
+    double sum = 0.0;
+#pragma unroll 4
+    for (int k = 0; k < kRun; ++k) {
+        const int i = i0 + k;
+        if (i < n) {
+            const float v = libm_expf(__fdiv_rn(__fsub_rn(scaled(x[i], inv_t, scale), m), t));
+            wr[i] = v;
+            sum += (double)v;
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0) sd[threadIdx.x / kWave] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kThreads / kWave; ++k) sum += sd[k];
+        st[c].wsum = sum;
+        if (c == 0) {
+            RowInfo ri;
+            ri.m = m;
+            ri.bad = bad;
+            ri.sum = 0.0f;
+            ri.pad = 0;
+            rows[b] = ri;
+        }
+    }
+}
+
+// Element x of a chain: the weight (chain 0) or the weight over the float sum (chain 1).
+__device__ __forceinline__ float chain_elem(float wv, int chain, float sum) { return chain ? __fdiv_rn(wv, sum) : wv; }
+
+// Ordered composition of the block's per-thread maps; the result in thread 0.
+__device__ Map block_compose(Map m, Map *sh) {
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        Map o;
+        o.d0 = __shfl_down(m.d0, off, kWave);
+        o.d1 = __shfl_down(m.d1, off, kWave);
+        if ((lane & (2 * off - 1)) == 0 && lane + off < kWave) m = compose(m, o);
+    }
+    if (lane == 0) sh[wid] = m;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int k = 1; k < kThreads / kWave; ++k) m = compose(m, sh[k]);
+    return m;
+}
+
+// grid (chunks, batch): each chunk's map (chain 0: the weight sum; chain 1: the running sum
+// of the weights over the float sum) for the binades the chain can be in at its start
+__global__ __launch_bounds__(kThreads) void smp_maps(const float *__restrict__ w, int n, size_t ldw, int chain,
+                                                     const ChunkStat *__restrict__ stats,
+                                                     const RowInfo *__restrict__ rows, ChunkMaps *__restrict__ maps) {
+    __shared__ double sd[kThreads / kWave];
+    __shared__ Map sm[2][kThreads / kWave];
+    const int nch = gridDim.x, c = blockIdx.x, b = blockIdx.y;
+    const RowInfo ri = rows[b];
+    if (ri.bad) return;
+    const ChunkStat *st = stats + (size_t)b * nch;
+    // the exact sum of the earlier chunks' weights
+    double p = 0.0;
+    for (int k = threadIdx.x; k < c; k += kThreads) p += st[k].wsum;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) p += __shfl_xor(p, off, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0) sd[threadIdx.x / kWave] = p;
+    __syncthreads();
+    p = sd[0];
+    for (int k = 1; k < kThreads / kWave; ++k) p += sd[k];
+    // recursive summation of n nonnegative floats: relative error below (n + 2) 2^-24 (with
+    // margin); the quotients w / sum add 2^-24 relative each, and subnormal ones 2^-150
+    double rel = 2.0 * (n + 2) * 0x1p-24, abs_err = 0.0;
+    if (chain) {
+        p /= (double)ri.sum;
+        rel += 0x1p-22;
+        abs_err = (double)n * 0x1p-149;
+    }
+    const Reg lo = reg_of_bound(p * (1.0 - rel) - abs_err), hi = reg_of_bound(p * (1.0 + rel) + abs_err);
+    const float *wr = w + (size_t)b * ldw;
+    const int i0 = c * kChunk + threadIdx.x * kRun;
+    Map m0 = map_id(), m1 = map_id();
+    for (int k = 0; k < kRun; ++k) {
+        const int i = i0 + k;
+        if (i < n) {
+            const float x = chain_elem(wr[i], chain, ri.sum);
+            m0 = compose(m0, elem_map(x, lo));
+            if (hi.id != lo.id) m1 = compose(m1, elem_map(x, hi));
+        }
+    }
+    m0 = block_compose(m0, sm[0]);
+    m1 = block_compose(m1, sm[1]);
+    if (threadIdx.x == 0) {
+        ChunkMaps cm;
+        cm.reg[0] = lo.id;
+        cm.d[0][0] = m0.d0;
+        cm.d[0][1] = m0.d1;
+        cm.reg[1] = hi.id;
+        cm.d[1][0] = hi.id != lo.id ? m1.d0 : m0.d0;
+        cm.d[1][1] = hi.id != lo.id ? m1.d1 : m0.d1;
+        maps[(size_t)b * nch + c] = cm;
+    }
+}
+
+// grid (batch): the chain walk. chain 0 stores the float sum of the weights in RowInfo;
+// chain 1 finds the first index whose running sum reaches the row's draw r (draws[step *
+// batch + b], step = *d_step or 0) and writes the token (n - 1 if none, or for a bad row).
+__global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w, int n, size_t ldw, int chain,
+                                                     int nch, const ChunkMaps *__restrict__ maps,
+                                                     RowInfo *__restrict__ rows, const float *__restrict__ draws,
+                                                     const int *__restrict__ d_step, int batch,
+                                                     int *__restrict__ tokens) {
+    __shared__ ChunkMaps cm[kMaxChunks];
+    __shared__ float vals[kChunk];
+    __shared__ int mend[kThreads];
+    __shared__ float sh_v;
+    __shared__ int sh_c, sh_pos, sh_found, sh_first;
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const RowInfo ri = rows[b];
+    if (ri.bad) {
+        if (chain && tid == 0) tokens[b] = n - 1;
+        return;
+    }
+    const float r = chain ? draws[(size_t)(d_step ? *d_step : 0) * batch + b] : INFINITY;
+    const float *wr = w + (size_t)b * ldw;
+    for (int k = tid; k < nch; k += kThreads) cm[k] = maps[(size_t)b * nch + k];
+    __syncthreads();
+    float v = 0.0f;
+    int c = 0, found = -1;
+    for (;;) {
+        if (tid == 0) {
+            // skip the chunks whose map moves the chain within its binade and short of r
+            for (; c < nch; ++c) {
+                const Reg R = reg_of(v);
+                const ChunkMaps &q = cm[c];
+                const int k = q.reg[0] == R.id ? 0 : (q.reg[1] == R.id ? 1 : -1);
+                if (k < 0) break;
+                const int M = apply(m_of(v, R), Map{q.d[k][0], q.d[k][1]});
+                if (M >= R.mlim) break;
+                const float nv = val_of(M, R);
+                if (r <= nv) break;
+                v = nv;
+            }
+            sh_c = c;
+            sh_v = v;
+        }
+        __syncthreads();
+        c = sh_c;
+        v = sh_v;
+        if (c >= nch) break;
+        // chunk c element by element: stage its elements
+        const int base = c * kChunk, cnt = min(kChunk, n - base);
+        for (int k = tid; k < cnt; k += kThreads) vals[k] = chain_elem(wr[base + k], chain, ri.sum);
+        __syncthreads();
+        int pos = 0;
+        while (pos < cnt) {
+            if (tid == 0) {
+                const int e = min(cnt, pos + kGallop);
+                for (; pos < e; ++pos) {
+                    v = __fadd_rn(v, vals[pos]);
+                    if (r <= v) {
+                        found = base + pos;
+                        break;
+                    }
+                }
+                sh_v = v;
+                sh_pos = pos;
+                sh_found = found;
+                sh_first = kThreads;
+            }
+            __syncthreads();
+            v = sh_v;
+            pos = sh_pos;
+            found = sh_found;
+            if (found >= 0 || pos >= cnt) break;
+            // the rest of the chunk in runs of kRun: the first run where the binade changes
+            // or r is reached
+            const Reg R = reg_of(v);
+            const int M0 = m_of(v, R);
+            const int rs = pos + tid * kRun, re = min(cnt, rs + kRun);
+            Map m = map_id();
+            for (int k = rs; k < re; ++k) m = compose(m, elem_map(vals[k], R));
+            // inclusive scan of the maps in thread order
+            const int lane = tid & (kWave - 1);
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                Map o;
+                o.d0 = __shfl_up(m.d0, off, kWave);
+                o.d1 = __shfl_up(m.d1, off, kWave);
+                if (lane >= off) m = compose(o, m);
+            }
+            // the chain after this thread's run: M0 through the earlier waves, then this prefix
+            __shared__ Map wtot[kThreads / kWave];
+            if (lane == kWave - 1) wtot[tid / kWave] = m;
+            __syncthreads();
+            Map pre = map_id();
+            for (int k = 0; k < tid / kWave; ++k) pre = compose(pre, wtot[k]);
+            const int Me = apply(apply(M0, pre), m);
+            mend[tid] = Me;
+            if (rs < cnt && (Me >= R.mlim || r <= val_of(Me, R))) atomicMin(&sh_first, tid);
+            __syncthreads();
+            const int first = sh_first;
+            if (first == kThreads) {                      // the whole rest stays in the binade
+                const int last = (cnt - 1 - pos) / kRun;
+                v = val_of(mend[last], R);
+                pos = cnt;
+                __syncthreads();
+                break;
+            }
+            if (tid == first) {
+                float vv = first ? val_of(mend[first - 1], R) : v;
+                int k = rs;
+                for (; k < re; ++k) {
+                    vv = __fadd_rn(vv, vals[k]);
+                    if (r <= vv) {
+                        found = base + k;
+                        break;
+                    }
+                }
+                sh_v = vv;
+                sh_pos = re;
+                sh_found = found;
+            }
+            __syncthreads();
+            v = sh_v;
+            pos = sh_pos;
+            found = sh_found;
+            __syncthreads();
+            if (found >= 0) break;
+        }
+        if (found >= 0) break;
+        ++c;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        if (chain) tokens[b] = found >= 0 ? found : n - 1;
+        else rows[b].sum = v;
+    }
+}
+
+// grid (batch): sample_greedy from the chunk statistics: the first maximum, 0 when logits[0]
+// is NaN
+__global__ void smp_greedy(const ChunkStat *__restrict__ stats, int nch, int *__restrict__ tokens) {
+    const ChunkStat *st = stats + (size_t)blockIdx.x * nch;
+    if (threadIdx.x != 0) return;
+    if (st[0].nan0) {
+        tokens[blockIdx.x] = 0;
+        return;
+    }
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int c = 0; c < nch; ++c)
+        if (better(st[c].max, st[c].arg, bv, bi)) {
+            bv = st[c].max;
+            bi = st[c].arg;
+        }
+    tokens[blockIdx.x] = bi < 0 ? 0 : bi;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+int sample_chunks(int n) { return (n + kChunk - 1) / kChunk; }
+
+size_t sample_workspace_bytes(int n, int batch) {
+    const size_t cells = (size_t)sample_chunks(n) * batch;
+    return align256(cells * sizeof(ChunkStat)) + 2 * align256(cells * sizeof(ChunkMaps)) +
+           align256((size_t)batch * sizeof(RowInfo));
+}
+
+bool sample_supported(int n, int batch) { return n > 0 && batch > 0 && sample_chunks(n) <= kMaxChunks; }
+
+int launch_sample(const float *logits, int n, int batch, size_t ld, float temperature, float *w, size_t ldw,
+                  const float *draws, const int *d_step, int *tokens, void *ws, hipStream_t s) {
+    if (!sample_supported(n, batch)) {
+        set_error("sampling supports 1..%d logits per row", kMaxChunks * kChunk);
+        return -1;
+    }
+    const int nch = sample_chunks(n);
+    const size_t cells = (size_t)nch * batch;
+    char *p = static_cast<char *>(ws);
+    auto *stats = reinterpret_cast<ChunkStat *>(p);
+    p += align256(cells * sizeof(ChunkStat));
+    auto *maps0 = reinterpret_cast<ChunkMaps *>(p);
+    p += align256(cells * sizeof(ChunkMaps));
+    auto *maps1 = reinterpret_cast<ChunkMaps *>(p);
+    p += align256(cells * sizeof(ChunkMaps));
+    auto *rows = reinterpret_cast<RowInfo *>(p);
+    const dim3 grid(nch, batch);
+    if (temperature <= 0.0f) {
+        hipLaunchKernelGGL(smp_stats, grid, dim3(kThreads), 0, s, logits, n, ld, 1.0f, 0, stats);
+        if (!hip_ok(hipGetLastError(), "sample stats launch")) return -1;
+        hipLaunchKernelGGL(smp_greedy, dim3(batch), dim3(kWave), 0, s, stats, nch, tokens);
+        return hip_ok(hipGetLastError(), "sample greedy launch") ? 0 : -1;
+    }
+    // vec_scale skips s == 1.0f; a product with 1.0f changes no value either way. A NaN
+    // temperature (not scaled there) makes every weight NaN either way: token n - 1.
+    const float inv_t = 1.0f / temperature;
+    const int scale = inv_t != 1.0f;
+    hipLaunchKernelGGL(smp_stats, grid, dim3(kThreads), 0, s, logits, n, ld, inv_t, scale, stats);
+    if (!hip_ok(hipGetLastError(), "sample stats launch")) return -1;
+    hipLaunchKernelGGL(smp_weights, grid, dim3(kThreads), 0, s, logits, n, ld, inv_t, scale, temperature, w, ldw,
+                       stats, rows);
+    if (!hip_ok(hipGetLastError(), "sample weights launch")) return -1;
+    hipLaunchKernelGGL(smp_maps, grid, dim3(kThreads), 0, s, w, n, ldw, 0, stats, rows, maps0);
+    if (!hip_ok(hipGetLastError(), "sample maps launch")) return -1;
+    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 0, nch, maps0, rows, draws, d_step,
+                       batch, tokens);
+    if (!hip_ok(hipGetLastError(), "sample sum walk launch")) return -1;
+    hipLaunchKernelGGL(smp_maps, grid, dim3(kThreads), 0, s, w, n, ldw, 1, stats, rows, maps1);
+    if (!hip_ok(hipGetLastError(), "sample maps launch")) return -1;
+    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 1, nch, maps1, rows, draws, d_step,
+                       batch, tokens);
+    return hip_ok(hipGetLastError(), "sample draw walk launch") ? 0 : -1;
+}
+
+}  // namespace sapphire

@@ -56,6 +56,8 @@ def _protos(L):
     L.sapphire_decoder_set_workgroups.argtypes = [C.c_void_p, C.c_int]
     L.sapphire_decoder_workgroups.restype = C.c_int
     L.sapphire_decoder_workgroups.argtypes = [C.c_void_p]
+    L.sapphire_decoder_set_sampling.restype = C.c_int
+    L.sapphire_decoder_set_sampling.argtypes = [C.c_void_p, C.c_float, C.c_void_p, C.c_int]
     L.sapphire_decoder_prefill.restype = C.c_int
     L.sapphire_decoder_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]
     L.sapphire_decoder_generate_batch.restype = C.c_int
@@ -136,6 +138,14 @@ class Decoder:
 
     def set_workgroups(self, groups: int) -> None:
         self._check(self.lib.sapphire_decoder_set_workgroups(self.ptr, int(groups)), "set_workgroups")
+
+    def set_sampling(self, temperature: float, draws=None) -> None:
+        """temperature > 0: later generate calls draw tokens as sample_temperature does, with
+        draws[s * batch + b] for step s of a call and sequence b; <= 0: greedy."""
+        d = np.ascontiguousarray(draws if draws is not None else [], np.float32)
+        self._check(self.lib.sapphire_decoder_set_sampling(self.ptr, float(temperature),
+                                                           d.ctypes.data if d.size else None, int(d.size)),
+                    "set_sampling")
 
     def generate_batch(self, tokens, pos, steps: int, keep_logits: bool = False):
         """(tokens[steps, batch], logits[steps, batch, vocab] or None, device milliseconds)."""
