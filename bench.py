@@ -48,36 +48,83 @@ def traffic_from_profiles():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(x, w8, w4, budget_s: float = 12.0):
-    """The reference's own pooled kernel_gemv (compiled from its sources into
-    oracle/_ref) on this host, or the oracle's restatement when that was not built."""
+def host_cpu() -> dict:
+    """The host's CPU model, its logical CPU count and the CPUs this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": usable}
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU legs: the CPUs this process may use, capped by OMP_NUM_THREADS
+    (the box's CPU share) and 16."""
+    usable = host_cpu()["usable_cpus"]
+    return max(1, min(usable, int(os.environ.get("OMP_NUM_THREADS", usable)), 16))
+
+
+def cpu_baseline(x, w8, w4, min_reps: int = 20, min_reps_1t: int = 5, budget_s: float = 20.0):
+    """The reference's own pooled kernel_gemv (compiled from its sources into oracle/_ref) on
+    this host, or the oracle's restatement when that was not built: the median over reps of one
+    Q8_0 + one Q4_0 GEMV 262144x640, with the box's threads and with one thread."""
     from oracle.oracle import Oracle, Reference
     from sapphire_amd import synth
-    try:
-        ncpu = len(os.sched_getaffinity(0))
-    except AttributeError:
-        ncpu = os.cpu_count() or 1
-    threads = max(1, min(ncpu, int(os.environ.get("OMP_NUM_THREADS", ncpu)), 16))
+    threads = cpu_threads()
     if Reference.available():
         ref, kind = Reference(), "reference"
-        run = lambda dt, w: ref.gemv(dt, w, x, nthreads=threads)   # noqa: E731
+        run = lambda dt, w, n: ref.gemv(dt, w, x, nthreads=n)   # noqa: E731
     else:
         orc, kind = Oracle(), "port"
-        run = lambda dt, w: orc.gemv(dt, w, x, nthreads=threads)   # noqa: E731
-    total_bytes, total_t, reps = 0, 0.0, 0
-    t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s:
-        for dt, w in ((synth.Q8_0, w8), (synth.Q4_0, w4)):
+        run = lambda dt, w, n: orc.gemv(dt, w, x, nthreads=n)   # noqa: E731
+    pair = gemv_bytes(synth.Q8_0, M_LM, K_LM) + gemv_bytes(synth.Q4_0, M_LM, K_LM)
+
+    def median_rate(nth, reps_min):
+        rates, t_start = [], time.perf_counter()
+        run(synth.Q8_0, w8, nth)                      # warm-up (pool start, page faults)
+        while len(rates) < reps_min or (time.perf_counter() - t_start < budget_s / 2 and len(rates) < 200):
             t0 = time.perf_counter()
-            run(dt, w)
-            total_t += time.perf_counter() - t0
-            total_bytes += gemv_bytes(dt, M_LM, K_LM)
-        reps += 1
+            run(synth.Q8_0, w8, nth)
+            run(synth.Q4_0, w4, nth)
+            rates.append(pair / (time.perf_counter() - t0) / 1e9)
+        return float(np.median(rates)), len(rates), time.perf_counter() - t_start
+
+    med, reps, secs = median_rate(threads, min_reps)
+    med1, reps1, secs1 = median_rate(1, min_reps_1t)
     return {
-        "value": round(total_bytes / total_t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
-        "sample": f"{reps} x (Q8_0 + Q4_0 GEMV 262144x640) with the pooled kernel_gemv, "
-                  f"{threads} threads, {total_t:.1f} s",
+        "value": round(med, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+        "value_1_thread": round(med1, 2), **host_cpu(),
+        "sample": f"median of {reps} reps of (Q8_0 + Q4_0 GEMV 262144x640) with the pooled kernel_gemv on "
+                  f"{threads} threads ({secs:.1f} s), and of {reps1} reps on 1 thread ({secs1:.1f} s)",
     }
+
+
+def ref_decode_rate(m, k, v, tok, prefill, n):
+    """Tokens/s of the reference engine (oracle/_ref, or the oracle's restatement when it was not
+    built) over n greedy steps from the given KV cache, session set-up excluded: the time of n + 1
+    steps minus that of one step. Returns (tok/s, kind, tokens of the n + 1 steps)."""
+    from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
+    if ref_decode_available():
+        go, kind = (lambda steps: ref_decode(m, k.copy(), v.copy(), tok, prefill, steps)[0]), "reference"
+    else:
+        orc = Oracle()
+        go, kind = (lambda steps: oracle_decode(orc, m, k.copy(), v.copy(), tok, prefill, steps,
+                                                nthreads=cpu_threads())[0]), "port"
+    t0 = time.perf_counter()
+    go(1)
+    t1 = time.perf_counter()
+    toks = go(n + 1)
+    t2 = time.perf_counter()
+    return n / ((t2 - t1) - (t1 - t0)), kind, [int(t) for t in toks]
 
 
 def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024):
@@ -108,22 +155,14 @@ def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024)
                                                                     kv=(k, v)).items()
                                 if kk in ("ms_per_token", "tok_per_s", "weight_bytes_per_token", "first_tokens")}
     if cpu:
-        from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
         tok = smodel.start_token(m.cfg, seed)
-        n = 6
-        t0 = time.perf_counter()
-        if ref_decode_available():
-            toks, _ = ref_decode(m, k.copy(), v.copy(), tok, prefill, n)
-            kind = "reference"
-        else:
-            toks, _ = oracle_decode(Oracle(), m, k.copy(), v.copy(), tok, prefill, n, nthreads=os.cpu_count() or 1)
-            kind = "port"
-        dt = time.perf_counter() - t0
+        rate, kind, toks = ref_decode_rate(m, k, v, tok, prefill, steps)
         out["cpu_baseline"] = {
-            "tok_per_s": round(n / dt, 2), "kind": kind, "cores": os.cpu_count(),
-            "sample": f"{n} greedy steps of the same model and KV cache through the reference's session and "
-                      f"layer functions ({dt:.2f} s, thread pool of nproc threads)",
-            "tokens_match_gpu": [int(t) for t in toks] == out["first_tokens"][:n],
+            "tok_per_s": round(rate, 2), "kind": kind, "cores": os.cpu_count(), **host_cpu(),
+            "sample": f"{steps} greedy steps of the same model and KV cache through the reference's session and "
+                      f"layer functions (session set-up excluded); its pool starts one thread per online CPU "
+                      f"(pool.c:159)",
+            "tokens_match_gpu": toks[:len(out["first_tokens"])] == out["first_tokens"],
         }
     return out
 
@@ -175,21 +214,12 @@ def decode_batch_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int =
                                                                           prefill=prefill, m=tied, kv=(k, v)).items()
                                 if kk in ("ms_per_step", "tok_per_s", "weight_bytes_per_step")}
     if cpu:
-        from oracle.oracle import oracle_decode, Oracle, ref_decode, ref_decode_available
-        n = 3
-        tok = out["first_tokens"][0]
-        t0 = time.perf_counter()
-        if ref_decode_available():
-            ref_decode(m, k.copy(), v.copy(), tok, prefill, n)
-            kind = "reference"
-        else:
-            oracle_decode(Oracle(), m, k.copy(), v.copy(), tok, prefill, n, nthreads=os.cpu_count() or 1)
-            kind = "port"
-        dt = time.perf_counter() - t0
+        rate, kind, _ = ref_decode_rate(m, k, v, out["first_tokens"][0], prefill, steps)
         out["cpu_baseline"] = {
-            "tok_per_s": round(n / dt, 2), "kind": kind, "cores": os.cpu_count(),
-            "sample": f"{n} greedy steps of one sequence of the same model through the reference's session and "
-                      f"layer functions ({dt:.2f} s incl. session set-up, thread pool of nproc threads)",
+            "tok_per_s": round(rate, 2), "kind": kind, "cores": os.cpu_count(), **host_cpu(),
+            "sample": f"{steps} greedy steps of one sequence of the same model through the reference's session "
+                      f"and layer functions (session set-up excluded); its pool starts one thread per online "
+                      f"CPU (pool.c:159)",
         }
     return out
 

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import ctypes as C
+import sys
 
 import numpy as np
 
@@ -60,6 +61,10 @@ class DeviceArray:
             self.ptr = None
 
     def __del__(self):
+        # at interpreter exit the process ends and the runtime reclaims everything: no HIP
+        # calls from finalizers then
+        if sys.is_finalizing():
+            return
         try:
             self.free()
         except Exception:
@@ -143,6 +148,10 @@ class Timer:
         return float(L.sapphire_event_elapsed_ms(self.a, self.b))
 
     def __del__(self):
+        # at interpreter exit the process ends and the runtime reclaims everything: no HIP
+        # calls from finalizers then
+        if sys.is_finalizing():
+            return
         try:
             L = lib()
             L.sapphire_event_destroy(self.a)

@@ -7,6 +7,7 @@ activations, the KV cache and the sampled tokens stay in HBM.
 from __future__ import annotations
 
 import ctypes as C
+import sys
 
 import numpy as np
 
@@ -186,6 +187,10 @@ class Decoder:
             self.ptr = None
 
     def __del__(self):
+        # at interpreter exit the process ends and the runtime reclaims everything: no HIP
+        # calls from finalizers then
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
