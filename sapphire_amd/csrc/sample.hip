@@ -10,13 +10,15 @@
 // * while a chain v <- fl(v + x) (x >= 0) stays inside one binade [2^e, 2^(e+1)), whose
 //   spacing is u, it is integer arithmetic on M = v / u: fl(v + x) = (M + k) u with k = x / u
 //   rounded to nearest, and on a tie (x / u = f + 1/2) the even one of M + f and M + f + 1.
-//   Each element is the map M -> M + d[M & 1]; maps compose (associatively), so a chunk of
-//   kChunk elements is one pair (d0, d1) for a given binade. The binades a chain can occupy
-//   at a chunk's start are fixed to at most two by the exact prefix sum and the error bound
-//   of recursive summation (|fl-sum - sum| <= n 2^-24 sum for nonnegative terms);
-// * one workgroup per row walks the chunks with these maps and, in a chunk where the binade
-//   changes or the draw is reached, scans its runs' maps to find the run where that happens
-//   and adds that run's elements with real float adds (the reference's own operation).
+//   Each element is the map M -> M + d[M & 1] (k and the tie read from the element's float
+//   bits in integer arithmetic); maps compose (associatively), so a sub-chunk of kSub elements
+//   is one pair (d0, d1) for a given binade. The binades a chain can occupy at a chunk's start
+//   are fixed to at most two by the exact prefix sum and the error bound of recursive
+//   summation (|fl-sum - sum| <= n 2^-24 sum for nonnegative terms);
+// * one workgroup per row walks the chunks of kChunk elements with these maps and, in a chunk
+//   where the binade changes or the draw is reached, scans its runs' maps to find the run
+//   where that happens and adds that run's elements with real float adds (the reference's own
+//   operation).
 // The weights come from libm_expf, glibc's expf bit for bit.
 #include "internal.h"
 #include "libm_expf.h"
@@ -28,21 +30,25 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int kThreads = 256;
-constexpr int kRun = 16;                        // consecutive elements per thread
-constexpr int kChunk = kThreads * kRun;         // elements per chunk
+constexpr int kPer = 4;                         // elements per thread in the grid kernels
+constexpr int kSub = kThreads * kPer;           // elements per sub-chunk (one grid workgroup)
+constexpr int kRun = 16;                        // consecutive elements per thread in the walk
+constexpr int kChunk = kThreads * kRun;         // elements per chunk of the walk
+constexpr int kSubsPerChunk = kChunk / kSub;
 constexpr int kMaxChunks = 512;                 // n <= 2^21 keeps the error bound below 1/4
-constexpr int kGallop = 32;                     // real adds tried before a chunk's run scan
+constexpr int kMaxSubs = kMaxChunks * kSubsPerChunk;
+constexpr int kGallop = 16;                     // real adds tried before a chunk's run scan
 constexpr int kCap = 1 << 28;                   // saturation of map increments
-constexpr int kZero = -1000, kSub = -127;       // binade ids of 0 and of the subnormals
+constexpr int kZero = -1000, kSub_ = -127;      // binade ids of 0 and of the subnormals
 
-struct ChunkStat {       // per row and chunk
+struct SubStat {         // per row and sub-chunk
     float max;           // largest non-NaN scaled logit (+-inf included)
-    int arg;             // its first index, -1 if the chunk is all NaN
-    int nan;             // whether the chunk holds a NaN
-    int nan0;            // chunk 0 only: whether the row's first scaled logit is NaN
-    double wsum;         // sum of the chunk's weights (exact enough for the bounds)
+    int arg;             // its first index, -1 if the sub-chunk is all NaN
+    int nan;             // whether the sub-chunk holds a NaN
+    int nan0;            // sub-chunk 0 only: whether the row's first scaled logit is NaN
+    double wsum;         // sum of the sub-chunk's weights (exact enough for the bounds)
 };
-struct ChunkMaps {       // per row and chunk: the chunk's map for up to two binades
+struct SubMaps {         // per row and sub-chunk: its map for the chunk's (up to) two binades
     int reg[2];
     int d[2][2];
 };
@@ -60,17 +66,17 @@ struct Reg {
 __device__ __forceinline__ Reg reg_zero() { return {kZero, 0, 1}; }
 __device__ __forceinline__ Reg reg_id(int id) {
     if (id == kZero) return reg_zero();
-    if (id == kSub) return {kSub, -149, 1 << 23};
+    if (id == kSub_) return {kSub_, -149, 1 << 23};
     return {id, id - 23, 1 << 24};
 }
 __device__ __forceinline__ Reg reg_of(float v) {
     if (v == 0.0f) return reg_zero();
-    if (v < 0x1p-126f) return reg_id(kSub);
+    if (v < 0x1p-126f) return reg_id(kSub_);
     return reg_id(ilogbf(v));
 }
 __device__ __forceinline__ Reg reg_of_bound(double x) {
     if (!(x > 0.0)) return reg_zero();
-    if (x < 0x1p-126) return reg_id(kSub);
+    if (x < 0x1p-126) return reg_id(kSub_);
     return reg_id(min(ilogb(x), 127));
 }
 __device__ __forceinline__ int m_of(float v, const Reg &R) {
@@ -92,14 +98,24 @@ __device__ __forceinline__ Map compose(Map a, Map b) {
 }
 __device__ __forceinline__ int apply(int M, Map m) { return M + min((M & 1) ? m.d1 : m.d0, kCap); }
 
-__device__ __forceinline__ Map elem_map(float x, const Reg &R) {
-    if (R.id == kZero) return x > 0.0f ? Map{kCap, kCap} : map_id();
-    const double q = ldexp((double)x, -R.uexp);   // exact
-    if (q >= 0x1p25) return {kCap, kCap};
-    const double f = floor(q), fr = q - f;
+// The map of element x (bits xb of a float >= +0) in binade R: k = x / u rounded to nearest,
+// a tie to the even sum. x = mx 2^e2, so x / u = mx 2^(e2 - uexp) in integers.
+__device__ __forceinline__ Map elem_map(uint32_t xb, const Reg &R) {
+    if (R.id == kZero) return xb ? Map{kCap, kCap} : map_id();
+    const uint32_t ex = xb >> 23;
+    const uint32_t mx = ex ? (xb & 0x7fffffu) | 0x800000u : xb;
+    const int sh = (ex ? (int)ex - 150 : -149) - R.uexp;
+    if (sh >= 0) {
+        const uint64_t k = (uint64_t)mx << min(sh, 40);
+        if (k >= (1u << 25)) return {kCap, kCap};
+        return {(int)k, (int)k};
+    }
+    const int s = -sh;
+    if (s >= 26) return map_id();              // x / u < 2^24 2^-26
+    const uint32_t f = mx >> s, rem = mx & ((1u << s) - 1u), half = 1u << (s - 1);
     const int fi = (int)f;
-    if (fr > 0.5) return {fi + 1, fi + 1};
-    if (fr < 0.5) return {fi, fi};
+    if (rem > half) return {fi + 1, fi + 1};
+    if (rem < half) return {fi, fi};
     return {fi + (fi & 1), fi + ((fi & 1) ^ 1)};
 }
 
@@ -109,18 +125,18 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return bi < 0 || (i >= 0 && (v > bv || (v == bv && i < bi)));
 }
 
-// grid (chunks, batch): ChunkStat of each chunk of the (scaled) logits
+// grid (sub-chunks, batch): SubStat of each sub-chunk of the (scaled) logits
 __global__ __launch_bounds__(kThreads) void smp_stats(const float *__restrict__ logits, int n, size_t ld,
-                                                      float inv_t, int scale, ChunkStat *__restrict__ stats) {
+                                                      float inv_t, int scale, SubStat *__restrict__ stats) {
     __shared__ float sv[kThreads / kWave];
     __shared__ int si[kThreads / kWave], sn[kThreads / kWave];
-    const int nch = gridDim.x, c = blockIdx.x, b = blockIdx.y;
+    const int nsub = gridDim.x, q = blockIdx.x, b = blockIdx.y;
     const float *x = logits + (size_t)b * ld;
-    const int i0 = c * kChunk + threadIdx.x * kRun;
+    const int i0 = q * kSub + threadIdx.x * kPer;
     float bv = -INFINITY;
     int bi = -1, nan = 0;
 #pragma unroll
-    for (int k = 0; k < kRun; ++k) {
+    for (int k = 0; k < kPer; ++k) {
         const int i = i0 + k;
         if (i < n) {
             const float s = scaled(x[i], inv_t, scale);
@@ -156,25 +172,25 @@ __global__ __launch_bounds__(kThreads) void smp_stats(const float *__restrict__ 
             }
             nan |= sn[w];
         }
-        ChunkStat st;
+        SubStat st;
         st.max = bv;
         st.arg = bi;
         st.nan = nan;
-        st.nan0 = c == 0 ? (int)(scaled(x[0], inv_t, scale) != scaled(x[0], inv_t, scale)) : 0;
+        st.nan0 = q == 0 ? (int)(scaled(x[0], inv_t, scale) != scaled(x[0], inv_t, scale)) : 0;
         st.wsum = 0.0;
-        stats[(size_t)b * nch + c] = st;
+        stats[(size_t)b * nsub + q] = st;
     }
 }
 
-// The reference's max and the row's status from the chunk statistics (all threads).
-__device__ void row_max(const ChunkStat *__restrict__ st, int nch, float *m_out, int *bad_out) {
+// The reference's max and the row's status from the sub-chunk statistics (all threads).
+__device__ void row_max(const SubStat *__restrict__ st, int nsub, float *m_out, int *bad_out) {
     __shared__ float sm[kThreads / kWave];
     __shared__ int sb[kThreads / kWave];
     float m = -INFINITY;
     int nan = 0;
-    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
-        m = fmaxf(m, st[c].max);
-        nan |= st[c].nan;
+    for (int q = threadIdx.x; q < nsub; q += blockDim.x) {
+        m = fmaxf(m, st[q].max);
+        nan |= st[q].nan;
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -199,23 +215,23 @@ __device__ void row_max(const ChunkStat *__restrict__ st, int nch, float *m_out,
     *bad_out = nan || m != m || m == INFINITY || m == -INFINITY;
 }
 
-// grid (chunks, batch): w = expf((s - m) / T) written to w (may alias the logits), the
-// chunk's weight sum into its ChunkStat, the row's RowInfo (chunk 0)
+// grid (sub-chunks, batch): w = expf((s - m) / T) written to w (may alias the logits), the
+// sub-chunk's weight sum into its SubStat, the row's RowInfo (sub-chunk 0)
 __global__ __launch_bounds__(kThreads) void smp_weights(const float *logits, int n, size_t ld, float inv_t,
                                                         int scale, float t, float *w, size_t ldw,
-                                                        ChunkStat *__restrict__ stats, RowInfo *__restrict__ rows) {
+                                                        SubStat *__restrict__ stats, RowInfo *__restrict__ rows) {
     __shared__ double sd[kThreads / kWave];
-    const int nch = gridDim.x, c = blockIdx.x, b = blockIdx.y;
-    ChunkStat *st = stats + (size_t)b * nch;
+    const int nsub = gridDim.x, q = blockIdx.x, b = blockIdx.y;
+    SubStat *st = stats + (size_t)b * nsub;
     float m;
     int bad;
-    row_max(st, nch, &m, &bad);
+    row_max(st, nsub, &m, &bad);
     const float *x = logits + (size_t)b * ld;
     float *wr = w + (size_t)b * ldw;
-    const int i0 = c * kChunk + threadIdx.x * kRun;
+    const int i0 = q * kSub + threadIdx.x * kPer;
     double sum = 0.0;
-#pragma unroll 4
-    for (int k = 0; k < kRun; ++k) {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
         const int i = i0 + k;
         if (i < n) {
             const float v = libm_expf(__fdiv_rn(__fsub_rn(scaled(x[i], inv_t, scale), m), t));
@@ -229,8 +245,8 @@ __global__ __launch_bounds__(kThreads) void smp_weights(const float *logits, int
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int k = 1; k < kThreads / kWave; ++k) sum += sd[k];
-        st[c].wsum = sum;
-        if (c == 0) {
+        st[q].wsum = sum;
+        if (q == 0) {
             RowInfo ri;
             ri.m = m;
             ri.bad = bad;
@@ -241,8 +257,11 @@ __global__ __launch_bounds__(kThreads) void smp_weights(const float *logits, int
     }
 }
 
-// Element x of a chain: the weight (chain 0) or the weight over the float sum (chain 1).
-__device__ __forceinline__ float chain_elem(float wv, int chain, float sum) { return chain ? __fdiv_rn(wv, sum) : wv; }
+// Element x of a chain, as float bits: the weight (chain 0) or the weight over the float sum
+// (chain 1).
+__device__ __forceinline__ uint32_t chain_elem(float wv, int chain, float sum) {
+    return __float_as_uint(chain ? __fdiv_rn(wv, sum) : wv);
+}
 
 // Ordered composition of the block's per-thread maps; the result in thread 0.
 __device__ Map block_compose(Map m, Map *sh) {
@@ -261,20 +280,22 @@ __device__ Map block_compose(Map m, Map *sh) {
     return m;
 }
 
-// grid (chunks, batch): each chunk's map (chain 0: the weight sum; chain 1: the running sum
-// of the weights over the float sum) for the binades the chain can be in at its start
+// grid (sub-chunks, batch): each sub-chunk's map (chain 0: the weight sum; chain 1: the
+// running sum of the weights over the float sum) for the binades the chain can be in at the
+// start of the sub-chunk's chunk. The sub-chunks of one chunk compute the same two binades.
 __global__ __launch_bounds__(kThreads) void smp_maps(const float *__restrict__ w, int n, size_t ldw, int chain,
-                                                     const ChunkStat *__restrict__ stats,
-                                                     const RowInfo *__restrict__ rows, ChunkMaps *__restrict__ maps) {
+                                                     const SubStat *__restrict__ stats,
+                                                     const RowInfo *__restrict__ rows, SubMaps *__restrict__ maps) {
     __shared__ double sd[kThreads / kWave];
     __shared__ Map sm[2][kThreads / kWave];
-    const int nch = gridDim.x, c = blockIdx.x, b = blockIdx.y;
+    const int nsub = gridDim.x, q = blockIdx.x, b = blockIdx.y;
     const RowInfo ri = rows[b];
     if (ri.bad) return;
-    const ChunkStat *st = stats + (size_t)b * nch;
-    // the exact sum of the earlier chunks' weights
+    const SubStat *st = stats + (size_t)b * nsub;
+    // the exact sum of the weights before this chunk
+    const int q0 = q - q % kSubsPerChunk;
     double p = 0.0;
-    for (int k = threadIdx.x; k < c; k += kThreads) p += st[k].wsum;
+    for (int k = threadIdx.x; k < q0; k += kThreads) p += st[k].wsum;
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) p += __shfl_xor(p, off, kWave);
     if ((threadIdx.x & (kWave - 1)) == 0) sd[threadIdx.x / kWave] = p;
@@ -291,27 +312,28 @@ __global__ __launch_bounds__(kThreads) void smp_maps(const float *__restrict__ w
     }
     const Reg lo = reg_of_bound(p * (1.0 - rel) - abs_err), hi = reg_of_bound(p * (1.0 + rel) + abs_err);
     const float *wr = w + (size_t)b * ldw;
-    const int i0 = c * kChunk + threadIdx.x * kRun;
+    const int i0 = q * kSub + threadIdx.x * kPer;
     Map m0 = map_id(), m1 = map_id();
-    for (int k = 0; k < kRun; ++k) {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
         const int i = i0 + k;
         if (i < n) {
-            const float x = chain_elem(wr[i], chain, ri.sum);
+            const uint32_t x = chain_elem(wr[i], chain, ri.sum);
             m0 = compose(m0, elem_map(x, lo));
-            if (hi.id != lo.id) m1 = compose(m1, elem_map(x, hi));
+            m1 = compose(m1, elem_map(x, hi));
         }
     }
     m0 = block_compose(m0, sm[0]);
     m1 = block_compose(m1, sm[1]);
     if (threadIdx.x == 0) {
-        ChunkMaps cm;
+        SubMaps cm;
         cm.reg[0] = lo.id;
         cm.d[0][0] = m0.d0;
         cm.d[0][1] = m0.d1;
         cm.reg[1] = hi.id;
-        cm.d[1][0] = hi.id != lo.id ? m1.d0 : m0.d0;
-        cm.d[1][1] = hi.id != lo.id ? m1.d1 : m0.d1;
-        maps[(size_t)b * nch + c] = cm;
+        cm.d[1][0] = m1.d0;
+        cm.d[1][1] = m1.d1;
+        maps[(size_t)b * nsub + q] = cm;
     }
 }
 
@@ -319,13 +341,14 @@ __global__ __launch_bounds__(kThreads) void smp_maps(const float *__restrict__ w
 // chain 1 finds the first index whose running sum reaches the row's draw r (draws[step *
 // batch + b], step = *d_step or 0) and writes the token (n - 1 if none, or for a bad row).
 __global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w, int n, size_t ldw, int chain,
-                                                     int nch, const ChunkMaps *__restrict__ maps,
+                                                     int nsub, const SubMaps *__restrict__ maps,
                                                      RowInfo *__restrict__ rows, const float *__restrict__ draws,
                                                      const int *__restrict__ d_step, int batch,
                                                      int *__restrict__ tokens) {
-    __shared__ ChunkMaps cm[kMaxChunks];
-    __shared__ float vals[kChunk];
+    __shared__ SubMaps cm[kMaxSubs];
+    __shared__ uint32_t vals[kChunk];
     __shared__ int mend[kThreads];
+    __shared__ Map wtot[kThreads / kWave];
     __shared__ float sh_v;
     __shared__ int sh_c, sh_pos, sh_found, sh_first;
     const int b = blockIdx.x, tid = threadIdx.x;
@@ -336,7 +359,8 @@ __global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w
     }
     const float r = chain ? draws[(size_t)(d_step ? *d_step : 0) * batch + b] : INFINITY;
     const float *wr = w + (size_t)b * ldw;
-    for (int k = tid; k < nch; k += kThreads) cm[k] = maps[(size_t)b * nch + k];
+    const int nch = (nsub + kSubsPerChunk - 1) / kSubsPerChunk;
+    for (int k = tid; k < nsub; k += kThreads) cm[k] = maps[(size_t)b * nsub + k];
     __syncthreads();
     float v = 0.0f;
     int c = 0, found = -1;
@@ -345,10 +369,12 @@ __global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w
             // skip the chunks whose map moves the chain within its binade and short of r
             for (; c < nch; ++c) {
                 const Reg R = reg_of(v);
-                const ChunkMaps &q = cm[c];
-                const int k = q.reg[0] == R.id ? 0 : (q.reg[1] == R.id ? 1 : -1);
+                const int q0 = c * kSubsPerChunk, q1 = min(nsub, q0 + kSubsPerChunk);
+                const int k = cm[q0].reg[0] == R.id ? 0 : (cm[q0].reg[1] == R.id ? 1 : -1);
                 if (k < 0) break;
-                const int M = apply(m_of(v, R), Map{q.d[k][0], q.d[k][1]});
+                Map mc = map_id();
+                for (int q = q0; q < q1; ++q) mc = compose(mc, Map{cm[q].d[k][0], cm[q].d[k][1]});
+                const int M = apply(m_of(v, R), mc);
                 if (M >= R.mlim) break;
                 const float nv = val_of(M, R);
                 if (r <= nv) break;
@@ -370,7 +396,7 @@ __global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w
             if (tid == 0) {
                 const int e = min(cnt, pos + kGallop);
                 for (; pos < e; ++pos) {
-                    v = __fadd_rn(v, vals[pos]);
+                    v = __fadd_rn(v, __uint_as_float(vals[pos]));
                     if (r <= v) {
                         found = base + pos;
                         break;
@@ -403,7 +429,6 @@ __global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w
                 if (lane >= off) m = compose(o, m);
             }
             // the chain after this thread's run: M0 through the earlier waves, then this prefix
-            __shared__ Map wtot[kThreads / kWave];
             if (lane == kWave - 1) wtot[tid / kWave] = m;
             __syncthreads();
             Map pre = map_id();
@@ -424,7 +449,7 @@ __global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w
                 float vv = first ? val_of(mend[first - 1], R) : v;
                 int k = rs;
                 for (; k < re; ++k) {
-                    vv = __fadd_rn(vv, vals[k]);
+                    vv = __fadd_rn(vv, __uint_as_float(vals[k]));
                     if (r <= vv) {
                         found = base + k;
                         break;
@@ -451,60 +476,65 @@ __global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w
     }
 }
 
-// grid (batch): sample_greedy from the chunk statistics: the first maximum, 0 when logits[0]
-// is NaN
-__global__ void smp_greedy(const ChunkStat *__restrict__ stats, int nch, int *__restrict__ tokens) {
-    const ChunkStat *st = stats + (size_t)blockIdx.x * nch;
-    if (threadIdx.x != 0) return;
-    if (st[0].nan0) {
-        tokens[blockIdx.x] = 0;
-        return;
-    }
+// grid (batch), one wave: sample_greedy from the sub-chunk statistics: the first maximum, 0
+// when logits[0] is NaN
+__global__ __launch_bounds__(kWave) void smp_greedy(const SubStat *__restrict__ stats, int nsub,
+                                                    int *__restrict__ tokens) {
+    const SubStat *st = stats + (size_t)blockIdx.x * nsub;
     float bv = -INFINITY;
     int bi = -1;
-    for (int c = 0; c < nch; ++c)
-        if (better(st[c].max, st[c].arg, bv, bi)) {
-            bv = st[c].max;
-            bi = st[c].arg;
+    for (int q = threadIdx.x; q < nsub; q += kWave)
+        if (better(st[q].max, st[q].arg, bv, bi)) {
+            bv = st[q].max;
+            bi = st[q].arg;
         }
-    tokens[blockIdx.x] = bi < 0 ? 0 : bi;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, kWave);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (threadIdx.x == 0) tokens[blockIdx.x] = st[0].nan0 || bi < 0 ? 0 : bi;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+int subs_of(int n) { return (n + kSub - 1) / kSub; }
+
 }  // namespace
 
-int sample_chunks(int n) { return (n + kChunk - 1) / kChunk; }
-
 size_t sample_workspace_bytes(int n, int batch) {
-    const size_t cells = (size_t)sample_chunks(n) * batch;
-    return align256(cells * sizeof(ChunkStat)) + 2 * align256(cells * sizeof(ChunkMaps)) +
+    const size_t cells = (size_t)subs_of(n) * batch;
+    return align256(cells * sizeof(SubStat)) + 2 * align256(cells * sizeof(SubMaps)) +
            align256((size_t)batch * sizeof(RowInfo));
 }
 
-bool sample_supported(int n, int batch) { return n > 0 && batch > 0 && sample_chunks(n) <= kMaxChunks; }
+bool sample_supported(int n, int batch) { return n > 0 && batch > 0 && subs_of(n) <= kMaxSubs; }
 
 int launch_sample(const float *logits, int n, int batch, size_t ld, float temperature, float *w, size_t ldw,
                   const float *draws, const int *d_step, int *tokens, void *ws, hipStream_t s) {
     if (!sample_supported(n, batch)) {
-        set_error("sampling supports 1..%d logits per row", kMaxChunks * kChunk);
+        set_error("sampling supports 1..%d logits per row", kMaxSubs * kSub);
         return -1;
     }
-    const int nch = sample_chunks(n);
-    const size_t cells = (size_t)nch * batch;
+    const int nsub = subs_of(n);
+    const size_t cells = (size_t)nsub * batch;
     char *p = static_cast<char *>(ws);
-    auto *stats = reinterpret_cast<ChunkStat *>(p);
-    p += align256(cells * sizeof(ChunkStat));
-    auto *maps0 = reinterpret_cast<ChunkMaps *>(p);
-    p += align256(cells * sizeof(ChunkMaps));
-    auto *maps1 = reinterpret_cast<ChunkMaps *>(p);
-    p += align256(cells * sizeof(ChunkMaps));
+    auto *stats = reinterpret_cast<SubStat *>(p);
+    p += align256(cells * sizeof(SubStat));
+    auto *maps0 = reinterpret_cast<SubMaps *>(p);
+    p += align256(cells * sizeof(SubMaps));
+    auto *maps1 = reinterpret_cast<SubMaps *>(p);
+    p += align256(cells * sizeof(SubMaps));
     auto *rows = reinterpret_cast<RowInfo *>(p);
-    const dim3 grid(nch, batch);
+    const dim3 grid(nsub, batch);
     if (temperature <= 0.0f) {
         hipLaunchKernelGGL(smp_stats, grid, dim3(kThreads), 0, s, logits, n, ld, 1.0f, 0, stats);
         if (!hip_ok(hipGetLastError(), "sample stats launch")) return -1;
-        hipLaunchKernelGGL(smp_greedy, dim3(batch), dim3(kWave), 0, s, stats, nch, tokens);
+        hipLaunchKernelGGL(smp_greedy, dim3(batch), dim3(kWave), 0, s, stats, nsub, tokens);
         return hip_ok(hipGetLastError(), "sample greedy launch") ? 0 : -1;
     }
     // vec_scale skips s == 1.0f; a product with 1.0f changes no value either way. A NaN
@@ -518,12 +548,12 @@ int launch_sample(const float *logits, int n, int batch, size_t ld, float temper
     if (!hip_ok(hipGetLastError(), "sample weights launch")) return -1;
     hipLaunchKernelGGL(smp_maps, grid, dim3(kThreads), 0, s, w, n, ldw, 0, stats, rows, maps0);
     if (!hip_ok(hipGetLastError(), "sample maps launch")) return -1;
-    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 0, nch, maps0, rows, draws, d_step,
+    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 0, nsub, maps0, rows, draws, d_step,
                        batch, tokens);
     if (!hip_ok(hipGetLastError(), "sample sum walk launch")) return -1;
     hipLaunchKernelGGL(smp_maps, grid, dim3(kThreads), 0, s, w, n, ldw, 1, stats, rows, maps1);
     if (!hip_ok(hipGetLastError(), "sample maps launch")) return -1;
-    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 1, nch, maps1, rows, draws, d_step,
+    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 1, nsub, maps1, rows, draws, d_step,
                        batch, tokens);
     return hip_ok(hipGetLastError(), "sample draw walk launch") ? 0 : -1;
 }
