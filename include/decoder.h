@@ -1,16 +1,17 @@
 /*
- * decoder.h - device-resident greedy decode of a Gemma-3-shaped model on one MI355X.
+ * decoder.h - device-resident decode (greedy or temperature-sampled) of a Gemma-3-shaped
+ * model on one MI355X.
  *
  * The reference runs a decode step as inference_forward (src/inference/inference.c:612-651):
  * sapphire_embed_lookup, then sapphire_transformer_layer for every layer (attention stage
  * attention.c:311-375, FFN stage transformer.c:96-171, finalize transformer.c:211-283),
- * then lm_head (transformer.c:393-408) and sample_greedy (utils.c:145-156), calling
- * kernel_gemv and the vector primitives with host buffers. Those entry points take the
- * reference's own inference_session_t, so a drop-in at that level would put a PCIe round
- * trip behind every GEMV. This engine is the MI355X-native form of the same step: weights,
- * activations, the KV cache and the sampled token stay in HBM, and one step is a captured
- * HIP graph of fused kernels. The host engine keeps its model loader and session and hands
- * the weights over once (sapphire_decoder_create below).
+ * then lm_head (transformer.c:393-408) and sample_greedy / sample_temperature (utils.c:145-180),
+ * calling kernel_gemv and the vector primitives with host buffers. The library also exports
+ * those transformer.h entry points on the engine's own session (one PCIe round trip per layer
+ * call). This engine is the MI355X-native form of the whole step: weights, activations, the KV
+ * cache and the sampled token stay in HBM, and one step is a captured HIP graph of fused
+ * kernels. The host engine keeps its model loader and session and hands the weights over once
+ * (sapphire_decoder_create below).
  *
  * Not a reference interface: the reference has no device engine. Semantics follow the
  * functions cited above; weights are the reference's Q4_0 / Q8_0 block arrays
@@ -66,9 +67,9 @@ void sapphire_decoder_destroy(sapphire_decoder_t *dec);
 int sapphire_decoder_set_kv(sapphire_decoder_t *dec, const float *k, const float *v);
 int sapphire_decoder_get_kv(sapphire_decoder_t *dec, float *k, float *v);
 
-/* Greedy decode: `steps` steps starting with `token` at position `pos`; step s feeds
- * tokens_out[s-1] back (token for s = 0). tokens_out[steps] receives the argmax of every
- * step (lowest index on ties). logits_out, if not NULL, receives [steps][vocab] logits
+/* Decode: `steps` steps starting with `token` at position `pos`; step s feeds tokens_out[s-1]
+ * back (token for s = 0). tokens_out[steps] receives every step's token: the greedy one (the
+ * lowest index among equal maxima), or the sampled one (sapphire_decoder_set_sampling). logits_out, if not NULL, receives [steps][vocab] logits
  * (copied back after each step, which costs time). elapsed_ms, if not NULL, receives the
  * device time of the steps (HIP events on the decoder's stream). 0 / -1. */
 int sapphire_decoder_generate(sapphire_decoder_t *dec, int token, int pos, int steps, int *tokens_out,
@@ -94,6 +95,13 @@ int sapphire_decoder_prefill(sapphire_decoder_t *dec, int seq, const int *tokens
 int sapphire_decoder_set_workgroups(sapphire_decoder_t *dec, int groups);
 /* The current form: workgroups of the persistent step, 0 for the multi-launch step. */
 int sapphire_decoder_workgroups(const sapphire_decoder_t *dec);
+/* No counterpart in the reference; for tests of the persistent step. Its stages tag exchanged
+ * values with epochs (steps since the last reset x 8 x (n_layers + 1) + stage) that must stay
+ * below 2^32, so generate starts them over (clearing every exchange word) before a call would
+ * pass that. This sets the count of steps since the last reset, on the device and the host, as
+ * if that many steps had run: a test can start just below the reset and decode across it.
+ * No effect on the multi-launch step. 0 / -1 (count past the range). */
+int sapphire_decoder_set_epoch_count(sapphire_decoder_t *dec, uint32_t steps);
 
 /* How the following generate calls pick tokens (inference.c:262-266 and 297). temperature <= 0
  * (the default): greedy, sample_greedy (utils.c:145-156). temperature > 0: each step scales
@@ -106,7 +114,7 @@ int sapphire_decoder_set_sampling(sapphire_decoder_t *dec, float temperature, co
 
 /* ---- batched decode ----
  * `batch` (2..16) independent sequences decoded in lock step, each with its own KV cache,
- * position and greedy token: one step runs every projection as one matrix-core GEMM over
+ * position and token: one step runs every projection as one matrix-core GEMM over
  * the batch (the reference decodes one sequence per inference_forward call). Shapes:
  * hidden, n_heads*head_dim and ffn multiples of 128, hidden <= 1152. Weights as for
  * sapphire_decoder_create. A decoder made by sapphire_decoder_create has batch 1; the
@@ -119,7 +127,7 @@ int sapphire_decoder_batch(const sapphire_decoder_t *dec);
 int sapphire_decoder_set_kv_seq(sapphire_decoder_t *dec, int seq, const float *k, const float *v);
 int sapphire_decoder_get_kv_seq(sapphire_decoder_t *dec, int seq, float *k, float *v);
 /* tokens[batch] and pos[batch] start every sequence; tokens_out receives [steps][batch]
- * greedy tokens; logits_out, if not NULL, [steps][batch][vocab]. */
+ * tokens (greedy or sampled); logits_out, if not NULL, [steps][batch][vocab]. */
 int sapphire_decoder_generate_batch(sapphire_decoder_t *dec, const int *tokens, const int *pos, int steps,
                                     int *tokens_out, float *logits_out, float *elapsed_ms);
 

@@ -1012,6 +1012,26 @@ int sapphire_decoder_set_workgroups(sapphire_decoder_t *d, int groups) {
 
 int sapphire_decoder_workgroups(const sapphire_decoder_t *d) { return d ? d->groups : -1; }
 
+int sapphire_decoder_set_epoch_count(sapphire_decoder_t *d, uint32_t steps) {
+    if (!d) {
+        set_error("sapphire_decoder_set_epoch_count: bad arguments");
+        return -1;
+    }
+    if (d->groups <= 0) return 0;
+    if ((uint64_t)(steps + 1ull) * persist_epochs_per_step(d->cfg.n_layers) > 0xFFFFFFFFull) {
+        set_error("sapphire_decoder_set_epoch_count: %u steps are past the epoch range", steps);
+        return -1;
+    }
+    SPH_CHECK(hipSetDevice(d->device));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    // every exchange word is stale (tag 0) for any epoch above 0; the device counter and the
+    // host's count of steps since the last reset move together
+    SPH_CHECK(hipMemset(d->tbuf, 0, d->tbuf_words * sizeof(uint64_t)));
+    SPH_CHECK(hipMemcpy(d->seq, &steps, sizeof(uint32_t), hipMemcpyHostToDevice));
+    d->persist_steps = steps;
+    return 0;
+}
+
 int sapphire_decoder_set_sampling(sapphire_decoder_t *d, float temperature, const float *draws, int n_draws) {
     if (!d || temperature != temperature || (temperature > 0.0f && (!draws || n_draws <= 0))) {
         set_error("sapphire_decoder_set_sampling: bad arguments");

@@ -57,6 +57,8 @@ def _protos(L):
     L.sapphire_decoder_set_workgroups.argtypes = [C.c_void_p, C.c_int]
     L.sapphire_decoder_workgroups.restype = C.c_int
     L.sapphire_decoder_workgroups.argtypes = [C.c_void_p]
+    L.sapphire_decoder_set_epoch_count.restype = C.c_int
+    L.sapphire_decoder_set_epoch_count.argtypes = [C.c_void_p, C.c_uint32]
     L.sapphire_decoder_set_sampling.restype = C.c_int
     L.sapphire_decoder_set_sampling.argtypes = [C.c_void_p, C.c_float, C.c_void_p, C.c_int]
     L.sapphire_decoder_prefill.restype = C.c_int

@@ -171,6 +171,33 @@ def test_decode_persistent_epochs_across_calls(oracle):
         dec.close()
 
 
+def test_decode_persistent_epochs_across_the_reset(oracle):
+    """Epochs just below 2^32: a first call whose stages use the last epochs before the reset,
+    then calls whose start clears the exchange words and restarts the epochs. Every call
+    decodes the oracle's tokens from the same state."""
+    from sapphire_amd.engine import Decoder
+    cfg = smodel.TINY
+    m = smodel.synthetic_model(cfg, 38)
+    k, v = m.kv_prefill(30)
+    tok = smodel.start_token(cfg, 38)
+    steps = 6
+    ref_toks, _ = oracle_decode(oracle, m, k.copy(), v.copy(), tok, 30, steps, nthreads=4)
+    per = 8 * (cfg.n_layers + 1)
+    last = (1 << 32) // per - 1          # the last step count whose epochs fit
+    dec = Decoder(m)
+    try:
+        assert dec.workgroups > 0
+        # steps + 1 more fit: no reset before this call, its epochs end just below 2^32
+        assert dec.lib.sapphire_decoder_set_epoch_count(dec.ptr, last - steps - 1) == 0
+        for _ in range(3):                  # the second call starts over, the third continues
+            dec.set_kv(k, v)
+            got, _, _ = dec.generate(tok, 30, steps)
+            assert list(got) == list(ref_toks)
+        assert dec.lib.sapphire_decoder_set_epoch_count(dec.ptr, last + 1) == -1
+    finally:
+        dec.close()
+
+
 def test_decode_repeatable(oracle):
     """Two generate calls on one decoder (the captured graph is replayed, the state reset)."""
     from sapphire_amd.engine import Decoder
