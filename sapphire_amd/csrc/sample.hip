@@ -12,13 +12,13 @@
 //   rounded to nearest, and on a tie (x / u = f + 1/2) the even one of M + f and M + f + 1.
 //   Each element is the map M -> M + d[M & 1] (k and the tie read from the element's float
 //   bits in integer arithmetic); maps compose (associatively), so a sub-chunk of kSub elements
-//   is one pair (d0, d1) for a given binade. The binades a chain can occupy at a chunk's start
-//   are fixed to at most two by the exact prefix sum and the error bound of recursive
+//   is one pair (d0, d1) for a given binade. The binades a chain can occupy at a sub-chunk's
+//   start are fixed to at most two by the exact prefix sum and the error bound of recursive
 //   summation (|fl-sum - sum| <= n 2^-24 sum for nonnegative terms);
-// * one workgroup per row walks the chunks of kChunk elements with these maps and, in a chunk
-//   where the binade changes or the draw is reached, scans its runs' maps to find the run
-//   where that happens and adds that run's elements with real float adds (the reference's own
-//   operation).
+// * one wave per row walks the sub-chunks with these maps, 64 at a time, and in a sub-chunk
+//   where the binade changes or the draw is reached scans its lanes' maps (16 elements each)
+//   to find the lane where that happens; that lane adds its elements with real float adds
+//   (the reference's own operation).
 // The weights come from libm_expf, glibc's expf bit for bit.
 #include "internal.h"
 #include "libm_expf.h"
@@ -32,12 +32,8 @@ constexpr int kWave = 64;
 constexpr int kThreads = 256;
 constexpr int kPer = 4;                         // elements per thread in the grid kernels
 constexpr int kSub = kThreads * kPer;           // elements per sub-chunk (one grid workgroup)
-constexpr int kRun = 16;                        // consecutive elements per thread in the walk
-constexpr int kChunk = kThreads * kRun;         // elements per chunk of the walk
-constexpr int kSubsPerChunk = kChunk / kSub;
-constexpr int kMaxChunks = 512;                 // n <= 2^21 keeps the error bound below 1/4
-constexpr int kMaxSubs = kMaxChunks * kSubsPerChunk;
-constexpr int kGallop = 16;                     // real adds tried before a chunk's run scan
+constexpr int kRun = kSub / kWave;              // consecutive elements per lane in the walk
+constexpr int kMaxSubs = 2048;                  // n <= 2^21 keeps the error bound below 1/4
 constexpr int kCap = 1 << 28;                   // saturation of map increments
 constexpr int kZero = -1000, kSub_ = -127;      // binade ids of 0 and of the subnormals
 
@@ -282,7 +278,7 @@ __device__ Map block_compose(Map m, Map *sh) {
 
 // grid (sub-chunks, batch): each sub-chunk's map (chain 0: the weight sum; chain 1: the
 // running sum of the weights over the float sum) for the binades the chain can be in at the
-// start of the sub-chunk's chunk. The sub-chunks of one chunk compute the same two binades.
+// sub-chunk's start.
 __global__ __launch_bounds__(kThreads) void smp_maps(const float *__restrict__ w, int n, size_t ldw, int chain,
                                                      const SubStat *__restrict__ stats,
                                                      const RowInfo *__restrict__ rows, SubMaps *__restrict__ maps) {
@@ -292,10 +288,9 @@ __global__ __launch_bounds__(kThreads) void smp_maps(const float *__restrict__ w
     const RowInfo ri = rows[b];
     if (ri.bad) return;
     const SubStat *st = stats + (size_t)b * nsub;
-    // the exact sum of the weights before this chunk
-    const int q0 = q - q % kSubsPerChunk;
+    // the exact sum of the weights before this sub-chunk
     double p = 0.0;
-    for (int k = threadIdx.x; k < q0; k += kThreads) p += st[k].wsum;
+    for (int k = threadIdx.x; k < q; k += kThreads) p += st[k].wsum;
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) p += __shfl_xor(p, off, kWave);
     if ((threadIdx.x & (kWave - 1)) == 0) sd[threadIdx.x / kWave] = p;
@@ -337,140 +332,130 @@ __global__ __launch_bounds__(kThreads) void smp_maps(const float *__restrict__ w
     }
 }
 
-// grid (batch): the chain walk. chain 0 stores the float sum of the weights in RowInfo;
-// chain 1 finds the first index whose running sum reaches the row's draw r (draws[step *
-// batch + b], step = *d_step or 0) and writes the token (n - 1 if none, or for a bad row).
-__global__ __launch_bounds__(kThreads) void smp_walk(const float *__restrict__ w, int n, size_t ldw, int chain,
-                                                     int nsub, const SubMaps *__restrict__ maps,
-                                                     RowInfo *__restrict__ rows, const float *__restrict__ draws,
-                                                     const int *__restrict__ d_step, int batch,
-                                                     int *__restrict__ tokens) {
+// One DPP move of both halves of a map; lanes without a source (and rows outside row_mask)
+// read 0, the identity map.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ Map dpp_map(Map m) {
+    return {__builtin_amdgcn_update_dpp(0, m.d0, CTRL, ROW_MASK, 0xf, true),
+            __builtin_amdgcn_update_dpp(0, m.d1, CTRL, ROW_MASK, 0xf, true)};
+}
+
+// Inclusive scan of the wave's maps in lane order (lane l gets m_0 ... m_l composed): shifts
+// by 1, 2, 4, 8 within each 16-lane row, then the last lane of row 0 (and of row 2) into the
+// next row, then lane 31 into rows 2 and 3.
+__device__ __forceinline__ Map wave_scan(Map m) {
+    m = compose(dpp_map<0x111, 0xf>(m), m);   // row_shr:1
+    m = compose(dpp_map<0x112, 0xf>(m), m);   // row_shr:2
+    m = compose(dpp_map<0x114, 0xf>(m), m);   // row_shr:4
+    m = compose(dpp_map<0x118, 0xf>(m), m);   // row_shr:8
+    m = compose(dpp_map<0x142, 0xa>(m), m);   // row_bcast:15 into rows 1 and 3
+    m = compose(dpp_map<0x143, 0xc>(m), m);   // row_bcast:31 into rows 2 and 3
+    return m;
+}
+
+__device__ __forceinline__ int first_lane(unsigned long long bal) { return __builtin_ctzll(bal); }
+
+// grid (batch), one wave per row: the chain walk. chain 0 stores the float sum of the weights
+// in RowInfo; chain 1 finds the first index whose running sum reaches the row's draw r
+// (draws[step * batch + b], step = *d_step or 0) and writes the token (n - 1 if none, or for
+// a bad row). The wave takes 64 sub-chunks at a time, one per lane: a scan of their maps in
+// the chain's binade finds the first sub-chunk in which the binade changes or r is reached
+// (or whose binades were not prepared). In that sub-chunk each lane holds 16 consecutive
+// elements, a scan of the lanes' maps finds the first lane where the same happens, and that
+// lane adds its elements with real float adds; the scan resumes after it.
+__global__ __launch_bounds__(kWave) void smp_walk(const float *__restrict__ w, int n, size_t ldw, int chain,
+                                                  int nsub, const SubMaps *__restrict__ maps,
+                                                  RowInfo *__restrict__ rows, const float *__restrict__ draws,
+                                                  const int *__restrict__ d_step, int batch,
+                                                  int *__restrict__ tokens) {
     __shared__ SubMaps cm[kMaxSubs];
-    __shared__ uint32_t vals[kChunk];
-    __shared__ int mend[kThreads];
-    __shared__ Map wtot[kThreads / kWave];
-    __shared__ float sh_v;
-    __shared__ int sh_c, sh_pos, sh_found, sh_first;
-    const int b = blockIdx.x, tid = threadIdx.x;
+    const int b = blockIdx.x, lane = threadIdx.x;
     const RowInfo ri = rows[b];
     if (ri.bad) {
-        if (chain && tid == 0) tokens[b] = n - 1;
+        if (chain && lane == 0) tokens[b] = n - 1;
         return;
     }
     const float r = chain ? draws[(size_t)(d_step ? *d_step : 0) * batch + b] : INFINITY;
     const float *wr = w + (size_t)b * ldw;
-    const int nch = (nsub + kSubsPerChunk - 1) / kSubsPerChunk;
-    for (int k = tid; k < nsub; k += kThreads) cm[k] = maps[(size_t)b * nsub + k];
+    for (int k = lane; k < nsub; k += kWave) cm[k] = maps[(size_t)b * nsub + k];
     __syncthreads();
     float v = 0.0f;
-    int c = 0, found = -1;
-    for (;;) {
-        if (tid == 0) {
-            // skip the chunks whose map moves the chain within its binade and short of r
-            for (; c < nch; ++c) {
-                const Reg R = reg_of(v);
-                const int q0 = c * kSubsPerChunk, q1 = min(nsub, q0 + kSubsPerChunk);
-                const int k = cm[q0].reg[0] == R.id ? 0 : (cm[q0].reg[1] == R.id ? 1 : -1);
-                if (k < 0) break;
-                Map mc = map_id();
-                for (int q = q0; q < q1; ++q) mc = compose(mc, Map{cm[q].d[k][0], cm[q].d[k][1]});
-                const int M = apply(m_of(v, R), mc);
-                if (M >= R.mlim) break;
-                const float nv = val_of(M, R);
-                if (r <= nv) break;
-                v = nv;
+    int q = 0, found = -1;
+    while (q < nsub && found < 0) {
+        // sub-chunks q .. q + 63 in the current binade
+        {
+            const Reg R = reg_of(v);
+            const int M0 = m_of(v, R), qi = q + lane;
+            Map m = map_id();
+            if (qi < nsub) {
+                const SubMaps &c = cm[qi];
+                const int k = c.reg[0] == R.id ? 0 : (c.reg[1] == R.id ? 1 : -1);
+                m = k < 0 ? Map{kCap, kCap} : Map{c.d[k][0], c.d[k][1]};
             }
-            sh_c = c;
-            sh_v = v;
+            const int Me = apply(M0, wave_scan(m));
+            const bool stop = qi < nsub && (Me >= R.mlim || r <= val_of(Me, R));
+            const unsigned long long bal = __ballot(stop);
+            if (bal == 0) {
+                const int last = min(kWave, nsub - q) - 1;
+                v = val_of(__shfl(Me, last, kWave), R);
+                q += kWave;
+                continue;
+            }
+            const int s = first_lane(bal);
+            const int Mprev = __shfl(Me, s > 0 ? s - 1 : 0, kWave);
+            if (s > 0) v = val_of(Mprev, R);
+            q += s;
         }
-        __syncthreads();
-        c = sh_c;
-        v = sh_v;
-        if (c >= nch) break;
-        // chunk c element by element: stage its elements
-        const int base = c * kChunk, cnt = min(kChunk, n - base);
-        for (int k = tid; k < cnt; k += kThreads) vals[k] = chain_elem(wr[base + k], chain, ri.sum);
-        __syncthreads();
-        int pos = 0;
-        while (pos < cnt) {
-            if (tid == 0) {
-                const int e = min(cnt, pos + kGallop);
-                for (; pos < e; ++pos) {
-                    v = __fadd_rn(v, __uint_as_float(vals[pos]));
-                    if (r <= v) {
-                        found = base + pos;
-                        break;
-                    }
-                }
-                sh_v = v;
-                sh_pos = pos;
-                sh_found = found;
-                sh_first = kThreads;
-            }
-            __syncthreads();
-            v = sh_v;
-            pos = sh_pos;
-            found = sh_found;
-            if (found >= 0 || pos >= cnt) break;
-            // the rest of the chunk in runs of kRun: the first run where the binade changes
-            // or r is reached
+        // sub-chunk q element by element: lane l holds elements base + 16 l .. + 15
+        const int base = q * kSub, e0 = base + lane * kRun;
+        uint32_t x[kRun];
+#pragma unroll
+        for (int j = 0; j < kRun; ++j) {
+            const int i = e0 + j;
+            x[j] = i < n ? chain_elem(wr[i], chain, ri.sum) : 0u;
+        }
+        const int nval = max(0, min(kRun, n - e0));   // this lane's elements
+        int from = 0;                                  // the first lane not yet added
+        while (from < kWave) {
             const Reg R = reg_of(v);
             const int M0 = m_of(v, R);
-            const int rs = pos + tid * kRun, re = min(cnt, rs + kRun);
             Map m = map_id();
-            for (int k = rs; k < re; ++k) m = compose(m, elem_map(vals[k], R));
-            // inclusive scan of the maps in thread order
-            const int lane = tid & (kWave - 1);
+            if (lane >= from)
 #pragma unroll
-            for (int off = 1; off < kWave; off <<= 1) {
-                Map o;
-                o.d0 = __shfl_up(m.d0, off, kWave);
-                o.d1 = __shfl_up(m.d1, off, kWave);
-                if (lane >= off) m = compose(o, m);
-            }
-            // the chain after this thread's run: M0 through the earlier waves, then this prefix
-            if (lane == kWave - 1) wtot[tid / kWave] = m;
-            __syncthreads();
-            Map pre = map_id();
-            for (int k = 0; k < tid / kWave; ++k) pre = compose(pre, wtot[k]);
-            const int Me = apply(apply(M0, pre), m);
-            mend[tid] = Me;
-            if (rs < cnt && (Me >= R.mlim || r <= val_of(Me, R))) atomicMin(&sh_first, tid);
-            __syncthreads();
-            const int first = sh_first;
-            if (first == kThreads) {                      // the whole rest stays in the binade
-                const int last = (cnt - 1 - pos) / kRun;
-                v = val_of(mend[last], R);
-                pos = cnt;
-                __syncthreads();
+                for (int j = 0; j < kRun; ++j)
+                    if (j < nval) m = compose(m, elem_map(x[j], R));
+            const int Me = apply(M0, wave_scan(m));
+            const bool stop = lane >= from && nval > 0 && (Me >= R.mlim || r <= val_of(Me, R));
+            const unsigned long long bal = __ballot(stop);
+            if (bal == 0) {                            // the rest of the sub-chunk stays in the binade
+                const unsigned long long has = __ballot(nval > 0);
+                const int last = has ? 63 - __builtin_clzll(has) : -1;
+                if (last >= from) v = val_of(__shfl(Me, last, kWave), R);
                 break;
             }
-            if (tid == first) {
-                float vv = first ? val_of(mend[first - 1], R) : v;
-                int k = rs;
-                for (; k < re; ++k) {
-                    vv = __fadd_rn(vv, __uint_as_float(vals[k]));
-                    if (r <= vv) {
-                        found = base + k;
-                        break;
+            const int s = first_lane(bal);
+            const int Mprev = __shfl(Me, s > 0 ? s - 1 : 0, kWave);
+            float vv = s > from ? val_of(Mprev, R) : v;
+            int fnd = -1;
+            if (lane == s) {
+#pragma unroll
+                for (int j = 0; j < kRun; ++j)
+                    if (j < nval && fnd < 0) {
+                        vv = __fadd_rn(vv, __uint_as_float(x[j]));
+                        if (r <= vv) fnd = e0 + j;
                     }
-                }
-                sh_v = vv;
-                sh_pos = re;
-                sh_found = found;
             }
-            __syncthreads();
-            v = sh_v;
-            pos = sh_pos;
-            found = sh_found;
-            __syncthreads();
-            if (found >= 0) break;
+            v = __shfl(vv, s, kWave);
+            fnd = __shfl(fnd, s, kWave);
+            if (fnd >= 0) {
+                found = fnd;
+                break;
+            }
+            from = s + 1;
         }
-        if (found >= 0) break;
-        ++c;
-        __syncthreads();
+        ++q;
     }
-    if (tid == 0) {
+    if (lane == 0) {
         if (chain) tokens[b] = found >= 0 ? found : n - 1;
         else rows[b].sum = v;
     }
@@ -548,12 +533,12 @@ int launch_sample(const float *logits, int n, int batch, size_t ld, float temper
     if (!hip_ok(hipGetLastError(), "sample weights launch")) return -1;
     hipLaunchKernelGGL(smp_maps, grid, dim3(kThreads), 0, s, w, n, ldw, 0, stats, rows, maps0);
     if (!hip_ok(hipGetLastError(), "sample maps launch")) return -1;
-    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 0, nsub, maps0, rows, draws, d_step,
+    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kWave), 0, s, w, n, ldw, 0, nsub, maps0, rows, draws, d_step,
                        batch, tokens);
     if (!hip_ok(hipGetLastError(), "sample sum walk launch")) return -1;
     hipLaunchKernelGGL(smp_maps, grid, dim3(kThreads), 0, s, w, n, ldw, 1, stats, rows, maps1);
     if (!hip_ok(hipGetLastError(), "sample maps launch")) return -1;
-    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kThreads), 0, s, w, n, ldw, 1, nsub, maps1, rows, draws, d_step,
+    hipLaunchKernelGGL(smp_walk, dim3(batch), dim3(kWave), 0, s, w, n, ldw, 1, nsub, maps1, rows, draws, d_step,
                        batch, tokens);
     return hip_ok(hipGetLastError(), "sample draw walk launch") ? 0 : -1;
 }
