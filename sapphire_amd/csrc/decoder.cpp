@@ -422,12 +422,12 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         qi.w_norm = L.n_attn;
         qi.eps = c.eps;
         if (l > 0) {
-            // the previous down projection's K-chunk partial sums, added once by a short kernel
-            // (cheaper than every staging workgroup adding them)
-            if (launch_sum_parts(r.dparts, nsd, (size_t)B * H, B, H, r.dout, H, s) != 0) return -1;
-            qi.parts = r.dout;
-            qi.nparts = 1;
+            // the previous down projection's K-chunk partial sums, added in chunk order by the
+            // GEMM's input pass
+            qi.parts = r.dparts;
+            qi.nparts = nsd;
             qi.ldp = H;
+            qi.part_stride = (size_t)B * H;
             qi.w_delta = d->layers[l - 1].n_ffn_post;
             qi.resid_out = r.resid[1 - cur];
             qi.ldr = H;
@@ -525,8 +525,8 @@ int enqueue_step_batch(sapphire_decoder *d) {
     const int cur = enqueue_layers_batch(d, r);
     if (cur < 0) return -1;
     // last finalize + final norm (transformer.c:400-406), LM head, greedy tokens
-    if (launch_sum_parts(d->dparts, nsd, (size_t)B * H, B, H, d->dout, H, s) != 0) return -1;
     if (c.lm_dtype == DT_BF16) {
+        if (launch_sum_parts(d->dparts, nsd, (size_t)B * H, B, H, d->dout, H, s) != 0) return -1;
         // weight tying: the embedding table times the final norms, on the matrix cores
         GemvIn fin;
         fin.resid_in = d->resid[cur];
@@ -544,9 +544,10 @@ int enqueue_step_batch(sapphire_decoder *d) {
     GemmIn li;
     li.x = d->resid[cur];
     li.ldx = H;
-    li.parts = d->dout;
-    li.nparts = 1;
+    li.parts = d->dparts;
+    li.nparts = nsd;
     li.ldp = H;
+    li.part_stride = (size_t)B * H;
     li.w_delta = d->layers[c.n_layers - 1].n_ffn_post;
     li.w_norm = d->norm_final;
     li.eps = c.eps;

@@ -226,12 +226,169 @@ __device__ float chunk_fold(const NfChunk &c, const uint8_t *__restrict__ wq, co
     return a;
 }
 
+// The staged operands of one K chunk, formed once per GEMM by gemm_prep_kernel instead of in
+// every workgroup: the LDS image of the A operands [block][hi/lo][lane 16m + seq], and per
+// sequence the range scale and the non-finite record (1 in nf when the sequence has a NaN or
+// infinite activation in this chunk).
+struct PrepChunk {
+    h8 a[kChunkBlocks * 2 * kWave];
+    float xsc[kBatchMax];
+    uint32_t inf[kBatchMax][2][kChunkBlocks];
+    int nan[kBatchMax];
+    int nf[kBatchMax];
+};
+
+constexpr int kPrepThreads = 256;
+constexpr int kPrepParts = 8;                  // partial sums in flight per prep thread
+static_assert(kPrepThreads >= kChunkBlocks * 4, "one (block, quarter) pair per prep thread");
+
+// grid (sequences, K chunks): the input transform of the staging below for one sequence and
+// chunk, with the same arithmetic (so the operands are bit-identical): the delta's sum of
+// parts and rmsnorm_delta, the residual, the pre-norm, the range scale over the finite values,
+// the non-finite record, the hi / lo fp16 split. Thread t takes pair t (8 activations).
+template <int DT>
+__global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int K, int cb, PrepChunk *prep) {
+    __shared__ float raw[kRawLd];
+    __shared__ float npart[kBatchMax][8];
+    __shared__ float rinv[kBatchMax];
+    __shared__ float wmx[kPrepThreads / kWave];
+    __shared__ int wflag[kPrepThreads / kWave];
+    const int seq = blockIdx.x, chunk = blockIdx.y, p = threadIdx.x;
+    const int lane = p & (kWave - 1), wid = p / kWave;
+    const int nb = K / kBlock, b0 = chunk * cb, b1 = min(nb, b0 + cb);
+    const int pairs = (b1 - b0) * 4, kb = b0 * kBlock;
+    const bool on = p < pairs;
+    PrepChunk &pc = prep[chunk];
+    float v[8], xv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = xv[e] = 0.f;
+    if (on) {
+        const int k = kb + p * 8;
+        if (in.x) load8(in.x + (size_t)seq * in.ldx + k, in.parts ? xv : v);
+        if (in.parts) load8(in.parts + (size_t)seq * in.ldp + k, v);
+    }
+    if (in.parts) {
+        // every partial's loads go out before the sum (in chunk order) uses them
+        for (int c0 = 1; c0 < in.nparts; c0 += kPrepParts) {
+            float t[kPrepParts][8];
+#pragma unroll
+            for (int c = 0; c < kPrepParts; ++c)
+                if (on && c0 + c < in.nparts) load8(in.parts + (c0 + c) * in.part_stride + (size_t)seq * in.ldp + kb + p * 8, t[c]);
+#pragma unroll
+            for (int c = 0; c < kPrepParts; ++c)
+                if (on && c0 + c < in.nparts)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = __fadd_rn(v[e], t[c][e]);
+        }
+        if (in.w_delta) {
+            if (on)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) raw[p * 8 + e] = v[e];
+            __syncthreads();
+            rows_rms_inv(raw, kRawLd, K, 1, in.eps, npart, rinv);
+            const float r = rinv[0];
+            if (on) {
+                float w[8];
+                load8(in.w_delta + kb + p * 8, w);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, w[e]));
+            }
+        }
+        if (in.x)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __fadd_rn(xv[e], v[e]);
+    }
+    if (in.resid_out && on) {
+        float4 *dst = reinterpret_cast<float4 *>(in.resid_out + (size_t)seq * in.ldr + kb + p * 8);
+        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (in.w_norm) {
+        __syncthreads();                               // raw may still be read by the delta norm
+        if (on)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) raw[p * 8 + e] = v[e];
+        __syncthreads();
+        rows_rms_inv(raw, kRawLd, K, 1, in.eps, npart, rinv);
+        const float r = rinv[0];
+        if (on) {
+            float w[8];
+            load8(in.w_norm + kb + p * 8, w);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, w[e]));
+        }
+    }
+    // non-finite activations recorded and zeroed, the range over the rest
+    bool nan = false;
+    uint32_t pinf = 0, ninf = 0;
+    float mx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float t = v[e];
+        nan |= t != t;
+        pinf |= (t == INFINITY ? 1u : 0u) << e;
+        ninf |= (t == -INFINITY ? 1u : 0u) << e;
+        v[e] = nonfinite::is_nf(t) ? 0.f : t;
+        mx = fmaxf(mx, fabsf(v[e]));
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    const bool wnan = __any(nan) != 0, wnf = __any(nan || pinf != 0 || ninf != 0) != 0;
+    if (lane == 0) {
+        wmx[wid] = mx;
+        wflag[wid] = (wnan ? 1 : 0) | (wnf ? 2 : 0);
+    }
+    // the four pairs of a block sit in threads 4 bl .. 4 bl + 3
+    pinf <<= 8 * (p & 3);
+    ninf <<= 8 * (p & 3);
+    pinf |= __shfl_xor(pinf, 1, kWave);
+    ninf |= __shfl_xor(ninf, 1, kWave);
+    pinf |= __shfl_xor(pinf, 2, kWave);
+    ninf |= __shfl_xor(ninf, 2, kWave);
+    if (on && (p & 3) == 0) {
+        pc.inf[seq][0][p >> 2] = pinf;
+        pc.inf[seq][1][p >> 2] = ninf;
+    }
+    __syncthreads();
+    mx = 0.f;
+    int fl = 0;
+#pragma unroll
+    for (int w = 0; w < kPrepThreads / kWave; ++w) {
+        mx = fmaxf(mx, wmx[w]);
+        fl |= wflag[w];
+    }
+    int e = 0;
+    if (mx > 0.f) {
+        int ex;
+        frexpf(mx, &ex);
+        e = ex - 15;
+    }
+    if (p == 0) {
+        pc.xsc[seq] = ldexpf(1.0f, e);
+        pc.nan[seq] = fl & 1;
+        pc.nf[seq] = (fl >> 1) & 1;
+    }
+    if (on) {
+        h8 hv, lv;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float s = ldexpf(v[k_order<DT>(k)], -e) * k_factor<DT>(k);
+            const _Float16 h = (_Float16)s;
+            hv[k] = h;
+            lv[k] = (_Float16)(s - (float)h);
+        }
+        const int bl = p >> 2, m = p & 3;
+        pc.a[(bl * 2 + 0) * kWave + m * 16 + seq] = hv;
+        pc.a[(bl * 2 + 1) * kWave + m * 16 + seq] = lv;
+    }
+}
+
 // grid.x: workgroups over the tiles (grid-stride), grid.y: K chunks of `cb` blocks.
 // Four waves per SIMD (two workgroups per CU): at most 128 VGPRs.
-template <int DT>
+template <int DT, bool PREP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_mfma_kernel(
     const uint8_t *__restrict__ wq, uint32_t q_bytes, const uint8_t *__restrict__ wsc, uint32_t s_bytes, GemmIn in,
-    int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp) {
+    int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp, const PrepChunk *__restrict__ prep) {
     __shared__ h8 xs[kStageH8];
     __shared__ float wmax[kWaves][kBatchMax];
     __shared__ float xsc[kBatchMax];
@@ -260,9 +417,58 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // and outside them the fp16 exponent of 1024, inside them the bits that undo nib ^ 8
     BConst bk = {0x000F000Fu, 0x00F000F0u, 0x64086408u, 0x64806480u};
     asm volatile("" : "+v"(bk.lo_mask), "+v"(bk.hi_mask), "+v"(bk.lo_bits), "+v"(bk.hi_bits));
+    // ---- the first kRing-1 units' weight loads ----
+    Unit ring[kRing];
+    // issue pointer: group offset (tile * G + g) of unit u + kRing - 1; loads past the last
+    // unit repeat it. The offset goes in the scalar offset field, which the buffer range
+    // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
+    int igb = (idle ? 0 : t0) * G + g0, ig = 0, issued = 0;
+    auto prime = [&]() {
+#pragma unroll
+        for (int p = 0; p < kRing - 1; ++p) {
+            unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
+            if (issued < U - 1) {
+                ++issued;
+                if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
+            }
+        }
+    };
     // ---- stage the chunk: input transform, range scale per sequence, hi/lo operands ----
-    bool any_nf;                                       // a NaN / inf activation in this chunk
-    {
+    bool any_nf = false;                               // a NaN / inf activation in this chunk
+    if constexpr (PREP) {
+        // formed by gemm_prep_kernel: copy the chunk's operands (sequences past the batch
+        // zero). The weight loads go out first: they do not wait for the operands.
+        prime();
+        const PrepChunk &pc = prep[blockIdx.y];
+        const int na = (b1 - b0) * 2 * kWave;
+        constexpr int kCopy = (kChunkBlocks * 2 * kWave + kThreads - 1) / kThreads;
+        h8 val[kCopy];
+#pragma unroll
+        for (int j = 0; j < kCopy; ++j) {             // all loads first
+            const int i = tid + j * kThreads;
+            val[j] = i < na ? pc.a[i] : h8{};
+        }
+#pragma unroll
+        for (int j = 0; j < kCopy; ++j) {
+            const int i = tid + j * kThreads;
+            if (i < na) xs[i] = (i & 15) < batch ? val[j] : h8{};
+        }
+        if (tid < kBatchMax) xsc[tid] = tid < batch ? pc.xsc[tid] : 1.0f;
+        for (int q = 0; q < batch; ++q) any_nf |= pc.nf[q] != 0;
+        if (any_nf) {
+            const int nbl = b1 - b0;
+            for (int i = tid; i < batch * 2 * nbl; i += kThreads) {
+                const int q = i / (2 * nbl), sg = (i / nbl) & 1, bl = i % nbl;
+                nfc.inf[q][sg][bl] = pc.inf[q][sg][bl];
+            }
+            if (tid == 0) {
+                uint32_t bits = 0;
+                for (int q = 0; q < batch; ++q) bits |= (pc.nan[q] ? 1u : 0u) << q;
+                nfc.nan = bits;
+            }
+        }
+        __syncthreads();
+    } else {
         const int seq = tid & (kBatchMax - 1), q = tid / kBatchMax;   // q: 0..31
         const int pairs = (b1 - b0) * 4;
         const int kb = b0 * kBlock;
@@ -443,20 +649,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         __syncthreads();
     }
 
-    // ---- the first kRing-1 units' weight loads ----
-    Unit ring[kRing];
-    // issue pointer: group offset (tile * G + g) of unit u + kRing - 1; loads past the last
-    // unit repeat it. The offset goes in the scalar offset field, which the buffer range
-    // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
-    int igb = (idle ? 0 : t0) * G + g0, ig = 0, issued = 0;
-#pragma unroll
-    for (int p = 0; p < kRing - 1; ++p) {
-        unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
-        if (issued < U - 1) {
-            ++issued;
-            if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
-        }
-    }
+    if constexpr (!PREP) prime();
     // ---- stream the tiles: units (tile, group) through the register ring ----
     float sc[4];
 #pragma unroll
@@ -551,11 +744,25 @@ void k_chunks(int K, int *nsplit, int *cb) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// One pass of at most 16 sequences.
+size_t partials_bytes(int M, int nsplit) { return nsplit > 1 ? (size_t)nsplit * kBatchMax * M * sizeof(float) : 0; }
+size_t prep_offset(int M, int nsplit) { return (partials_bytes(M, nsplit) + 255) & ~size_t(255); }
+size_t prep_stride() { return (sizeof(PrepChunk) + 255) & ~size_t(255); }
+
+// One pass of at most 16 sequences. With `prep` the input transform runs once per sequence
+// and chunk (gemm_prep_kernel, into the workspace) instead of in every workgroup.
 int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out, void *ws,
-              hipStream_t st) {
+              hipStream_t st, bool prep = false) {
     int nsplit = 1, cb = 0;
     k_chunks(K, &nsplit, &cb);
+    PrepChunk *pc = nullptr;
+    if (prep) {
+        pc = reinterpret_cast<PrepChunk *>(static_cast<char *>(ws) + prep_offset(M, nsplit));
+        if (dt == DT_Q4_0)
+            hipLaunchKernelGGL(gemm_prep_kernel<DT_Q4_0>, dim3(batch, nsplit), dim3(kPrepThreads), 0, st, in, K, cb, pc);
+        else
+            hipLaunchKernelGGL(gemm_prep_kernel<DT_Q8_0>, dim3(batch, nsplit), dim3(kPrepThreads), 0, st, in, K, cb, pc);
+        if (!hip_ok(hipGetLastError(), "gemm_prep launch")) return -1;
+    }
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     const size_t so = q_tiled_scales_offset(dt, M, K);
     const size_t sbytes = q_tiled_bytes(dt, M, K) - so;
@@ -565,12 +772,10 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
     const int gx = std::max(1, std::min({sets, (2 * cus() + nsplit - 1) / nsplit, kMaxGrid}));
     const dim3 grid((unsigned)gx, (unsigned)nsplit);
     float *Yp = static_cast<float *>(ws);
-    if (dt == DT_Q4_0)
-        hipLaunchKernelGGL(gemm_mfma_kernel<DT_Q4_0>, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so,
-                           (uint32_t)sbytes, in, batch, M, K, cb, out, Yp);
-    else
-        hipLaunchKernelGGL(gemm_mfma_kernel<DT_Q8_0>, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so,
-                           (uint32_t)sbytes, in, batch, M, K, cb, out, Yp);
+    const auto kern = dt == DT_Q4_0 ? (pc ? gemm_mfma_kernel<DT_Q4_0, true> : gemm_mfma_kernel<DT_Q4_0, false>)
+                                    : (pc ? gemm_mfma_kernel<DT_Q8_0, true> : gemm_mfma_kernel<DT_Q8_0, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so, (uint32_t)sbytes, in, batch, M,
+                       K, cb, out, Yp, (const PrepChunk *)pc);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
     if (nsplit > 1 && !out.parts) return launch_sum_parts(Yp, nsplit, (size_t)batch * M, batch, M, out.y, out.ldy, st);
     return 0;
@@ -586,7 +791,7 @@ int gemm_splits(int K) {
 
 size_t gemm_workspace_bytes(int M, int K) {
     const int nsplit = gemm_splits(K);
-    return 256 + (nsplit > 1 ? (size_t)nsplit * kBatchMax * M * sizeof(float) : 0);
+    return prep_offset(M, nsplit) + (size_t)nsplit * prep_stride();
 }
 
 int launch_sum_parts(const float *parts, int nparts, size_t stride, int batch, int M, float *y, int ldy,
@@ -615,7 +820,7 @@ int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const G
         set_error("batched GEMM: unsupported arguments (batch=%d M=%d K=%d nsplit=%d)", batch, M, K, nsplit);
         return -1;
     }
-    return gemm_pass(dt, w, M, K, batch, in, out, ws, st);
+    return gemm_pass(dt, w, M, K, batch, in, out, ws, st, ws != nullptr);
 }
 
 int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws,
