@@ -122,12 +122,36 @@ __global__ __launch_bounds__(kThreads) void dec_kv_write_kernel(AttnArgs a) {
     }
 }
 
+// p[0..DPL) as one vector load (p aligned to DPL floats).
+template <int DPL>
+struct Lanes {
+    float v[DPL];
+};
+template <int DPL>
+__device__ __forceinline__ Lanes<DPL> load_lanes(const float *p) {
+    Lanes<DPL> r;
+    if constexpr (DPL == 4) {
+        const float4 x = *reinterpret_cast<const float4 *>(p);
+        r.v[0] = x.x;
+        r.v[1] = x.y;
+        r.v[2] = x.z;
+        r.v[3] = x.w;
+    } else if constexpr (DPL == 2) {
+        const float2 x = *reinterpret_cast<const float2 *>(p);
+        r.v[0] = x.x;
+        r.v[1] = x.y;
+    } else {
+        r.v[0] = p[0];
+    }
+    return r;
+}
+
 // Workgroup b takes positions [t0, t1) of the layer's attention range; each wave walks
 // every fourth of them with a running (max, sum, weighted V) per head; the waves are then
 // merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL). Scores are
 // summed by DPP into wave-uniform values and the weights are powers of two of log2-scaled
-// scores (one exp2 each).
-template <int DPL, int NH>
+// scores (one exp2 each). NKV: the K/V heads (1 or 2, a.nkv).
+template <int DPL, int NH, int NKV>
 __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     {   // sequence blockIdx.y of a batch
         const size_t b = blockIdx.y;
@@ -146,44 +170,80 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     __shared__ float wo[kThreads / kWave][NH][kWave * DPL];
     __shared__ float wx[kThreads / kWave][NH];   // wave merge weights
     __shared__ float wmax[NH], wtot[NH];
-    const int hd = a.hd, nkv = a.nkv;
+    const int hd = a.hd, half = hd / 2;
+    constexpr int nkv = NKV;
+    // Loads that wait for nothing go out first: q | k | v as projected and the QK-norm gammas
+    // (thread t applies the norm and RoPE to pair i = t mod hd/2 of every head, the same i for
+    // every head as 256 is a multiple of hd/2).
+    constexpr int kRawRegs = (kAttnMaxQ + 2 * kAttnMaxKV) / kThreads;
+    const int nraw = (NH + 2 * nkv) * hd;
+    float rv[kRawRegs];
+#pragma unroll
+    for (int e = 0; e < kRawRegs; ++e) {
+        const int i = threadIdx.x + e * kThreads;
+        rv[e] = i < nraw ? a.qkv[i] : 0.f;
+    }
+    const int pi = threadIdx.x % half;
+    const float gq0 = a.qn[pi], gq1 = a.qn[pi + half], gk0 = a.kn[pi], gk1 = a.kn[pi + half];
     const int pos = *a.d_pos, seq = pos + 1;
+    const float rc = a.cos_t[(size_t)pos * hd + pi], rs = a.sin_t[(size_t)pos * hd + pi];
     const int start = (a.window > 0 && seq > a.window) ? seq - a.window : 0;
     const int len = seq - start, nsplit = gridDim.x;
     const int chunk = (len + nsplit - 1) / nsplit;
     const int t0 = start + blockIdx.x * chunk, t1 = min(seq, t0 + chunk);
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    const int group = NH / nkv;
+    constexpr int group = NH / NKV;
     // The wave's positions t0 + wid + 4j, PF at a time. The rows of the next batch are loaded
     // while the current one is used (two register sets). Rows come from the cache; the row of
     // the current position is taken from this kernel's own K (after RoPE) and V.
-    constexpr int PF = 4;
+    constexpr int PF = 8 / NKV;
     constexpr int NW = kThreads / kWave;
-    float kr[PF][2][DPL], vr[PF][2][DPL];   // up to two K/V heads per row
-    float nk[PF][2][DPL], nv[PF][2][DPL];   // the next batch
-    auto load_batch = [&](int tb, float(&K)[PF][2][DPL], float(&V)[PF][2][DPL]) {
+    float kr[PF][NKV][DPL], vr[PF][NKV][DPL];
+    float nk[PF][NKV][DPL], nv[PF][NKV][DPL];   // the next batch
+    // A row outside the slice (or the current position's) reads row 0 instead, in bounds, and
+    // is dropped: every row is one vector load per lane.
+    auto load_batch = [&](int tb, float(&K)[PF][NKV][DPL], float(&V)[PF][NKV][DPL]) {
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
             const int t = tb + j * NW;
 #pragma unroll
-            for (int hk = 0; hk < 2; ++hk) {
-                const bool ok = t < t1 && t != pos && hk < nkv;
-                const size_t off = ok ? ((size_t)hk * a.max_ctx + t) * hd : 0;
+            for (int hk = 0; hk < NKV; ++hk) {
+                const bool ok = t < t1 && t != pos;
+                const size_t off = (ok ? ((size_t)hk * a.max_ctx + t) * hd : 0) + lane * DPL;
+                const Lanes<DPL> kv = load_lanes<DPL>(a.kc + off);
+                const Lanes<DPL> vv = load_lanes<DPL>(a.vc + off);
 #pragma unroll
                 for (int d = 0; d < DPL; ++d) {
-                    K[j][hk][d] = ok ? a.kc[off + lane * DPL + d] : 0.f;
-                    V[j][hk][d] = ok ? a.vc[off + lane * DPL + d] : 0.f;
+                    K[j][hk][d] = ok ? kv.v[d] : 0.f;
+                    V[j][hk][d] = ok ? vv.v[d] : 0.f;
                 }
             }
         }
     };
     if (t0 + wid < t1) load_batch(t0 + wid, kr, vr);   // in flight during the prologue
 
-    for (int i = threadIdx.x; i < (NH + 2 * nkv) * hd; i += blockDim.x) raw[i] = a.qkv[i];
+#pragma unroll
+    for (int e = 0; e < kRawRegs; ++e) {
+        const int i = threadIdx.x + e * kThreads;
+        if (i < nraw) raw[i] = rv[e];
+    }
     __syncthreads();
-    const float *cs = a.cos_t + (size_t)pos * hd, *sn = a.sin_t + (size_t)pos * hd;
-    norm_rope_heads(raw, NH, hd, a.qn, cs, sn, a.eps, qs, part8, ss);
-    norm_rope_heads(raw + NH * hd, nkv, hd, a.kn, cs, sn, a.eps, ks, part8, ss);
+    // QK-norm and RoPE of the query heads and the K heads in one pass: per head the
+    // arithmetic of norm_rope_heads (the sums of squares of every head at once)
+    vectors_sum_sq(raw, NH + nkv, hd, part8, ss);
+    if (threadIdx.x < NH + nkv) ss[threadIdx.x] = rms_inv_of(ss[threadIdx.x], hd, a.eps);
+    __syncthreads();
+    for (int v = threadIdx.x / half; v < NH + nkv; v += kThreads / half) {
+        const bool isq = v < NH;
+        const float r = ss[v], g0 = isq ? gq0 : gk0, g1 = isq ? gq1 : gk1;
+        const float *p = raw + (size_t)v * hd;
+        const float x0 = __fmul_rn(__fmul_rn(p[pi], r), __fadd_rn(1.0f, g0));
+        const float x1 = __fmul_rn(__fmul_rn(p[pi + half], r), __fadd_rn(1.0f, g1));
+        float *dst = isq ? qs + v * hd : ks + (v - NH) * hd;
+        dst[pi] = __builtin_fmaf(x0, rc, -__fmul_rn(x1, rs));
+        dst[pi + half] = __builtin_fmaf(x1, rc, __fmul_rn(x0, rs));
+    }
+    __syncthreads();
     const float *vnew = raw + (NH + nkv) * hd;
     if (blockIdx.x == 0 && !a.kv_written)   // kv_cache_write_token: [head][pos][dim]
         for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) {
@@ -213,11 +273,11 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
             if (t >= t1) break;
             if (t == pos) {
 #pragma unroll
-                for (int hk = 0; hk < 2; ++hk)
+                for (int hk = 0; hk < NKV; ++hk)
 #pragma unroll
                     for (int d = 0; d < DPL; ++d) {
-                        kr[j][hk][d] = hk < nkv ? ks[hk * hd + lane * DPL + d] : 0.f;
-                        vr[j][hk][d] = hk < nkv ? vnew[hk * hd + lane * DPL + d] : 0.f;
+                        kr[j][hk][d] = ks[hk * hd + lane * DPL + d];
+                        vr[j][hk][d] = vnew[hk * hd + lane * DPL + d];
                     }
             }
 #pragma unroll
@@ -226,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
                 float dp = 0.f;
 #pragma unroll
                 for (int d = 0; d < DPL; ++d)
-                    dp = __builtin_fmaf(qs[h * hd + lane * DPL + d], hk == 0 ? kr[j][0][d] : kr[j][1][d], dp);
+                    dp = __builtin_fmaf(qs[h * hd + lane * DPL + d], kr[j][hk][d], dp);
                 const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
                 const float mn = fmaxf(m[h], score);
                 const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
@@ -234,7 +294,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
                 s[h] = __builtin_fmaf(s[h], c, p);
 #pragma unroll
                 for (int d = 0; d < DPL; ++d)
-                    o[h][d] = __builtin_fmaf(o[h][d], c, p * (hk == 0 ? vr[j][0][d] : vr[j][1][d]));
+                    o[h][d] = __builtin_fmaf(o[h][d], c, p * vr[j][hk][d]);
                 m[h] = mn;
             }
         }
@@ -242,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 #pragma unroll
             for (int j = 0; j < PF; ++j)
 #pragma unroll
-                for (int hk = 0; hk < 2; ++hk)
+                for (int hk = 0; hk < NKV; ++hk)
 #pragma unroll
                     for (int d = 0; d < DPL; ++d) {
                         kr[j][hk][d] = nk[j][hk][d];
@@ -290,36 +350,33 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 
 // out[h*hd + d] = sum_b e_b o_b[d] / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) (the
 // partials' maxima are in log2 units): the softmax-weighted sum of values of
-// attention.c:140-158 over all slices. One workgroup per head, one thread per dim.
+// attention.c:140-158 over all slices. One workgroup per head, one thread per dim. Every load
+// goes out at once: each wave forms the slice weights itself (lane b holds slice b's maximum
+// and sum), so no load waits for another.
 template <int NS>
 __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float *__restrict__ part, int nh, int hd,
                                                                     float *__restrict__ out, size_t out_stride) {
-    static_assert(NS <= kWave, "one lane of wave 0 per slice");
-    __shared__ float es[NS];
-    __shared__ float S;
-    const int h = blockIdx.x, t = threadIdx.x;
+    static_assert(NS <= kWave, "one lane per slice");
+    const int h = blockIdx.x, t = threadIdx.x, lane = t & (kWave - 1);
     part += (size_t)blockIdx.y * NS * nh * (hd + 2);   // sequence blockIdx.y
     out += (size_t)blockIdx.y * out_stride;
-    if (t < kWave) {
-        const float *p = part + ((size_t)t * nh + h) * (hd + 2);
-        const float mb = t < NS ? p[hd] : -INFINITY;
-        const float sb = t < NS ? p[hd + 1] : 0.f;
-        float M = mb;
+    const size_t hs = (size_t)nh * (hd + 2);             // stride between slices
+    const float *ph = part + (size_t)h * (hd + 2);
+    const float mb = lane < NS ? ph[lane * hs + hd] : -INFINITY;
+    const float sb = lane < NS ? ph[lane * hs + hd + 1] : 0.f;
+    float o[NS];
+    const int d = t;                                     // head_dim <= 256 = one dim per thread
 #pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
-        const float e = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
-        if (t < NS) es[t] = e;
-        const float tot = wave_sum(e * sb);
-        if (t == 0) S = tot;
-    }
-    __syncthreads();
-    const float inv = 1.0f / S;
-    for (int d = t; d < hd; d += blockDim.x) {
-        float O = 0.f;
-#pragma unroll 16
-        for (int b = 0; b < NS; ++b) O = __builtin_fmaf(part[((size_t)b * nh + h) * (hd + 2) + d], es[b], O);
-        out[h * hd + d] = O * inv;
-    }
+    for (int b = 0; b < NS; ++b) o[b] = d < hd ? ph[b * hs + d] : 0.f;
+    float M = mb;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
+    const float e = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
+    const float inv = 1.0f / wave_sum(e * sb);
+    float O = 0.f;
+#pragma unroll
+    for (int b = 0; b < NS; ++b) O = __builtin_fmaf(o[b], lane_value(e, b), O);
+    if (d < hd) out[h * hd + d] = O * inv;
 }
 
 __global__ void dec_embed_kernel(const uint16_t *__restrict__ embed, int hidden, int vocab, float es,
@@ -485,11 +542,12 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     // splits per sequence: enough workgroups in total, without cutting a sequence's positions
     // into slivers once a batch fills the GPU
     const int ns = a.batch >= 4 ? kAttnSplitBatch : kAttnSplit;
-#define SPH_ATTN(DPLV, NHV)                                                                                  \
-    if (dpl == DPLV && a.nh == NHV) {                                                                        \
-        hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV>), dim3(ns, a.batch), dim3(kThreads), 0, s, a);   \
+#define SPH_ATTN(DPLV, NHV, NKVV)                                                                              \
+    if (dpl == DPLV && a.nh == NHV && a.nkv == NKVV) {                                                         \
+        hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV, NKVV>), dim3(ns, a.batch), dim3(kThreads), 0, s, a); \
     } else
-    SPH_ATTN(1, 4) SPH_ATTN(2, 4) SPH_ATTN(4, 4) SPH_ATTN(1, 8) SPH_ATTN(2, 8) SPH_ATTN(4, 8) {
+    SPH_ATTN(1, 4, 1) SPH_ATTN(2, 4, 1) SPH_ATTN(4, 4, 1) SPH_ATTN(1, 8, 1) SPH_ATTN(2, 8, 1) SPH_ATTN(4, 8, 1)
+    SPH_ATTN(1, 4, 2) SPH_ATTN(2, 4, 2) SPH_ATTN(4, 4, 2) SPH_ATTN(1, 8, 2) SPH_ATTN(2, 8, 2) SPH_ATTN(4, 8, 2) {
         set_error("attention with %d heads of dim %d not instantiated", a.nh, a.hd);
         return -1;
     }

@@ -155,6 +155,7 @@ __device__ __forceinline__ void unit_mfma(const Unit &u, const h8 *__restrict__ 
 // Reference-order sums of squares of the staged rows (sum_sq_avx2, normalization.c:12-32:
 // eight strided chains, then ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)) and the tail), turned into
 // the rmsnorm factor 1/sqrtf(sum/dim + eps) of every sequence. raw: [seq][ld] fp32 in LDS.
+template <int U = 8>
 __device__ void rows_rms_inv(const float *raw, int ld, int dim, int batch, float eps, float (*part)[8], float *rinv) {
     const int t = threadIdx.x;
     if (t < kBatchMax * 8) {
@@ -164,12 +165,12 @@ __device__ void rows_rms_inv(const float *raw, int ld, int dim, int batch, float
             const float *r = raw + seq * ld + l;
             const int n8 = dim >> 3;
             int j = 0;
-            for (; j + 8 <= n8; j += 8) {   // eight loads in flight, then the chain
-                float x[8];
+            for (; j + U <= n8; j += U) {   // U loads in flight, then the chain
+                float x[U];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) x[u] = r[(j + u) * 8];
+                for (int u = 0; u < U; ++u) x[u] = r[(j + u) * 8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) s = __builtin_fmaf(x[u], x[u], s);
+                for (int u = 0; u < U; ++u) s = __builtin_fmaf(x[u], x[u], s);
             }
             for (; j < n8; ++j) s = __builtin_fmaf(r[j * 8], r[j * 8], s);
         }
@@ -259,13 +260,15 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
     const int pairs = (b1 - b0) * 4, kb = b0 * kBlock;
     const bool on = p < pairs;
     PrepChunk &pc = prep[chunk];
-    float v[8], xv[8];
+    float v[8], xv[8], wd[8], wn[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = xv[e] = 0.f;
-    if (on) {
+    for (int e = 0; e < 8; ++e) v[e] = xv[e] = wd[e] = wn[e] = 0.f;
+    if (on) {                                          // every independent load goes out first
         const int k = kb + p * 8;
         if (in.x) load8(in.x + (size_t)seq * in.ldx + k, in.parts ? xv : v);
         if (in.parts) load8(in.parts + (size_t)seq * in.ldp + k, v);
+        if (in.w_delta && in.parts) load8(in.w_delta + k, wd);
+        if (in.w_norm) load8(in.w_norm + k, wn);
     }
     if (in.parts) {
         // every partial's loads go out before the sum (in chunk order) uses them
@@ -285,14 +288,11 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
 #pragma unroll
                 for (int e = 0; e < 8; ++e) raw[p * 8 + e] = v[e];
             __syncthreads();
-            rows_rms_inv(raw, kRawLd, K, 1, in.eps, npart, rinv);
+            rows_rms_inv<36>(raw, kRawLd, K, 1, in.eps, npart, rinv);
             const float r = rinv[0];
-            if (on) {
-                float w[8];
-                load8(in.w_delta + kb + p * 8, w);
+            if (on)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, w[e]));
-            }
+                for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, wd[e]));
         }
         if (in.x)
 #pragma unroll
@@ -309,14 +309,11 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
 #pragma unroll
             for (int e = 0; e < 8; ++e) raw[p * 8 + e] = v[e];
         __syncthreads();
-        rows_rms_inv(raw, kRawLd, K, 1, in.eps, npart, rinv);
+        rows_rms_inv<36>(raw, kRawLd, K, 1, in.eps, npart, rinv);
         const float r = rinv[0];
-        if (on) {
-            float w[8];
-            load8(in.w_norm + kb + p * 8, w);
+        if (on)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, w[e]));
-        }
+            for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, wn[e]));
     }
     // non-finite activations recorded and zeroed, the range over the rest
     bool nan = false;
@@ -385,7 +382,11 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
 
 // grid.x: workgroups over the tiles (grid-stride), grid.y: K chunks of `cb` blocks.
 // Four waves per SIMD (two workgroups per CU): at most 128 VGPRs.
-template <int DT, bool PREP>
+// How a workgroup forms its A operands: the full input transform, a copy of the chunk that
+// gemm_prep_kernel formed, or a plain x (no sum of parts, norm or residual).
+enum StageMode { kStageFull = 0, kStagePrepared = 1, kStagePlain = 2 };
+
+template <int DT, int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_mfma_kernel(
     const uint8_t *__restrict__ wq, uint32_t q_bytes, const uint8_t *__restrict__ wsc, uint32_t s_bytes, GemmIn in,
     int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp, const PrepChunk *__restrict__ prep) {
@@ -435,16 +436,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     };
     // ---- stage the chunk: input transform, range scale per sequence, hi/lo operands ----
     bool any_nf = false;                               // a NaN / inf activation in this chunk
-    if constexpr (PREP) {
+    if constexpr (MODE == kStagePrepared) {
         // formed by gemm_prep_kernel: copy the chunk's operands (sequences past the batch
         // zero). The weight loads go out first: they do not wait for the operands.
         prime();
         const PrepChunk &pc = prep[blockIdx.y];
         const int na = (b1 - b0) * 2 * kWave;
         constexpr int kCopy = (kChunkBlocks * 2 * kWave + kThreads - 1) / kThreads;
+        // all loads first: the range scales and non-finite flags with the operands
+        const float sc = tid < batch ? pc.xsc[tid] : 1.0f;
+        const int nfv = tid < batch ? pc.nf[tid] : 0;
         h8 val[kCopy];
 #pragma unroll
-        for (int j = 0; j < kCopy; ++j) {             // all loads first
+        for (int j = 0; j < kCopy; ++j) {
             const int i = tid + j * kThreads;
             val[j] = i < na ? pc.a[i] : h8{};
         }
@@ -453,8 +457,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             const int i = tid + j * kThreads;
             if (i < na) xs[i] = (i & 15) < batch ? val[j] : h8{};
         }
-        if (tid < kBatchMax) xsc[tid] = tid < batch ? pc.xsc[tid] : 1.0f;
-        for (int q = 0; q < batch; ++q) any_nf |= pc.nf[q] != 0;
+        if (tid < kBatchMax) xsc[tid] = sc;
+        if (tid < kWave) {                             // the sequences sit in wave 0
+            const bool a = __any(nfv != 0) != 0;
+            if (tid == 0) wnf[0] = a;
+        }
+        __syncthreads();
+        any_nf = wnf[0] != 0;
         if (any_nf) {
             const int nbl = b1 - b0;
             for (int i = tid; i < batch * 2 * nbl; i += kThreads) {
@@ -466,9 +475,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 for (int q = 0; q < batch; ++q) bits |= (pc.nan[q] ? 1u : 0u) << q;
                 nfc.nan = bits;
             }
+            __syncthreads();
         }
-        __syncthreads();
     } else {
+        constexpr bool plain = MODE == kStagePlain;
+        // the weights do not wait for x either (Q8_0's larger units do not fit beside it)
+        if constexpr (plain && DT == DT_Q4_0) prime();
         const int seq = tid & (kBatchMax - 1), q = tid / kBatchMax;   // q: 0..31
         const int pairs = (b1 - b0) * 4;
         const int kb = b0 * kBlock;
@@ -483,11 +495,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             for (int e = 0; e < 8; ++e) v[i][e] = xv[i][e] = 0.f;
             if (p < pairs && seq < batch) {
                 const int k = kb + p * 8;
-                if (in.x) load8(in.x + (size_t)seq * in.ldx + k, in.parts ? xv[i] : v[i]);
-                if (in.parts) load8(in.parts + (size_t)seq * in.ldp + k, v[i]);
+                if (in.x) load8(in.x + (size_t)seq * in.ldx + k, !plain && in.parts ? xv[i] : v[i]);
+                if (!plain && in.parts) load8(in.parts + (size_t)seq * in.ldp + k, v[i]);
             }
         }
-        if (in.parts) {
+        if (!plain && in.parts) {
             for (int c = 1; c < in.nparts; ++c)
 #pragma unroll
                 for (int i = 0; i < kStagePairs; ++i) {
@@ -527,7 +539,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
                     for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(xv[i][e], v[i][e]);
         }
-        if (in.resid_out && blockIdx.x == 0 && blockIdx.y == 0)
+        if (!plain && in.resid_out && blockIdx.x == 0 && blockIdx.y == 0)
 #pragma unroll
             for (int i = 0; i < kStagePairs; ++i) {
                 const int p = q + i * (kThreads / kBatchMax);
@@ -537,7 +549,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                     dst[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
                 }
             }
-        if (in.w_norm) {
+        if (!plain && in.w_norm) {
             __syncthreads();                           // raw may still be read by the delta norm
 #pragma unroll
             for (int i = 0; i < kStagePairs; ++i) {
@@ -649,7 +661,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         __syncthreads();
     }
 
-    if constexpr (!PREP) prime();
+    if constexpr (MODE == kStageFull || (MODE == kStagePlain && DT != DT_Q4_0)) prime();
     // ---- stream the tiles: units (tile, group) through the register ring ----
     float sc[4];
 #pragma unroll
@@ -772,8 +784,14 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
     const int gx = std::max(1, std::min({sets, (2 * cus() + nsplit - 1) / nsplit, kMaxGrid}));
     const dim3 grid((unsigned)gx, (unsigned)nsplit);
     float *Yp = static_cast<float *>(ws);
-    const auto kern = dt == DT_Q4_0 ? (pc ? gemm_mfma_kernel<DT_Q4_0, true> : gemm_mfma_kernel<DT_Q4_0, false>)
-                                    : (pc ? gemm_mfma_kernel<DT_Q8_0, true> : gemm_mfma_kernel<DT_Q8_0, false>);
+    const int mode = pc ? kStagePrepared
+                        : (!in.parts && !in.w_delta && !in.w_norm && !in.resid_out) ? kStagePlain : kStageFull;
+    const auto kern = dt == DT_Q4_0 ? (mode == kStagePrepared ? gemm_mfma_kernel<DT_Q4_0, kStagePrepared>
+                                       : mode == kStagePlain  ? gemm_mfma_kernel<DT_Q4_0, kStagePlain>
+                                                              : gemm_mfma_kernel<DT_Q4_0, kStageFull>)
+                                    : (mode == kStagePrepared ? gemm_mfma_kernel<DT_Q8_0, kStagePrepared>
+                                       : mode == kStagePlain  ? gemm_mfma_kernel<DT_Q8_0, kStagePlain>
+                                                              : gemm_mfma_kernel<DT_Q8_0, kStageFull>);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so, (uint32_t)sbytes, in, batch, M,
                        K, cb, out, Yp, (const PrepChunk *)pc);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
@@ -820,7 +838,9 @@ int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const G
         set_error("batched GEMM: unsupported arguments (batch=%d M=%d K=%d nsplit=%d)", batch, M, K, nsplit);
         return -1;
     }
-    return gemm_pass(dt, w, M, K, batch, in, out, ws, st, ws != nullptr);
+    // inputs with a sum of parts or a norm are prepared once; a plain x is staged by every
+    // workgroup (a copy costs about what the prep launch would)
+    return gemm_pass(dt, w, M, K, batch, in, out, ws, st, ws != nullptr && (norms || in.parts));
 }
 
 int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int batch, float *Y, void *ws,

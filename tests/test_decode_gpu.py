@@ -34,6 +34,9 @@ def _compare(ref_toks, ref_logits, got_toks, got_logits):
 MID = smodel.DecodeConfig(n_layers=6, hidden=256, n_heads=4, n_kv_heads=1, head_dim=128, ffn=512, vocab=8192,
                           max_ctx=160, sliding_window=48, global_layers=(5,))
 TINY_Q8 = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "wdtype": synth.Q8_0, "lm_dtype": synth.Q8_0})
+# two K/V heads shared by two query heads each (grouped-query attention, attention.c:131-135)
+GQA2 = smodel.DecodeConfig(n_layers=3, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=4096,
+                           max_ctx=96, sliding_window=24, global_layers=(2,))
 # the reference's own LM head: the BF16 embedding table (weight tying, transformer.c:393-408)
 TINY_TIED = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF16})
 
@@ -51,8 +54,9 @@ TINY_TIED = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF1
     (MID, 33, 40, 24, 96),
     (TINY_TIED, 37, 40, 12, None),
     (TINY_TIED, 37, 40, 12, 0),
+    (GQA2, 41, 40, 12, 0),                # two K/V heads (multi-launch step only)
 ], ids=["tiny", "tiny_graph", "tiny_g16", "tiny_g256", "tiny_q8", "tiny_q8_graph", "mid_window", "mid_window_graph",
-        "mid_window_g96", "tiny_tied_bf16", "tiny_tied_bf16_graph"])
+        "mid_window_g96", "tiny_tied_bf16", "tiny_tied_bf16_graph", "gqa2_graph"])
 def test_decode_matches_oracle(oracle, cfg, seed, prefill, steps, groups):
     from sapphire_amd.engine import Decoder
     print(f"decode cfg={cfg.n_layers}x{cfg.hidden} seed={seed} prefill={prefill} steps={steps} groups={groups}",
