@@ -389,7 +389,7 @@ enum StageMode { kStageFull = 0, kStagePrepared = 1, kStagePlain = 2 };
 template <int DT, int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_mfma_kernel(
     const uint8_t *__restrict__ wq, uint32_t q_bytes, const uint8_t *__restrict__ wsc, uint32_t s_bytes, GemmIn in,
-    int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp, const PrepChunk *__restrict__ prep) {
+    int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp, const PrepChunk *__restrict__ prep, int ks) {
     __shared__ h8 xs[kStageH8];
     __shared__ float wmax[kWaves][kBatchMax];
     __shared__ float xsc[kBatchMax];
@@ -407,10 +407,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int n = lane & 15, m = lane >> 4;
     const int ntiles = (M + kTileRows - 1) / kTileRows;
     const int g0 = b0 / kGroupBlocks, gc = (b1 - b0) / kGroupBlocks;
-    const int tstride = gridDim.x * kWaves;
-    const int t0 = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(wid);
+    // ks waves share a tile (ks <= gc, and then every wave has at most one tile): wave `part`
+    // of tile slot `slot` takes groups gs .. gs + gcw - 1 of the chunk
+    const int wu = __builtin_amdgcn_readfirstlane(wid);
+    const int slot = wu / ks, part = wu - slot * ks;
+    const int gs = part * gc / ks, gcw = (part + 1) * gc / ks - gs;
+    const int tstride = gridDim.x * (kWaves / ks);
+    const int t0 = blockIdx.x * (kWaves / ks) + slot;
     const bool idle = t0 >= ntiles;           // no tile: stages, then leaves
-    const int U = idle ? 0 : (ntiles - t0 + tstride - 1) / tstride * gc;   // units of this wave
+    const int U = idle ? 0 : (ntiles - t0 + tstride - 1) / tstride * gcw;   // units of this wave
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(wq, q_bytes);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(wsc, s_bytes);
 
@@ -423,14 +428,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // issue pointer: group offset (tile * G + g) of unit u + kRing - 1; loads past the last
     // unit repeat it. The offset goes in the scalar offset field, which the buffer range
     // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
-    int igb = (idle ? 0 : t0) * G + g0, ig = 0, issued = 0;
+    int igb = idle ? g0 : t0 * G + g0 + gs, ig = 0, issued = 0;
     auto prime = [&]() {
 #pragma unroll
         for (int p = 0; p < kRing - 1; ++p) {
             unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
             if (issued < U - 1) {
                 ++issued;
-                if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
+                if (++ig == gcw) { ig = 0; igb += tstride * G - (gcw - 1); } else { ++igb; }
             }
         }
     };
@@ -676,6 +681,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         dst = Yp + (size_t)blockIdx.y * batch * M;
         ldd = M;
     }
+    // the results of tile ct: rows (or GeGLU pairs) times the range scales, plus the non-finite fold
+    auto store_tile = [&](int ct, const f4 &a) {
+        if (out.geglu) {
+            // lanes n < 8 hold gate rows 8t'+n, lanes n + 8 the matching up rows
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float val = a[r] * sc[r];
+                if (any_nf && 4 * m + r < batch)
+                    val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, ct * kTileRows + n, 4 * m + r);
+                const float up = __shfl_xor(val, 8, kWave);
+                const int j = ct * 8 + n;
+                if (n < 8 && 4 * m + r < batch && 2 * j < M)
+                    dst[(size_t)(4 * m + r) * ldd + j] = __fmul_rn(devmath::gelu_ref(val), up);
+            }
+        } else {
+            const int row = ct * kTileRows + n;
+            if (row < M)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (4 * m + r < batch) {
+                        float val = a[r] * sc[r];
+                        if (any_nf) val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, row, 4 * m + r);
+                        dst[(size_t)(4 * m + r) * ldd + row] = val;
+                    }
+        }
+    };
     int ct = t0, cg = 0;                               // tile and group of the unit multiplied
     f4 acc = {0.f, 0.f, 0.f, 0.f};
     // Every pass issues the loads of all kRing slots (past the last unit they repeat it), so
@@ -688,39 +719,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             unit_issue<DT>(ring[(p + kRing - 1) % kRing], rq, rs, (uint32_t)igb, lane, n);
             if (issued < U - 1) {
                 ++issued;
-                if (++ig == gc) { ig = 0; igb += tstride * G - (gc - 1); } else { ++igb; }
+                if (++ig == gcw) { ig = 0; igb += tstride * G - (gcw - 1); } else { ++igb; }
             }
             if (base + p < U) {
-                unit_mfma<DT>(ring[p], xs, cg * kGroupBlocks, lane, acc, bk);
-                if (++cg == gc) {
-                    if (out.geglu) {
-                        // lanes n < 8 hold gate rows 8t'+n, lanes n + 8 the matching up rows
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            float val = acc[r] * sc[r];
-                            if (any_nf && 4 * m + r < batch)
-                                val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, ct * kTileRows + n, 4 * m + r);
-                            const float up = __shfl_xor(val, 8, kWave);
-                            const int j = ct * 8 + n;
-                            if (n < 8 && 4 * m + r < batch && 2 * j < M)
-                                dst[(size_t)(4 * m + r) * ldd + j] = __fmul_rn(devmath::gelu_ref(val), up);
-                        }
-                    } else {
-                        const int row = ct * kTileRows + n;
-                        if (row < M)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                if (4 * m + r < batch) {
-                                    float val = acc[r] * sc[r];
-                                    if (any_nf) val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, row, 4 * m + r);
-                                    dst[(size_t)(4 * m + r) * ldd + row] = val;
-                                }
-                    }
+                unit_mfma<DT>(ring[p], xs, (gs + cg) * kGroupBlocks, lane, acc, bk);
+                if (++cg == gcw && ks == 1) {
+                    store_tile(ct, acc);
                     acc = f4{0.f, 0.f, 0.f, 0.f};
                     cg = 0;
                     ct += tstride;
                 }
             }
+        }
+    }
+    if (ks > 1) {
+        // the tile's share sums, in part order, through LDS (the operands are no longer read)
+        __syncthreads();
+        f4 *red = reinterpret_cast<f4 *>(xs);
+        if (part > 0 && !idle) red[(slot * (ks - 1) + part - 1) * kWave + lane] = acc;
+        __syncthreads();
+        if (part == 0 && !idle) {
+            for (int q = 1; q < ks; ++q) acc += red[(slot * (ks - 1) + q - 1) * kWave + lane];
+            store_tile(t0, acc);
         }
     }
 }
@@ -779,9 +799,19 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
     const size_t so = q_tiled_scales_offset(dt, M, K);
     const size_t sbytes = q_tiled_bytes(dt, M, K) - so;
     const int ntiles = (M + kTileRows - 1) / kTileRows;
-    const int sets = (ntiles + kWaves - 1) / kWaves;
+    // Waves per tile: a tile's groups are split over ks waves when then every wave still has
+    // at most one tile and the launch fits on the CUs once (the layer shapes of a decode
+    // step); a streaming launch (the LM head) keeps one wave per tile.
+    const int nb = K / kBlock, min_gc = (nb - (nsplit - 1) * cb) / kGroupBlocks;   // the last chunk's groups
+    int ks = 1;
+    for (int k : {4, 2})
+        if (k <= min_gc && (ntiles * k + kWaves - 1) / kWaves * nsplit <= cus()) {
+            ks = k;
+            break;
+        }
+    const int sets = (ntiles * ks + kWaves - 1) / kWaves;
     // two 72 KiB workgroups per CU
-    const int gx = std::max(1, std::min({sets, (2 * cus() + nsplit - 1) / nsplit, kMaxGrid}));
+    const int gx = ks > 1 ? sets : std::max(1, std::min({sets, (2 * cus() + nsplit - 1) / nsplit, kMaxGrid}));
     const dim3 grid((unsigned)gx, (unsigned)nsplit);
     float *Yp = static_cast<float *>(ws);
     const int mode = pc ? kStagePrepared
@@ -793,7 +823,7 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
                                        : mode == kStagePlain  ? gemm_mfma_kernel<DT_Q8_0, kStagePlain>
                                                               : gemm_mfma_kernel<DT_Q8_0, kStageFull>);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so, (uint32_t)sbytes, in, batch, M,
-                       K, cb, out, Yp, (const PrepChunk *)pc);
+                       K, cb, out, Yp, (const PrepChunk *)pc, ks);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
     if (nsplit > 1 && !out.parts) return launch_sum_parts(Yp, nsplit, (size_t)batch * M, batch, M, out.y, out.ldy, st);
     return 0;
