@@ -264,14 +264,21 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 #pragma unroll
         for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
     }
+    float qr[NH][DPL];
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) qr[h][d] = qs[h * hd + lane * DPL + d];
+    // positions whose scores are formed together (independent wave sums), then one rescale per
+    // head: the running maximum moves to the largest score of the group
+    constexpr int SB = 32 / NH < PF ? 32 / NH : PF;
     for (int tb = t0 + wid; tb < t1; tb += PF * NW) {
         const int tn = tb + PF * NW;
         if (tn < t1) load_batch(tn, nk, nv);
+        const int nj = min(PF, (t1 - tb + NW - 1) / NW);      // positions of this batch in the slice
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const int t = tb + j * NW;
-            if (t >= t1) break;
-            if (t == pos) {
+        for (int j = 0; j < PF; ++j)
+            if (j < nj && tb + j * NW == pos) {
 #pragma unroll
                 for (int hk = 0; hk < NKV; ++hk)
 #pragma unroll
@@ -281,20 +288,38 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
                     }
             }
 #pragma unroll
+        for (int j0 = 0; j0 < PF; j0 += SB) {
+            if (j0 >= nj) break;
+            float sc[SB][NH];
+#pragma unroll
+            for (int jj = 0; jj < SB; ++jj)
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    const int hk = h / group;
+                    float dp = 0.f;
+#pragma unroll
+                    for (int d = 0; d < DPL; ++d) dp = __builtin_fmaf(qr[h][d], kr[j0 + jj][hk][d], dp);
+                    sc[jj][h] = j0 + jj < nj ? __fmul_rn(wave_sum_uniform(dp), sl2) : -INFINITY;
+                }
+#pragma unroll
             for (int h = 0; h < NH; ++h) {
                 const int hk = h / group;
-                float dp = 0.f;
+                float mb = sc[0][h];
 #pragma unroll
-                for (int d = 0; d < DPL; ++d)
-                    dp = __builtin_fmaf(qs[h * hd + lane * DPL + d], kr[j][hk][d], dp);
-                const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
-                const float mn = fmaxf(m[h], score);
+                for (int jj = 1; jj < SB; ++jj) mb = fmaxf(mb, sc[jj][h]);
+                const float mn = fmaxf(m[h], mb);
                 const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
-                const float p = __builtin_amdgcn_exp2f(score - mn);
-                s[h] = __builtin_fmaf(s[h], c, p);
+                s[h] = __fmul_rn(s[h], c);
 #pragma unroll
-                for (int d = 0; d < DPL; ++d)
-                    o[h][d] = __builtin_fmaf(o[h][d], c, p * vr[j][hk][d]);
+                for (int d = 0; d < DPL; ++d) o[h][d] = __fmul_rn(o[h][d], c);
+#pragma unroll
+                for (int jj = 0; jj < SB; ++jj)
+                    if (j0 + jj < nj) {
+                        const float p = __builtin_amdgcn_exp2f(sc[jj][h] - mn);
+                        s[h] = __fadd_rn(s[h], p);
+#pragma unroll
+                        for (int d = 0; d < DPL; ++d) o[h][d] = __builtin_fmaf(p, vr[j0 + jj][hk][d], o[h][d]);
+                    }
                 m[h] = mn;
             }
         }

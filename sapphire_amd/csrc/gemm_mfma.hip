@@ -577,18 +577,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 }
             }
         }
+        // the range and whether any value is NaN / inf: the largest exponent field is all ones
+        // (one integer maximum per value; no per-value flag stays live for the rare path below)
         float mx = 0.f;
-        bool bad = false;
+        uint32_t emax = 0;
 #pragma unroll
         for (int i = 0; i < kStagePairs; ++i)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 mx = fmaxf(mx, fabsf(v[i][e]));
-                bad |= nonfinite::is_nf(v[i][e]);
+                emax = max(emax, __float_as_uint(v[i][e]) & 0x7f800000u);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const bool wbad = __any(bad) != 0;
+        const bool wbad = __any(emax == 0x7f800000u) != 0;
         if (lane < kBatchMax) wmax[wid][lane] = mx;
         if (lane == 0) wnf[wid] = wbad;
         __syncthreads();                               // also ends every read of raw
