@@ -119,7 +119,13 @@ int sapphire_gemm_q_dev(int dtype, int layout, const void *w, int M, int K, cons
  * out.geglu, W's rows are gate and up rows interleaved by eight and y[b * ldy + j] =
  * gelu(gate_j) * up_j for j < M/2 (transformer.c:141-157). Pointers 16-byte aligned,
  * leading dimensions multiples of 4; ws as for sapphire_gemm_q_dev (NULL allowed when
- * K <= 1152 or out.parts is set). batch <= 16. */
+ * K <= 1152 or out.parts is set). batch <= 16.
+ * Block order (x_blocked, y_blocked): a vector set of 16 slots in which element k of
+ * sequence b sits at (k / 32) * 512 + ((k / 8) % 4) * 128 + b * 8 + k % 8 (16 * K floats,
+ * ldx / ldy unused), the order of the matrix-core operands, so a GEMM reads it with
+ * contiguous loads. x_blocked only for a plain x (no parts, norms or resid_out); y_blocked
+ * only when K <= 1152 and out.parts is unset (with geglu, over the M/2 outputs). A step
+ * passes the GeGLU output to the down projection this way. */
 typedef struct {
     const float *x;
     int ldx;
@@ -131,12 +137,14 @@ typedef struct {
     int ldr;
     const float *w_norm;
     float eps;
+    int x_blocked;
 } sapphire_gemm_input_t;
 typedef struct {
     float *y;
     int ldy;
     float *parts;
     int geglu;
+    int y_blocked;
 } sapphire_gemm_output_t;
 int sapphire_gemm_splits(int K);
 int sapphire_gemm_q_fused_dev(int dtype, const void *w_tiled, int M, int K, int batch, const sapphire_gemm_input_t *in,

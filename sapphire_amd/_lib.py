@@ -15,12 +15,12 @@ class GemmInput(C.Structure):
     """sapphire_gemm_input_t (include/sapphire_hip.h)."""
     _fields_ = [("x", C.c_void_p), ("ldx", C.c_int), ("parts", C.c_void_p), ("nparts", C.c_int), ("ldp", C.c_int),
                 ("part_stride", C.c_size_t), ("w_delta", C.c_void_p), ("resid_out", C.c_void_p), ("ldr", C.c_int),
-                ("w_norm", C.c_void_p), ("eps", C.c_float)]
+                ("w_norm", C.c_void_p), ("eps", C.c_float), ("x_blocked", C.c_int)]
 
 
 class GemmOutput(C.Structure):
     """sapphire_gemm_output_t (include/sapphire_hip.h)."""
-    _fields_ = [("y", C.c_void_p), ("ldy", C.c_int), ("parts", C.c_void_p), ("geglu", C.c_int)]
+    _fields_ = [("y", C.c_void_p), ("ldy", C.c_int), ("parts", C.c_void_p), ("geglu", C.c_int), ("y_blocked", C.c_int)]
 
 
 def _proto(lib, name, res, args):

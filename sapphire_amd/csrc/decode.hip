@@ -380,11 +380,12 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 // and sum), so no load waits for another.
 template <int NS>
 __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float *__restrict__ part, int nh, int hd,
-                                                                    float *__restrict__ out, size_t out_stride) {
+                                                                    float *__restrict__ out, size_t out_stride,
+                                                                    bool blocked) {
     static_assert(NS <= kWave, "one lane per slice");
     const int h = blockIdx.x, t = threadIdx.x, lane = t & (kWave - 1);
     part += (size_t)blockIdx.y * NS * nh * (hd + 2);   // sequence blockIdx.y
-    out += (size_t)blockIdx.y * out_stride;
+    if (!blocked) out += (size_t)blockIdx.y * out_stride;
     const size_t hs = (size_t)nh * (hd + 2);             // stride between slices
     const float *ph = part + (size_t)h * (hd + 2);
     const float mb = lane < NS ? ph[lane * hs + hd] : -INFINITY;
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float 
     float O = 0.f;
 #pragma unroll
     for (int b = 0; b < NS; ++b) O = __builtin_fmaf(o[b], lane_value(e, b), O);
-    if (d < hd) out[h * hd + d] = O * inv;
+    if (d < hd) out[blocked ? block_order_index(blockIdx.y, h * hd + d) : (size_t)h * hd + d] = O * inv;
 }
 
 __global__ void dec_embed_kernel(const uint16_t *__restrict__ embed, int hidden, int vocab, float es,
@@ -559,7 +560,8 @@ size_t attn_part_floats(int nh, int hd) { return (size_t)kAttnSplit * nh * (hd +
 
 int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     if (a.nh * a.hd > kAttnMaxQ || a.nkv * a.hd > kAttnMaxKV || a.nkv <= 0 || a.nkv > 2 || a.nh % a.nkv != 0 ||
-        a.hd % kWave != 0 || a.hd > 4 * kWave || a.nh + a.nkv > 16 || a.batch < 1 || a.batch > 65535) {
+        a.hd % kWave != 0 || a.hd > 4 * kWave || a.nh + a.nkv > 16 || a.batch < 1 || a.batch > 65535 ||
+        (a.out_blocked && a.batch > kGemmSeqs)) {
         set_error("attention shape not supported (heads %d/%d, head_dim %d)", a.nh, a.nkv, a.hd);
         return -1;
     }
@@ -580,10 +582,10 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     if (!hip_ok(hipGetLastError(), "attention launch")) return -1;
     if (ns == kAttnSplit)
         hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplit>, dim3(a.nh, a.batch), dim3(kThreads), 0, s, a.part,
-                           a.nh, a.hd, out, a.out_stride);
+                           a.nh, a.hd, out, a.out_stride, a.out_blocked);
     else
         hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplitBatch>, dim3(a.nh, a.batch), dim3(kThreads), 0, s,
-                           a.part, a.nh, a.hd, out, a.out_stride);
+                           a.part, a.nh, a.hd, out, a.out_stride, a.out_blocked);
     return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
 }
 

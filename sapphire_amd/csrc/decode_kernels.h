@@ -59,6 +59,9 @@ struct AttnArgs {
     // the attention kernel writes none (a prefill chunk of one sequence, whose tokens read
     // each other's rows)
     bool kv_written = false;
+    // the combined output in block order (block_order_index(b, h * hd + d), out_stride unused):
+    // the input of a batched GEMM
+    bool out_blocked = false;
 };
 // QK-norm, RoPE, KV write and split attention partials, then their combination into
 // out[nh*hd] (attention.c:93-163, 271-309; kv_cache.c:252-278). part holds

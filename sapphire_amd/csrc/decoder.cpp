@@ -235,6 +235,7 @@ bool layer_is_global(const sapphire_decoder_config_t &c, int l) {   // attention
 
 // Tokens of one prefill chunk: the batched GEMM's widest batch.
 constexpr int kPrefillChunk = 16;
+static_assert(kPrefillChunk == kGemmSeqs, "a prefill chunk is one batched GEMM pass (block-order buffers of 16 slots)");
 
 // Shapes the TILED matrix-core GEMM takes: every projection K a multiple of 128 and the
 // hidden size at most 36 blocks (the norms are formed inside one K chunk).
@@ -458,6 +459,7 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         at.qkv_stride = (size_t)nqkv;
         at.kv_stride = r.kv_stride;
         at.out_stride = (size_t)nq;
+        at.out_blocked = true;          // the o projection stages it with contiguous loads
         if (r.prefill) {
             if (dec_kv_write(at, s) != 0) return -1;
             at.kv_written = true;
@@ -465,7 +467,7 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         if (dec_attention(at, r.attn, s) != 0) return -1;
         GemmIn oi;
         oi.x = r.attn;
-        oi.ldx = nq;
+        oi.x_blocked = true;
         GemmOut oo;
         oo.y = r.o;
         oo.ldy = H;
@@ -486,12 +488,12 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         cur = 1 - cur;
         GemmOut fo;
         fo.y = r.g;
-        fo.ldy = c.ffn;
         fo.geglu = true;
+        fo.y_blocked = true;            // the down projection stages it with contiguous loads
         if (launch_gemm_tiled_ex(c.wdtype, L.t_gu, 2 * c.ffn, H, B, fi, fo, r.gws, s) != 0) return -1;
         GemmIn di;
         di.x = r.g;
-        di.ldx = c.ffn;
+        di.x_blocked = true;
         GemmOut dout;
         dout.parts = r.dparts;
         if (launch_gemm_tiled_ex(c.wdtype, L.t_down, H, c.ffn, B, di, dout, r.gws, s) != 0) return -1;
@@ -752,9 +754,11 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
         !hip_ok(hipMemset(d->vc, 0, kv * sizeof(float)), "kv zero"))
         return fail();
     const size_t b = (size_t)B;
+    // a batched step keeps the attention output and the GeGLU output in block order (16 slots)
+    const size_t bo = B > 1 ? (size_t)kGemmSeqs : b;
     if (!dev_alloc_t(d, &d->resid[0], b * H, "resid") || !dev_alloc_t(d, &d->resid[1], b * H, "resid") ||
-        !dev_alloc_t(d, &d->qkv, b * (nq + 2 * nk), "qkv") || !dev_alloc_t(d, &d->attn, b * nq, "attn") ||
-        !dev_alloc_t(d, &d->o, b * H, "o") || !dev_alloc_t(d, &d->g, b * c.ffn, "g") ||
+        !dev_alloc_t(d, &d->qkv, b * (nq + 2 * nk), "qkv") || !dev_alloc_t(d, &d->attn, bo * nq, "attn") ||
+        !dev_alloc_t(d, &d->o, b * H, "o") || !dev_alloc_t(d, &d->g, bo * c.ffn, "g") ||
         !dev_alloc_t(d, &d->ffn_out, H, "ffn_out") || !dev_alloc_t(d, &d->xfin, b * H, "xfin") ||
         !dev_alloc_t(d, &d->logits, b * c.vocab, "logits") ||
         !dev_alloc_t(d, &d->attn_part, b * attn_part_floats(c.n_heads, hd), "attn partials") ||

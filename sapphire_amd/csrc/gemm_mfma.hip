@@ -500,7 +500,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             for (int e = 0; e < 8; ++e) v[i][e] = xv[i][e] = 0.f;
             if (p < pairs && seq < batch) {
                 const int k = kb + p * 8;
-                if (in.x) load8(in.x + (size_t)seq * in.ldx + k, !plain && in.parts ? xv[i] : v[i]);
+                // block order: the 64 lanes of a wave read 2 KiB in one piece
+                if (plain && in.x_blocked) load8(in.x + block_order_index(seq, k), v[i]);
+                else if (in.x) load8(in.x + (size_t)seq * in.ldx + k, !plain && in.parts ? xv[i] : v[i]);
                 if (!plain && in.parts) load8(in.parts + (size_t)seq * in.ldp + k, v[i]);
             }
         }
@@ -695,7 +697,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 const float up = __shfl_xor(val, 8, kWave);
                 const int j = ct * 8 + n;
                 if (n < 8 && 4 * m + r < batch && 2 * j < M)
-                    dst[(size_t)(4 * m + r) * ldd + j] = __fmul_rn(devmath::gelu_ref(val), up);
+                    dst[out.y_blocked ? block_order_index(4 * m + r, j) : (size_t)(4 * m + r) * ldd + j] =
+                        __fmul_rn(devmath::gelu_ref(val), up);
             }
         } else {
             const int row = ct * kTileRows + n;
@@ -705,7 +708,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                     if (4 * m + r < batch) {
                         float val = a[r] * sc[r];
                         if (any_nf) val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, row, 4 * m + r);
-                        dst[(size_t)(4 * m + r) * ldd + row] = val;
+                        dst[out.y_blocked ? block_order_index(4 * m + r, row) : (size_t)(4 * m + r) * ldd + row] = val;
                     }
         }
     };
@@ -857,15 +860,18 @@ int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const G
     const int nsplit = gemm_splits(K);
     const bool norms = in.w_delta || in.w_norm;
     const bool ok = batch >= 1 && batch <= kBatchMax && M > 0 && K > 0 && K % (kGroupBlocks * kBlock) == 0 &&
-                    (in.x || in.parts) && (!in.x || (aligned16(in.x) && in.ldx % 4 == 0 && in.ldx >= K)) &&
+                    (in.x || in.parts) &&
+                    (!in.x || (aligned16(in.x) && (in.x_blocked || (in.ldx % 4 == 0 && in.ldx >= K)))) &&
                     (!in.parts || (aligned16(in.parts) && in.nparts >= 1 && in.ldp % 4 == 0 && in.ldp >= K &&
                                    in.part_stride % 4 == 0)) &&
                     (!in.w_delta || in.parts) && (!in.resid_out || (aligned16(in.resid_out) && in.ldr % 4 == 0)) &&
                     (!norms || (nsplit == 1 && aligned16(in.w_delta ? in.w_delta : in.w_norm) &&
                                 (!in.w_norm || aligned16(in.w_norm)))) &&
-                    (out.parts || (out.y && out.ldy >= (out.geglu ? M / 2 : M))) &&
+                    (out.parts || (out.y && (out.y_blocked || out.ldy >= (out.geglu ? M / 2 : M)))) &&
                     (!out.geglu || (nsplit == 1 && M % 16 == 0 && !out.parts)) &&
-                    (out.parts || nsplit == 1 || ((reinterpret_cast<uintptr_t>(ws) & 255u) == 0 && ws));
+                    (out.parts || nsplit == 1 || ((reinterpret_cast<uintptr_t>(ws) & 255u) == 0 && ws)) &&
+                    (!in.x_blocked || (in.x && !in.parts && !norms && !in.resid_out)) &&
+                    (!out.y_blocked || (nsplit == 1 && !out.parts && out.y));
     if (!ok) {
         set_error("batched GEMM: unsupported arguments (batch=%d M=%d K=%d nsplit=%d)", batch, M, K, nsplit);
         return -1;

@@ -62,6 +62,14 @@ int launch_gemm_tiled(int dt, const void *w, int M, int K, const float *X, int b
                       hipStream_t s);
 // Number of K chunks (partial sums) of a batched GEMM with inner dimension K.
 int gemm_splits(int K);
+// Sequences of one batched GEMM pass.
+constexpr int kGemmSeqs = 16;
+// The block order of a batched GEMM's activations: element k of sequence s (s < 16) at
+// (k / 32) * 512 + ((k / 8) % 4) * 128 + s * 8 + k % 8, the order in which a K chunk's
+// matrix-core operands sit (so a GEMM stages it with contiguous loads). 16 * K floats.
+__host__ __device__ inline size_t block_order_index(int s, int k) {
+    return (size_t)(k >> 5) * 512 + ((k >> 3) & 3) * 128 + s * 8 + (k & 7);
+}
 // y[b * ldy + r] = sum over c < nparts of parts[c * stride + b * M + r] (chunk order).
 int launch_sum_parts(const float *parts, int nparts, size_t stride, int batch, int M, float *y, int ldy,
                      hipStream_t s);
@@ -83,6 +91,9 @@ struct GemmIn {
     int ldr = 0;
     const float *w_norm = nullptr;
     float eps = 1e-6f;
+    // x in block order (block_order_index; ldx unused): only with neither parts, norms nor
+    // resid_out
+    bool x_blocked = false;
 };
 // Output of a batched GEMM. parts set: the K chunks' partial sums go to parts[c][b][M] (an
 // input of the next GEMM's GemmIn), nothing else is written. geglu: the weight rows are
@@ -93,6 +104,9 @@ struct GemmOut {
     int ldy = 0;
     float *parts = nullptr;
     bool geglu = false;
+    // y in block order (block_order_index over the M or M / 2 outputs; ldy unused): one K
+    // chunk only, no parts
+    bool y_blocked = false;
 };
 int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
                          void *ws, hipStream_t s);

@@ -216,11 +216,13 @@ int sapphire_gemm_q_fused_dev(int dt, const void *w, int M, int K, int batch, co
     gi.ldr = in->ldr;
     gi.w_norm = in->w_norm;
     gi.eps = in->eps;
+    gi.x_blocked = in->x_blocked != 0;
     GemmOut go;
     go.y = out->y;
     go.ldy = out->ldy;
     go.parts = out->parts;
     go.geglu = out->geglu != 0;
+    go.y_blocked = out->y_blocked != 0;
     return launch_gemm_tiled_ex(dt, w, M, K, batch, gi, go, ws, as_stream(stream));
 }
 

@@ -317,3 +317,46 @@ def test_gemm_fused_rejects(hip):
     gin = _GemmIn(dx.ptr, 6912, None, 0, 0, 0, None, None, 0, None, 1e-6)
     assert hip.sapphire_gemm_q_fused_dev(qm.dtype, qm.ptr(), 64, 6912, 17, C.byref(gin),
                                          C.byref(_GemmOut(dy.ptr, 64, None, 0)), None, None) == -1   # batch > 16
+
+
+def _block_order_index(b, k):
+    """Element k of sequence b in the block order of x_blocked / y_blocked (16 sequence slots)."""
+    k = np.asarray(k)
+    return (k >> 5) * 512 + ((k >> 3) & 3) * 128 + b * 8 + (k & 7)
+
+
+@pytest.mark.parametrize("dtype", [synth.Q4_0, synth.Q8_0], ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("batch", [16, 5])
+def test_gemm_fused_block_order(hip, oracle, dtype, batch):
+    """The GeGLU output in block order (y_blocked) holds the row-major output's values, bit for
+    bit, at the block-order positions; the down projection reading it (x_blocked) leaves the
+    same partial sums, bit for bit, as from the row-major rows. Slots of sequences past the
+    batch hold NaN and must not be read."""
+    from sapphire_amd.device import DeviceArray, QMatrix
+    k, ffn = 1152, 6912
+    st = synth.quant_matrix(dtype, 2 * ffn, k, seed=44, tensor_id=1)
+    qgu = QMatrix(dtype, st, layout=TILED)
+    qd = QMatrix(dtype, synth.quant_matrix(dtype, k, ffn, seed=44, tensor_id=2), layout=TILED)
+    x = synth.normal_f32((batch, k), 44, 3)
+    dx = DeviceArray.from_numpy(x)
+    g_rows, g_blk = DeviceArray.empty(batch * ffn), DeviceArray.from_numpy(np.full(16 * ffn, np.nan, np.float32))
+    none_in = dict(parts=None, nparts=0, ldp=0, part_stride=0, w_delta=None, resid_out=None, ldr=0, w_norm=None,
+                   eps=1e-6)
+    _fused(hip, qgu, batch, _GemmIn(x=dx.ptr, ldx=k, **none_in), _GemmOut(y=g_rows.ptr, ldy=ffn, geglu=1))
+    _fused(hip, qgu, batch, _GemmIn(x=dx.ptr, ldx=k, **none_in), _GemmOut(y=g_blk.ptr, geglu=1, y_blocked=1))
+    rows = g_rows.numpy().reshape(batch, ffn)
+    blk = g_blk.numpy()
+    j = np.arange(ffn)
+    for b in range(batch):
+        assert np.array_equal(blk[_block_order_index(b, j)].view(np.uint32), rows[b].view(np.uint32)), b
+    ns = hip.sapphire_gemm_splits(ffn)
+    p_rows, p_blk = DeviceArray.empty(ns * batch * k), DeviceArray.empty(ns * batch * k)
+    _fused(hip, qd, batch, _GemmIn(x=g_rows.ptr, ldx=ffn, **none_in), _GemmOut(parts=p_rows.ptr))
+    _fused(hip, qd, batch, _GemmIn(x=g_blk.ptr, x_blocked=1, **none_in), _GemmOut(parts=p_blk.ptr))
+    assert np.array_equal(p_rows.numpy().view(np.uint32), p_blk.numpy().view(np.uint32))
+    # and they are the oracle's product (norm-wise per sequence: the GeGLU outputs are heavy-tailed,
+    # so outputs near zero are differences of large terms; test_gemm_fused_partials_chain holds
+    # the element-wise bound on N(0, 1) inputs)
+    d = _ref(oracle, dtype, synth.quant_matrix(dtype, k, ffn, seed=44, tensor_id=2), rows).astype(np.float64)
+    got = p_rows.numpy().reshape(ns, batch, k).sum(axis=0, dtype=np.float64)
+    assert np.all(np.abs(got - d).max(axis=1) <= 1e-5 * np.abs(d).max(axis=1))
