@@ -32,8 +32,8 @@ namespace sapphire {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kWaves = 8;                              // waves per workgroup
-constexpr int kThreads = kWave * kWaves;
+constexpr int kWaves = 8;                              // waves per workgroup (two per CU)
+constexpr int kWavesWide = 16;                         // the same for a streaming launch (one per CU)
 constexpr int kTileRows = 16;
 constexpr int kGroupBlocks = 4;
 constexpr int kChunkBlocks = 36;                       // A operands staged per workgroup (72 KiB)
@@ -41,8 +41,6 @@ constexpr int kBatchMax = 16;
 constexpr int kRing = 6;                               // units in flight per wave
 constexpr int kNT = 2;                                 // streaming (non-temporal) weight loads
 constexpr int kMaxGrid = 1024;                         // workgroups over the tiles
-// (block, quarter) pairs of a chunk handled by one staging thread
-constexpr int kStagePairs = (kChunkBlocks * 4 + kThreads / kBatchMax - 1) / (kThreads / kBatchMax);
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -381,22 +379,25 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
 }
 
 // grid.x: workgroups over the tiles (grid-stride), grid.y: K chunks of `cb` blocks.
-// Four waves per SIMD (two workgroups per CU): at most 128 VGPRs.
+// Four waves per SIMD (two workgroups of 8 waves, or one of 16, per CU): at most 128 VGPRs.
 // How a workgroup forms its A operands: the full input transform, a copy of the chunk that
 // gemm_prep_kernel formed, or a plain x (no sum of parts, norm or residual).
 enum StageMode { kStageFull = 0, kStagePrepared = 1, kStagePlain = 2 };
 
-template <int DT, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_mfma_kernel(
+template <int DT, int MODE, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4))) void gemm_mfma_kernel(
     const uint8_t *__restrict__ wq, uint32_t q_bytes, const uint8_t *__restrict__ wsc, uint32_t s_bytes, GemmIn in,
     int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp, const PrepChunk *__restrict__ prep, int ks) {
+    constexpr int NT = NW * kWave;                 // threads
+    constexpr int RING = DT == DT_Q8_0 ? kRing - 1 : kRing;   // Q8_0's units are larger
+    constexpr int NP = (kChunkBlocks * 4 + NT / kBatchMax - 1) / (NT / kBatchMax);   // pairs per staging thread
     __shared__ h8 xs[kStageH8];
-    __shared__ float wmax[kWaves][kBatchMax];
+    __shared__ float wmax[NW][kBatchMax];
     __shared__ float xsc[kBatchMax];
     __shared__ float npart[kBatchMax][8];
     __shared__ float rinv[kBatchMax];
     __shared__ NfChunk nfc;
-    __shared__ int wnf[kWaves];
+    __shared__ int wnf[NW];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     if (tid == 0) nfc.nan = 0;
     const int nb = K / kBlock, G = nb / kGroupBlocks;
@@ -412,8 +413,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int wu = __builtin_amdgcn_readfirstlane(wid);
     const int slot = wu / ks, part = wu - slot * ks;
     const int gs = part * gc / ks, gcw = (part + 1) * gc / ks - gs;
-    const int tstride = gridDim.x * (kWaves / ks);
-    const int t0 = blockIdx.x * (kWaves / ks) + slot;
+    const int tstride = gridDim.x * (NW / ks);
+    const int t0 = blockIdx.x * (NW / ks) + slot;
     const bool idle = t0 >= ntiles;           // no tile: stages, then leaves
     const int U = idle ? 0 : (ntiles - t0 + tstride - 1) / tstride * gcw;   // units of this wave
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(wq, q_bytes);
@@ -423,15 +424,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // and outside them the fp16 exponent of 1024, inside them the bits that undo nib ^ 8
     BConst bk = {0x000F000Fu, 0x00F000F0u, 0x64086408u, 0x64806480u};
     asm volatile("" : "+v"(bk.lo_mask), "+v"(bk.hi_mask), "+v"(bk.lo_bits), "+v"(bk.hi_bits));
-    // ---- the first kRing-1 units' weight loads ----
-    Unit ring[kRing];
-    // issue pointer: group offset (tile * G + g) of unit u + kRing - 1; loads past the last
+    // ---- the first RING-1 units' weight loads ----
+    Unit ring[RING];
+    // issue pointer: group offset (tile * G + g) of unit u + RING - 1; loads past the last
     // unit repeat it. The offset goes in the scalar offset field, which the buffer range
     // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
     int igb = idle ? g0 : t0 * G + g0 + gs, ig = 0, issued = 0;
     auto prime = [&]() {
 #pragma unroll
-        for (int p = 0; p < kRing - 1; ++p) {
+        for (int p = 0; p < RING - 1; ++p) {
             unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
             if (issued < U - 1) {
                 ++issued;
@@ -447,19 +448,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         prime();
         const PrepChunk &pc = prep[blockIdx.y];
         const int na = (b1 - b0) * 2 * kWave;
-        constexpr int kCopy = (kChunkBlocks * 2 * kWave + kThreads - 1) / kThreads;
+        constexpr int kCopy = (kChunkBlocks * 2 * kWave + NT - 1) / NT;
         // all loads first: the range scales and non-finite flags with the operands
         const float sc = tid < batch ? pc.xsc[tid] : 1.0f;
         const int nfv = tid < batch ? pc.nf[tid] : 0;
         h8 val[kCopy];
 #pragma unroll
         for (int j = 0; j < kCopy; ++j) {
-            const int i = tid + j * kThreads;
+            const int i = tid + j * NT;
             val[j] = i < na ? pc.a[i] : h8{};
         }
 #pragma unroll
         for (int j = 0; j < kCopy; ++j) {
-            const int i = tid + j * kThreads;
+            const int i = tid + j * NT;
             if (i < na) xs[i] = (i & 15) < batch ? val[j] : h8{};
         }
         if (tid < kBatchMax) xsc[tid] = sc;
@@ -471,7 +472,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         any_nf = wnf[0] != 0;
         if (any_nf) {
             const int nbl = b1 - b0;
-            for (int i = tid; i < batch * 2 * nbl; i += kThreads) {
+            for (int i = tid; i < batch * 2 * nbl; i += NT) {
                 const int q = i / (2 * nbl), sg = (i / nbl) & 1, bl = i % nbl;
                 nfc.inf[q][sg][bl] = pc.inf[q][sg][bl];
             }
@@ -490,12 +491,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const int pairs = (b1 - b0) * 4;
         const int kb = b0 * kBlock;
         float *raw = reinterpret_cast<float *>(xs);
-        float v[kStagePairs][8];    // the delta (parts given), else h
-        float xv[kStagePairs][8];   // x when it is added to the delta
+        float v[NP][8];    // the delta (parts given), else h
+        float xv[NP][8];   // x when it is added to the delta
         // every load of the staging's first stage goes out before any is used
 #pragma unroll
-        for (int i = 0; i < kStagePairs; ++i) {
-            const int p = q + i * (kThreads / kBatchMax);
+        for (int i = 0; i < NP; ++i) {
+            const int p = q + i * (NT / kBatchMax);
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[i][e] = xv[i][e] = 0.f;
             if (p < pairs && seq < batch) {
@@ -509,8 +510,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         if (!plain && in.parts) {
             for (int c = 1; c < in.nparts; ++c)
 #pragma unroll
-                for (int i = 0; i < kStagePairs; ++i) {
-                    const int p = q + i * (kThreads / kBatchMax);
+                for (int i = 0; i < NP; ++i) {
+                    const int p = q + i * (NT / kBatchMax);
                     if (p < pairs && seq < batch) {
                         float t[8];
                         load8(in.parts + c * in.part_stride + (size_t)seq * in.ldp + kb + p * 8, t);
@@ -520,8 +521,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 }
             if (in.w_delta) {
 #pragma unroll
-                for (int i = 0; i < kStagePairs; ++i) {
-                    const int p = q + i * (kThreads / kBatchMax);
+                for (int i = 0; i < NP; ++i) {
+                    const int p = q + i * (NT / kBatchMax);
                     if (p < pairs)
 #pragma unroll
                         for (int e = 0; e < 8; ++e) raw[seq * kRawLd + p * 8 + e] = v[i][e];
@@ -530,8 +531,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 rows_rms_inv(raw, kRawLd, K, batch, in.eps, npart, rinv);
                 const float r = rinv[seq];
 #pragma unroll
-                for (int i = 0; i < kStagePairs; ++i) {
-                    const int p = q + i * (kThreads / kBatchMax);
+                for (int i = 0; i < NP; ++i) {
+                    const int p = q + i * (NT / kBatchMax);
                     if (p < pairs && seq < batch) {
                         float w[8];
                         load8(in.w_delta + kb + p * 8, w);
@@ -542,14 +543,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             }
             if (in.x)
 #pragma unroll
-                for (int i = 0; i < kStagePairs; ++i)
+                for (int i = 0; i < NP; ++i)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) v[i][e] = __fadd_rn(xv[i][e], v[i][e]);
         }
         if (!plain && in.resid_out && blockIdx.x == 0 && blockIdx.y == 0)
 #pragma unroll
-            for (int i = 0; i < kStagePairs; ++i) {
-                const int p = q + i * (kThreads / kBatchMax);
+            for (int i = 0; i < NP; ++i) {
+                const int p = q + i * (NT / kBatchMax);
                 if (p < pairs && seq < batch) {
                     float4 *dst = reinterpret_cast<float4 *>(in.resid_out + (size_t)seq * in.ldr + kb + p * 8);
                     dst[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
@@ -559,8 +560,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         if (!plain && in.w_norm) {
             __syncthreads();                           // raw may still be read by the delta norm
 #pragma unroll
-            for (int i = 0; i < kStagePairs; ++i) {
-                const int p = q + i * (kThreads / kBatchMax);
+            for (int i = 0; i < NP; ++i) {
+                const int p = q + i * (NT / kBatchMax);
                 if (p < pairs)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) raw[seq * kRawLd + p * 8 + e] = v[i][e];
@@ -569,8 +570,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             rows_rms_inv(raw, kRawLd, K, batch, in.eps, npart, rinv);
             const float r = rinv[seq];
 #pragma unroll
-            for (int i = 0; i < kStagePairs; ++i) {
-                const int p = q + i * (kThreads / kBatchMax);
+            for (int i = 0; i < NP; ++i) {
+                const int p = q + i * (NT / kBatchMax);
                 if (p < pairs && seq < batch) {
                     float w[8];
                     load8(in.w_norm + kb + p * 8, w);
@@ -584,7 +585,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         float mx = 0.f;
         uint32_t emax = 0;
 #pragma unroll
-        for (int i = 0; i < kStagePairs; ++i)
+        for (int i = 0; i < NP; ++i)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 mx = fmaxf(mx, fabsf(v[i][e]));
@@ -598,10 +599,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         __syncthreads();                               // also ends every read of raw
         mx = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wmax[w][seq]);
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, wmax[w][seq]);
         any_nf = false;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) any_nf |= wnf[w] != 0;
+        for (int w = 0; w < NW; ++w) any_nf |= wnf[w] != 0;
         if (any_nf) {
             // NaN / inf activations (workgroup-uniform, rare): record where they are, zero them,
             // and take the range maxima again over the rest. Pairs p = 4 bl .. 4 bl + 3 of block
@@ -609,8 +610,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             __syncthreads();                           // every wave has read wmax
             mx = 0.f;
 #pragma unroll
-            for (int i = 0; i < kStagePairs; ++i) {
-                const int p = q + i * (kThreads / kBatchMax);
+            for (int i = 0; i < NP; ++i) {
+                const int p = q + i * (NT / kBatchMax);
                 uint32_t pinf = 0, ninf = 0;
                 bool nan = false;
 #pragma unroll
@@ -640,7 +641,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             __syncthreads();
             mx = 0.f;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wmax[w][seq]);
+            for (int w = 0; w < NW; ++w) mx = fmaxf(mx, wmax[w][seq]);
         }
         // e: the chunk's largest |x| * 2^-e in [2^14, 2^15) (finite in fp16, lo term normal)
         int e = 0;
@@ -651,8 +652,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
         if (q == 0) xsc[seq] = ldexpf(1.0f, e);
 #pragma unroll
-        for (int i = 0; i < kStagePairs; ++i) {
-            const int p = q + i * (kThreads / kBatchMax);
+        for (int i = 0; i < NP; ++i) {
+            const int p = q + i * (NT / kBatchMax);
             if (p < pairs) {
                 h8 hv, lv;
 #pragma unroll
@@ -714,14 +715,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     };
     int ct = t0, cg = 0;                               // tile and group of the unit multiplied
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    // Every pass issues the loads of all kRing slots (past the last unit they repeat it), so
-    // each path through the loop has the same load order and the waits stay kRing-1 units
+    // Every pass issues the loads of all RING slots (past the last unit they repeat it), so
+    // each path through the loop has the same load order and the waits stay RING-1 units
     // deep; only the multiplication of units past the end is skipped. (An idle wave has
     // U = 0.)
-    for (int base = 0; base < U; base += kRing) {
+    for (int base = 0; base < U; base += RING) {
 #pragma unroll
-        for (int p = 0; p < kRing; ++p) {
-            unit_issue<DT>(ring[(p + kRing - 1) % kRing], rq, rs, (uint32_t)igb, lane, n);
+        for (int p = 0; p < RING; ++p) {
+            unit_issue<DT>(ring[(p + RING - 1) % RING], rq, rs, (uint32_t)igb, lane, n);
             if (issued < U - 1) {
                 ++issued;
                 if (++ig == gcw) { ig = 0; igb += tstride * G - (gcw - 1); } else { ++igb; }
@@ -814,20 +815,30 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
             ks = k;
             break;
         }
-    const int sets = (ntiles * ks + kWaves - 1) / kWaves;
-    // two 72 KiB workgroups per CU
-    const int gx = ks > 1 ? sets : std::max(1, std::min({sets, (2 * cus() + nsplit - 1) / nsplit, kMaxGrid}));
+    // A streaming launch (one wave per tile, at least two tiles per wave) runs one workgroup of
+    // 16 waves per CU: the chunk is staged once per CU, and no second workgroup on the CU
+    // finishes behind the first. Else workgroups of 8 waves, two per CU.
+    const bool wide = ks == 1 && nsplit == 1 && ntiles >= 2 * kWavesWide * cus();
+    const int nw = wide ? kWavesWide : kWaves;
+    const int sets = (ntiles * ks + nw - 1) / nw;
+    const int gx = ks > 1 ? sets
+                          : std::max(1, std::min({sets, ((wide ? 1 : 2) * cus() + nsplit - 1) / nsplit, kMaxGrid}));
     const dim3 grid((unsigned)gx, (unsigned)nsplit);
     float *Yp = static_cast<float *>(ws);
     const int mode = pc ? kStagePrepared
                         : (!in.parts && !in.w_delta && !in.w_norm && !in.resid_out) ? kStagePlain : kStageFull;
-    const auto kern = dt == DT_Q4_0 ? (mode == kStagePrepared ? gemm_mfma_kernel<DT_Q4_0, kStagePrepared>
-                                       : mode == kStagePlain  ? gemm_mfma_kernel<DT_Q4_0, kStagePlain>
-                                                              : gemm_mfma_kernel<DT_Q4_0, kStageFull>)
-                                    : (mode == kStagePrepared ? gemm_mfma_kernel<DT_Q8_0, kStagePrepared>
-                                       : mode == kStagePlain  ? gemm_mfma_kernel<DT_Q8_0, kStagePlain>
-                                                              : gemm_mfma_kernel<DT_Q8_0, kStageFull>);
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, wb, (uint32_t)so, wb + so, (uint32_t)sbytes, in, batch, M,
+    decltype(&gemm_mfma_kernel<DT_Q4_0, kStageFull, kWaves>) kern;
+#define SPH_GEMM_PICK(DTV, NWV)                                                                                    \
+    kern = mode == kStagePrepared ? gemm_mfma_kernel<DTV, kStagePrepared, NWV>                                     \
+           : mode == kStagePlain  ? gemm_mfma_kernel<DTV, kStagePlain, NWV>                                        \
+                                  : gemm_mfma_kernel<DTV, kStageFull, NWV>;
+    if (dt == DT_Q4_0) {
+        if (wide) { SPH_GEMM_PICK(DT_Q4_0, kWavesWide) } else { SPH_GEMM_PICK(DT_Q4_0, kWaves) }
+    } else {
+        if (wide) { SPH_GEMM_PICK(DT_Q8_0, kWavesWide) } else { SPH_GEMM_PICK(DT_Q8_0, kWaves) }
+    }
+#undef SPH_GEMM_PICK
+    hipLaunchKernelGGL(kern, grid, dim3(nw * kWave), 0, st, wb, (uint32_t)so, wb + so, (uint32_t)sbytes, in, batch, M,
                        K, cb, out, Yp, (const PrepChunk *)pc, ks);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
     if (nsplit > 1 && !out.parts) return launch_sum_parts(Yp, nsplit, (size_t)batch * M, batch, M, out.y, out.ldy, st);
