@@ -150,6 +150,29 @@ __device__ __forceinline__ void unit_mfma(const Unit &u, const h8 *__restrict__ 
     }
 }
 
+// The same for two tiles at once (the same groups of two tiles): each A operand read from LDS
+// feeds both tiles' MFMAs; per tile the arithmetic and its order are unit_mfma's.
+template <int DT>
+__device__ __forceinline__ void unit_mfma2(const Unit &ua, const Unit &ub, const h8 *__restrict__ xs, int bl,
+                                           int lane, f4 &acca, f4 &accb, const BConst &k) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const h8 ahi = xs[((bl + j) * 2 + 0) * kWave + lane], alo = xs[((bl + j) * 2 + 1) * kWave + lane];
+        const h8 ba = b_operand<DT>(ua.a, j, k.lo_mask, k.hi_mask, k.lo_bits, k.hi_bits);
+        const h8 bb = b_operand<DT>(ub.a, j, k.lo_mask, k.hi_mask, k.lo_bits, k.hi_bits);
+        f4 C = {0.f, 0.f, 0.f, 0.f}, D = {0.f, 0.f, 0.f, 0.f};
+        C = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, ba, C, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bb, D, 0, 0, 0);
+        C = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, ba, C, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bb, D, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acca[r] = __builtin_fmaf(C[r], ua.s[j], acca[r]);
+            accb[r] = __builtin_fmaf(D[r], ub.s[j], accb[r]);
+        }
+    }
+}
+
 // Reference-order sums of squares of the staged rows (sum_sq_avx2, normalization.c:12-32:
 // eight strided chains, then ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)) and the tail), turned into
 // the rmsnorm factor 1/sqrtf(sum/dim + eps) of every sequence. raw: [seq][ld] fp32 in LDS.
@@ -425,18 +448,51 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
     BConst bk = {0x000F000Fu, 0x00F000F0u, 0x64086408u, 0x64806480u};
     asm volatile("" : "+v"(bk.lo_mask), "+v"(bk.hi_mask), "+v"(bk.lo_bits), "+v"(bk.hi_bits));
     // ---- the first RING-1 units' weight loads ----
-    Unit ring[RING];
+    // Streaming form (16 waves, one wave per tile): the wave's tiles go in pairs (its tiles
+    // 2i and 2i + 1), one pair-unit per group, RP pair-units through the ring.
+    constexpr bool PAIR = NW == kWavesWide;
+    constexpr int RP = DT == DT_Q8_0 ? 2 : 3;
+    Unit ring[PAIR ? 2 * RP : RING];
     // issue pointer: group offset (tile * G + g) of unit u + RING - 1; loads past the last
     // unit repeat it. The offset goes in the scalar offset field, which the buffer range
     // check does not cover, so it must stay inside the matrix: an idle wave reads tile 0.
     int igb = idle ? g0 : t0 * G + g0 + gs, ig = 0, issued = 0;
+    // pairs: the wave's tile count, pair-units, and the second tile's offset (a missing
+    // second tile repeats the first's loads)
+    const int ntw = idle ? 0 : (ntiles - t0 + tstride - 1) / tstride;
+    const int PU = (ntw + 1) / 2 * gcw;
+    int ip = 0, igb2 = ntw > 1 ? igb + tstride * G : igb;
+    auto padvance = [&]() {
+        if (issued < PU - 1) {
+            ++issued;
+            if (++ig == gcw) {
+                ig = 0;
+                ++ip;
+                const int ta = t0 + 2 * ip * tstride;
+                igb = ta * G + g0;
+                igb2 = 2 * ip + 1 < ntw ? igb + tstride * G : igb;
+            } else {
+                ++igb;
+                ++igb2;
+            }
+        }
+    };
     auto prime = [&]() {
+        if constexpr (PAIR) {
 #pragma unroll
-        for (int p = 0; p < RING - 1; ++p) {
-            unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
-            if (issued < U - 1) {
-                ++issued;
-                if (++ig == gcw) { ig = 0; igb += tstride * G - (gcw - 1); } else { ++igb; }
+            for (int p = 0; p < RP - 1; ++p) {
+                unit_issue<DT>(ring[2 * p], rq, rs, (uint32_t)igb, lane, n);
+                unit_issue<DT>(ring[2 * p + 1], rq, rs, (uint32_t)igb2, lane, n);
+                padvance();
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < RING - 1; ++p) {
+                unit_issue<DT>(ring[p], rq, rs, (uint32_t)igb, lane, n);
+                if (issued < U - 1) {
+                    ++issued;
+                    if (++ig == gcw) { ig = 0; igb += tstride * G - (gcw - 1); } else { ++igb; }
+                }
             }
         }
     };
@@ -715,6 +771,32 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
     };
     int ct = t0, cg = 0;                               // tile and group of the unit multiplied
     f4 acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (PAIR) {
+        f4 acc2 = {0.f, 0.f, 0.f, 0.f};
+        int cp = 0;                                    // the pair being multiplied
+        for (int base = 0; base < PU; base += RP) {
+#pragma unroll
+            for (int p = 0; p < RP; ++p) {
+                const int sl = (p + RP - 1) % RP;
+                unit_issue<DT>(ring[2 * sl], rq, rs, (uint32_t)igb, lane, n);
+                unit_issue<DT>(ring[2 * sl + 1], rq, rs, (uint32_t)igb2, lane, n);
+                padvance();
+                if (base + p < PU) {
+                    unit_mfma2<DT>(ring[2 * p], ring[2 * p + 1], xs, cg * kGroupBlocks, lane, acc, acc2, bk);
+                    if (++cg == gcw) {
+                        store_tile(ct, acc);
+                        if (2 * cp + 1 < ntw) store_tile(ct + tstride, acc2);
+                        acc = f4{0.f, 0.f, 0.f, 0.f};
+                        acc2 = f4{0.f, 0.f, 0.f, 0.f};
+                        cg = 0;
+                        ++cp;
+                        ct += 2 * tstride;
+                    }
+                }
+            }
+        }
+        return;
+    }
     // Every pass issues the loads of all RING slots (past the last unit they repeat it), so
     // each path through the loop has the same load order and the waits stay RING-1 units
     // deep; only the multiplication of units past the end is skipped. (An idle wave has
