@@ -190,11 +190,29 @@ def lm_head_gemm(blocks, batch: int, seed: int, iters: int = 20):
         run(i)
     us = t.stop() / iters * 1e3
     algo = m * (k // 32) * synth.BLOCK_BYTES[synth.Q4_0] + 4 * batch * (k + m)
-    return {
+    out = {
         "shape": f"{m}x{k} Q4_0, {batch} sequences", "us": round(us, 2),
         "GB/s": round(algo / (us * 1e-6) / 1e9, 1), "frac_hbm_peak": round(algo / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "TFLOP/s": round(2.0 * batch * m * k / (us * 1e-6) / 1e12, 1), "algorithmic_bytes": algo,
     }
+    # the form a greedy decode step runs: the same rows reduced to one token per sequence
+    # inside the GEMM (no logits stored), then one short kernel over the workgroups' partials
+    T = DeviceArray.empty(batch, np.int32)
+    run_g = lambda i: check(L.sapphire_gemm_q_greedy_dev(synth.Q4_0, qs[i % 2].ptr(), m, k, X.ptr, batch,  # noqa: E731
+                                                         T.ptr, ws.ptr, None))
+    for i in range(4):
+        run_g(i)
+    check(L.sapphire_synchronize())
+    t.start()
+    for i in range(iters):
+        run_g(i)
+    ug = t.stop() / iters * 1e3
+    algo_g = m * (k // 32) * synth.BLOCK_BYTES[synth.Q4_0] + 4 * batch * k + 4 * batch
+    out["greedy"] = {
+        "us": round(ug, 2), "GB/s": round(algo_g / (ug * 1e-6) / 1e9, 1),
+        "frac_hbm_peak": round(algo_g / (ug * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "algorithmic_bytes": algo_g,
+    }
+    return out
 
 
 def decode_batch_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024, batch: int = 16):

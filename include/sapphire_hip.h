@@ -104,6 +104,15 @@ size_t sapphire_gemm_workspace_bytes(int dtype, int M, int K);
 int sapphire_gemm_q_dev(int dtype, int layout, const void *w, int M, int K, const float *X, int batch,
                         float *Y, void *ws, void *stream);
 
+/* The batched LM head with the greedy pick fused: tokens[b] (device) = sample_greedy of
+ * W . X[b] (utils.c:145-156: the first index of the maximum; 0 when row 0 is NaN or no row
+ * is above -inf), for TILED weights with K <= 1152. The rows are formed as
+ * sapphire_gemm_q_dev forms them but never stored: each workgroup keeps the best row per
+ * sequence of the tiles it multiplies and leaves one partial in ws, and one short kernel picks
+ * the tokens. ws as for sapphire_gemm_q_dev. batch <= 16. */
+int sapphire_gemm_q_greedy_dev(int dtype, const void *w_tiled, int M, int K, const float *X, int batch,
+                               int *tokens, void *ws, void *stream);
+
 /* The batched GEMM with its input and output transforms, for a host engine that runs a
  * batched decode step (TILED weights only). Per sequence row b the input is formed while
  * the activations are staged:

@@ -81,6 +81,7 @@ def load_library(path: str):
     P("sapphire_gemv_softmax_noalloc_dev", i32, [i32, i32, vp, i32, i32, vp, vp, vp, vp, vp])
     P("sapphire_gemm_workspace_bytes", sz, [i32, i32, i32])
     P("sapphire_gemm_q_dev", i32, [i32, i32, vp, i32, i32, vp, i32, vp, vp, vp])
+    P("sapphire_gemm_q_greedy_dev", i32, [i32, vp, i32, i32, vp, i32, vp, vp, vp])
     P("sapphire_gemm_splits", i32, [i32])
     P("sapphire_gemm_q_fused_dev", i32, [i32, vp, i32, i32, i32, vp, vp, vp, vp])
     P("sapphire_rmsnorm_delta_dev", i32, [vp, vp, vp, f32, i32, i32, vp])

@@ -439,9 +439,7 @@ __global__ void dec_embed_batch_kernel(const uint16_t *__restrict__ embed, int h
 
 constexpr int kArgmaxParts = 64;     // workgroups per sequence in the first argmax pass
 
-// (value, index) order of sample_greedy (utils.c:145-156): a larger value wins, and of
-// equal values the lower index.
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return greedy_better(v, i, bv, bi); }
 
 __device__ __forceinline__ void wave_best(float &v, int &i) {
 #pragma unroll

@@ -66,6 +66,9 @@ struct sapphire_decoder {
     int *log = nullptr;     // [max_ctx] tokens of the steps; batched: [max_ctx][B]
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // whether the captured step writes the logits: a greedy batched step that returns no
+    // logits picks its tokens inside the LM-head GEMM instead
+    bool graph_logits = true;
     // batched decoder
     int batch = 1;
     float *dparts = nullptr;     // the down projection's K-chunk partial sums [splits][B][hidden]
@@ -554,6 +557,12 @@ int enqueue_step_batch(sapphire_decoder *d) {
     li.w_norm = d->norm_final;
     li.eps = c.eps;
     GemmOut lo;
+    if (d->temperature <= 0.0f && !d->graph_logits && gemm_splits(H) == 1) {
+        // greedy tokens straight from the LM-head GEMM: no logits written or read again
+        lo.tokens = d->state;
+        if (launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s) != 0) return -1;
+        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
+    }
     lo.y = d->logits;
     lo.ldy = c.vocab;
     if (launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s) != 0) return -1;
@@ -924,7 +933,16 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         return -1;
     }
     SPH_CHECK(hipSetDevice(d->device));
+    const bool want_logits = logits_out != nullptr || B == 1;
+    if (d->exec && d->graph_logits != want_logits) {
+        // the step's LM head changes form: capture again
+        (void)hipGraphExecDestroy(d->exec);
+        (void)hipGraphDestroy(d->graph);
+        d->exec = nullptr;
+        d->graph = nullptr;
+    }
     if (!d->exec) {
+        d->graph_logits = want_logits;
         SPH_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
         const int rc = B == 1 ? enqueue_step(d) : enqueue_step_batch(d);
         hipGraph_t g = nullptr;

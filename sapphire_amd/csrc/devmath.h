@@ -52,6 +52,12 @@ __device__ inline float block_sum_sq_ref(const float *__restrict__ in, int dim, 
     return sh[8];
 }
 
+// (value, index) order of sample_greedy (utils.c:145-156): a larger value wins, and of
+// equal values the lower index. A NaN never wins.
+__device__ __forceinline__ bool greedy_better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
 // gelu of activations.c:64-76 (tanh form; x + B*x^3 fused as in the reference build).
 __device__ __forceinline__ float gelu_ref(float x) {
     const float A = 0.7978845608f, B = 0.044715f;

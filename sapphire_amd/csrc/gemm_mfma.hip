@@ -22,9 +22,11 @@
 // in the GEMM itself (last workgroup to finish) needs device-scope fences, i.e. L2
 // write-backs across the XCDs, which cost more than the extra launch.
 #include <algorithm>
+#include <climits>
 
 #include "devmath.h"
 #include "internal.h"
+#include "lanes.h"
 #include "nonfinite.h"
 
 namespace sapphire {
@@ -407,7 +409,8 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
 // gemm_prep_kernel formed, or a plain x (no sum of parts, norm or residual).
 enum StageMode { kStageFull = 0, kStagePrepared = 1, kStagePlain = 2 };
 
-template <int DT, int MODE, int NW>
+// GREEDY: the greedy form (out.tokens): rows are reduced to per-sequence partials, not stored.
+template <int DT, int MODE, int NW, bool GREEDY = false>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4))) void gemm_mfma_kernel(
     const uint8_t *__restrict__ wq, uint32_t q_bytes, const uint8_t *__restrict__ wsc, uint32_t s_bytes, GemmIn in,
     int batch, int M, int K, int cb, GemmOut out, float *__restrict__ Yp, const PrepChunk *__restrict__ prep, int ks) {
@@ -742,8 +745,41 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
         dst = Yp + (size_t)blockIdx.y * batch * M;
         ldd = M;
     }
+    // greedy form: the best (value, row) so far of sequence 4m + r over the wave's tiles
+    float bv[4];
+    int bi[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        bv[r] = -INFINITY;
+        bi[r] = INT_MAX;
+    }
     // the results of tile ct: rows (or GeGLU pairs) times the range scales, plus the non-finite fold
     auto store_tile = [&](int ct, const f4 &a) {
+        if constexpr (GREEDY) {
+            // the tile's best row per sequence, over the 16 lanes n of each lane group m. A NaN in
+            // row 0 wins outright (sample_greedy keeps index 0, as no value compares greater than
+            // its starting NaN); other NaN rows and rows past M become (-inf, INT_MAX), which never
+            // wins, so every pair compares and no lane keeps a NaN that blocks its partners.
+            const int row = ct * kTileRows + n;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float val = a[r] * sc[r];
+                int idx = row;
+                if (row < M && any_nf && 4 * m + r < batch)
+                    val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, row, 4 * m + r);
+                if (row >= M || val != val) {
+                    const bool first = row == 0;
+                    val = first ? INFINITY : -INFINITY;
+                    idx = first ? 0 : INT_MAX;
+                }
+                lanes::row16_best(val, idx, devmath::greedy_better);
+                if (devmath::greedy_better(val, idx, bv[r], bi[r])) {
+                    bv[r] = val;
+                    bi[r] = idx;
+                }
+            }
+            return;
+        }
         if (out.geglu) {
             // lanes n < 8 hold gate rows 8t'+n, lanes n + 8 the matching up rows
 #pragma unroll
@@ -767,6 +803,32 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
                         if (any_nf) val += chunk_fold<DT>(nfc, wq, wsc, nb, b0, b1 - b0, row, 4 * m + r);
                         dst[out.y_blocked ? block_order_index(4 * m + r, row) : (size_t)(4 * m + r) * ldd + row] = val;
                     }
+        }
+    };
+    // greedy form: the workgroup's best per sequence, from the waves' through LDS once every
+    // wave is past its last operand read; one (value, index) partial per sequence and workgroup
+    auto greedy_finish = [&]() {
+        __syncthreads();
+        float *wv = reinterpret_cast<float *>(xs);
+        int *wi = reinterpret_cast<int *>(xs) + NW * kBatchMax;
+        if (n == 0)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                wv[wid * kBatchMax + 4 * m + r] = bv[r];
+                wi[wid * kBatchMax + 4 * m + r] = bi[r];
+            }
+        __syncthreads();
+        if (tid < batch) {
+            float v = wv[tid];
+            int i = wi[tid];
+            for (int w = 1; w < NW; ++w)
+                if (devmath::greedy_better(wv[w * kBatchMax + tid], wi[w * kBatchMax + tid], v, i)) {
+                    v = wv[w * kBatchMax + tid];
+                    i = wi[w * kBatchMax + tid];
+                }
+            float *o = out.amax + ((size_t)tid * gridDim.x + blockIdx.x) * 2;
+            o[0] = v;
+            o[1] = __int_as_float(i);
         }
     };
     int ct = t0, cg = 0;                               // tile and group of the unit multiplied
@@ -795,6 +857,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
                 }
             }
         }
+        if constexpr (GREEDY) greedy_finish();
         return;
     }
     // Every pass issues the loads of all RING slots (past the last unit they repeat it), so
@@ -831,6 +894,33 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4)))
             store_tile(t0, acc);
         }
     }
+    if constexpr (GREEDY) greedy_finish();
+}
+
+// grid (batch), one wave: tokens[b] = the best of sequence b's nparts workgroup partials
+// (sample_greedy, utils.c:145-156; 0 when no row is above -inf)
+__global__ void gemm_greedy_finish_kernel(const float *__restrict__ part, int nparts, int n, int *__restrict__ tokens) {
+    const float *p = part + (size_t)blockIdx.x * nparts * 2;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int j = threadIdx.x; j < nparts; j += kWave) {
+        const float v = p[2 * j];
+        const int i = __float_as_int(p[2 * j + 1]);
+        if (devmath::greedy_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, kWave);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (devmath::greedy_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (threadIdx.x == 0) tokens[blockIdx.x] = bi >= 0 && bi < n ? bi : 0;
 }
 
 // y[b * ldy + r] = sum over c of parts[c * stride + b * M + r], in chunk order.
@@ -867,6 +957,9 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 size_t partials_bytes(int M, int nsplit) { return nsplit > 1 ? (size_t)nsplit * kBatchMax * M * sizeof(float) : 0; }
 size_t prep_offset(int M, int nsplit) { return (partials_bytes(M, nsplit) + 255) & ~size_t(255); }
 size_t prep_stride() { return (sizeof(PrepChunk) + 255) & ~size_t(255); }
+// the greedy form's partials: (value, index) per sequence and workgroup, after the prep chunks
+size_t amax_offset(int M, int nsplit) { return prep_offset(M, nsplit) + (size_t)nsplit * prep_stride(); }
+constexpr size_t kAmaxBytes = (size_t)kBatchMax * kMaxGrid * 2 * sizeof(float);
 
 // One pass of at most 16 sequences. With `prep` the input transform runs once per sequence
 // and chunk (gemm_prep_kernel, into the workspace) instead of in every workgroup.
@@ -909,20 +1002,32 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
     float *Yp = static_cast<float *>(ws);
     const int mode = pc ? kStagePrepared
                         : (!in.parts && !in.w_delta && !in.w_norm && !in.resid_out) ? kStagePlain : kStageFull;
+    if (out.tokens && mode == kStageFull) {
+        set_error("batched GEMM: the greedy form needs a workspace");
+        return -1;
+    }
     decltype(&gemm_mfma_kernel<DT_Q4_0, kStageFull, kWaves>) kern;
 #define SPH_GEMM_PICK(DTV, NWV)                                                                                    \
-    kern = mode == kStagePrepared ? gemm_mfma_kernel<DTV, kStagePrepared, NWV>                                     \
-           : mode == kStagePlain  ? gemm_mfma_kernel<DTV, kStagePlain, NWV>                                        \
-                                  : gemm_mfma_kernel<DTV, kStageFull, NWV>;
+    kern = out.tokens ? (mode == kStagePrepared ? gemm_mfma_kernel<DTV, kStagePrepared, NWV, true>                 \
+                                                : gemm_mfma_kernel<DTV, kStagePlain, NWV, true>)                   \
+           : mode == kStagePrepared ? gemm_mfma_kernel<DTV, kStagePrepared, NWV>                                   \
+           : mode == kStagePlain    ? gemm_mfma_kernel<DTV, kStagePlain, NWV>                                      \
+                                    : gemm_mfma_kernel<DTV, kStageFull, NWV>;
     if (dt == DT_Q4_0) {
         if (wide) { SPH_GEMM_PICK(DT_Q4_0, kWavesWide) } else { SPH_GEMM_PICK(DT_Q4_0, kWaves) }
     } else {
         if (wide) { SPH_GEMM_PICK(DT_Q8_0, kWavesWide) } else { SPH_GEMM_PICK(DT_Q8_0, kWaves) }
     }
 #undef SPH_GEMM_PICK
+    GemmOut o = out;
+    if (o.tokens) o.amax = reinterpret_cast<float *>(static_cast<char *>(ws) + amax_offset(M, nsplit));
     hipLaunchKernelGGL(kern, grid, dim3(nw * kWave), 0, st, wb, (uint32_t)so, wb + so, (uint32_t)sbytes, in, batch, M,
-                       K, cb, out, Yp, (const PrepChunk *)pc, ks);
+                       K, cb, o, Yp, (const PrepChunk *)pc, ks);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
+    if (o.tokens) {
+        hipLaunchKernelGGL(gemm_greedy_finish_kernel, dim3(batch), dim3(kWave), 0, st, o.amax, gx, M, o.tokens);
+        return hip_ok(hipGetLastError(), "greedy finish launch") ? 0 : -1;
+    }
     if (nsplit > 1 && !out.parts) return launch_sum_parts(Yp, nsplit, (size_t)batch * M, batch, M, out.y, out.ldy, st);
     return 0;
 }
@@ -937,7 +1042,7 @@ int gemm_splits(int K) {
 
 size_t gemm_workspace_bytes(int M, int K) {
     const int nsplit = gemm_splits(K);
-    return prep_offset(M, nsplit) + (size_t)nsplit * prep_stride();
+    return amax_offset(M, nsplit) + kAmaxBytes;
 }
 
 int launch_sum_parts(const float *parts, int nparts, size_t stride, int batch, int M, float *y, int ldy,
@@ -960,7 +1065,9 @@ int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const G
                     (!in.w_delta || in.parts) && (!in.resid_out || (aligned16(in.resid_out) && in.ldr % 4 == 0)) &&
                     (!norms || (nsplit == 1 && aligned16(in.w_delta ? in.w_delta : in.w_norm) &&
                                 (!in.w_norm || aligned16(in.w_norm)))) &&
-                    (out.parts || (out.y && (out.y_blocked || out.ldy >= (out.geglu ? M / 2 : M)))) &&
+                    (out.parts || out.tokens || (out.y && (out.y_blocked || out.ldy >= (out.geglu ? M / 2 : M)))) &&
+                    (!out.tokens || (nsplit == 1 && !out.parts && !out.geglu && !out.y_blocked && ws &&
+                                     (reinterpret_cast<uintptr_t>(ws) & 255u) == 0)) &&
                     (!out.geglu || (nsplit == 1 && M % 16 == 0 && !out.parts)) &&
                     (out.parts || nsplit == 1 || ((reinterpret_cast<uintptr_t>(ws) & 255u) == 0 && ws)) &&
                     (!in.x_blocked || (in.x && !in.parts && !norms && !in.resid_out)) &&

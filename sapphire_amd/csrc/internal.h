@@ -107,6 +107,11 @@ struct GemmOut {
     // y in block order (block_order_index over the M or M / 2 outputs; ldy unused): one K
     // chunk only, no parts
     bool y_blocked = false;
+    // greedy form: instead of y, tokens[b] = the first index of the maximum of sequence b's
+    // rows (sample_greedy, utils.c:145-156). One K chunk only, no parts or GeGLU; the
+    // workgroups' partials go to the workspace, which is then required.
+    int *tokens = nullptr;
+    float *amax = nullptr;   // set by the launch: the partials in the workspace
 };
 int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
                          void *ws, hipStream_t s);

@@ -31,5 +31,22 @@ __device__ __forceinline__ float row16_max(float v) {
     return v;
 }
 
+// The greedy (value, index) best over each row of 16 lanes, left in every lane of the row: the
+// steps of row16_max, each pairing a lane with a partner that takes the same pair, under
+// `better` (a total order on (value, index) pairs, so every lane ends with the same pair).
+template <class Better>
+__device__ __forceinline__ void row16_best(float &v, int &i, Better better) {
+    auto step = [&](float ov, int oi) {
+        if (better(ov, oi, v, i)) {
+            v = ov;
+            i = oi;
+        }
+    };
+    step(dpp_mov<0xB1>(v), __float_as_int(dpp_mov<0xB1>(__int_as_float(i))));
+    step(dpp_mov<0x4E>(v), __float_as_int(dpp_mov<0x4E>(__int_as_float(i))));
+    step(dpp_mov<0x141>(v), __float_as_int(dpp_mov<0x141>(__int_as_float(i))));
+    step(dpp_mov<0x140>(v), __float_as_int(dpp_mov<0x140>(__int_as_float(i))));
+}
+
 }  // namespace lanes
 }  // namespace sapphire

@@ -195,6 +195,25 @@ int sapphire_gemm_q_dev(int dt, int layout, const void *w, int M, int K, const f
     return launch_gemm_tiled(dt, w, M, K, X, batch, Y, ws, s);
 }
 
+int sapphire_gemm_q_greedy_dev(int dt, const void *w, int M, int K, const float *X, int batch, int *tokens, void *ws,
+                               void *stream) {
+    if (!valid_quant_args(dt, w, M, K) || !X || !tokens || !ws || batch <= 0 || batch > 16) {
+        if (batch <= 0 || batch > 16) set_error("greedy GEMM: batch must be 1..16 (got %d)", batch);
+        else if (!ws) set_error("greedy GEMM: needs a workspace");
+        return -1;
+    }
+    if (!tiled_layout_ok(dt, M, K) || gemm_splits(K) != 1) {
+        set_error("greedy GEMM: TILED weights with K a multiple of 128 and at most 1152 (K=%d)", K);
+        return -1;
+    }
+    GemmIn gi;
+    gi.x = X;
+    gi.ldx = K;
+    GemmOut go;
+    go.tokens = tokens;
+    return launch_gemm_tiled_ex(dt, w, M, K, batch, gi, go, ws, as_stream(stream));
+}
+
 int sapphire_gemm_splits(int K) { return K > 0 && K % kBlock == 0 ? gemm_splits(K) : 0; }
 
 int sapphire_gemm_q_fused_dev(int dt, const void *w, int M, int K, int batch, const sapphire_gemm_input_t *in,
