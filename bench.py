@@ -5,9 +5,9 @@ Workload (the LM-head configuration, 262144 x 640): one step is
   * Q8_0 GEMV 262144 x 640 (36-byte blocks) -> fp32 logits -> fused softmax + argmax
   * Q4_0 GEMV 262144 x 640 (20-byte blocks) -> fp32 logits -> fused softmax + argmax
 on seeded synthetic weights (scale |N(0,0.01)|, uniform quants) and an N(0,1) hidden
-vector, all resident in HBM before timing. Copies of the weights are rotated (two of the
-Q8_0 matrix, 380 MB; three of the Q4_0 one, 318 MB) so that no step finds its weights in
-the 256 MB last-level cache.
+vector, all resident in HBM before timing. Copies of the weights are rotated (four of the
+Q8_0 matrix, 760 MB; six of the Q4_0 one, 636 MB) so that the steps read their weights from
+HBM, not the 256 MB last-level cache.
 
 value = algorithmic bytes of a step (M*ceil(K/32)*B_blk + 4K + 4M per GEMV, plus 1 MiB
 read + 1 MiB written per softmax) / step time.
@@ -170,16 +170,16 @@ def decode_leg(steps: int, cpu: bool, seed: int = 20260101, prefill: int = 1024)
 
 def lm_head_gemm(blocks, batch: int, seed: int, iters: int = 20):
     """The batched decode's dominant kernel alone: Q4_0 262144 x 1152 times 16 vectors on the
-    matrix cores (two weight copies rotated, 2 x 189 MB > the 256 MB last-level cache)."""
+    matrix cores (four weight copies rotated, 4 x 189 MB > the 256 MB last-level cache)."""
     from sapphire_amd import load, synth
     from sapphire_amd.device import DeviceArray, QMatrix, Timer, check
     L = load()
     m, k = blocks.shape[0], blocks.shape[1] * 32
-    qs = [QMatrix(synth.Q4_0, blocks, layout=2) for _ in range(2)]
+    qs = [QMatrix(synth.Q4_0, blocks, layout=2) for _ in range(4)]
     X = DeviceArray.from_numpy(synth.normal_f32((batch, k), seed, 77))
     Y = DeviceArray.empty(batch * m)
     ws = DeviceArray(L.sapphire_gemm_workspace_bytes(synth.Q4_0, m, k))
-    run = lambda i: check(L.sapphire_gemm_q_dev(synth.Q4_0, 2, qs[i % 2].ptr(), m, k, X.ptr, batch, Y.ptr,  # noqa: E731
+    run = lambda i: check(L.sapphire_gemm_q_dev(synth.Q4_0, 2, qs[i % 4].ptr(), m, k, X.ptr, batch, Y.ptr,  # noqa: E731
                                                 ws.ptr, None))
     for i in range(4):
         run(i)
@@ -198,7 +198,7 @@ def lm_head_gemm(blocks, batch: int, seed: int, iters: int = 20):
     # the form a greedy decode step runs: the same rows reduced to one token per sequence
     # inside the GEMM (no logits stored), then one short kernel over the workgroups' partials
     T = DeviceArray.empty(batch, np.int32)
-    run_g = lambda i: check(L.sapphire_gemm_q_greedy_dev(synth.Q4_0, qs[i % 2].ptr(), m, k, X.ptr, batch,  # noqa: E731
+    run_g = lambda i: check(L.sapphire_gemm_q_greedy_dev(synth.Q4_0, qs[i % 4].ptr(), m, k, X.ptr, batch,  # noqa: E731
                                                          T.ptr, ws.ptr, None))
     for i in range(4):
         run_g(i)
@@ -208,7 +208,7 @@ def lm_head_gemm(blocks, batch: int, seed: int, iters: int = 20):
         run_g(i)
     ug = t.stop() / iters * 1e3
     algo_g = m * (k // 32) * synth.BLOCK_BYTES[synth.Q4_0] + 4 * batch * k + 4 * batch
-    out["greedy"] = {
+    out["greedy_with_finish_kernel"] = {
         "us": round(ug, 2), "GB/s": round(algo_g / (ug * 1e-6) / 1e9, 1),
         "frac_hbm_peak": round(algo_g / (ug * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "algorithmic_bytes": algo_g,
     }
@@ -272,8 +272,12 @@ def main() -> int:
     w8 = synth.quant_matrix(synth.Q8_0, M_LM, K_LM, seed, 1)
     w4 = synth.quant_matrix(synth.Q4_0, M_LM, K_LM, seed, 2)
     x = synth.normal_f32(K_LM, seed, 3)
-    n_sets = 2        # Q8_0 copies: 2 x 190 MB
-    n_sets4 = 3       # Q4_0 copies: 3 x 106 MB (two would fit the 256 MB last-level cache)
+    # Weight copies rotated so that the launches read HBM, not the 256 MB last-level cache. Of
+    # copies read back to back the first of each cycle keeps part of itself in that cache (about
+    # 10 % faster in a read-only probe), so the rotation is long: at most one launch in four (six)
+    # finds its copy partly cached.
+    n_sets = 4        # Q8_0 copies: 4 x 190 MB (also the BF16 / F32 copies)
+    n_sets4 = 6       # Q4_0 copies: 6 x 106 MB
     LAY = 2   # TILED: the matrix-core layout kernel_gemv uses for matrices this long
     q8 = [QMatrix(synth.Q8_0, w8, layout=LAY) for _ in range(n_sets)]
     q4 = [QMatrix(synth.Q4_0, w4, layout=LAY) for _ in range(n_sets4)]
@@ -336,7 +340,7 @@ def main() -> int:
     sm_ms = time_alone(lambda i: check(L.sapphire_softmax_argmax_dev(logits.ptr, M_LM, probs.ptr, arg.ptr, stream)))
 
     # The same LM head held as BF16 / F32 rows (a weight-tied embedding), on the element
-    # types' own GEMV kernel; two copies of each rotate so the weights come from HBM.
+    # types' own GEMV kernel; four copies of each rotate so the weights come from HBM.
     # the small GEMVs of one decode layer (Gemma-3-270M MLP shapes), PACKED layout: per call
     # time of 200 back-to-back launches on the bench stream (weights stay in the 256 MB MALL,
     # so these are launch- and latency-bound, not HBM-bound)
