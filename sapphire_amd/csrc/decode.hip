@@ -146,13 +146,19 @@ __device__ __forceinline__ Lanes<DPL> load_lanes(const float *p) {
     return r;
 }
 
-// Workgroup b takes positions [t0, t1) of the layer's attention range; each wave walks
-// every fourth of them with a running (max, sum, weighted V) per head; the waves are then
+// Threads of the attention workgroup over a batch's slices (16 per sequence): eight waves.
+// Measured on the Gemma-3-1B step with 16 sequences: 1.543 ms per step against 1.576 ms with
+// four waves (one per SIMD, every dependent step of the position loop exposed) and 1.586 ms
+// with sixteen (four positions in flight per wave to fit 128 VGPRs).
+constexpr int kAttnThreadsBatch = 512;
+
+// Workgroup b takes positions [t0, t1) of the layer's attention range; each of its NT / 64
+// waves walks every (NT / 64)-th of them with a running (max, sum, weighted V) per head; the waves are then
 // merged and the slice's partial stored. Lane l owns dims [l*DPL, l*DPL + DPL). Scores are
 // summed by DPP into wave-uniform values and the weights are powers of two of log2-scaled
 // scores (one exp2 each). NKV: the K/V heads (1 or 2, a.nkv).
-template <int DPL, int NH, int NKV>
-__global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
+template <int DPL, int NH, int NKV, int NT>
+__global__ __launch_bounds__(NT) void dec_attn_part_kernel(AttnArgs a) {
     {   // sequence blockIdx.y of a batch
         const size_t b = blockIdx.y;
         a.qkv += b * a.qkv_stride;
@@ -166,21 +172,21 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     __shared__ float ks[kAttnMaxKV];
     __shared__ float part8[8 * 16];
     __shared__ float ss[16];
-    __shared__ float wm[kThreads / kWave][NH], wsum[kThreads / kWave][NH];
-    __shared__ float wo[kThreads / kWave][NH][kWave * DPL];
-    __shared__ float wx[kThreads / kWave][NH];   // wave merge weights
+    __shared__ float wm[NT / kWave][NH], wsum[NT / kWave][NH];
+    __shared__ float wo[NT / kWave][NH][kWave * DPL];
+    __shared__ float wx[NT / kWave][NH];   // wave merge weights
     __shared__ float wmax[NH], wtot[NH];
     const int hd = a.hd, half = hd / 2;
     constexpr int nkv = NKV;
     // Loads that wait for nothing go out first: q | k | v as projected and the QK-norm gammas
     // (thread t applies the norm and RoPE to pair i = t mod hd/2 of every head, the same i for
-    // every head as 256 is a multiple of hd/2).
-    constexpr int kRawRegs = (kAttnMaxQ + 2 * kAttnMaxKV) / kThreads;
+    // every head as NT is a multiple of hd/2).
+    constexpr int kRawRegs = (kAttnMaxQ + 2 * kAttnMaxKV) / NT;
     const int nraw = (NH + 2 * nkv) * hd;
     float rv[kRawRegs];
 #pragma unroll
     for (int e = 0; e < kRawRegs; ++e) {
-        const int i = threadIdx.x + e * kThreads;
+        const int i = threadIdx.x + e * NT;
         rv[e] = i < nraw ? a.qkv[i] : 0.f;
     }
     const int pi = threadIdx.x % half;
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     // while the current one is used (two register sets). Rows come from the cache; the row of
     // the current position is taken from this kernel's own K (after RoPE) and V.
     constexpr int PF = 8 / NKV;
-    constexpr int NW = kThreads / kWave;
+    constexpr int NW = NT / kWave;
     float kr[PF][NKV][DPL], vr[PF][NKV][DPL];
     float nk[PF][NKV][DPL], nv[PF][NKV][DPL];   // the next batch
     // A row outside the slice (or the current position's) reads row 0 instead, in bounds, and
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
 
 #pragma unroll
     for (int e = 0; e < kRawRegs; ++e) {
-        const int i = threadIdx.x + e * kThreads;
+        const int i = threadIdx.x + e * NT;
         if (i < nraw) raw[i] = rv[e];
     }
     __syncthreads();
@@ -233,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void dec_attn_part_kernel(AttnArgs a) {
     vectors_sum_sq(raw, NH + nkv, hd, part8, ss);
     if (threadIdx.x < NH + nkv) ss[threadIdx.x] = rms_inv_of(ss[threadIdx.x], hd, a.eps);
     __syncthreads();
-    for (int v = threadIdx.x / half; v < NH + nkv; v += kThreads / half) {
+    for (int v = threadIdx.x / half; v < NH + nkv; v += NT / half) {
         const bool isq = v < NH;
         const float r = ss[v], g0 = isq ? gq0 : gk0, g1 = isq ? gq1 : gk1;
         const float *p = raw + (size_t)v * hd;
@@ -567,9 +573,17 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     // splits per sequence: enough workgroups in total, without cutting a sequence's positions
     // into slivers once a batch fills the GPU
     const int ns = a.batch >= 4 ? kAttnSplitBatch : kAttnSplit;
+    // a batch's slices are longer: eight waves per workgroup walk them (one wave per SIMD would
+    // expose every dependent step of the position loop)
+    const bool wide = ns == kAttnSplitBatch;
 #define SPH_ATTN(DPLV, NHV, NKVV)                                                                              \
     if (dpl == DPLV && a.nh == NHV && a.nkv == NKVV) {                                                         \
-        hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV, NKVV>), dim3(ns, a.batch), dim3(kThreads), 0, s, a); \
+        if (wide)                                                                                              \
+            hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV, NKVV, kAttnThreadsBatch>), dim3(ns, a.batch),    \
+                               dim3(kAttnThreadsBatch), 0, s, a);                                               \
+        else                                                                                                   \
+            hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV, NKVV, kThreads>), dim3(ns, a.batch),             \
+                               dim3(kThreads), 0, s, a);                                                        \
     } else
     SPH_ATTN(1, 4, 1) SPH_ATTN(2, 4, 1) SPH_ATTN(4, 4, 1) SPH_ATTN(1, 8, 1) SPH_ATTN(2, 8, 1) SPH_ATTN(4, 8, 1)
     SPH_ATTN(1, 4, 2) SPH_ATTN(2, 4, 2) SPH_ATTN(4, 4, 2) SPH_ATTN(1, 8, 2) SPH_ATTN(2, 8, 2) SPH_ATTN(4, 8, 2) {
