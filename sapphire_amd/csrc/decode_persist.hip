@@ -138,18 +138,6 @@ __device__ __forceinline__ float par_sum_sq(const float *v, int K, float *sh) {
     return (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
-// resid += rmsnorm_delta(dl, w) (attention.c:358-366, transformer.c:231-239)
-__device__ __forceinline__ void add_norm_delta(float *resid, const float *dl, const VecRegs &w, int K, float eps,
-                                               float *sh) {
-    const float r = rms_inv_of(par_sum_sq(dl, K, sh), K, eps);
-#pragma unroll
-    for (int e = 0; e < kVecRegs; ++e) {
-        const int i = threadIdx.x + e * kThreads;
-        if (i < K) resid[i] = __fadd_rn(resid[i], __fmul_rn(__fmul_rn(dl[i], r), __fadd_rn(1.0f, w.v[e])));
-    }
-    __syncthreads();
-}
-
 // xs = rmsnorm_delta(resid, w) (normalization.c:104-117)
 __device__ __forceinline__ void norm_to(float *xs, const float *resid, const VecRegs &w, int K, float eps,
                                         float *sh) {
@@ -158,6 +146,39 @@ __device__ __forceinline__ void norm_to(float *xs, const float *resid, const Vec
     for (int e = 0; e < kVecRegs; ++e) {
         const int i = threadIdx.x + e * kThreads;
         if (i < K) xs[i] = __fmul_rn(__fmul_rn(resid[i], r), __fadd_rn(1.0f, w.v[e]));
+    }
+    __syncthreads();
+}
+
+// resid += rmsnorm_delta(dl, wd) (attention.c:358-366, transformer.c:231-239), then
+// xs = rmsnorm_delta(resid, wn) with the arithmetic of norm_to. Each thread sums the squares of
+// the residual elements it has just updated, which are the elements par_sum_sq gives it, in
+// its order, so the second norm is bit-identical to norm_to on the stored residual but needs no
+// barrier before its sum and no second read of the residual from LDS. Its wave sums go to
+// sh[4..7]: other waves may still be reading the first sum's sh[0..3].
+__device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, const float *dl, const VecRegs &wd,
+                                                    const VecRegs &wn, int K, float eps, float *sh) {
+    const float r1 = rms_inv_of(par_sum_sq(dl, K, sh), K, eps);
+    float nv[kVecRegs];
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < kVecRegs; ++e) {
+        const int i = threadIdx.x + e * kThreads;
+        nv[e] = 0.f;
+        if (i < K) {
+            nv[e] = __fadd_rn(resid[i], __fmul_rn(__fmul_rn(dl[i], r1), __fadd_rn(1.0f, wd.v[e])));
+            resid[i] = nv[e];
+            acc = __builtin_fmaf(nv[e], nv[e], acc);
+        }
+    }
+    acc = wave_sum_uniform(acc);
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[4 + threadIdx.x / kWave] = acc;
+    __syncthreads();
+    const float r2 = rms_inv_of((sh[4] + sh[5]) + (sh[6] + sh[7]), K, eps);
+#pragma unroll
+    for (int e = 0; e < kVecRegs; ++e) {
+        const int i = threadIdx.x + e * kThreads;
+        if (i < K) xs[i] = __fmul_rn(__fmul_rn(nv[e], r2), __fadd_rn(1.0f, wn.v[e]));
     }
     __syncthreads();
 }
@@ -494,9 +515,10 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
                 VecRegs wd;
                 wd.load(a.layers[l - 1].n_ffn_post, H);
                 if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag)) return;
-                add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
+                add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
+            } else {
+                norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
             }
-            norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
             g.finish(s.xs, a.t_qkv, ep + 1);
         }
         if (!attn_stage<DPL, NH>(a, L, pos, ep + 1, ep + 2, s)) return;
@@ -514,8 +536,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             wd.load(L.n_attn_post, H);
             wn.load(L.n_ffn, H);
             if (!gather<kVecRegs>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag)) return;
-            add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
-            norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
+            add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
             g.finish(s.xs, a.t_g, ep + 5);
         }
         {   // 6: down
@@ -531,8 +552,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     wn.load(a.norm_final, H);
     const uint32_t ep_last = base + 8u * (uint32_t)(a.n_layers - 1) + 6u;
     if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag)) return;
-    add_norm_delta(s.resid, s.dl, wd, H, a.eps, s.sh);
-    norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
+    add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < H; i += kThreads) a.xfin[i] = s.xs[i];
 }
