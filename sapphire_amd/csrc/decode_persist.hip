@@ -70,10 +70,13 @@ struct alignas(16) PersistLds {
 // dst[j] = value of word *src(j) for j < n, once its tag equals `tag`; thread t takes
 // j = t + 256 e. All loads are issued first, then only stale words are polled again. Returns
 // false when a word is still stale after spin_limit polls (and counts the failure in *err).
-// Synchronises the workgroup; the result is the same in every thread.
+// Synchronises the workgroup; the result is the same in every thread. With sq set, the wave
+// sums of the squares of the gathered values go to sq[0..3] before that barrier: each thread
+// sums its own values in the order par_sum_sq takes them, so (sq[0] + sq[1]) + (sq[2] + sq[3])
+// afterwards is par_sum_sq(dst, n), bit for bit.
 template <int MAXE, class Src>
 __device__ __forceinline__ bool gather(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
-                                       int *flag) {
+                                       int *flag, float *sq = nullptr) {
     uint64_t w[MAXE];
 #pragma unroll
     for (int e = 0; e < MAXE; ++e) {
@@ -96,10 +99,19 @@ __device__ __forceinline__ bool gather(Src src, int n, uint32_t tag, float *dst,
             if (j < n && !tag_is(w[e], tag)) w[e] = get_tagged(src(j));
         }
     }
+    float acc = 0.f;
 #pragma unroll
     for (int e = 0; e < MAXE; ++e) {
         const int j = threadIdx.x + e * kThreads;
-        if (j < n) dst[j] = __uint_as_float((uint32_t)w[e]);
+        if (j < n) {
+            const float v = __uint_as_float((uint32_t)w[e]);
+            dst[j] = v;
+            acc = __builtin_fmaf(v, v, acc);
+        }
+    }
+    if (sq) {
+        acc = wave_sum_uniform(acc);
+        if ((threadIdx.x & (kWave - 1)) == 0) sq[threadIdx.x / kWave] = acc;
     }
     __syncthreads();
     const bool ok = *flag == 0;
@@ -151,14 +163,15 @@ __device__ __forceinline__ void norm_to(float *xs, const float *resid, const Vec
 }
 
 // resid += rmsnorm_delta(dl, wd) (attention.c:358-366, transformer.c:231-239), then
-// xs = rmsnorm_delta(resid, wn) with the arithmetic of norm_to. Each thread sums the squares of
-// the residual elements it has just updated, which are the elements par_sum_sq gives it, in
-// its order, so the second norm is bit-identical to norm_to on the stored residual but needs no
-// barrier before its sum and no second read of the residual from LDS. Its wave sums go to
-// sh[4..7]: other waves may still be reading the first sum's sh[0..3].
+// xs = rmsnorm_delta(resid, wn) with the arithmetic of norm_to. dl was gathered with its wave
+// sums of squares in sh[0..3] (gather's sq). Each thread sums the squares of the residual
+// elements it has just updated, which are the elements par_sum_sq gives it, in its order, so
+// the second norm is bit-identical to norm_to on the stored residual but needs no barrier
+// before its sum and no second read of the residual from LDS. Its wave sums go to sh[4..7]:
+// other waves may still be reading sh[0..3].
 __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, const float *dl, const VecRegs &wd,
                                                     const VecRegs &wn, int K, float eps, float *sh) {
-    const float r1 = rms_inv_of(par_sum_sq(dl, K, sh), K, eps);
+    const float r1 = rms_inv_of((sh[0] + sh[1]) + (sh[2] + sh[3]), K, eps);
     float nv[kVecRegs];
     float acc = 0.f;
 #pragma unroll
@@ -514,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             if (l > 0) {
                 VecRegs wd;
                 wd.load(a.layers[l - 1].n_ffn_post, H);
-                if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag)) return;
+                if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
                 add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
             } else {
                 norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
@@ -535,7 +548,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             VecRegs wd, wn;
             wd.load(L.n_attn_post, H);
             wn.load(L.n_ffn, H);
-            if (!gather<kVecRegs>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag)) return;
+            if (!gather<kVecRegs>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
             add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
             g.finish(s.xs, a.t_g, ep + 5);
         }
@@ -551,7 +564,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     wd.load(a.layers[a.n_layers - 1].n_ffn_post, H);
     wn.load(a.norm_final, H);
     const uint32_t ep_last = base + 8u * (uint32_t)(a.n_layers - 1) + 6u;
-    if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag)) return;
+    if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
     add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < H; i += kThreads) a.xfin[i] = s.xs[i];
