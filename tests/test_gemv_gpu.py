@@ -50,8 +50,13 @@ def test_gemv_matches_oracle(hip, oracle, dtype, layout, shape):
     assert ok, f"max abs err {err}"
 
 
+# On a 256-CU device 43963 and 55997 rows leave tiles after the full rounds of the grid
+# stride that are split over a workgroup's waves (Q8_0 at 43963: two tail tiles per
+# workgroup, two waves each; Q4_0 at 55997 and 65536: one per workgroup over three waves),
+# with the last tile ragged; K = 640 runs the double-buffered walk, K = 1152 the single one.
 TILED_SHAPES = [
     (16, 640), (1000, 640), (4099, 1024), (333, 1152), (17, 1152), (65536, 640), (20000, 1152),
+    (43963, 640), (55997, 640), (43963, 1152), (55997, 1152),
 ]
 
 
