@@ -38,7 +38,7 @@ namespace {
 constexpr int kLpr = 16;                          // lanes per GEMV row
 constexpr int kRpw = kWave / kLpr;                // rows per wave-step
 constexpr int kSlots = 4;                         // (wave-step, block) slots per lane in one GEMV stage
-constexpr int kCombMax = 4096;                    // gathered partial words per workgroup in the combine
+constexpr int kCombMax = 2048;                    // gathered partial words per workgroup in the combine
 constexpr int kVecRegs = kDecMaxK / kThreads;     // vector elements per thread
 
 __device__ __forceinline__ void put_tagged(uint64_t *p, float v, uint32_t tag) {
@@ -327,7 +327,7 @@ __device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L
         sn[e] = ok ? L.sin_t[(size_t)pos * hd + i] : 0.f;
     }
 
-    if (!gather<(kAttnMaxQ + 2 * kAttnMaxKV) / kThreads>(Contig{a.t_qkv}, (NH + 2 * nkv) * hd, tag_in, s.raw,
+    if (!gather<((NH + 2 * nkv) * kWave * DPL + kThreads - 1) / kThreads>(Contig{a.t_qkv}, (NH + 2 * nkv) * hd, tag_in, s.raw,
                                                           a.spin_limit, a.err, &s.flag))
         return false;
     // rmsnorm_delta of every q and k head vector, then the half-split rotation
