@@ -39,7 +39,7 @@ constexpr int kLpr = 16;                          // lanes per GEMV row
 constexpr int kRpw = kWave / kLpr;                // rows per wave-step
 constexpr int kSlots = 4;                         // (wave-step, block) slots per lane in one GEMV stage
 constexpr int kCombMax = 2048;                    // gathered partial words per workgroup in the combine
-constexpr int kVecRegs = kDecMaxK / kThreads;     // vector elements per thread
+constexpr int kVecRegs = kDecMaxK / kThreads;     // vector elements per thread (longest vector)
 
 __device__ __forceinline__ void put_tagged(uint64_t *p, float v, uint32_t tag) {
     __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -125,11 +125,12 @@ struct Contig {
 };
 
 // Elements t + 256 e of a K-long weight vector in registers (loaded before a wait).
+template <int R>
 struct VecRegs {
-    float v[kVecRegs];
+    float v[R];
     __device__ __forceinline__ void load(const float *__restrict__ p, int K) {
 #pragma unroll
-        for (int e = 0; e < kVecRegs; ++e) {
+        for (int e = 0; e < R; ++e) {
             const int i = threadIdx.x + e * kThreads;
             v[e] = i < K ? p[i] : 0.f;
         }
@@ -151,11 +152,12 @@ __device__ __forceinline__ float par_sum_sq(const float *v, int K, float *sh) {
 }
 
 // xs = rmsnorm_delta(resid, w) (normalization.c:104-117)
-__device__ __forceinline__ void norm_to(float *xs, const float *resid, const VecRegs &w, int K, float eps,
+template <int R>
+__device__ __forceinline__ void norm_to(float *xs, const float *resid, const VecRegs<R> &w, int K, float eps,
                                         float *sh) {
     const float r = rms_inv_of(par_sum_sq(resid, K, sh), K, eps);
 #pragma unroll
-    for (int e = 0; e < kVecRegs; ++e) {
+    for (int e = 0; e < R; ++e) {
         const int i = threadIdx.x + e * kThreads;
         if (i < K) xs[i] = __fmul_rn(__fmul_rn(resid[i], r), __fadd_rn(1.0f, w.v[e]));
     }
@@ -169,13 +171,14 @@ __device__ __forceinline__ void norm_to(float *xs, const float *resid, const Vec
 // the second norm is bit-identical to norm_to on the stored residual but needs no barrier
 // before its sum and no second read of the residual from LDS. Its wave sums go to sh[4..7]:
 // other waves may still be reading sh[0..3].
-__device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, const float *dl, const VecRegs &wd,
-                                                    const VecRegs &wn, int K, float eps, float *sh) {
+template <int R>
+__device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, const float *dl, const VecRegs<R> &wd,
+                                                    const VecRegs<R> &wn, int K, float eps, float *sh) {
     const float r1 = rms_inv_of((sh[0] + sh[1]) + (sh[2] + sh[3]), K, eps);
-    float nv[kVecRegs];
+    float nv[R];
     float acc = 0.f;
 #pragma unroll
-    for (int e = 0; e < kVecRegs; ++e) {
+    for (int e = 0; e < R; ++e) {
         const int i = threadIdx.x + e * kThreads;
         nv[e] = 0.f;
         if (i < K) {
@@ -189,7 +192,7 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
     __syncthreads();
     const float r2 = rms_inv_of((sh[4] + sh[5]) + (sh[6] + sh[7]), K, eps);
 #pragma unroll
-    for (int e = 0; e < kVecRegs; ++e) {
+    for (int e = 0; e < R; ++e) {
         const int i = threadIdx.x + e * kThreads;
         if (i < K) xs[i] = __fmul_rn(__fmul_rn(nv[e], r2), __fadd_rn(1.0f, wn.v[e]));
     }
@@ -498,8 +501,11 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag
     return true;
 }
 
-template <int DT, int DPL, int NH>
+// HR: elements per thread of an H-long vector (the residual stream, its deltas, norm weights);
+// the attention output (NH heads of 64 DPL) takes NQR, the FFN activations kVecRegs.
+template <int DT, int DPL, int NH, int HR>
 __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
+    constexpr int NQR = (NH * kWave * DPL + kThreads - 1) / kThreads;
     __shared__ PersistLds<NH, DPL> s;
     // a wait of an earlier step of this generate call timed out: its results are void, and
     // every later step ends at once instead of timing out again
@@ -522,12 +528,12 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         {   // 1: previous layer's finalize, pre-attention norm, QKV
             GemvStage<DT, false> g;
             g.load(L.qkv, L.qkv);
-            VecRegs wn;
+            VecRegs<HR> wn;
             wn.load(L.n_attn, H);
             if (l > 0) {
-                VecRegs wd;
+                VecRegs<HR> wd;
                 wd.load(a.layers[l - 1].n_ffn_post, H);
-                if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
+                if (!gather<HR>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
                 add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
             } else {
                 norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
@@ -539,16 +545,16 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         {   // 4: o-proj
             GemvStage<DT, false> g;
             g.load(L.o, L.o);
-            if (!gather<kVecRegs>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
+            if (!gather<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
             g.finish(s.xs, a.t_o, ep + 4);
         }
         {   // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU
             GemvStage<DT, true> g;
             g.load(L.gate, L.up);
-            VecRegs wd, wn;
+            VecRegs<HR> wd, wn;
             wd.load(L.n_attn_post, H);
             wn.load(L.n_ffn, H);
-            if (!gather<kVecRegs>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
+            if (!gather<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
             add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
             g.finish(s.xs, a.t_g, ep + 5);
         }
@@ -560,11 +566,11 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         }
     }
     // last finalize + final norm (transformer.c:400-406)
-    VecRegs wd, wn;
+    VecRegs<HR> wd, wn;
     wd.load(a.layers[a.n_layers - 1].n_ffn_post, H);
     wn.load(a.norm_final, H);
     const uint32_t ep_last = base + 8u * (uint32_t)(a.n_layers - 1) + 6u;
-    if (!gather<kVecRegs>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
+    if (!gather<HR>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
     add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < H; i += kThreads) a.xfin[i] = s.xs[i];
@@ -572,19 +578,23 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
 
 using PersistKernel = void (*)(PersistArgs);
 
-template <int DT>
+template <int DT, int HR>
 PersistKernel pick(int dpl, int nh) {
 #define SPH_PK(DPLV, NHV) \
-    if (dpl == DPLV && nh == NHV) return dec_persist_kernel<DT, DPLV, NHV>;
+    if (dpl == DPLV && nh == NHV) return dec_persist_kernel<DT, DPLV, NHV, HR>;
     SPH_PK(1, 4) SPH_PK(2, 4) SPH_PK(4, 4) SPH_PK(1, 8) SPH_PK(2, 8) SPH_PK(4, 8)
 #undef SPH_PK
     return nullptr;
 }
 
-PersistKernel kernel_for(int dt, int nh, int hd) {
-    if (hd % kWave) return nullptr;
+// H up to 1024 takes four elements per thread, longer vectors (up to kDecMaxK) eight: the
+// registers the H-long vectors hold through every stage are those the model needs.
+PersistKernel kernel_for(int dt, int nh, int hd, int H) {
+    if (hd % kWave || H <= 0 || H > kDecMaxK) return nullptr;
     const int dpl = hd / kWave;
-    return dt == DT_Q4_0 ? pick<DT_Q4_0>(dpl, nh) : dt == DT_Q8_0 ? pick<DT_Q8_0>(dpl, nh) : nullptr;
+    if (H <= 4 * kThreads)
+        return dt == DT_Q4_0 ? pick<DT_Q4_0, 4>(dpl, nh) : dt == DT_Q8_0 ? pick<DT_Q8_0, 4>(dpl, nh) : nullptr;
+    return dt == DT_Q4_0 ? pick<DT_Q4_0, kVecRegs>(dpl, nh) : dt == DT_Q8_0 ? pick<DT_Q8_0, kVecRegs>(dpl, nh) : nullptr;
 }
 
 // (wave-step, block) slots per lane of an M x K GEMV stage over `groups` workgroups.
@@ -601,7 +611,7 @@ size_t persist_words(int H, int nh, int nkv, int hd, int ffn) {
 }
 
 bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int ffn) {
-    const PersistKernel k = kernel_for(dt, nh, hd);
+    const PersistKernel k = kernel_for(dt, nh, hd, H);
     const int nq = nh * hd;
     if (!k || nkv != 1 || nq > kAttnMaxQ || hd > kAttnMaxKV) {
         set_error("persistent decode: %d heads of dim %d / %d KV heads not instantiated (one KV head)", nh, hd, nkv);
@@ -635,7 +645,7 @@ bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int f
 }
 
 int dec_persist(int dt, const PersistArgs &a, int groups, hipStream_t s) {
-    const PersistKernel k = kernel_for(dt, a.nh, a.hd);
+    const PersistKernel k = kernel_for(dt, a.nh, a.hd, a.H);
     if (!k) {
         set_error("persistent decode: shape not instantiated");
         return -1;
