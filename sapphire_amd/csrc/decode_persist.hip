@@ -203,11 +203,11 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
 // lane q of a row takes blocks q, q + 16, ... (bpl = ceil(K / 512) of them), and the row's
 // lanes are summed by DPP. The S = ceil(M / 4) wave-steps are split into contiguous ranges of
 // ceil(S / G) per workgroup; wave w takes every fourth step of its workgroup's range. A lane
-// holds kSlots (step, block) slots, slot = step * bpl + block (steps per wave x bpl <= kSlots,
+// holds SL (step, block) slots, slot = step * bpl + block (steps per wave x bpl <= SL,
 // checked by the host). load() issues the weight loads; finish() forms the rows.
-template <int DT, bool GEGLU>
+template <int DT, bool GEGLU, int SL = kSlots>
 struct GemvStage {
-    LaneBlock<DT> b0[kSlots], b1[kSlots];
+    LaneBlock<DT> b0[SL], b1[GEGLU ? SL : 1];
     int M, nb, bpl, q, rin, s0, s1;
 
     __device__ __forceinline__ void load(const QMat &w0, const QMat &w1) {
@@ -221,7 +221,7 @@ struct GemvStage {
         s0 = min(S, (int)blockIdx.x * per);
         s1 = min(S, s0 + per);
 #pragma unroll
-        for (int slot = 0; slot < kSlots; ++slot) {
+        for (int slot = 0; slot < SL; ++slot) {
             const int k = slot / bpl, j = slot - k * bpl;
             const int st = s0 + wid + 4 * k;
             if (st < s1) {
@@ -238,7 +238,7 @@ struct GemvStage {
         const int wid = threadIdx.x / kWave;
         float p0 = 0.f, p1 = 0.f;
 #pragma unroll
-        for (int slot = 0; slot < kSlots; ++slot) {
+        for (int slot = 0; slot < SL; ++slot) {
             const int k = slot / bpl, j = slot - k * bpl;
             const int st = s0 + wid + 4 * k;
             if (st < s1) {
@@ -502,8 +502,10 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag
 }
 
 // HR: elements per thread of an H-long vector (the residual stream, its deltas, norm weights);
-// the attention output (NH heads of 64 DPL) takes NQR, the FFN activations kVecRegs.
-template <int DT, int DPL, int NH, int HR>
+// the attention output (NH heads of 64 DPL) takes NQR, the FFN activations kVecRegs. SL: the
+// weight slots per lane of the QKV, o-proj and gate/up stages (the down projection's longer
+// rows keep kSlots).
+template <int DT, int DPL, int NH, int HR, int SL>
 __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     constexpr int NQR = (NH * kWave * DPL + kThreads - 1) / kThreads;
     __shared__ PersistLds<NH, DPL> s;
@@ -526,7 +528,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         const PLayer &L = a.layers[l];
         const uint32_t ep = base + 8u * (uint32_t)l;
         {   // 1: previous layer's finalize, pre-attention norm, QKV
-            GemvStage<DT, false> g;
+            GemvStage<DT, false, SL> g;
             g.load(L.qkv, L.qkv);
             VecRegs<HR> wn;
             wn.load(L.n_attn, H);
@@ -543,13 +545,13 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         if (!attn_stage<DPL, NH>(a, L, pos, ep + 1, ep + 2, s)) return;
         if (!combine_stage<NH, DPL>(a, ep + 2, ep + 3, s)) return;
         {   // 4: o-proj
-            GemvStage<DT, false> g;
+            GemvStage<DT, false, SL> g;
             g.load(L.o, L.o);
             if (!gather<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
             g.finish(s.xs, a.t_o, ep + 4);
         }
         {   // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU
-            GemvStage<DT, true> g;
+            GemvStage<DT, true, SL> g;
             g.load(L.gate, L.up);
             VecRegs<HR> wd, wn;
             wd.load(L.n_attn_post, H);
@@ -578,23 +580,13 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
 
 using PersistKernel = void (*)(PersistArgs);
 
-template <int DT, int HR>
+template <int DT, int HR, int SL>
 PersistKernel pick(int dpl, int nh) {
 #define SPH_PK(DPLV, NHV) \
-    if (dpl == DPLV && nh == NHV) return dec_persist_kernel<DT, DPLV, NHV, HR>;
+    if (dpl == DPLV && nh == NHV) return dec_persist_kernel<DT, DPLV, NHV, HR, SL>;
     SPH_PK(1, 4) SPH_PK(2, 4) SPH_PK(4, 4) SPH_PK(1, 8) SPH_PK(2, 8) SPH_PK(4, 8)
 #undef SPH_PK
     return nullptr;
-}
-
-// H up to 1024 takes four elements per thread, longer vectors (up to kDecMaxK) eight: the
-// registers the H-long vectors hold through every stage are those the model needs.
-PersistKernel kernel_for(int dt, int nh, int hd, int H) {
-    if (hd % kWave || H <= 0 || H > kDecMaxK) return nullptr;
-    const int dpl = hd / kWave;
-    if (H <= 4 * kThreads)
-        return dt == DT_Q4_0 ? pick<DT_Q4_0, 4>(dpl, nh) : dt == DT_Q8_0 ? pick<DT_Q8_0, 4>(dpl, nh) : nullptr;
-    return dt == DT_Q4_0 ? pick<DT_Q4_0, kVecRegs>(dpl, nh) : dt == DT_Q8_0 ? pick<DT_Q8_0, kVecRegs>(dpl, nh) : nullptr;
 }
 
 // (wave-step, block) slots per lane of an M x K GEMV stage over `groups` workgroups.
@@ -604,6 +596,28 @@ int slots_per_lane(int M, int K, int groups) {
     return (per + 3) / 4 * bpl;
 }
 
+// Slots per lane the QKV, o-proj and gate/up stages need.
+int light_slots(int groups, int H, int nh, int nkv, int hd, int ffn) {
+    const int nq = nh * hd;
+    return std::max({slots_per_lane(nq + 2 * nkv * hd, H, groups), slots_per_lane(H, nq, groups),
+                     slots_per_lane(ffn, H, groups)});
+}
+
+// H up to 1024 takes four elements per thread, longer vectors (up to kDecMaxK) eight, and the
+// QKV / o-proj / gate-up stages two weight slots per lane where two suffice: the registers
+// held across every wait are those the model and the workgroup count need.
+PersistKernel kernel_for(int dt, int nh, int hd, int H, int slots) {
+    if (hd % kWave || H <= 0 || H > kDecMaxK) return nullptr;
+    const int dpl = hd / kWave;
+    if (H <= 4 * kThreads && slots <= 2)
+        return dt == DT_Q4_0 ? pick<DT_Q4_0, 4, 2>(dpl, nh) : dt == DT_Q8_0 ? pick<DT_Q8_0, 4, 2>(dpl, nh) : nullptr;
+    if (H <= 4 * kThreads)
+        return dt == DT_Q4_0 ? pick<DT_Q4_0, 4, kSlots>(dpl, nh)
+                             : dt == DT_Q8_0 ? pick<DT_Q8_0, 4, kSlots>(dpl, nh) : nullptr;
+    return dt == DT_Q4_0 ? pick<DT_Q4_0, kVecRegs, kSlots>(dpl, nh)
+                         : dt == DT_Q8_0 ? pick<DT_Q8_0, kVecRegs, kSlots>(dpl, nh) : nullptr;
+}
+
 }  // namespace
 
 size_t persist_words(int H, int nh, int nkv, int hd, int ffn) {
@@ -611,7 +625,7 @@ size_t persist_words(int H, int nh, int nkv, int hd, int ffn) {
 }
 
 bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int ffn) {
-    const PersistKernel k = kernel_for(dt, nh, hd, H);
+    const PersistKernel k = kernel_for(dt, nh, hd, H, light_slots(groups, H, nh, nkv, hd, ffn));
     const int nq = nh * hd;
     if (!k || nkv != 1 || nq > kAttnMaxQ || hd > kAttnMaxKV) {
         set_error("persistent decode: %d heads of dim %d / %d KV heads not instantiated (one KV head)", nh, hd, nkv);
@@ -645,7 +659,7 @@ bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int f
 }
 
 int dec_persist(int dt, const PersistArgs &a, int groups, hipStream_t s) {
-    const PersistKernel k = kernel_for(dt, a.nh, a.hd, a.H);
+    const PersistKernel k = kernel_for(dt, a.nh, a.hd, a.H, light_slots(groups, a.H, a.nh, a.nkv, a.hd, a.ffn));
     if (!k) {
         set_error("persistent decode: shape not instantiated");
         return -1;
