@@ -199,25 +199,28 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
     __syncthreads();
 }
 
-// The rows of one GEMV stage owned by this workgroup. A wave-step is 4 rows, 16 lanes each;
-// lane q of a row takes blocks q, q + 16, ... (bpl = ceil(K / 512) of them), and the row's
+// The rows of one GEMV stage owned by this workgroup. A wave-step is 64 / LPR rows of LPR lanes
+// (16, or 32 for the down projection's 2048-long rows); lane q of a row takes blocks q, q + LPR,
+// ... (bpl = ceil(K / (32 LPR)) of them), and the row's
 // lanes are summed by DPP. The S = ceil(M / 4) wave-steps are split into contiguous ranges of
 // ceil(S / G) per workgroup; wave w takes every fourth step of its workgroup's range. A lane
 // holds SL (step, block) slots, slot = step * bpl + block (steps per wave x bpl <= SL,
 // checked by the host). load() issues the weight loads; finish() forms the rows.
-template <int DT, bool GEGLU, int SL = kSlots>
+template <int DT, bool GEGLU, int SL = kSlots, int LPR = kLpr>
 struct GemvStage {
+    static_assert(LPR == 16 || LPR == 32, "rows of 16 or 32 lanes");
+    static constexpr int RPW = kWave / LPR;   // rows per wave-step
     LaneBlock<DT> b0[SL], b1[GEGLU ? SL : 1];
     int M, nb, bpl, q, rin, s0, s1;
 
     __device__ __forceinline__ void load(const QMat &w0, const QMat &w1) {
         M = w0.M;
         nb = w0.K / kBlock;
-        bpl = (nb + kLpr - 1) / kLpr;
+        bpl = (nb + LPR - 1) / LPR;
         const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-        q = lane & (kLpr - 1);
-        rin = lane / kLpr;
-        const int S = (M + kRpw - 1) / kRpw, per = (S + (int)gridDim.x - 1) / (int)gridDim.x;
+        q = lane & (LPR - 1);
+        rin = lane / LPR;
+        const int S = (M + RPW - 1) / RPW, per = (S + (int)gridDim.x - 1) / (int)gridDim.x;
         s0 = min(S, (int)blockIdx.x * per);
         s1 = min(S, s0 + per);
 #pragma unroll
@@ -225,9 +228,9 @@ struct GemvStage {
             const int k = slot / bpl, j = slot - k * bpl;
             const int st = s0 + wid + 4 * k;
             if (st < s1) {
-                const int blk = q + kLpr * j;
-                load_lane_block<DT>(w0, st * kRpw + rin, blk, nb, blk < nb, b0[slot]);
-                if constexpr (GEGLU) load_lane_block<DT>(w1, st * kRpw + rin, blk, nb, blk < nb, b1[slot]);
+                const int blk = q + LPR * j;
+                load_lane_block<DT>(w0, st * RPW + rin, blk, nb, blk < nb, b0[slot]);
+                if constexpr (GEGLU) load_lane_block<DT>(w1, st * RPW + rin, blk, nb, blk < nb, b1[slot]);
             }
         }
     }
@@ -242,7 +245,7 @@ struct GemvStage {
             const int k = slot / bpl, j = slot - k * bpl;
             const int st = s0 + wid + 4 * k;
             if (st < s1) {
-                const int blk = q + kLpr * j;
+                const int blk = q + LPR * j;
                 const bool on = blk < nb;
                 float xv[32];
                 const float4 *xp = reinterpret_cast<const float4 *>(xs + blk * kBlock);
@@ -267,7 +270,11 @@ struct GemvStage {
                 if (j == bpl - 1) {   // the step's last block: sum the row's lanes and store
                     p0 = row16_sum(p0);
                     if constexpr (GEGLU) p1 = row16_sum(p1);
-                    const int row = st * kRpw + rin;
+                    if constexpr (LPR == 32) {   // the row's two 16-lane halves
+                        p0 += __shfl_xor(p0, 16, kWave);
+                        if constexpr (GEGLU) p1 += __shfl_xor(p1, 16, kWave);
+                    }
+                    const int row = st * RPW + rin;
                     if (q == 0 && row < M) put_tagged(y + row, GEGLU ? __fmul_rn(gelu_ref(p0), p1) : p0, tag);
                     p0 = 0.f;
                     p1 = 0.f;
@@ -507,8 +514,7 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag
 
 // HR: elements per thread of an H-long vector (the residual stream, its deltas, norm weights);
 // the attention output (NH heads of 64 DPL) takes NQR, the FFN activations kVecRegs. SL: the
-// weight slots per lane of the QKV, o-proj and gate/up stages (the down projection's longer
-// rows keep kSlots).
+// weight slots per lane of the GEMV stages.
 template <int DT, int DPL, int NH, int HR, int SL>
 __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     constexpr int NQR = (NH * kWave * DPL + kThreads - 1) / kThreads;
@@ -565,7 +571,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             g.finish(s.xs, a.t_g, ep + 5);
         }
         {   // 6: down
-            GemvStage<DT, false> g;
+            GemvStage<DT, false, SL, 32> g;
             g.load(L.down, L.down);
             if (!gather<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag)) return;
             g.finish(s.xs, a.t_dn, ep + 6);
@@ -594,21 +600,22 @@ PersistKernel pick(int dpl, int nh) {
 }
 
 // (wave-step, block) slots per lane of an M x K GEMV stage over `groups` workgroups.
-int slots_per_lane(int M, int K, int groups) {
-    const int S = (M + kRpw - 1) / kRpw, per = (S + groups - 1) / groups;
-    const int bpl = (K / kBlock + kLpr - 1) / kLpr;
+int slots_per_lane(int M, int K, int groups, int lpr = kLpr) {
+    const int rpw = kWave / lpr;
+    const int S = (M + rpw - 1) / rpw, per = (S + groups - 1) / groups;
+    const int bpl = (K / kBlock + lpr - 1) / lpr;
     return (per + 3) / 4 * bpl;
 }
 
-// Slots per lane the QKV, o-proj and gate/up stages need.
+// Slots per lane the GEMV stages need (the down projection in rows of 32 lanes).
 int light_slots(int groups, int H, int nh, int nkv, int hd, int ffn) {
     const int nq = nh * hd;
     return std::max({slots_per_lane(nq + 2 * nkv * hd, H, groups), slots_per_lane(H, nq, groups),
-                     slots_per_lane(ffn, H, groups)});
+                     slots_per_lane(ffn, H, groups), slots_per_lane(H, ffn, groups, 32)});
 }
 
 // H up to 1024 takes four elements per thread, longer vectors (up to kDecMaxK) eight, and the
-// QKV / o-proj / gate-up stages two weight slots per lane where two suffice: the registers
+// GEMV stages two weight slots per lane where two suffice: the registers
 // held across every wait are those the model and the workgroup count need.
 PersistKernel kernel_for(int dt, int nh, int hd, int H, int slots) {
     if (hd % kWave || H <= 0 || H > kDecMaxK) return nullptr;
@@ -643,8 +650,7 @@ bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int f
         set_error("persistent decode: GEMV inputs must be multiples of 32 and at most %d", kDecMaxK);
         return false;
     }
-    const int worst = std::max({slots_per_lane(nq + 2 * nkv * hd, H, groups), slots_per_lane(H, nq, groups),
-                                slots_per_lane(ffn, H, groups), slots_per_lane(H, ffn, groups)});
+    const int worst = light_slots(groups, H, nh, nkv, hd, ffn);
     const int E = (nq + groups - 1) / groups;
     if (worst > kSlots || groups * (E + 4) > kCombMax) {
         set_error("persistent decode: %d workgroups are too few for these shapes", groups);
