@@ -199,10 +199,10 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
     __syncthreads();
 }
 
-// The rows of one GEMV stage owned by this workgroup. A wave-step is 64 / LPR rows of LPR lanes
-// (16, or 32 for the down projection's 2048-long rows); lane q of a row takes blocks q, q + LPR,
-// ... (bpl = ceil(K / (32 LPR)) of them), and the row's
-// lanes are summed by DPP. The S = ceil(M / 4) wave-steps are split into contiguous ranges of
+// The rows of one GEMV stage owned by this workgroup. A wave-step is 64 / LPR rows of LPR
+// lanes (16, or 32 for the o-proj's and the down projection's longer rows); lane q of a row
+// takes blocks q, q + LPR, ... (bpl = ceil(K / (32 LPR)) of them), and the row's lanes are
+// summed by DPP. The S = ceil(M / (64 / LPR)) wave-steps are split into contiguous ranges of
 // ceil(S / G) per workgroup; wave w takes every fourth step of its workgroup's range. A lane
 // holds SL (step, block) slots, slot = step * bpl + block (steps per wave x bpl <= SL,
 // checked by the host). load() issues the weight loads; finish() forms the rows.
@@ -555,7 +555,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         if (!attn_stage<DPL, NH>(a, L, pos, ep + 1, ep + 2, s)) return;
         if (!combine_stage<NH, DPL>(a, ep + 2, ep + 3, s)) return;
         {   // 4: o-proj
-            GemvStage<DT, false, SL> g;
+            GemvStage<DT, false, SL, 32> g;
             g.load(L.o, L.o);
             if (!gather<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
             g.finish(s.xs, a.t_o, ep + 4);
@@ -607,10 +607,10 @@ int slots_per_lane(int M, int K, int groups, int lpr = kLpr) {
     return (per + 3) / 4 * bpl;
 }
 
-// Slots per lane the GEMV stages need (the down projection in rows of 32 lanes).
+// Slots per lane the GEMV stages need (o-proj and down in rows of 32 lanes).
 int light_slots(int groups, int H, int nh, int nkv, int hd, int ffn) {
     const int nq = nh * hd;
-    return std::max({slots_per_lane(nq + 2 * nkv * hd, H, groups), slots_per_lane(H, nq, groups),
+    return std::max({slots_per_lane(nq + 2 * nkv * hd, H, groups), slots_per_lane(H, nq, groups, 32),
                      slots_per_lane(ffn, H, groups), slots_per_lane(H, ffn, groups, 32)});
 }
 
