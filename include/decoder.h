@@ -85,8 +85,8 @@ int sapphire_decoder_generate(sapphire_decoder_t *dec, int token, int pos, int s
  * otherwise). elapsed_ms, if not NULL, receives the device time. 0 / -1. */
 int sapphire_decoder_prefill(sapphire_decoder_t *dec, int seq, const int *tokens, int n, int pos,
                              float *elapsed_ms);
-/* The form of a one-sequence step. groups > 0: the layers run as one persistent cooperative
- * kernel of `groups` workgroups (all co-resident) whose stages exchange epoch-tagged vectors
+/* The form of a one-sequence step. groups > 0: the layers run as one persistent kernel of
+ * `groups` workgroups (all co-resident) whose stages exchange epoch-tagged vectors
  * instead of waiting for kernel boundaries; this is the default (128 workgroups, or the value
  * of the SAPPHIRE_DECODE_WORKGROUPS environment variable at create time) where the shapes and
  * the device allow it. groups == 0: six fused launches per layer in a HIP graph. Both forms

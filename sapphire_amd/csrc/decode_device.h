@@ -88,7 +88,7 @@ __device__ __forceinline__ void load_lane_block(const QMat &w, int row, int blk,
     const u32x4 *qp = reinterpret_cast<const u32x4 *>(w.q + bi * QB<DT>::BYTES);
 #pragma unroll
     for (int i = 0; i < QB<DT>::WORDS / 4; ++i) {
-        const u32x4 t = __builtin_nontemporal_load(qp + i);
+        const u32x4 t = qp[i];
         b.q[4 * i + 0] = t.x; b.q[4 * i + 1] = t.y; b.q[4 * i + 2] = t.z; b.q[4 * i + 3] = t.w;
     }
     b.s = ok ? w.s[bi] : 0.f;

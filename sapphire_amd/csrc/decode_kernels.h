@@ -86,7 +86,7 @@ int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, uint32_t 
 struct PLayer {
     QMat qkv, o, gate, up, down;
     const float *n_attn, *n_attn_post, *n_ffn, *n_ffn_post, *qn, *kn;
-    const float *cos_t, *sin_t;      // RoPE tables of the layer (global or local base)
+    const float *cos_t, *sin_t;      // RoPE rows of the layer's base (row p at p * rope_stride)
     float *kc, *vc;                  // [nkv][max_ctx][hd]
     int window;                      // sliding window, 0 for a global layer
 };
@@ -101,6 +101,7 @@ struct PersistArgs {
     float es = 1.f;                   // embedding scale sqrt(H)
     const float *norm_final = nullptr;
     int H = 0, nh = 0, nkv = 0, hd = 0, ffn = 0, max_ctx = 0;
+    int rope_stride = 0;              // floats between consecutive positions' rows of cos_t / sin_t
     float scale = 1.f, eps = 1e-6f;
     const int *state = nullptr;       // [0] token, [1] position
     const uint32_t *seq = nullptr;    // step counter that makes the epochs unique
@@ -111,13 +112,14 @@ struct PersistArgs {
     int spin_limit = 0;
 };
 constexpr int kPersistMaxGroups = 256;
+constexpr int kPersistMaxLayers = 48;   // layer descriptors the persistent step keeps in LDS
 // 64-bit words of the tagged exchange buffers for a model shape (all six, contiguous in this
 // order: qkv, partials for kPersistMaxGroups workgroups, attention output, o, g, down).
 size_t persist_words(int H, int nh, int nkv, int hd, int ffn);
 // Whether `groups` workgroups can run the persistent step for these shapes on the current
 // device (co-residency included); sets the error message when not.
-bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int ffn);
-// Cooperative launch of the persistent step (capturable into a HIP graph).
+bool persist_supported(int dt, int groups, int n_layers, int H, int nh, int nkv, int hd, int ffn);
+// Launch of the persistent step, all workgroups co-resident (capturable into a HIP graph).
 int dec_persist(int dt, const PersistArgs &a, int groups, hipStream_t s);
 // Epoch stride of one step: 8 stages per layer plus the final one.
 __host__ __device__ inline uint32_t persist_epochs_per_step(int n_layers) { return 8u * (uint32_t)(n_layers + 1); }

@@ -1,9 +1,9 @@
 // decode_persist.hip - the layers of one Gemma-3 decode step as one persistent kernel.
 //
 // The multi-launch step (decode.hip) separates its stages by kernel boundaries; each of its
-// ~110 launches per token costs a launch and a cold start of its memory loads. Here one
-// cooperative grid of G workgroups (all co-resident) runs every layer, and the stages are
-// separated by data instead:
+// ~110 launches per token costs a launch and a cold start of its memory loads. Here one grid
+// of G workgroups, all resident at once (the host checks the occupancy), runs every layer, and
+// the stages are separated by data instead:
 //
 // * Every exchanged vector element is one 64-bit word: the fp32 value in the low half and the
 //   epoch of the stage that produced it in the high half. Words are stored and loaded with
@@ -36,7 +36,6 @@ namespace sapphire {
 namespace {
 
 constexpr int kLpr = 16;                          // lanes per GEMV row
-constexpr int kRpw = kWave / kLpr;                // rows per wave-step
 constexpr int kSlots = 4;                         // (wave-step, block) slots per lane in one GEMV stage
 constexpr int kCombMax = 2048;                    // gathered partial words per workgroup in the combine
 constexpr int kVecRegs = kDecMaxK / kThreads;     // vector elements per thread (longest vector)
@@ -49,74 +48,112 @@ __device__ __forceinline__ uint64_t get_tagged(const uint64_t *p) {
 }
 __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 
+constexpr int kAttnRows = 12;                     // K/V rows of one attention batch
+
+// One hd-long fp32 row (hd = 64 DPL) from global memory into LDS by DMA (no VGPRs): the
+// wave's lanes load 16 B each (DPL 4) or 4 B per 64-dim chunk; the data lands in natural
+// dim order at lds_row, which must be the same for the whole wave. Completion is counted by
+// vmcnt like any other load.
+template <int DPL>
+__device__ __forceinline__ void row_to_lds(const float *src_row, float *lds_row) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if constexpr (DPL == 4) {
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src_row + lane * 4),
+                                         (__attribute__((address_space(3))) void *)lds_row, 16, 0, 0);
+    } else {
+#pragma unroll
+        for (int c = 0; c < DPL; ++c)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src_row + c * kWave + lane),
+                                             (__attribute__((address_space(3))) void *)(lds_row + c * kWave), 4, 0, 0);
+    }
+}
+
 template <int NH, int DPL>
 struct alignas(16) PersistLds {
     float resid[kDecMaxK];                       // the residual stream
     float xs[kDecMaxK];                          // input of the current GEMV
     float dl[kDecMaxK];                          // gathered delta vector
-    float raw[kAttnMaxQ + 2 * kAttnMaxKV];       // q | k | v as projected
-    float qk[kAttnMaxQ + kAttnMaxKV];            // q | k after QK-norm and RoPE
-    float part8[8 * 16];
-    float ss[16];
-    float wm[kThreads / kWave][NH], wsum[kThreads / kWave][NH];
-    float wo[kThreads / kWave][NH][kWave * DPL];
-    float wx[kThreads / kWave][NH];              // wave merge weights
-    float wmax[NH], wtot[NH];
     float comb[kCombMax];
+    // K / V rows of the attention slice's current batch (natural dim order), filled by DMA
+    float kvk[kAttnRows][kWave * DPL], kvv[kAttnRows][kWave * DPL];
+    // the layer descriptors (PLayer), copied once per step: read from here, not with scalar
+    // loads of global memory that a step's streaming has long evicted from every cache
+    alignas(16) uint32_t layer_words[kPersistMaxLayers * sizeof(PLayer) / 4];
+    __device__ __forceinline__ const PLayer &layer(int l) const {
+        return reinterpret_cast<const PLayer *>(layer_words)[l];
+    }
     float sh[16];
     int flag;
 };
 
 // dst[j] = value of word *src(j) for j < n, once its tag equals `tag`; thread t takes
-// j = t + 256 e. All loads are issued first, then only stale words are polled again. Returns
-// false when a word is still stale after spin_limit polls (and counts the failure in *err).
-// Synchronises the workgroup; the result is the same in every thread. With sq set, the wave
-// sums of the squares of the gathered values go to sq[0..3] before that barrier: each thread
-// sums its own values in the order par_sum_sq takes them, so (sq[0] + sq[1]) + (sq[2] + sq[3])
-// afterwards is par_sum_sq(dst, n), bit for bit.
+// j = t + 256 e. begin() issues the first load of every word; end() polls the stale words
+// again until all have the tag. A stage issues begin() before its prefetch loads (weights,
+// norm weights, K/V rows), so that the first check of the words waits only for their own
+// loads: vector memory loads complete in issue order, and a check issued after the prefetch
+// would wait for all of it. end() returns false when a word is still stale after spin_limit
+// polls (and counts the failure in *err). It synchronises the workgroup; the result is the
+// same in every thread. With sq set, the wave sums of the squares of the gathered values go
+// to sq[0..3] before that barrier: each thread sums its own values in the order par_sum_sq
+// takes them, so (sq[0] + sq[1]) + (sq[2] + sq[3]) afterwards is par_sum_sq(dst, n), bit for
+// bit.
 template <int MAXE, class Src>
-__device__ __forceinline__ bool gather(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
-                                       int *flag, float *sq = nullptr) {
+struct Gather {
     uint64_t w[MAXE];
-#pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-        const int j = threadIdx.x + e * kThreads;
-        w[e] = j < n ? get_tagged(src(j)) : (uint64_t)tag << 32;
-    }
-    for (int spins = 0;; ++spins) {
-        bool ready = true;
-#pragma unroll
-        for (int e = 0; e < MAXE; ++e) ready = ready && tag_is(w[e], tag);
-        if (ready) break;
-        if (spins >= spin_limit) {
-            *flag = 1;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
+
+    __device__ __forceinline__ void begin(Src src, int n, uint32_t tag) {
 #pragma unroll
         for (int e = 0; e < MAXE; ++e) {
             const int j = threadIdx.x + e * kThreads;
-            if (j < n && !tag_is(w[e], tag)) w[e] = get_tagged(src(j));
+            w[e] = j < n ? get_tagged(src(j)) : (uint64_t)tag << 32;
         }
     }
-    float acc = 0.f;
+
+    __device__ __forceinline__ bool end(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
+                                        int *flag, float *sq = nullptr) {
+        for (int spins = 0;; ++spins) {
+            bool ready = true;
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-        const int j = threadIdx.x + e * kThreads;
-        if (j < n) {
-            const float v = __uint_as_float((uint32_t)w[e]);
-            dst[j] = v;
-            acc = __builtin_fmaf(v, v, acc);
+            for (int e = 0; e < MAXE; ++e) ready = ready && tag_is(w[e], tag);
+            if (ready) break;
+            if (spins >= spin_limit) {
+                *flag = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+            for (int e = 0; e < MAXE; ++e) {
+                const int j = threadIdx.x + e * kThreads;
+                if (j < n && !tag_is(w[e], tag)) w[e] = get_tagged(src(j));
+            }
         }
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < MAXE; ++e) {
+            const int j = threadIdx.x + e * kThreads;
+            if (j < n) {
+                const float v = __uint_as_float((uint32_t)w[e]);
+                dst[j] = v;
+                acc = __builtin_fmaf(v, v, acc);
+            }
+        }
+        if (sq) {
+            acc = wave_sum_uniform(acc);
+            if ((threadIdx.x & (kWave - 1)) == 0) sq[threadIdx.x / kWave] = acc;
+        }
+        __syncthreads();
+        const bool ok = *flag == 0;
+        if (!ok && threadIdx.x == 0) atomicAdd(err, 1);
+        return ok;
     }
-    if (sq) {
-        acc = wave_sum_uniform(acc);
-        if ((threadIdx.x & (kWave - 1)) == 0) sq[threadIdx.x / kWave] = acc;
-    }
-    __syncthreads();
-    const bool ok = *flag == 0;
-    if (!ok && threadIdx.x == 0) atomicAdd(err, 1);
-    return ok;
+};
+
+template <int MAXE, class Src>
+__device__ __forceinline__ bool gather(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
+                                       int *flag, float *sq = nullptr) {
+    Gather<MAXE, Src> g;
+    g.begin(src, n, tag);
+    return g.end(src, n, tag, dst, spin_limit, err, flag, sq);
 }
 
 struct Contig {
@@ -288,191 +325,216 @@ struct GemvStage {
 };
 
 // Stage 2: QK-norm, RoPE and the KV write of the token, then this workgroup's partial
-// (o, max in log2 units, sum per head) over its slice of the layer's positions:
-// dec_attn_part_kernel with one slice per workgroup. The gammas, RoPE rows and the first K/V rows of the slice are
-// loaded before the wait for q, k, v; scores are summed by DPP into wave-uniform values.
+// (o, max in log2 units, sum per head) over its slice of the layer's positions
+// (attention.c:140-158 over the slice; dec_attn_part_kernel with one slice per workgroup).
+// Wave w owns query heads w, w + 4, ...: it gathers those heads and the K and V vectors of
+// the token into registers (lane l holds dims l*DPL .. l*DPL+DPL-1 of each), normalises them
+// by DPP sums, rotates them with the partner dims in lane l ^ 32, and walks every position of
+// the slice for its heads. No LDS and no workgroup barrier: each wave stores its heads'
+// partials as soon as its own inputs have arrived. prefetch() loads the slice's first K/V
+// rows, the gammas and the RoPE row entries; the kernel calls it a stage ahead, before the
+// QKV GEMV, so that the loads have returned when run() polls for q, k and v.
 template <int DPL, int NH>
-__device__ __forceinline__ bool attn_stage(const PersistArgs &a, const PLayer &L, int pos, uint32_t tag_in,
-                                           uint32_t tag_out, PersistLds<NH, DPL> &s) {
-    const int hd = a.hd, half = hd / 2;
-    constexpr int nkv = 1;
-    const int seq = pos + 1;
-    const int start = (L.window > 0 && seq > L.window) ? seq - L.window : 0;
-    const int len = seq - start, G = gridDim.x;
-    const int chunk = (len + G - 1) / G;
-    const int t0 = min(seq, start + (int)blockIdx.x * chunk), t1 = min(seq, t0 + chunk);
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    // K/V rows per wave and batch, loaded before the wait for q, k, v. Three cover a slice of
-    // up to 12 positions (a 1536-position range over 128 workgroups) in one batch; longer
-    // slices take further batches. Measured against four (one register batch more held
-    // across the wait): 0.550 against 0.556 ms per token at the 270M shape, KV at 1024.
-    constexpr int PF = 3;
-    constexpr int NW = kThreads / kWave;
-    float kr[PF][DPL], vr[PF][DPL];   // one K/V head: its rows are [max_ctx][hd]
-    auto load_batch = [&](int tb) {
+struct AttnStage {
+    static constexpr int NW = kThreads / kWave;
+    static_assert(NH % NW == 0, "query heads in whole heads per wave");
+    static constexpr int HPW = NH / NW;                // query heads per wave
+    // K/V rows of positions t0 .. t0 + PF - 1 (one K/V head: rows [max_ctx][hd]); a slice of
+    // up to PF positions (a 1536-position range over 128 workgroups) is one batch
+    static constexpr int PF = kAttnRows;
+    float gq[DPL], gk[DPL], cs[DPL], sn[DPL];
+    int t0, t1;
+
+    // DMA of the batch's K and V rows into LDS, rows spread over the waves (row pos is
+    // written by this step and taken from registers instead)
+    __device__ __forceinline__ void load_batch(const PLayer &L, int hd, int pos, int tb, PersistLds<NH, DPL> &s) {
+        const int wid = threadIdx.x / kWave;
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
-            const int t = tb + j * NW;
-            const bool ok = t < t1 && t != pos;
-            const size_t off = ok ? (size_t)t * hd : 0;
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) {
-                kr[j][d] = ok ? L.kc[off + lane * DPL + d] : 0.f;
-                vr[j][d] = ok ? L.vc[off + lane * DPL + d] : 0.f;
+            const int t = tb + j;
+            if (j % NW == wid && t < t1 && t != pos) {   // wave-uniform
+                row_to_lds<DPL>(L.kc + (size_t)t * hd, s.kvk[j]);
+                row_to_lds<DPL>(L.vc + (size_t)t * hd, s.kvv[j]);
             }
         }
-    };
-    if (t0 + wid < t1) load_batch(t0 + wid);   // in flight during the wait for q, k, v
-
-    // rotation pairs (vector v, index i < half) of the q heads then the k heads: their
-    // gammas and RoPE row entries (rope.c:99-117; q/k norms attention.c:221-226)
-    constexpr int MAXP = (NH + 1) * kWave * DPL / 2 / kThreads + 1;
-    const int npairs = (NH + nkv) * half;
-    float g0[MAXP], g1[MAXP], cs[MAXP], sn[MAXP];
-#pragma unroll
-    for (int e = 0; e < MAXP; ++e) {
-        const int p = threadIdx.x + e * kThreads;
-        const bool ok = p < npairs;
-        const int v = ok ? p / half : 0, i = ok ? p - v * half : 0;
-        const float *gam = v < NH ? L.qn : L.kn;
-        g0[e] = ok ? gam[i] : 0.f;
-        g1[e] = ok ? gam[i + half] : 0.f;
-        cs[e] = ok ? L.cos_t[(size_t)pos * hd + i] : 0.f;
-        sn[e] = ok ? L.sin_t[(size_t)pos * hd + i] : 0.f;
     }
 
-    if (!gather<((NH + 2 * nkv) * kWave * DPL + kThreads - 1) / kThreads>(Contig{a.t_qkv}, (NH + 2 * nkv) * hd, tag_in, s.raw,
-                                                          a.spin_limit, a.err, &s.flag))
-        return false;
-    // rmsnorm_delta of every q and k head vector, then the half-split rotation
-    {   // sum of squares of each head vector: 16-lane row v takes vector v (tree order)
-        const int v = threadIdx.x / 16, q16 = threadIdx.x & 15;
-        if (v < NH + nkv) {
-            float acc = 0.f;
-            for (int i = q16; i < hd; i += 16) acc = __builtin_fmaf(s.raw[v * hd + i], s.raw[v * hd + i], acc);
-            acc = row16_sum(acc);
-            if (q16 == 0) s.ss[v] = rms_inv_of(acc, hd, a.eps);
+    __device__ __forceinline__ void prefetch(const PersistArgs &a, const PLayer &L, int pos, PersistLds<NH, DPL> &s) {
+        const int hd = a.hd;
+        const int seq = pos + 1;
+        const int start = (L.window > 0 && seq > L.window) ? seq - L.window : 0;
+        const int len = seq - start, G = gridDim.x;
+        const int chunk = (len + G - 1) / G;
+        t0 = min(seq, start + (int)blockIdx.x * chunk);
+        t1 = min(seq, t0 + chunk);
+        const int lane = threadIdx.x & (kWave - 1), d0 = lane * DPL;
+        load_batch(L, hd, pos, t0, s);
+        // gammas (one head_dim vector for every q head, one for k: attention.c:228-269) and the
+        // RoPE row of pos at (dim mod half) (rope.c:99-117)
+        const size_t ci = (size_t)pos * a.rope_stride + (size_t)(lane & (kWave / 2 - 1)) * DPL;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+            gq[i] = L.qn[d0 + i];
+            gk[i] = L.kn[d0 + i];
+            cs[i] = L.cos_t[ci + i];
+            sn[i] = L.sin_t[ci + i];
         }
+    }
+
+    // on_arrival() runs once the workgroup's q, k, v have arrived (it issues the next stage's
+    // loads).
+    template <class F>
+    __device__ __forceinline__ bool run(const PersistArgs &a, const PLayer &L, int pos, uint32_t tag_in,
+                                        uint32_t tag_out, PersistLds<NH, DPL> &s, F on_arrival) {
+        const int hd = a.hd;
+        const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+        const int d0 = lane * DPL;                     // this lane's first dim
+        // the wave's words: q of its heads, then k, then v (t_qkv holds q | k | v)
+        constexpr int NWD = (HPW + 2) * DPL;
+        uint64_t w[NWD];
+        auto src = [&](int e) -> const uint64_t * {
+            const int v = e / DPL, i = e - v * DPL;
+            const int vec = v < HPW ? wid + NW * v : NH + (v - HPW);   // q head, k (NH) or v (NH + 1)
+            return a.t_qkv + (size_t)vec * hd + d0 + i;
+        };
+#pragma unroll
+        for (int e = 0; e < NWD; ++e) w[e] = get_tagged(src(e));
+        for (int spins = 0;; ++spins) {
+            bool ready = true;
+#pragma unroll
+            for (int e = 0; e < NWD; ++e) ready = ready && tag_is(w[e], tag_in);
+            if (__all(ready)) break;
+            if (spins >= a.spin_limit) {
+                // no partial is stored: the combine of every workgroup times out in turn
+                if (lane == 0) s.flag = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+            for (int e = 0; e < NWD; ++e)
+                if (!tag_is(w[e], tag_in)) w[e] = get_tagged(src(e));
+        }
+        // every wave's K/V DMA (issued before its polls) has landed; then the rows are shared
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-    }
+        on_arrival();
+        if (s.flag) return true;
+        float xv[HPW + 2][DPL];
 #pragma unroll
-    for (int e = 0; e < MAXP; ++e) {
-        const int p = threadIdx.x + e * kThreads;
-        if (p < npairs) {
-            const int v = p / half, i = p - v * half;
-            const float r = s.ss[v];
-            const float *src = s.raw + (size_t)v * hd;
-            const float x0 = __fmul_rn(__fmul_rn(src[i], r), __fadd_rn(1.0f, g0[e]));
-            const float x1 = __fmul_rn(__fmul_rn(src[i + half], r), __fadd_rn(1.0f, g1[e]));
-            s.qk[v * hd + i] = __builtin_fmaf(x0, cs[e], -__fmul_rn(x1, sn[e]));
-            s.qk[v * hd + i + half] = __builtin_fmaf(x1, cs[e], __fmul_rn(x0, sn[e]));
+        for (int v = 0; v < HPW + 2; ++v)
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) xv[v][i] = __uint_as_float((uint32_t)w[v * DPL + i]);
+
+        // rmsnorm_delta of each q head and of k over its hd dims (wave sums of the lanes'
+        // squares), then the half-split rotation: dim d < half pairs with d + half in lane l ^ 32
+        // (rope.c:113-115: x[i] = x0 c - x1 s, x[i + half] = x1 c + x0 s)
+        const bool upper = lane >= kWave / 2;
+        float qk[HPW + 1][DPL];
+#pragma unroll
+        for (int v = 0; v < HPW + 1; ++v) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) acc = __builtin_fmaf(xv[v][i], xv[v][i], acc);
+            const float r = rms_inv_of(wave_sum_uniform(acc), hd, a.eps);
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) {
+                const float g = v < HPW ? gq[i] : gk[i];
+                const float xn = __fmul_rn(__fmul_rn(xv[v][i], r), __fadd_rn(1.0f, g));
+                const float xp = __shfl_xor(xn, kWave / 2, kWave);
+                qk[v][i] = upper ? __builtin_fmaf(xn, cs[i], __fmul_rn(xp, sn[i]))
+                                 : __builtin_fmaf(xn, cs[i], -__fmul_rn(xp, sn[i]));
+            }
         }
-    }
-    __syncthreads();
-    const float *ks = s.qk + NH * hd;
-    const float *vnew = s.raw + (NH + nkv) * hd;
-    if (t0 <= pos && pos < t1)   // kv_cache_write_token: [head][pos][dim]
-        for (int i = threadIdx.x; i < nkv * hd; i += kThreads) {
-            const int h = i / hd, d = i - h * hd;
-            const size_t off = ((size_t)h * a.max_ctx + pos) * hd + d;
-            L.kc[off] = ks[i];
-            L.vc[off] = vnew[i];
+        const float *vnew = xv[HPW + 1];
+        if (wid == 0 && t0 <= pos && pos < t1) {   // kv_cache_write_token: [head][pos][dim]
+            const size_t off = (size_t)pos * hd + d0;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) {
+                L.kc[off + i] = qk[HPW][i];
+                L.vc[off + i] = vnew[i];
+            }
         }
 
-    // scores in log2 units, so that every softmax weight is one exp2 (v_exp_f32)
-    const float sl2 = __fmul_rn(a.scale, 1.44269504088896341f);
-    float qr[NH][DPL];
+        // scores in log2 units, so that every softmax weight is one exp2 (v_exp_f32)
+        const float sl2 = __fmul_rn(a.scale, 1.44269504088896341f);
+        float m[HPW], sm[HPW], o[HPW][DPL];
 #pragma unroll
-    for (int h = 0; h < NH; ++h)
+        for (int h = 0; h < HPW; ++h) {
+            m[h] = -INFINITY;
+            sm[h] = 0.f;
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) qr[h][d] = s.qk[h * hd + lane * DPL + d];
-    float m[NH], sm[NH], o[NH][DPL];
+            for (int i = 0; i < DPL; ++i) o[h][i] = 0.f;
+        }
+        for (int tb = t0; tb < t1; tb += PF) {
+            if (tb != t0) {   // a further batch: every wave is done with the rows in LDS
+                __syncthreads();
+                load_batch(L, hd, pos, tb, s);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            }
 #pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        m[h] = -INFINITY;
-        sm[h] = 0.f;
+            for (int j = 0; j < PF; ++j) {
+                const int t = tb + j;
+                if (t >= t1) break;
+                float kr[DPL], vr[DPL];
+                if (t == pos) {
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) o[h][d] = 0.f;
-    }
-    for (int tb = t0 + wid; tb < t1; tb += PF * NW) {
-        if (tb != t0 + wid) load_batch(tb);
+                    for (int i = 0; i < DPL; ++i) {
+                        kr[i] = qk[HPW][i];
+                        vr[i] = vnew[i];
+                    }
+                } else {
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const int t = tb + j * NW;
-            if (t >= t1) break;
-            if (t == pos) {
+                    for (int i = 0; i < DPL; ++i) {
+                        kr[i] = s.kvk[j][d0 + i];
+                        vr[i] = s.kvv[j][d0 + i];
+                    }
+                }
 #pragma unroll
-                for (int d = 0; d < DPL; ++d) {
-                    kr[j][d] = ks[lane * DPL + d];
-                    vr[j][d] = vnew[lane * DPL + d];
+                for (int h = 0; h < HPW; ++h) {
+                    float dp = 0.f;
+#pragma unroll
+                    for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qk[h][i], kr[i], dp);
+                    const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
+                    const float mn = fmaxf(m[h], score);
+                    const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
+                    const float p = __builtin_amdgcn_exp2f(score - mn);
+                    sm[h] = __builtin_fmaf(sm[h], c, p);
+#pragma unroll
+                    for (int i = 0; i < DPL; ++i) o[h][i] = __builtin_fmaf(o[h][i], c, p * vr[i]);
+                    m[h] = mn;
                 }
             }
+        }
+        // this wave's heads' partials of the slice
+        uint64_t *out = a.t_part + (size_t)blockIdx.x * NH * (hd + 2);
 #pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                float dp = 0.f;
+        for (int h = 0; h < HPW; ++h) {
+            uint64_t *oh = out + (size_t)(wid + NW * h) * (hd + 2);
 #pragma unroll
-                for (int d = 0; d < DPL; ++d) dp = __builtin_fmaf(qr[h][d], kr[j][d], dp);
-                const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
-                const float mn = fmaxf(m[h], score);
-                const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
-                const float p = __builtin_amdgcn_exp2f(score - mn);
-                sm[h] = __builtin_fmaf(sm[h], c, p);
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) o[h][d] = __builtin_fmaf(o[h][d], c, p * vr[j][d]);
-                m[h] = mn;
+            for (int i = 0; i < DPL; ++i) put_tagged(oh + d0 + i, o[h][i], tag_out);
+            if (lane == 0) {
+                put_tagged(oh + hd, m[h], tag_out);
+                put_tagged(oh + hd + 1, sm[h], tag_out);
             }
         }
+        return true;
     }
-    // merge the four waves and store the slice's partial: the (wave, head) weights
-    // exp2(m_w - M) are formed once, then every element is a weighted sum
-#pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        if (lane == 0) {
-            s.wm[wid][h] = m[h];
-            s.wsum[wid][h] = sm[h];
-        }
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) s.wo[wid][h][lane * DPL + d] = o[h][d];
-    }
-    __syncthreads();
-    if (threadIdx.x < NH) {
-        const int h = threadIdx.x;
-        float M = -INFINITY;
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, s.wm[w][h]);
-        float S = 0.f;
-        for (int w = 0; w < NW; ++w) {
-            const float e = s.wm[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s.wm[w][h] - M);
-            s.wx[w][h] = e;
-            S = __builtin_fmaf(s.wsum[w][h], e, S);
-        }
-        s.wmax[h] = M;
-        s.wtot[h] = S;
-    }
-    __syncthreads();
-    uint64_t *out = a.t_part + (size_t)blockIdx.x * NH * (hd + 2);
-    for (int idx = threadIdx.x; idx < NH * hd; idx += kThreads) {
-        const int h = idx / hd, d = idx - h * hd;
-        float O = 0.f;
-        for (int w = 0; w < NW; ++w) O = __builtin_fmaf(s.wo[w][h][d], s.wx[w][h], O);
-        put_tagged(out + h * (hd + 2) + d, O, tag_out);
-        if (d == 0) {
-            put_tagged(out + h * (hd + 2) + hd, s.wmax[h], tag_out);
-            put_tagged(out + h * (hd + 2) + hd + 1, s.wtot[h], tag_out);
-        }
-    }
-    return true;
-}
+};
 
 // Stage 3: attention elements [e0, e1) of this workgroup, E = ceil(NH*hd / G) each:
 // out = sum_b e_b o_b / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) over every workgroup's
 // partial b (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes.
-template <int NH, int DPL>
+template <int NH, int DPL, class F>
 __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag_in, uint32_t tag_out,
-                                              PersistLds<NH, DPL> &s) {
+                                              PersistLds<NH, DPL> &s, F on_arrival) {
     const int hd = a.hd, nq = NH * hd, G = gridDim.x;
     const int E = (nq + G - 1) / G;
     const int e0 = min(nq, (int)blockIdx.x * E), e1 = min(nq, e0 + E);
-    if (e0 >= e1) return true;
+    if (e0 >= e1) {
+        on_arrival();
+        return true;
+    }
     const int h_lo = e0 / hd, h_hi = (e1 - 1) / hd;   // E <= hd: at most two heads
     const int per = E + 4;                            // E values, then (m, s) of h_lo and h_hi
     const uint64_t *part = a.t_part;
@@ -489,6 +551,7 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag
         return part + off;
     };
     if (!gather<kCombMax / kThreads>(src, G * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag)) return false;
+    on_arrival();
     // 16-lane row r takes elements k = r, r + 16, ...; lane q of the row takes partials
     // b = q, q + 16, ...; max, weights and sums are reduced over the row by DPP
     const int q = threadIdx.x & 15;
@@ -532,58 +595,72 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             const float v = __uint_as_float((uint32_t)a.embed[row + i] << 16);
             s.resid[i] = a.es != 1.0f ? __fmul_rn(v, a.es) : v;
         }
+        static_assert(sizeof(PLayer) % 4 == 0, "descriptors copied as words");
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.layers);
+        uint32_t *dst = s.layer_words;
+        const int nw = a.n_layers * (int)(sizeof(PLayer) / 4);
+        for (int i = threadIdx.x; i < nw; i += kThreads) dst[i] = src[i];
     }
     __syncthreads();
+    // Every stage issues the next stage's weight loads as soon as its own input has arrived,
+    // before its own arithmetic: the loads then return during that arithmetic and the next
+    // wait, and the next stage's first check of its input (vector loads complete in issue
+    // order) does not wait on them.
+    GemvStage<DT, false, SL> gq;               // the layer's QKV
+    VecRegs<HR> wn_attn, wd_prev;              // its pre-norm; the previous layer's post-FFN norm
+    gq.load(s.layer(0).qkv, s.layer(0).qkv);
+    wn_attn.load(s.layer(0).n_attn, H);
     for (int l = 0; l < a.n_layers; ++l) {
-        const PLayer &L = a.layers[l];
+        const PLayer &L = s.layer(l);
         const uint32_t ep = base + 8u * (uint32_t)l;
-        {   // 1: previous layer's finalize, pre-attention norm, QKV
-            GemvStage<DT, false, SL> g;
-            g.load(L.qkv, L.qkv);
-            VecRegs<HR> wn;
-            wn.load(L.n_attn, H);
-            if (l > 0) {
-                VecRegs<HR> wd;
-                wd.load(a.layers[l - 1].n_ffn_post, H);
-                if (!gather<HR>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
-                add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
-            } else {
-                norm_to(s.xs, s.resid, wn, H, a.eps, s.sh);
-            }
-            g.finish(s.xs, a.t_qkv, ep + 1);
+        AttnStage<DPL, NH> at;
+        // 1: previous layer's finalize, pre-attention norm, QKV (the attention's loads go out first)
+        if (l > 0) {
+            if (!gather<HR>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
+            at.prefetch(a, L, pos, s);
+            add_norm_delta_norm(s.resid, s.xs, s.dl, wd_prev, wn_attn, H, a.eps, s.sh);
+        } else {
+            at.prefetch(a, L, pos, s);
+            norm_to(s.xs, s.resid, wn_attn, H, a.eps, s.sh);
         }
-        if (!attn_stage<DPL, NH>(a, L, pos, ep + 1, ep + 2, s)) return;
-        if (!combine_stage<NH, DPL>(a, ep + 2, ep + 3, s)) return;
-        {   // 4: o-proj
-            GemvStage<DT, false, SL, 32> g;
-            g.load(L.o, L.o);
-            if (!gather<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
-            g.finish(s.xs, a.t_o, ep + 4);
+        gq.finish(s.xs, a.t_qkv, ep + 1);
+        // 2: attention (the o-proj's weights go out when q, k, v have arrived)
+        GemvStage<DT, false, SL, 32> go;
+        if (!at.run(a, L, pos, ep + 1, ep + 2, s, [&] { go.load(L.o, L.o); })) return;
+        // 3: combine (the gate/up weights and the norm weights of stage 5 go out)
+        GemvStage<DT, true, SL> gu;
+        VecRegs<HR> wd_attn, wn_ffn;
+        if (!combine_stage<NH, DPL>(a, ep + 2, ep + 3, s, [&] {
+                gu.load(L.gate, L.up);
+                wd_attn.load(L.n_attn_post, H);
+                wn_ffn.load(L.n_ffn, H);
+            }))
+            return;
+        // 4: o-proj
+        if (!gather<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
+        go.finish(s.xs, a.t_o, ep + 4);
+        // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU (the down
+        // projection's weights go out)
+        GemvStage<DT, false, SL, 32> gd;
+        if (!gather<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
+        gd.load(L.down, L.down);
+        add_norm_delta_norm(s.resid, s.xs, s.dl, wd_attn, wn_ffn, H, a.eps, s.sh);
+        gu.finish(s.xs, a.t_g, ep + 5);
+        // 6: down (the next layer's QKV and norm weights, or the final norm's, go out)
+        if (!gather<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag)) return;
+        if (l + 1 < a.n_layers) {
+            gq.load(s.layer(l + 1).qkv, s.layer(l + 1).qkv);
+            wn_attn.load(s.layer(l + 1).n_attn, H);
+        } else {
+            wn_attn.load(a.norm_final, H);
         }
-        {   // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU
-            GemvStage<DT, true, SL> g;
-            g.load(L.gate, L.up);
-            VecRegs<HR> wd, wn;
-            wd.load(L.n_attn_post, H);
-            wn.load(L.n_ffn, H);
-            if (!gather<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
-            add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
-            g.finish(s.xs, a.t_g, ep + 5);
-        }
-        {   // 6: down
-            GemvStage<DT, false, SL, 32> g;
-            g.load(L.down, L.down);
-            if (!gather<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag)) return;
-            g.finish(s.xs, a.t_dn, ep + 6);
-        }
+        wd_prev.load(L.n_ffn_post, H);
+        gd.finish(s.xs, a.t_dn, ep + 6);
     }
     // last finalize + final norm (transformer.c:400-406)
-    VecRegs<HR> wd, wn;
-    wd.load(a.layers[a.n_layers - 1].n_ffn_post, H);
-    wn.load(a.norm_final, H);
     const uint32_t ep_last = base + 8u * (uint32_t)(a.n_layers - 1) + 6u;
     if (!gather<HR>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
-    add_norm_delta_norm(s.resid, s.xs, s.dl, wd, wn, H, a.eps, s.sh);
+    add_norm_delta_norm(s.resid, s.xs, s.dl, wd_prev, wn_attn, H, a.eps, s.sh);
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < H; i += kThreads) a.xfin[i] = s.xs[i];
 }
@@ -635,11 +712,15 @@ size_t persist_words(int H, int nh, int nkv, int hd, int ffn) {
     return (size_t)(nh + 2 * nkv) * hd + (size_t)kPersistMaxGroups * nh * (hd + 2) + (size_t)nh * hd + H + ffn + H;
 }
 
-bool persist_supported(int dt, int groups, int H, int nh, int nkv, int hd, int ffn) {
+bool persist_supported(int dt, int groups, int n_layers, int H, int nh, int nkv, int hd, int ffn) {
     const PersistKernel k = kernel_for(dt, nh, hd, H, light_slots(groups, H, nh, nkv, hd, ffn));
     const int nq = nh * hd;
     if (!k || nkv != 1 || nq > kAttnMaxQ || hd > kAttnMaxKV) {
         set_error("persistent decode: %d heads of dim %d / %d KV heads not instantiated (one KV head)", nh, hd, nkv);
+        return false;
+    }
+    if (n_layers < 1 || n_layers > kPersistMaxLayers) {
+        set_error("persistent decode: %d layers (at most %d)", n_layers, kPersistMaxLayers);
         return false;
     }
     if (groups < nh || groups > kPersistMaxGroups) {
@@ -674,13 +755,11 @@ int dec_persist(int dt, const PersistArgs &a, int groups, hipStream_t s) {
         set_error("persistent decode: shape not instantiated");
         return -1;
     }
-    PersistArgs args = a;
-    void *params[] = {&args};
-    return hip_ok(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k), dim3(groups), dim3(kThreads), params,
-                                             0, s),
-                  "persistent decode launch")
-               ? 0
-               : -1;
+    // An ordinary launch: persist_supported has checked that `groups` workgroups fit on the
+    // device at once, so they are all dispatched together on an otherwise idle device; if
+    // they were not, the bounded waits would end the kernel with an error, never a hang.
+    hipLaunchKernelGGL(k, dim3(groups), dim3(kThreads), 0, s, a);
+    return hip_ok(hipGetLastError(), "persistent decode launch") ? 0 : -1;
 }
 
 }  // namespace sapphire

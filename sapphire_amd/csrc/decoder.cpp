@@ -5,9 +5,10 @@
 // width allows, else PACKED. One decode step is recorded once into a HIP graph and
 // replayed: embedding of the token in device memory, 18 x (QKV GEMV, attention, o-proj,
 // gate/up GEMV, down GEMV), final norm, LM head with its argmax epilogue writing the next
-// token, and a one-thread kernel that logs the token and advances the position. The host
+// token, and a one-thread kernel that logs the token and advances the position (a greedy
+// TILED LM head does both in its own epilogue: its last workgroup picks the token). The host
 // only launches the graph; nothing crosses PCIe between steps. By default the layers of the
-// step run as one persistent cooperative kernel (decode_persist.hip) instead of six launches
+// step run as one persistent kernel (decode_persist.hip) instead of six launches
 // per layer; sapphire_decoder_set_workgroups selects either form.
 //
 // A batched decoder (sapphire_decoder_create_batch) runs 2..16 sequences in lock step, each
@@ -58,10 +59,15 @@ struct sapphire_decoder {
     int lm_layout = LAYOUT_PACKED;
     float *kc = nullptr, *vc = nullptr;
     float *cos_g = nullptr, *sin_g = nullptr, *cos_l = nullptr, *sin_l = nullptr;
+    const float *rope_rows = nullptr;   // persistent step: [max_ctx][4][head_dim] (see create)
     float *resid[2] = {nullptr, nullptr};
     float *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr, *ffn_out = nullptr, *xfin = nullptr;
     float *logits = nullptr, *attn_part = nullptr;
     void *lm_scratch = nullptr;
+    // a greedy TILED LM head's per-workgroup keys and its 1 + kGreedyGroups counters (zero
+    // between steps): the LM head that picks the token also advances the state
+    unsigned long long *gkeys = nullptr;
+    unsigned *gcount = nullptr;
     int *state = nullptr;   // [0] token, [1] position, [2] step; batched: tokens[B], pos[B], step
     int *log = nullptr;     // [max_ctx] tokens of the steps; batched: [max_ctx][B]
     hipGraph_t graph = nullptr;
@@ -258,7 +264,8 @@ int enqueue_sample(sapphire_decoder *d, const int *d_step, hipStream_t s) {
                          d->state, d->smp_ws, s);
 }
 
-// LM head on d->xfin with the greedy (or sampled) token into d->state[0], then the advance.
+// LM head on d->xfin with the greedy (or sampled) token into d->state[0], then the advance
+// (for a greedy TILED head both happen in the LM head's own epilogue).
 int enqueue_lm_head(sapphire_decoder *d) {
     const auto &c = d->cfg;
     hipStream_t s = d->stream;
@@ -272,10 +279,19 @@ int enqueue_lm_head(sapphire_decoder *d) {
             launch_softmax_argmax(d->logits, c.vocab, nullptr, d->state, static_cast<float *>(d->lm_scratch), s) != 0)
             return -1;
     } else if (d->lm_layout == LAYOUT_TILED) {
-        if ((greedy ? launch_gemv_tiled_softmax(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, nullptr, d->state,
-                                                d->lm_scratch, s)
-                    : launch_gemv_tiled(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, s)) != 0)
-            return -1;
+        if (greedy) {
+            // the logits, the token and the advance in one launch
+            GreedyStep gs;
+            gs.keys = d->gkeys;
+            gs.count = d->gcount;
+            gs.tok = d->state;
+            gs.pos = d->state + 1;
+            gs.step = d->state + 2;
+            gs.log = d->log;
+            gs.seq = d->groups > 0 ? d->seq : nullptr;
+            return launch_gemv_tiled_greedy_step(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, gs, s);
+        }
+        if (launch_gemv_tiled(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
     } else {
         if (launch_gemv_q(c.lm_dtype, LAYOUT_PACKED, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
         if (greedy &&
@@ -308,6 +324,7 @@ int enqueue_step(sapphire_decoder *d) {
         pa.hd = hd;
         pa.ffn = c.ffn;
         pa.max_ctx = c.max_ctx;
+        pa.rope_stride = 4 * hd;
         pa.scale = scale;
         pa.eps = c.eps;
         pa.state = d->state;
@@ -694,17 +711,44 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
                 !upload_tiled(d, c.wdtype, {{w->wdown[l], H}}, c.ffn, false, &L.t_down, "wdown"))
                 return fail();
         }
-        if (!(L.n_attn = upload_f32(d, w->norm_attn[l], H, "norm_attn")) ||
-            !(L.n_attn_post = upload_f32(d, w->norm_attn_post[l], H, "norm_attn_post")) ||
-            !(L.n_ffn = upload_f32(d, w->norm_ffn[l], H, "norm_ffn")) ||
-            !(L.n_ffn_post = upload_f32(d, w->norm_ffn_post[l], H, "norm_ffn_post")) ||
-            !(L.qn = upload_f32(d, w->q_norm[l], hd, "q_norm")) || !(L.kn = upload_f32(d, w->k_norm[l], hd, "k_norm")))
+    }
+    // Every layer's norm weights and QK gammas, and the final norm, in one block: the step
+    // reads a few of them in every stage, and one block keeps them in one translation page.
+    {
+        const size_t vh = (H + 63) & ~size_t(63), vd = (hd + 63) & ~size_t(63);
+        const size_t per = 4 * vh + 2 * vd;
+        std::vector<float> hv((size_t)c.n_layers * per + vh, 0.f);
+        for (int l = 0; l < c.n_layers; ++l) {
+            float *o = hv.data() + (size_t)l * per;
+            memcpy(o, w->norm_attn[l], sizeof(float) * H);
+            memcpy(o + vh, w->norm_attn_post[l], sizeof(float) * H);
+            memcpy(o + 2 * vh, w->norm_ffn[l], sizeof(float) * H);
+            memcpy(o + 3 * vh, w->norm_ffn_post[l], sizeof(float) * H);
+            memcpy(o + 4 * vh, w->q_norm[l], sizeof(float) * hd);
+            memcpy(o + 4 * vh + vd, w->k_norm[l], sizeof(float) * hd);
+        }
+        if (!w->norm_final) {
+            set_error("decoder weights: norm_final is NULL");
             return fail();
+        }
+        memcpy(hv.data() + (size_t)c.n_layers * per, w->norm_final, sizeof(float) * H);
+        const float *dv = upload_f32(d, hv.data(), hv.size(), "norm weights");
+        if (!dv) return fail();
+        for (int l = 0; l < c.n_layers; ++l) {
+            Layer &L = d->layers[l];
+            const float *o = dv + (size_t)l * per;
+            L.n_attn = o;
+            L.n_attn_post = o + vh;
+            L.n_ffn = o + 2 * vh;
+            L.n_ffn_post = o + 3 * vh;
+            L.qn = o + 4 * vh;
+            L.kn = o + 4 * vh + vd;
+        }
+        d->norm_final = dv + (size_t)c.n_layers * per;
     }
     void *p = nullptr;
     if (!upload(d, w->embed_bf16, (size_t)c.vocab * H * sizeof(uint16_t), &p, "embed")) return fail();
     d->embed = static_cast<const uint16_t *>(p);
-    if (!(d->norm_final = upload_f32(d, w->norm_final, H, "norm_final"))) return fail();
     // LM head
     if (c.lm_dtype == DT_BF16) {
         if (B > 1 && !gemm_bf16_supported(d->embed, c.vocab, H)) {
@@ -752,10 +796,25 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
         if (!(d->cos_g = const_cast<float *>(upload_f32(d, cs.data(), cs.size(), "rope"))) ||
             !(d->sin_g = const_cast<float *>(upload_f32(d, sn.data(), sn.size(), "rope"))))
             return fail();
-        rope_tables(hd, c.max_ctx, c.rope_local_base, cs, sn);
-        if (!(d->cos_l = const_cast<float *>(upload_f32(d, cs.data(), cs.size(), "rope"))) ||
-            !(d->sin_l = const_cast<float *>(upload_f32(d, sn.data(), sn.size(), "rope"))))
+        std::vector<float> cl, sl;
+        rope_tables(hd, c.max_ctx, c.rope_local_base, cl, sl);
+        if (!(d->cos_l = const_cast<float *>(upload_f32(d, cl.data(), cl.size(), "rope"))) ||
+            !(d->sin_l = const_cast<float *>(upload_f32(d, sl.data(), sl.size(), "rope"))))
             return fail();
+        if (B == 1) {
+            // the persistent step's copy, one row per position: [pos][global cos | global sin |
+            // local cos | local sin][hd], so a step reads one 4*hd row instead of four tables
+            std::vector<float> il((size_t)c.max_ctx * 4 * hd);
+            for (int p = 0; p < c.max_ctx; ++p) {
+                const size_t r = (size_t)p * hd;
+                float *o = il.data() + (size_t)p * 4 * hd;
+                memcpy(o, cs.data() + r, sizeof(float) * hd);
+                memcpy(o + hd, sn.data() + r, sizeof(float) * hd);
+                memcpy(o + 2 * hd, cl.data() + r, sizeof(float) * hd);
+                memcpy(o + 3 * hd, sl.data() + r, sizeof(float) * hd);
+            }
+            if (!(d->rope_rows = upload_f32(d, il.data(), il.size(), "rope rows"))) return fail();
+        }
     }
     const size_t kv = (size_t)B * c.n_layers * c.n_kv_heads * c.max_ctx * hd;
     if (!dev_alloc_t(d, &d->kc, kv, "k cache") || !dev_alloc_t(d, &d->vc, kv, "v cache") ||
@@ -771,7 +830,11 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
         !dev_alloc_t(d, &d->ffn_out, H, "ffn_out") || !dev_alloc_t(d, &d->xfin, b * H, "xfin") ||
         !dev_alloc_t(d, &d->logits, b * c.vocab, "logits") ||
         !dev_alloc_t(d, &d->attn_part, b * attn_part_floats(c.n_heads, hd), "attn partials") ||
-        !dev_alloc_t(d, &d->state, 2 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log"))
+        !dev_alloc_t(d, &d->state, 2 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log") ||
+        !dev_alloc_t(d, &d->gkeys, tiled_greedy_key_slots(c.vocab), "greedy keys") ||
+        !dev_alloc_t(d, &d->gcount, 1 + kGreedyGroups, "greedy counters") ||
+        !hip_ok(hipMemset(d->gcount, 0, (1 + kGreedyGroups) * sizeof(unsigned)), "greedy counters zero") ||
+        !hip_ok(hipDeviceSynchronize(), "greedy counters zero"))
         return fail();
     if (B > 1 || d->pf_ok) {
         const size_t wsb = std::max({gemm_workspace_bytes(H, c.ffn), gemm_workspace_bytes(H, nq),
@@ -827,8 +890,9 @@ bool setup_persistent(sapphire_decoder *d) {
         P.n_ffn_post = L.n_ffn_post;
         P.qn = L.qn;
         P.kn = L.kn;
-        P.cos_t = L.global ? d->cos_g : d->cos_l;
-        P.sin_t = L.global ? d->sin_g : d->sin_l;
+        // rows of 4 * hd: global cos, global sin, local cos, local sin
+        P.cos_t = d->rope_rows + (L.global ? 0 : 2 * hd);
+        P.sin_t = P.cos_t + hd;
         P.kc = d->kc + (size_t)l * layer_kv;
         P.vc = d->vc + (size_t)l * layer_kv;
         P.window = L.global ? 0 : win;
@@ -843,7 +907,7 @@ bool setup_persistent(sapphire_decoder *d) {
         return false;
     int g = kDefaultGroups;
     if (const char *e = getenv("SAPPHIRE_DECODE_WORKGROUPS")) g = atoi(e);
-    d->groups = g > 0 && persist_supported(c.wdtype, g, c.hidden, c.n_heads, c.n_kv_heads, hd, c.ffn) ? g : 0;
+    d->groups = g > 0 && persist_supported(c.wdtype, g, c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, hd, c.ffn) ? g : 0;
     return true;
 }
 
@@ -1021,7 +1085,7 @@ int sapphire_decoder_set_workgroups(sapphire_decoder_t *d, int groups) {
             return -1;
         }
         SPH_CHECK(hipSetDevice(d->device));
-        if (!persist_supported(c.wdtype, groups, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn)) return -1;
+        if (!persist_supported(c.wdtype, groups, c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn)) return -1;
     }
     if (groups == d->groups) return 0;
     SPH_CHECK(hipStreamSynchronize(d->stream));

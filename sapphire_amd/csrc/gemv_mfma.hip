@@ -216,6 +216,25 @@ __device__ __forceinline__ SoftPart soft_shfl_xor(SoftPart p, int mask) {
     return SoftPart{__shfl_xor(p.m, mask, kWave), __shfl_xor(p.s, mask, kWave), __shfl_xor(p.i, mask, kWave)};
 }
 
+// sample_greedy's order (utils.c:145-156: best = 0, then every later strictly greater value)
+// as one unsigned 64-bit key, the larger key the better (value, index) pair: the value's
+// bits mapped to an unsigned order (-0 taken as +0, which compares equal to it) in the high
+// half, the complement of the index in the low half, so that equal values prefer the lower
+// index. A NaN never wins, except at index 0, which sample_greedy keeps (no value compares
+// greater than NaN): that key is the largest, and its low half decodes to index 0 too.
+__device__ __forceinline__ unsigned long long greedy_key(float v, int row) {
+    if (v != v) return row == 0 ? ~0ull : 0ull;
+    uint32_t u = v == 0.f ? 0u : __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (0xFFFFFFFFu - (uint32_t)row);
+}
+
+__device__ __forceinline__ unsigned long long key_max_shfl(unsigned long long k, int mask) {
+    const uint32_t lo = __shfl_xor((uint32_t)k, mask, kWave), hi = __shfl_xor((uint32_t)(k >> 32), mask, kWave);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    return o > k ? o : k;
+}
+
 // What tile_store needs for activations with NaN / inf elements (nf, wave-uniform): the
 // weight planes, the blocks per row and x itself, for the fold of its non-finite elements.
 struct NfCtx {
@@ -225,31 +244,43 @@ struct NfCtx {
     bool nf;
 };
 
+// Epilogues of the TILED GEMV: the logits only; the logits and each workgroup's softmax /
+// argmax partial; the logits and the greedy token with the decode step's advance.
+constexpr int kEpNone = 0, kEpSoftmax = 1, kEpGreedyStep = 2;
+static_assert(kGreedyGroups == 8, "one counter per XCD-interleaved group of workgroups");
+
 // The 16 columns of each row summed across the row group; lane 16m + 4r stores row
-// 4m + r and, with SM, folds it into its softmax partial.
-template <int DT, bool SM>
+// 4m + r and folds it into its softmax partial (kEpSoftmax) or its greedy key (kEpGreedyStep).
+template <int DT, int EP>
 __device__ __forceinline__ void tile_store(const float (&acc)[4], float *__restrict__ y, int M, int t, int lane,
-                                           SoftPart &sp, const NfCtx &nc) {
+                                           SoftPart &sp, unsigned long long &key, const NfCtx &nc) {
     const int n = lane & 15;
     float v = row16_scatter(acc, n);
     const int row = t * kTileRows + 4 * (lane >> 4) + ((n >> 2) & 3);
     if ((n & 3) == 0 && row < M) {
         if (nc.nf) v += nonfinite::fold<DT, LAYOUT_TILED>(nc.wq, nc.wsc, nc.nb, row, nc.x);
         y[row] = v;
-        if constexpr (SM) soft_push(sp, v, row);
+        if constexpr (EP == kEpSoftmax) soft_push(sp, v, row);
+        if constexpr (EP == kEpGreedyStep) {
+            const unsigned long long k = greedy_key(v, row);
+            key = k > key ? k : key;
+        }
     }
 }
 
 // Waves walk the 16-row tiles with a grid stride. Where two tiles' loads fit in registers
 // (DB) the next tile is loaded before the current one is consumed; otherwise its loads
 // are issued as soon as the current tile's MFMAs have read their operands. Each wave
-// builds its B digits once. With SM every workgroup also leaves the softmax/argmax partial
-// of its rows in part[blockIdx.x] (folded by softmax_finish_parts).
-template <int DT, int NG, bool SM>
+// builds its B digits once. With kEpSoftmax every workgroup also leaves the softmax/argmax
+// partial of its rows in part[blockIdx.x] (folded by softmax_finish_parts). With
+// kEpGreedyStep every workgroup leaves the greedy key of its rows in its slot of gs.keys and
+// counts itself done; the last one takes the maximum key, decodes the token and advances the
+// decode state (dec_advance_kernel's work), so the step needs no further launch.
+template <int DT, int NG, int EP>
 __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq, uint32_t q_bytes,
                                                  const uint8_t *__restrict__ wsc, uint32_t s_bytes,
                                                  const float *__restrict__ x, float *__restrict__ y, int M,
-                                                 int ntiles, SoftPart *__restrict__ part) {
+                                                 int ntiles, SoftPart *__restrict__ part, GreedyStep gs) {
     constexpr int NQ = DT == DT_Q8_0 ? 2 : 1;
     constexpr bool DB = NG * (NQ + 1) * 4 * 2 <= 128;   // VGPRs of two tiles' loads
     const int lane = threadIdx.x & (kWave - 1), nw_blk = blockDim.x / kWave;
@@ -276,17 +307,18 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
 
     float acc[4];
     SoftPart sp{-INFINITY, 0.f, 0x7fffffff};
+    unsigned long long key = 0;
     if constexpr (DB) {
         TileRegs<NG> RB;
         while (t < ntiles) {
             if (t + nwaves < ntiles) tile_issue<DT, NG>(RB, rq, rs, t + nwaves, lane);
             tile_mfma<DT, NG>(RA, bop, p, lane, acc);
-            tile_store<DT, SM>(acc, y, M, t, lane, sp, nc);
+            tile_store<DT, EP>(acc, y, M, t, lane, sp, key, nc);
             t += nwaves;
             if (t >= ntiles) break;
             if (t + nwaves < ntiles) tile_issue<DT, NG>(RA, rq, rs, t + nwaves, lane);
             tile_mfma<DT, NG>(RB, bop, p, lane, acc);
-            tile_store<DT, SM>(acc, y, M, t, lane, sp, nc);
+            tile_store<DT, EP>(acc, y, M, t, lane, sp, key, nc);
             t += nwaves;
         }
     } else {
@@ -294,11 +326,64 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
             tile_mfma<DT, NG>(RA, bop, p, lane, acc);
             const int tn = t + nwaves;
             if (tn < ntiles) tile_issue<DT, NG>(RA, rq, rs, tn, lane);
-            tile_store<DT, SM>(acc, y, M, t, lane, sp, nc);
+            tile_store<DT, EP>(acc, y, M, t, lane, sp, key, nc);
             t = tn;
         }
     }
-    if constexpr (SM) {
+    if constexpr (EP == kEpGreedyStep) {
+#pragma unroll
+        for (int mask = 1; mask < kWave; mask <<= 1) key = key_max_shfl(key, mask);
+        __shared__ unsigned long long wkeys[4];
+        __shared__ int last;
+        const int wid = threadIdx.x / kWave;
+        if (lane == 0) wkeys[wid] = key;
+        __syncthreads();
+        const unsigned nb = gridDim.x, ng = nb < kGreedyGroups ? nb : kGreedyGroups;
+        if (threadIdx.x == 0) {
+            unsigned long long b = wkeys[0];
+            for (int w = 1; w < nw_blk; ++w) b = wkeys[w] > b ? wkeys[w] : b;
+            // this workgroup's key in its own slot, acknowledged before the workgroup counts
+            // itself done: one count per workgroup on its group's counter (blockIdx % 8), one per
+            // group on the top counter, so no address takes more than nb / 8 atomics
+            __hip_atomic_store(gs.keys + blockIdx.x, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            const unsigned g = blockIdx.x % kGreedyGroups;
+            const unsigned gsize = nb / kGreedyGroups + (g < nb % kGreedyGroups ? 1u : 0u);
+            int is_last = 0;
+            if (__hip_atomic_fetch_add(gs.count + 1 + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1) {
+                __hip_atomic_store(gs.count + 1 + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                is_last = __hip_atomic_fetch_add(gs.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ng - 1;
+            }
+            last = is_last;
+        }
+        __syncthreads();
+        if (last) {
+            // every workgroup's key has been acknowledged: the maximum, then the advance
+            unsigned long long b = 0;
+            for (unsigned i = threadIdx.x; i < nb; i += blockDim.x) {
+                const unsigned long long k = __hip_atomic_load(gs.keys + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                b = k > b ? k : b;
+            }
+#pragma unroll
+            for (int mask = 1; mask < kWave; mask <<= 1) b = key_max_shfl(b, mask);
+            if (lane == 0) wkeys[wid] = b;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                unsigned long long k = wkeys[0];
+                for (int w = 1; w < nw_blk; ++w) k = wkeys[w] > k ? wkeys[w] : k;
+                const uint32_t r = 0xFFFFFFFFu - (uint32_t)k;
+                const int tok = k != 0 && r < (uint32_t)M ? (int)r : 0;
+                __hip_atomic_store(gs.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int s = *gs.step;
+                *gs.tok = tok;
+                gs.log[s] = tok;
+                *gs.step = s + 1;
+                *gs.pos = *gs.pos + 1;
+                if (gs.seq) *gs.seq = *gs.seq + 1u;
+            }
+        }
+    }
+    if constexpr (EP == kEpSoftmax) {
         // lanes 16m + 4r hold the wave's partials (the others are still empty)
         sp = soft_merge(sp, soft_shfl_xor(sp, 4));
         sp = soft_merge(sp, soft_shfl_xor(sp, 8));
@@ -473,25 +558,31 @@ unsigned tiled_blocks(int dt, int M) {
 }
 
 template <int DT, int NG>
-int launch_mfma_typed(const uint8_t *w, int M, int K, const float *x, float *y, SoftPart *part, hipStream_t st) {
+int launch_mfma_typed(const uint8_t *w, int M, int K, const float *x, float *y, SoftPart *part,
+                      const GreedyStep *gs, hipStream_t st) {
     const int ntiles = (M + kTileRows - 1) / kTileRows;
     const size_t so = q_tiled_scales_offset(DT, M, K);
     const size_t sbytes = q_tiled_bytes(DT, M, K) - so;
     const unsigned blocks = tiled_blocks(DT, M);
-    if (part)
-        hipLaunchKernelGGL((gemv_mfma<DT, NG, true>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
-                           (uint32_t)sbytes, x, y, M, ntiles, part);
+    const GreedyStep g = gs ? *gs : GreedyStep{};
+    if (gs)
+        hipLaunchKernelGGL((gemv_mfma<DT, NG, kEpGreedyStep>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so,
+                           w + so, (uint32_t)sbytes, x, y, M, ntiles, part, g);
+    else if (part)
+        hipLaunchKernelGGL((gemv_mfma<DT, NG, kEpSoftmax>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
+                           (uint32_t)sbytes, x, y, M, ntiles, part, g);
     else
-        hipLaunchKernelGGL((gemv_mfma<DT, NG, false>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
-                           (uint32_t)sbytes, x, y, M, ntiles, part);
+        hipLaunchKernelGGL((gemv_mfma<DT, NG, kEpNone>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so, w + so,
+                           (uint32_t)sbytes, x, y, M, ntiles, part, g);
     return hip_ok(hipGetLastError(), "gemv_mfma launch") ? 0 : -1;
 }
 
-int launch_tiled(int dt, const void *w, int M, int K, const float *x, float *y, SoftPart *part, hipStream_t st) {
+int launch_tiled(int dt, const void *w, int M, int K, const float *x, float *y, SoftPart *part, hipStream_t st,
+                 const GreedyStep *gs = nullptr) {
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     const int ng = K / (kGroupBlocks * kBlock);
 #define SPH_TILED_CASE(DTV, NGV) \
-    if (dt == DTV && ng == NGV) return launch_mfma_typed<DTV, NGV>(wb, M, K, x, y, part, st);
+    if (dt == DTV && ng == NGV) return launch_mfma_typed<DTV, NGV>(wb, M, K, x, y, part, gs, st);
     SPH_TILED_CASE(DT_Q4_0, 5) SPH_TILED_CASE(DT_Q4_0, 8) SPH_TILED_CASE(DT_Q4_0, 9)
     SPH_TILED_CASE(DT_Q8_0, 5) SPH_TILED_CASE(DT_Q8_0, 8) SPH_TILED_CASE(DT_Q8_0, 9)
 #undef SPH_TILED_CASE
@@ -571,6 +662,17 @@ int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *
 
 int launch_gemv_tiled(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t st) {
     return launch_tiled(dt, w, M, K, x, y, nullptr, st);
+}
+
+size_t tiled_greedy_key_slots(int M) { return std::max(tiled_blocks(DT_Q4_0, M), tiled_blocks(DT_Q8_0, M)); }
+
+int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const float *x, float *logits,
+                                  const GreedyStep &gs, hipStream_t st) {
+    if (!gs.keys || !gs.count || !gs.tok || !gs.pos || !gs.step || !gs.log) {
+        set_error("greedy LM head: missing state");
+        return -1;
+    }
+    return launch_tiled(dt, w, M, K, x, logits, nullptr, st, &gs);
 }
 
 }  // namespace sapphire

@@ -54,6 +54,22 @@ int launch_gemv_tiled(int dt, const void *w, int M, int K, const float *x, float
 size_t tiled_softmax_scratch_bytes(int M);
 int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *x, float *logits, float *probs,
                               int *argmax, void *scratch, hipStream_t s);
+// The decode state a greedy LM head advances (dec_advance_kernel's work). keys: one slot per
+// workgroup (tiled_greedy_key_slots); count: 1 + kGreedyGroups counters that are 0 before the
+// first launch and that every launch leaves at 0.
+constexpr int kGreedyGroups = 8;
+struct GreedyStep {
+    unsigned long long *keys = nullptr;  // each workgroup's best greedy key
+    unsigned *count = nullptr;           // [0] groups done, [1 + g] workgroups of group g done
+    int *tok = nullptr, *pos = nullptr, *step = nullptr, *log = nullptr;
+    uint32_t *seq = nullptr;             // the persistent step's counter (may be NULL)
+};
+size_t tiled_greedy_key_slots(int M);
+// TILED GEMV whose epilogue writes the logits, picks the greedy token (sample_greedy's
+// order) into *tok and log[*step], and advances *pos, *step and *seq: one launch for the LM
+// head, the argmax and the advance. Launches that share the state must be ordered.
+int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const float *x, float *logits,
+                                  const GreedyStep &gs, hipStream_t s);
 // Batched GEMM on the TILED layout (gemm_mfma.hip): Y[b][r] = W[r] . X[b] for b < batch, 16
 // sequences per pass. ws: gemm_workspace_bytes(M, K) bytes of 256-byte aligned device memory
 // (the K-split partial sums). Calls sharing a workspace must be ordered.

@@ -1,7 +1,8 @@
-"""The library as a link-level drop-in for the reference's kernels.h / tensor.h / rope.h, and
-its host-arithmetic exports (no GPU needed).
+"""The library as a link-level drop-in for the reference's kernels.h / tensor.h / rope.h /
+transformer.h, and its host-arithmetic exports (no GPU needed).
 
-* Every function the reference's kernels.h, tensor.h and rope.h declare is exported, except
+* Every function the reference's kernels.h, tensor.h, rope.h and transformer.h declare is
+  exported, except
   rope.h's strategy interface (apply_positional_encoding, rope_encoding_strategy,
   alibi_encoding_strategy of positional_encoding.c), which is not on the decode path and stays
   in the engine; the library's rope.h declares it for that file.
@@ -45,7 +46,7 @@ def _exports():
 
 
 @needs_reference
-@pytest.mark.parametrize("header", ["kernels.h", "tensor.h", "rope.h"])
+@pytest.mark.parametrize("header", ["kernels.h", "tensor.h", "rope.h", "transformer.h"])
 def test_exports_cover_reference_headers(header):
     declared = _declared_functions(os.path.join(REF_INCLUDE, header))
     assert len(declared) >= 7
