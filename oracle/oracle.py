@@ -425,7 +425,20 @@ def _ref_structs(model):
     return rc, rw, keep
 
 
-def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False):
+def patched_model(model, patch):
+    """A deep copy of `model` with ref_decode.c's apply_patch applied: patch 1 negates the first
+    block scale of every row of layer 0's q projection, patch 2 adds 0.25f to every element of
+    layer 0's norm_attn."""
+    import copy
+    m = copy.deepcopy(model)
+    if patch == 1:
+        m.weights["wq"][0, :, 0]["scale"] = -m.weights["wq"][0, :, 0]["scale"]
+    elif patch == 2:
+        m.norms["norm_attn"][0] = m.norms["norm_attn"][0] + np.float32(0.25)
+    return m
+
+
+def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False, patch=0):
     """Greedy decode through the compiled reference engine (oracle/_ref)."""
     cfg = model.cfg
     lib = C.CDLL(REF_DECODE_LIB)
@@ -436,14 +449,49 @@ def ref_decode(model, k_cache, v_cache, token, pos, steps, keep_logits=False):
         C.CDLL(REF_LIB).log_set_level(40)
     except AttributeError:
         pass
-    rc, rw, _keep = _ref_structs(model)
+    lib.ref_decode_patch_run.restype = C.c_int
+    lib.ref_decode_patch_run.argtypes = lib.ref_decode_run.argtypes + [C.c_int]
+    # a patch writes into the arrays the engine's tensor views wrap: give it a copy (kept
+    # alive for the call: the structs hold raw pointers into it)
+    run_model = copy_model(model) if patch else model
+    rc, rw, _keep = _ref_structs(run_model)
     tokens = np.empty(steps, np.int32)
     logits = np.empty((steps, cfg.vocab), np.float32) if keep_logits else None
-    r = lib.ref_decode_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data, int(token),
-                           int(pos), int(steps), tokens.ctypes.data,
-                           logits.ctypes.data if logits is not None else None)
+    r = lib.ref_decode_patch_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data, int(token),
+                                 int(pos), int(steps), tokens.ctypes.data,
+                                 logits.ctypes.data if logits is not None else None, int(patch))
     assert r == 0
     return tokens, logits
+
+
+def ref_forward_decode(model, k_cache, v_cache, prompt, token, pos, steps, stages=False):
+    """The compiled reference engine's own loop (engine_forward_run: inference_forward_batch over
+    the prompt in chunks of 32, then inference_forward + sample_greedy), or with stages=True the
+    same loop with every layer composed from the three transformer.h stage functions
+    (engine_stage_run). Returns (tokens[steps], logits[steps, vocab])."""
+    lib = C.CDLL(REF_DECODE_LIB)
+    fn = lib.engine_stage_run if stages else lib.engine_forward_run
+    fn.restype = C.c_int
+    fn.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                   C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    try:
+        C.CDLL(REF_LIB).log_set_level(40)
+    except AttributeError:
+        pass
+    rc, rw, _keep = _ref_structs(model)
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    tokens = np.empty(steps, np.int32)
+    logits = np.empty((steps, model.cfg.vocab), np.float32)
+    r = fn(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data,
+           prompt.ctypes.data if prompt.size else None, int(prompt.size), int(token), int(pos), int(steps),
+           tokens.ctypes.data, logits.ctypes.data)
+    assert r == 0
+    return tokens, logits
+
+
+def copy_model(model):
+    import copy
+    return copy.deepcopy(model)
 
 
 # ---------------------------------------------------------------------------
@@ -464,12 +512,14 @@ def _engine():
         # RTLD_GLOBAL: the engine's kv_cache_get_keys / _values become visible to the library,
         # as an executable's are
         lib = C.CDLL(ENGINE_HIP_LIB, mode=C.RTLD_GLOBAL)
-        for n in ("ref_decode_run", "engine_forward_run"):
+        for n in ("ref_decode_run", "ref_decode_patch_run", "engine_forward_run", "engine_stage_run"):
             getattr(lib, n).restype = C.c_int
         lib.ref_decode_run.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p,
                                        C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        lib.ref_decode_patch_run.argtypes = lib.ref_decode_run.argtypes + [C.c_int]
         lib.engine_forward_run.argtypes = [C.POINTER(RefCfg), C.POINTER(RefWeights), C.c_void_p, C.c_void_p,
                                            C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        lib.engine_stage_run.argtypes = lib.engine_forward_run.argtypes
         try:
             lib.log_set_level.argtypes = [C.c_int]
             lib.log_set_level(40)
@@ -490,6 +540,39 @@ def engine_layer_decode(model, k_cache, v_cache, token, pos, steps):
     logits = np.empty((steps, model.cfg.vocab), np.float32)
     r = lib.ref_decode_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data, int(token), int(pos),
                            int(steps), tokens.ctypes.data, logits.ctypes.data)
+    assert r == 0, "engine run failed"
+    return tokens, logits
+
+
+def engine_patch_decode(model, k_cache, v_cache, token, pos, steps, patch):
+    """engine_layer_decode with ref_decode.c's apply_patch(patch) between the first and the
+    second step, applied to a copy of the model (the library must notice the change: a host
+    weight rewritten and its device copy invalidated, or a norm weight set through
+    tensor_set_f32). Returns (tokens[steps], logits[steps, vocab])."""
+    lib = _engine()
+    run_model = copy_model(model)   # kept alive for the call: the structs hold raw pointers into it
+    rc, rw, _keep = _ref_structs(run_model)
+    tokens = np.empty(steps, np.int32)
+    logits = np.empty((steps, model.cfg.vocab), np.float32)
+    r = lib.ref_decode_patch_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data, int(token),
+                                 int(pos), int(steps), tokens.ctypes.data, logits.ctypes.data, int(patch))
+    assert r == 0, "engine run failed"
+    return tokens, logits
+
+
+def engine_stage_decode(model, k_cache, v_cache, prompt, token, pos, steps):
+    """engine_stage_run of the engine built on libsapphire_hip.so: engine_forward_decode with
+    every layer composed from compute_attention_stage, compute_ffn_stage and
+    finalize_layer_output (transformer.h:95-147), prompt chunks of up to 32 tokens.
+    Returns (tokens[steps], logits[steps, vocab])."""
+    lib = _engine()
+    rc, rw, _keep = _ref_structs(model)
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    tokens = np.empty(steps, np.int32)
+    logits = np.empty((steps, model.cfg.vocab), np.float32)
+    r = lib.engine_stage_run(C.byref(rc), C.byref(rw), k_cache.ctypes.data, v_cache.ctypes.data,
+                             prompt.ctypes.data if prompt.size else None, int(prompt.size), int(token), int(pos),
+                             int(steps), tokens.ctypes.data, logits.ctypes.data)
     assert r == 0, "engine run failed"
     return tokens, logits
 

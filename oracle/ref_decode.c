@@ -160,10 +160,34 @@ static void kv_out(inference_session_t *s, const ref_cfg_t *c, float *k_cache, f
     }
 }
 
-/* Returns 0 on success. tokens_out[steps]; logits_out[steps*vocab] may be NULL;
- * k_cache/v_cache [n_layers][n_kv][max_ctx][hd] are read in and written back. */
-int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache,
-                   int start_token, int start_pos, int steps, int *tokens_out, float *logits_out) {
+/* The library's call for engines that change a tensor's host data behind tensor_set_f32
+ * (absent from the reference, which reads host data on every call). */
+extern int sapphire_tensor_invalidate(tensor_t *t) __attribute__((weak));
+
+/* Changes to the model between the first and the second step (patch 1: every row's first
+ * block scale of layer 0's q_proj negated in place, then sapphire_tensor_invalidate where the
+ * library provides it; patch 2: 0.25f added to every element of layer 0's norm_attn through
+ * tensor_set_f32). The caller's oracle applies the same change to its copy. */
+static void apply_patch(built_t *b, const ref_cfg_t *c, int patch) {
+    model_layer_weights_t *lw = &b->model.layers[0];
+    if (patch == 1) {
+        tensor_t *q = lw->q_proj_weight;
+        int rows = c->n_heads * c->head_dim, nb = (c->hidden + 31) / 32;
+        char *d = (char *)tensor_data_mutable(q);
+        size_t bb = c->wdtype == DTYPE_Q4_0 ? 20 : 36;
+        for (int r = 0; r < rows; ++r) {
+            float *scale = (float *)(d + (size_t)r * nb * bb);   /* the block's leading fp32 scale */
+            *scale = -*scale;
+        }
+        if (sapphire_tensor_invalidate) sapphire_tensor_invalidate(q);
+    } else if (patch == 2) {
+        tensor_t *n = lw->norm_attn_weight;
+        for (int i = 0; i < c->hidden; ++i) tensor_set_f32(n, (size_t)i, tensor_get_f32(n, (size_t)i) + 0.25f);
+    }
+}
+
+static int decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache, int start_token,
+                      int start_pos, int steps, int *tokens_out, float *logits_out, int patch) {
     int L = c->n_layers, H = c->hidden;
     built_t b;
     if (build_model(c, w, &b) != 0) return -1;
@@ -196,6 +220,7 @@ int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, f
         token = sample_greedy(logits, c->vocab);
         tokens_out[st] = token;
         if (logits_out) memcpy(logits_out + (size_t)st * c->vocab, logits, sizeof(float) * (size_t)c->vocab);
+        if (st == 0 && patch) apply_patch(&b, c, patch);
     }
     kv_out(s, c, k_cache, v_cache);
     rc = 0;
@@ -205,6 +230,19 @@ out:
     free(logits);
     free_model(c, &b);
     return rc;
+}
+
+/* Returns 0 on success. tokens_out[steps]; logits_out[steps*vocab] may be NULL;
+ * k_cache/v_cache [n_layers][n_kv][max_ctx][hd] are read in and written back. */
+int ref_decode_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache,
+                   int start_token, int start_pos, int steps, int *tokens_out, float *logits_out) {
+    return decode_run(c, w, k_cache, v_cache, start_token, start_pos, steps, tokens_out, logits_out, 0);
+}
+
+/* ref_decode_run with apply_patch(patch) between the first and the second step. */
+int ref_decode_patch_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache,
+                         int start_token, int start_pos, int steps, int *tokens_out, float *logits_out, int patch) {
+    return decode_run(c, w, k_cache, v_cache, start_token, start_pos, steps, tokens_out, logits_out, patch);
 }
 
 /* The engine's own loop (tied BF16 LM head, as lm_head computes it): prompt[n_prompt] at
@@ -234,6 +272,107 @@ int engine_forward_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cach
         token = sample_greedy(logits, c->vocab);
         tokens_out[st] = token;
         if (logits_out) memcpy(logits_out + (size_t)st * c->vocab, logits, sizeof(float) * (size_t)c->vocab);
+    }
+    kv_out(s, c, k_cache, v_cache);
+    rc = 0;
+out:
+    if (s) destroy_inference_session(s);
+    free(logits);
+    free_model(c, &b);
+    return rc;
+}
+
+
+/* The buffers sapphire_transformer_layer(_batch) hands its stages: the scratch layout of
+ * init_layer_buffers (transformer.c:19-76), which transformer.h's stage functions expect from
+ * their caller. */
+static layer_buffers_t stage_buffers(const inference_session_t *s, const gemma3_270m_config_t *cfg, int d_model,
+                                     int head_dim, int batch) {
+    layer_buffers_t buf;
+    memset(&buf, 0, sizeof buf);
+    const int max_batch = 32;
+    buf.pm = s->padded_d_model;
+    buf.pi = s->padded_d_inner;
+    buf.pk = s->padded_d_kv;
+    buf.pf = s->padded_d_ff;
+    buf.batch_size = batch;
+    size_t bm = (size_t)max_batch * buf.pm, bi = (size_t)max_batch * buf.pi, bk = (size_t)max_batch * buf.pk,
+           bf = (size_t)max_batch * buf.pf;
+    buf.residual = s->scratch_buffer + bm;
+    buf.norm_buf = s->scratch_buffer + 2 * bm;
+    buf.q_proj = s->scratch_buffer + 3 * bm;
+    buf.k_proj = buf.q_proj + bi;
+    buf.v_proj = buf.k_proj + bk;
+    buf.attn_out = buf.v_proj + bk;
+    buf.ffn_gate_buf = buf.attn_out + bi;
+    buf.ffn_value_buf = buf.ffn_gate_buf + bf;
+    buf.geglu_buf = buf.ffn_value_buf + bf;
+    size_t scratch_floats = s->scratch_size / sizeof(float);
+    int need = d_model, qn = cfg->num_attention_heads * head_dim, kn = cfg->num_key_value_heads * head_dim;
+    if (qn > need) need = qn;
+    if (kn > need) need = kn;
+    buf.weight_scratch = (size_t)need <= scratch_floats ? s->scratch_buffer + (scratch_floats - need) : buf.q_proj;
+    return buf;
+}
+
+/* One layer for `batch` tokens at positions pos.. as sapphire_transformer_layer_batch
+ * composes its stages (transformer.c:318-345): attention, FFN, finalize. */
+static void layer_by_stages(inference_session_t *s, int l, int pos, int batch, float *hidden, const float *cs,
+                            const float *sn) {
+    llm_model_t *model = (llm_model_t *)s->model_spec->llm_model;
+    gemma3_270m_config_t *cfg = (gemma3_270m_config_t *)s->model_spec->variant_config;
+    int d_model = cfg->hidden_size;
+    int head_dim = cfg->head_dim > 0 ? cfg->head_dim : d_model / cfg->num_attention_heads;
+    layer_buffers_t buf = stage_buffers(s, cfg, d_model, head_dim, batch);
+    transformer_layer_ctx_t ctx;
+    memset(&ctx, 0, sizeof ctx);
+    ctx.session = s;
+    ctx.layer = &model->layers[l];
+    ctx.config = cfg;
+    ctx.layer_idx = l;
+    ctx.token_pos = pos;
+    ctx.batch_size = batch;
+    ctx.d_model = d_model;
+    ctx.head_dim = head_dim;
+    compute_attention_stage(buf, &ctx, hidden, cs, sn);
+    compute_ffn_stage(buf, &ctx, hidden);
+    finalize_layer_output(buf, &ctx, hidden);
+}
+
+/* engine_forward_run with every layer of every batch run through the three stage functions
+ * (inference_forward_batch, inference.c:616-651, with sapphire_transformer_layer_batch
+ * composed as transformer.c:318-345 composes it); tied BF16 LM head through lm_head. */
+int engine_stage_run(const ref_cfg_t *c, const ref_weights_t *w, float *k_cache, float *v_cache, const int *prompt,
+                     int n_prompt, int start_token, int start_pos, int steps, int *tokens_out, float *logits_out) {
+    built_t b;
+    if (build_model(c, w, &b) != 0) return -1;
+    int rc = -1;
+    float *logits = NULL;
+    inference_session_t *s = inference_session_create(&b.spec, c->max_ctx);
+    if (!s) goto out;
+    logits = malloc(sizeof(float) * (size_t)c->vocab);
+    if (!logits) goto out;
+    kv_in(s, c, k_cache, v_cache);
+    for (int p = 0; p <= n_prompt + steps - 1; ) {
+        /* a prompt chunk of up to 32 tokens, then one token per step */
+        int in_prompt = p < n_prompt;
+        int n = in_prompt ? (n_prompt - p > 32 ? 32 : n_prompt - p) : 1;
+        int st = p - n_prompt;
+        const int *ids = in_prompt ? prompt + p : &start_token;
+        sapphire_embed_lookup_batch(s, ids, n, s->scratch_buffer);
+        for (int l = 0; l < c->n_layers; ++l) {
+            int glob = s->layer_configs[l].config.attention.is_global;
+            layer_by_stages(s, l, start_pos + p, n, s->scratch_buffer,
+                            glob ? s->rope_freqs_cos_global : s->rope_freqs_cos_local,
+                            glob ? s->rope_freqs_sin_global : s->rope_freqs_sin_local);
+        }
+        if (!in_prompt) {
+            lm_head(s, s->scratch_buffer, logits);
+            start_token = sample_greedy(logits, c->vocab);
+            tokens_out[st] = start_token;
+            if (logits_out) memcpy(logits_out + (size_t)st * c->vocab, logits, sizeof(float) * (size_t)c->vocab);
+        }
+        p += n;
     }
     kv_out(s, c, k_cache, v_cache);
     rc = 0;

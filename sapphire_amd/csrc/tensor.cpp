@@ -130,6 +130,7 @@ int tensor_set_f32(tensor_t *t, size_t idx, float val) {
     static_cast<float *>(t->data)[idx] = val;
     std::lock_guard<std::mutex> g(t->dev_mu);
     t->dev_stale = t->dev != nullptr || t->dev_tiled != nullptr;
+    t->gen.fetch_add(1, std::memory_order_acq_rel);
     return 0;
 }
 
@@ -189,6 +190,7 @@ void drop_device_locked(tensor_t *t) {
     t->dev_tiled = nullptr;
     t->dev_bytes = 0;
     t->dev_stale = false;
+    t->gen.fetch_add(1, std::memory_order_acq_rel);
 }
 
 // Uploads the AoS blocks of a quantized tensor and converts them to `lay` on the device.

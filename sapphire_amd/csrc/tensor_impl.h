@@ -1,6 +1,7 @@
 // tensor_impl.h - private layout of tensor_t (not installed).
 #pragma once
 
+#include <atomic>
 #include <mutex>
 
 #include "../../include/tensor.h"
@@ -27,6 +28,9 @@ struct tensor_t {
     bool dev_stale = false;
     // unique for the life of the process (never reused, unlike the tensor's address)
     uint64_t serial = 0;
+    // advanced whenever the host data may have changed (tensor_set_f32) or the device copies
+    // are dropped (sapphire_tensor_invalidate): holders of derived device state compare it
+    std::atomic<uint64_t> gen{0};
 };
 
 namespace sapphire {
@@ -36,6 +40,8 @@ const void *tensor_device_weights(const tensor_t *t, int *layout, hipStream_t s)
 // the GEMV copy when that is TILED, else a second copy made on first use.
 const void *tensor_device_tiled(const tensor_t *t, hipStream_t s);
 void tensor_drop_device(tensor_t *t);
+// Current generation of t (see tensor_t::gen).
+inline uint64_t tensor_generation(const tensor_t *t) { return t->gen.load(std::memory_order_acquire); }
 // Called by tensor_release before a tensor is freed: drops the device state of an engine
 // session whose KV cache held it (transformer.cpp).
 void transformer_tensor_released(uint64_t serial);

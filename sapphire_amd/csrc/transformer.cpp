@@ -4,8 +4,12 @@
 // inference_session_t.
 //
 // Each engine session gets a device session on first use, keyed by the session's address and
-// checked against the serial numbers of its KV and embedding tensors (so a new session at a
-// recycled address is never served stale state). It holds the layers' weights (the device
+// checked on every call against the serial numbers and generations of every tensor it derived
+// state from (the KV tensors, each projection, norm weight and QK gamma, the embedding and the
+// final norm): a new session at a recycled address, a tensor replaced in the model, host data
+// changed through tensor_set_f32, or a device copy dropped by sapphire_tensor_invalidate all
+// make the next call rebuild it, and releasing any of those tensors drops it at once (so the
+// session never reads freed device memory). It holds the layers' weights (the device
 // copies kernel_gemv keeps for each tensor_t: PACKED Q4_0 / Q8_0), the norm weights as fp32,
 // device copies of the RoPE tables the engine passes, and a device mirror of the engine's KV
 // cache, uploaded once. A layer call moves only what the engine's API exchanges: the hidden
@@ -71,6 +75,9 @@ struct DevSession {
     const inference_session_t *key = nullptr;
     uint64_t kv_serial = 0, embed_serial = 0;
     std::vector<uint64_t> kv_serials;
+    // (serial, generation) of every model tensor the session derived state from, in
+    // for_each_model_tensor's order
+    std::vector<std::pair<uint64_t, uint64_t>> deps;
     int device = 0;
     hipStream_t stream = nullptr;
     int L = 0, H = 0, nh = 0, nkv = 0, hd = 0, ffn = 0, vocab = 0, max_ctx = 0, window = 0, wdt = 0;
@@ -82,6 +89,7 @@ struct DevSession {
     std::map<const float *, float *> rope;         // engine table -> device copy
     float *h = nullptr, *r2 = nullptr, *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr,
           *dn = nullptr, *part = nullptr, *xfin = nullptr, *logits = nullptr;
+    float *res = nullptr;                          // [kMaxBatch][H] residual rows of finalize_layer_output
     int *ints = nullptr;                           // [kMaxBatch] positions or tokens
     char *pin = nullptr;                           // pinned staging
     size_t pin_bytes = 0;
@@ -164,6 +172,35 @@ bool proj(DevSession *S, const tensor_t *t, int M, int K, QMat *out, const char 
     out->M = M;
     out->K = K;
     return true;
+}
+
+// Every model tensor a device session reads, layer by layer, then the embedding and the final
+// norm; f(nullptr) for a missing one.
+template <class F>
+void for_each_model_tensor(const llm_model_t *m, int n_layers, F f) {
+    for (int l = 0; l < n_layers; ++l) {
+        const model_layer_weights_t &w = m->layers[l];
+        for (const tensor_t *t : {w.q_proj_weight, w.k_proj_weight, w.v_proj_weight, w.out_proj_weight,
+                                  w.gate_proj_weight, w.up_proj_weight, w.down_proj_weight, w.norm_attn_weight,
+                                  w.norm_attn_post_weight, w.norm_ffn_weight, w.norm_ffn_post_weight, w.q_norm_weight,
+                                  w.k_norm_weight})
+            f(t);
+    }
+    f(m->embedding_weight);
+    f(m->norm_final_weight);
+}
+
+// Whether every tensor the session derived state from is still the same tensor, with the same
+// host data and device copy.
+bool deps_current(const DevSession &S, const llm_model_t *m) {
+    if (!m || !m->layers) return false;
+    size_t i = 0;
+    bool ok = true;
+    for_each_model_tensor(m, S.L, [&](const tensor_t *t) {
+        ok = ok && t && i < S.deps.size() && S.deps[i].first == t->serial && S.deps[i].second == tensor_generation(t);
+        ++i;
+    });
+    return ok && i == S.deps.size();
 }
 
 bool is_global_layer(const gemma3_270m_config_t *c, int l) {   // attention.c:104-111
@@ -263,6 +300,7 @@ std::shared_ptr<DevSession> build(const inference_session_t *s) {
     // work buffers
     const size_t B = kMaxBatch;
     if (!dalloc_t(S.get(), &S->h, B * S->H, "hidden") || !dalloc_t(S.get(), &S->r2, (size_t)S->H, "residual") ||
+        !dalloc_t(S.get(), &S->res, B * S->H, "finalize residual") ||
         !dalloc_t(S.get(), &S->qkv, (size_t)nq + 2 * nk, "qkv") || !dalloc_t(S.get(), &S->attn, (size_t)nq, "attn") ||
         !dalloc_t(S.get(), &S->o, (size_t)S->H, "o") || !dalloc_t(S.get(), &S->g, (size_t)S->ffn, "g") ||
         !dalloc_t(S.get(), &S->dn, (size_t)S->H, "down") ||
@@ -271,17 +309,19 @@ std::shared_ptr<DevSession> build(const inference_session_t *s) {
         !dalloc_t(S.get(), &S->logits, (size_t)S->vocab, "logits") ||
         !dalloc_t(S.get(), &S->ints, B, "positions"))
         return nullptr;
-    S->pin_bytes = std::max(sizeof(float) * (B * S->H + (size_t)S->vocab),
-                            sizeof(float) * B * S->H + B * sizeof(int) + sizeof(float) * 2 * B * nk);
+    S->pin_bytes = std::max({sizeof(float) * (B * S->H + (size_t)S->vocab),
+                             sizeof(float) * B * S->H + B * sizeof(int) + sizeof(float) * 2 * B * nk,
+                             sizeof(float) * 2 * B * S->H});
     void *p = nullptr;
     if (!hip_ok(hipHostMalloc(&p, S->pin_bytes, hipHostMallocDefault), "hipHostMalloc")) return nullptr;
     S->pin = static_cast<char *>(p);
     if (!hip_ok(hipStreamSynchronize(S->stream), "session upload")) return nullptr;
+    for_each_model_tensor(m, S->L, [&](const tensor_t *t) { S->deps.emplace_back(t->serial, tensor_generation(t)); });
     return S;
 }
 
-// The device session of s, built on first use; rebuilt when the session's KV cache or
-// embedding tensor changed (a new session at a recycled address).
+// The device session of s, built on first use; rebuilt when the session's KV cache changed (a
+// new session at a recycled address) or any model tensor it derived state from changed.
 std::shared_ptr<DevSession> session_of(const inference_session_t *s) {
     if (!s) {
         set_error("transformer: session is NULL");
@@ -295,7 +335,7 @@ std::shared_ptr<DevSession> session_of(const inference_session_t *s) {
             s->model_spec ? static_cast<const llm_model_t *>(s->model_spec->llm_model) : nullptr;
         const tensor_t *k0 = get_k && s->kv_cache ? get_k(s->kv_cache, 0) : nullptr;
         if (k0 && m && m->embedding_weight && k0->serial == it->second->kv_serial &&
-            m->embedding_weight->serial == it->second->embed_serial)
+            m->embedding_weight->serial == it->second->embed_serial && deps_current(*it->second, m))
             return it->second;
         g_sessions.erase(it);
     }
@@ -507,13 +547,16 @@ void transformer_tensor_released(uint64_t serial) {
     {
         std::lock_guard<std::mutex> g(g_mu);
         if (g_sessions.empty()) return;
-        for (auto it = g_sessions.begin(); it != g_sessions.end(); ++it)
-            for (uint64_t k : it->second->kv_serials)
-                if (k == serial) {
-                    dead = it->second;
-                    g_sessions.erase(it);
-                    goto done;
-                }
+        for (auto it = g_sessions.begin(); it != g_sessions.end(); ++it) {
+            bool uses = false;
+            for (uint64_t k : it->second->kv_serials) uses = uses || k == serial;
+            for (const auto &d : it->second->deps) uses = uses || d.first == serial;
+            if (uses) {
+                dead = it->second;
+                g_sessions.erase(it);
+                goto done;
+            }
+        }
     }
 done:
     dead.reset();   // frees the device state outside the registry lock
@@ -625,19 +668,18 @@ void finalize_layer_output(layer_buffers_t buf, transformer_layer_ctx_t *ctx, fl
     std::lock_guard<std::mutex> g(S->mu);
     if (!hip_ok(hipSetDevice(S->device), "hipSetDevice")) return;
     const int l = ctx->layer_idx, B = ctx->batch_size, H = S->H;
-    // hidden rows into S->h[0..B), the residual rows after them
-    if (B > kMaxBatch / 2) {
-        set_error("transformer: finalize batch of %d exceeds %d", B, kMaxBatch / 2);
-        return;
-    }
+    // hidden rows into S->h, the residual rows into S->res (up to the engine's 32 tokens each)
     float *ph = reinterpret_cast<float *>(S->pin);
     for (int b = 0; b < B; ++b) {
         memcpy(ph + (size_t)b * H, hidden + (size_t)b * ctx->d_model, sizeof(float) * H);
         memcpy(ph + (size_t)(B + b) * H, buf.residual + (size_t)b * buf.pm, sizeof(float) * H);
     }
-    if (!hip_ok(hipMemcpyAsync(S->h, ph, sizeof(float) * 2 * B * H, hipMemcpyHostToDevice, S->stream), "H2D")) return;
+    if (!hip_ok(hipMemcpyAsync(S->h, ph, sizeof(float) * B * H, hipMemcpyHostToDevice, S->stream), "H2D") ||
+        !hip_ok(hipMemcpyAsync(S->res, ph + (size_t)B * H, sizeof(float) * B * H, hipMemcpyHostToDevice, S->stream),
+                "H2D"))
+        return;
     for (int b = 0; b < B; ++b)
-        if (enqueue_residual(S.get(), S->h + (size_t)(B + b) * H, S->h + (size_t)b * H, S->layers[(size_t)l].n_ffn_post,
+        if (enqueue_residual(S.get(), S->res + (size_t)b * H, S->h + (size_t)b * H, S->layers[(size_t)l].n_ffn_post,
                              S->h + (size_t)b * H))
             return;
     if (download_rows(S.get(), S->h, hidden, B, H, (size_t)ctx->d_model)) return;

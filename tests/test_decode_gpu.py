@@ -58,6 +58,9 @@ TINY_TIED = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF1
 # epilogue picks the token and advances the step
 WIDE = smodel.DecodeConfig(n_layers=2, hidden=640, n_heads=4, n_kv_heads=1, head_dim=256, ffn=1024, vocab=8192,
                            max_ctx=96, sliding_window=24, global_layers=(1,))
+# hidden above 1024: the persistent step's eight-element-per-thread vector form
+H1280 = smodel.DecodeConfig(n_layers=2, hidden=1280, n_heads=4, n_kv_heads=1, head_dim=256, ffn=2048, vocab=8192,
+                            max_ctx=96, sliding_window=24, global_layers=(1,))
 
 
 # groups: workgroups of the persistent step (None: the decoder's default), 0: the multi-launch step
@@ -76,8 +79,11 @@ WIDE = smodel.DecodeConfig(n_layers=2, hidden=640, n_heads=4, n_kv_heads=1, head
     (GQA2, 41, 40, 12, 0),                # two K/V heads (multi-launch step only)
     (WIDE, 42, 40, 16, None),             # TILED LM head with the greedy-step epilogue
     (WIDE, 42, 40, 16, 0),
+    (H1280, 44, 40, 12, None),            # hidden 1280 (eight vector elements per thread)
+    (H1280, 44, 40, 12, 0),
 ], ids=["tiny", "tiny_graph", "tiny_g16", "tiny_g256", "tiny_q8", "tiny_q8_graph", "mid_window", "mid_window_graph",
-        "mid_window_g96", "tiny_tied_bf16", "tiny_tied_bf16_graph", "gqa2_graph", "wide", "wide_graph"])
+        "mid_window_g96", "tiny_tied_bf16", "tiny_tied_bf16_graph", "gqa2_graph", "wide", "wide_graph", "h1280",
+        "h1280_graph"])
 def test_decode_matches_oracle(oracle, cfg, seed, prefill, steps, groups):
     from sapphire_amd.engine import Decoder
     print(f"decode cfg={cfg.n_layers}x{cfg.hidden} seed={seed} prefill={prefill} steps={steps} groups={groups}",

@@ -163,6 +163,50 @@ def test_decode_matches_reference(oracle, cfg, seed, prefill, steps):
     assert np.array_equal(bits(k1), bits(k2)) and np.array_equal(bits(v1), bits(v2))
 
 
+@pytest.mark.skipif(not ref_decode_available(), reason="oracle/_ref decode harness not built")
+@pytest.mark.parametrize("patch", [1, 2], ids=["q_proj_scales", "norm_attn"])
+def test_patched_decode_matches_reference(oracle, patch):
+    """The expected result of the library's stale-state tests: the reference decodes with a
+    change to the model between its first and second step (a projection's block scales, or a
+    norm weight through tensor_set_f32); the oracle's first step on the model, then its further
+    steps on patched_model, match it bit for bit."""
+    from oracle.oracle import patched_model
+    m = smodel.synthetic_model(smodel.TINY, 9)
+    k1, v1 = m.kv_prefill(30)
+    k2, v2 = k1.copy(), v1.copy()
+    tok = smodel.start_token(smodel.TINY, 9)
+    steps = 6
+    t_ref, l_ref = ref_decode(m, k1, v1, tok, 30, steps, keep_logits=True, patch=patch)
+    t0, l0 = oracle_decode(oracle, m, k2, v2, tok, 30, 1, keep_logits=True)
+    t1, l1 = oracle_decode(oracle, patched_model(m, patch), k2, v2, int(t0[0]), 31, steps - 1, keep_logits=True)
+    assert list(t_ref) == [int(t0[0])] + list(t1)
+    assert np.array_equal(bits(l_ref), bits(np.concatenate([l0, l1])))
+    assert np.array_equal(bits(k1), bits(k2)) and np.array_equal(bits(v1), bits(v2))
+    # the patch changes the result: the test below would catch a library that ignores it
+    t_plain, l_plain = ref_decode(m, *m.kv_prefill(30), tok, 30, steps, keep_logits=True)
+    assert not np.array_equal(bits(l_plain[1:]), bits(l_ref[1:]))
+
+
+@pytest.mark.skipif(not ref_decode_available(), reason="oracle/_ref decode harness not built")
+def test_stage_composition_matches_reference_layer_batch():
+    """ref_decode.c's stage driver (buffers as init_layer_buffers lays them out, then
+    compute_attention_stage, compute_ffn_stage, finalize_layer_output per layer) reproduces the
+    reference's own inference_forward_batch loop bit for bit, including a 32-token prompt
+    chunk: the composition the library's stage exports are tested with is the reference's."""
+    from oracle.oracle import ref_forward_decode
+    cfg = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF16})
+    m = smodel.synthetic_model(cfg, 12)
+    k1, v1 = m.kv_prefill(10)
+    k2, v2 = k1.copy(), v1.copy()
+    prompt = synth.rng(12, 99).integers(0, cfg.vocab, size=40).astype(np.int32)
+    tok = smodel.start_token(cfg, 12)
+    t1, l1 = ref_forward_decode(m, k1, v1, prompt, tok, 10, 5)
+    t2, l2 = ref_forward_decode(m, k2, v2, prompt, tok, 10, 5, stages=True)
+    assert list(t1) == list(t2)
+    assert np.array_equal(bits(l1), bits(l2))
+    assert np.array_equal(bits(k1), bits(k2)) and np.array_equal(bits(v1), bits(v2))
+
+
 def test_scalar_activations_and_apply_rope(oracle, ref):
     """silu / relu / gelu / geglu (activations.c:16-105) and apply_rope (rope.c:17-25 through
     positional_encoding.c:16-104), bit for bit, including special values and odd head_dim."""
