@@ -44,8 +44,11 @@ typedef struct {
 /* Host pointers, read once by sapphire_decoder_create. Projection arrays hold one pointer
  * per layer to that layer's block array ([rows][ceil(K/32)] blocks): wq [H*hd x hidden],
  * wk/wv [n_kv*hd x hidden], wo [hidden x H*hd], wgate/wup [ffn x hidden], wdown [hidden x ffn].
- * Norm weights are fp32 and applied as (1 + w) (normalization.c:104-117); q_norm and k_norm
- * are head_dim long and shared by every head (attention.c:228-269). */
+ * Norm weights are applied as (1 + w) (normalization.c:104-117); q_norm and k_norm are
+ * head_dim long and shared by every head (attention.c:228-269). They are fp32, or, with
+ * norm_dtype DTYPE_BF16, bf16 values (uint16_t arrays behind the same pointers, as a
+ * safetensors checkpoint stores them), widened exactly as get_norm_weights does
+ * (utils.c:218-225). */
 typedef struct {
     const void *const *wq, *const *wk, *const *wv, *const *wo, *const *wgate, *const *wup, *const *wdown;
     const float *const *norm_attn, *const *norm_attn_post, *const *norm_ffn, *const *norm_ffn_post;
@@ -53,6 +56,8 @@ typedef struct {
     const uint16_t *embed_bf16;     /* [vocab][hidden] bf16, scaled by sqrt(hidden) on lookup */
     const float *norm_final;        /* [hidden] */
     const void *lm_head;            /* [vocab][hidden] blocks of lm_dtype; ignored for DTYPE_BF16 */
+    int norm_dtype;                 /* DTYPE_F32 (0) or DTYPE_BF16 (1): the element type of every norm
+                                     * array above (norm_*, q_norm, k_norm, norm_final) */
 } sapphire_decoder_weights_t;
 
 typedef struct sapphire_decoder sapphire_decoder_t;

@@ -717,21 +717,37 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
     {
         const size_t vh = (H + 63) & ~size_t(63), vd = (hd + 63) & ~size_t(63);
         const size_t per = 4 * vh + 2 * vd;
+        if (w->norm_dtype != DT_F32 && w->norm_dtype != DT_BF16) {
+            set_error("decoder weights: norm_dtype %d (F32 or BF16)", w->norm_dtype);
+            return fail();
+        }
+        // fp32 as given, or bf16 widened by its bits (get_norm_weights, utils.c:218-225)
+        auto put = [&](float *dst, const float *src, int n) {
+            if (w->norm_dtype == DT_F32) {
+                memcpy(dst, src, sizeof(float) * n);
+                return;
+            }
+            const uint16_t *b = reinterpret_cast<const uint16_t *>(src);
+            for (int i = 0; i < n; ++i) {
+                const uint32_t u = (uint32_t)b[i] << 16;
+                memcpy(dst + i, &u, sizeof u);
+            }
+        };
         std::vector<float> hv((size_t)c.n_layers * per + vh, 0.f);
         for (int l = 0; l < c.n_layers; ++l) {
             float *o = hv.data() + (size_t)l * per;
-            memcpy(o, w->norm_attn[l], sizeof(float) * H);
-            memcpy(o + vh, w->norm_attn_post[l], sizeof(float) * H);
-            memcpy(o + 2 * vh, w->norm_ffn[l], sizeof(float) * H);
-            memcpy(o + 3 * vh, w->norm_ffn_post[l], sizeof(float) * H);
-            memcpy(o + 4 * vh, w->q_norm[l], sizeof(float) * hd);
-            memcpy(o + 4 * vh + vd, w->k_norm[l], sizeof(float) * hd);
+            put(o, w->norm_attn[l], H);
+            put(o + vh, w->norm_attn_post[l], H);
+            put(o + 2 * vh, w->norm_ffn[l], H);
+            put(o + 3 * vh, w->norm_ffn_post[l], H);
+            put(o + 4 * vh, w->q_norm[l], hd);
+            put(o + 4 * vh + vd, w->k_norm[l], hd);
         }
         if (!w->norm_final) {
             set_error("decoder weights: norm_final is NULL");
             return fail();
         }
-        memcpy(hv.data() + (size_t)c.n_layers * per, w->norm_final, sizeof(float) * H);
+        put(hv.data() + (size_t)c.n_layers * per, w->norm_final, H);
         const float *dv = upload_f32(d, hv.data(), hv.size(), "norm weights");
         if (!dv) return fail();
         for (int l = 0; l < c.n_layers; ++l) {

@@ -13,6 +13,7 @@ import numpy as np
 
 from . import load
 from . import model as smodel
+from . import synth
 
 _VPP = C.POINTER(C.c_void_p)
 _FPP = C.POINTER(C.POINTER(C.c_float))
@@ -31,7 +32,8 @@ class DecoderConfig(C.Structure):
 class DecoderWeights(C.Structure):
     _fields_ = [(n, _VPP) for n in smodel.PROJ] + \
                [(n, _FPP) for n in ("norm_attn", "norm_attn_post", "norm_ffn", "norm_ffn_post", "q_norm", "k_norm")] + \
-               [("embed_bf16", C.c_void_p), ("norm_final", C.c_void_p), ("lm_head", C.c_void_p)]
+               [("embed_bf16", C.c_void_p), ("norm_final", C.c_void_p), ("lm_head", C.c_void_p),
+                ("norm_dtype", C.c_int)]
 
 
 def _protos(L):
@@ -72,7 +74,10 @@ class Decoder:
     """batch = 1: the one-sequence decoder (sapphire_decoder_create); batch 2..16: the
     batched decoder (sapphire_decoder_create_batch), sequences decoded in lock step."""
 
-    def __init__(self, m: "smodel.SyntheticModel", batch: int = 1):
+    def __init__(self, m: "smodel.SyntheticModel", batch: int = 1, norm_bf16: bool = False, norm_dtype=None):
+        """norm_bf16: hand the norm weights over as bf16 (their fp32 values' upper halves, exact
+        when the model's norms are bf16-representable), as a safetensors checkpoint holds them.
+        norm_dtype: overrides the norm_dtype field handed to the library (argument checks)."""
         self.lib = L = load()
         _protos(L)
         cfg = m.cfg
@@ -86,15 +91,19 @@ class Decoder:
             arrs = [np.ascontiguousarray(m.weights[n][l]) for l in range(cfg.n_layers)]
             self._keep.append(arrs)
             setattr(w, n, (C.c_void_p * cfg.n_layers)(*[a.ctypes.data for a in arrs]))
+        def norm_array(a):
+            a = np.ascontiguousarray(a, np.float32)
+            return np.ascontiguousarray(a.view(np.uint32) >> 16).astype(np.uint16) if norm_bf16 else a
         for n in ("norm_attn", "norm_attn_post", "norm_ffn", "norm_ffn_post", "q_norm", "k_norm"):
-            arrs = [np.ascontiguousarray(m.norms[n][l], np.float32) for l in range(cfg.n_layers)]
+            arrs = [norm_array(m.norms[n][l]) for l in range(cfg.n_layers)]
             self._keep.append(arrs)
             setattr(w, n, (C.POINTER(C.c_float) * cfg.n_layers)(
                 *[C.cast(a.ctypes.data, C.POINTER(C.c_float)) for a in arrs]))
-        for n, a in (("embed_bf16", m.embed_bf16), ("norm_final", m.norm_final), ("lm_head", m.lm_head)):
+        for n, a in (("embed_bf16", m.embed_bf16), ("norm_final", norm_array(m.norm_final)), ("lm_head", m.lm_head)):
             a = np.ascontiguousarray(a)
             self._keep.append(a)
             setattr(w, n, a.ctypes.data)
+        w.norm_dtype = (synth.BF16 if norm_bf16 else 0) if norm_dtype is None else int(norm_dtype)
         self.batch = batch
         if batch == 1:
             self.ptr = L.sapphire_decoder_create(C.byref(c), C.byref(w))
@@ -225,14 +234,34 @@ def bench_decode(steps: int = 64, seed: int = 20260101, prefill: int = 1024, rep
     layer_bytes = sum(int(m.weights[n][0].nbytes) for n in smodel.PROJ) * cfg.n_layers
     from . import synth
     lm_names = {synth.Q4_0: "Q4_0", synth.Q8_0: "Q8_0", synth.BF16: "BF16 (the embedding table, tied)"}
+    w_tok = layer_bytes + int(m.lm_head.nbytes)
+    kv_tok = kv_read_bytes(cfg, prefill, steps)
+    ms_tok = best / steps
     return {
         "model": f"Gemma-3-270M-shaped, Q4_0 weights (random init), 18 layers, hidden 640, vocab 262144, "
                  f"LM head {lm_names[cfg.lm_dtype]}",
-        "steps": steps, "kv_prefill": prefill, "ms_total": round(best, 3), "ms_per_token": round(best / steps, 4),
+        "steps": steps, "kv_prefill": prefill, "ms_total": round(best, 3), "ms_per_token": round(ms_tok, 4),
         "tok_per_s": round(steps / (best * 1e-3), 1), "first_tokens": [int(t) for t in toks[:8]],
-        "weight_bytes_per_token": layer_bytes + int(m.lm_head.nbytes),
+        "weight_bytes_per_token": w_tok, "kv_bytes_per_token": kv_tok,
+        "GB_per_s": round((w_tok + kv_tok) / (ms_tok * 1e-3) / 1e9, 1),
+        "frac_hbm_peak": round((w_tok + kv_tok) / (ms_tok * 1e-3) / HBM_PEAK, 4),
         "step_form": f"persistent, {groups} workgroups" if groups else "multi-launch graph",
     }
+
+
+HBM_PEAK = 8.0e12   # MI355X HBM3E, bytes/s
+
+
+def kv_read_bytes(cfg, prefill: int, steps: int) -> int:
+    """K and V bytes one sequence's steps read, averaged per step: step s at position
+    prefill + s attends to min(pos + 1, window) rows in a local layer and pos + 1 in a global
+    one (attention.c:122-127), each row n_kv_heads * head_dim fp32 for K and for V."""
+    win = cfg.sliding_window
+    total = 0
+    for s in range(steps):
+        p = prefill + s
+        total += sum((p + 1) if l in cfg.global_layers else min(p + 1, win) for l in range(cfg.n_layers))
+    return int(round(total / steps)) * cfg.n_kv_heads * cfg.head_dim * 4 * 2
 
 
 def bench_decode_batch(steps: int = 32, batch: int = 16, seed: int = 20260101, prefill: int = 1024, reps: int = 2,
@@ -265,10 +294,7 @@ def bench_decode_batch(steps: int = 32, batch: int = 16, seed: int = 20260101, p
     layer_w = (qb(nq + 2 * nk, cfg.hidden, cfg.wdtype) + qb(cfg.hidden, nq, cfg.wdtype) +
                qb(2 * cfg.ffn, cfg.hidden, cfg.wdtype) + qb(cfg.hidden, cfg.ffn, cfg.wdtype))
     w_step = layer_w * cfg.n_layers + qb(cfg.vocab, cfg.hidden, cfg.lm_dtype)
-    # K and V rows read by one step of one sequence at the first decode position
-    win = cfg.sliding_window
-    rows = sum((prefill + 1) if l in cfg.global_layers else min(prefill + 1, win) for l in range(cfg.n_layers))
-    kv_step = batch * rows * cfg.n_kv_heads * cfg.head_dim * 4 * 2
+    kv_step = batch * kv_read_bytes(cfg, prefill, steps)
     ms_step = best / steps
     return {
         "model": "Gemma-3-1B-shaped, Q4_0 weights (random init), 26 layers, hidden 1152, FFN 6912, vocab 262144"
@@ -277,5 +303,6 @@ def bench_decode_batch(steps: int = 32, batch: int = 16, seed: int = 20260101, p
         "ms_per_step": round(ms_step, 4), "tok_per_s": round(batch * steps / (best * 1e-3), 1),
         "weight_bytes_per_step": w_step, "kv_bytes_per_step": kv_step,
         "GB_per_s": round((w_step + kv_step) / (ms_step * 1e-3) / 1e9, 1),
+        "frac_hbm_peak": round((w_step + kv_step) / (ms_step * 1e-3) / HBM_PEAK, 4),
         "first_tokens": [int(t) for t in toks[0]],
     }

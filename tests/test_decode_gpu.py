@@ -137,6 +137,50 @@ def test_decode_gemma3_270m_64_steps(oracle):
         assert n == steps, f"groups={groups}: near-tie at step {n}: tokens agree on steps 0..{n - 1}"
 
 
+def _bf16_norms(m):
+    """The model with every norm weight rounded to a bf16 value (its upper 16 bits), so the
+    fp32 oracle and a decoder given the bf16 halves see the same numbers."""
+    import copy
+    m = copy.deepcopy(m)
+    trunc = lambda a: (np.ascontiguousarray(a, np.float32).view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    for n in m.norms:
+        m.norms[n] = trunc(m.norms[n])
+    m.norm_final = trunc(m.norm_final)
+    return m
+
+
+@pytest.mark.parametrize("cfg,seed,prefill,steps", [
+    (smodel.TINY, 61, 40, 12),
+    (smodel.GEMMA3_270M, 62, 1024, 16),
+], ids=["tiny", "gemma3_270m"])
+def test_decode_bf16_norm_weights(oracle, cfg, seed, prefill, steps):
+    """Norm weights handed over as bf16 (norm_dtype DTYPE_BF16, as a safetensors checkpoint
+    stores them) are widened as get_norm_weights does (utils.c:218-225): the decode matches the
+    oracle run on the same values in fp32, in the persistent and the multi-launch step."""
+    from sapphire_amd.engine import Decoder
+    m = _bf16_norms(smodel.synthetic_model(cfg, seed))
+    k, v = m.kv_prefill(prefill)
+    tok = smodel.start_token(cfg, seed)
+    ref_toks, ref_logits = oracle_decode(oracle, m, k, v, tok, prefill, steps, nthreads=16, keep_logits=True)
+    for groups in (None, 0):
+        dec = Decoder(m, norm_bf16=True)
+        if groups is not None:
+            dec.set_workgroups(groups)
+        dec.set_kv(k, v)
+        got_toks, got_logits, _ = dec.generate(tok, prefill, steps, keep_logits=True)
+        dec.close()
+        n = _compare(ref_toks, ref_logits, got_toks, got_logits, f"bf16 norms {cfg.n_layers}x{cfg.hidden} groups={groups}")
+        assert n == steps, f"groups={groups}: near-tie at step {n}"
+
+
+def test_decode_rejects_unknown_norm_dtype():
+    """A norm_dtype other than F32 / BF16 is refused at create time, with the reason."""
+    from sapphire_amd.engine import Decoder
+    m = smodel.synthetic_model(smodel.TINY, 63)
+    with pytest.raises(RuntimeError, match="norm_dtype"):
+        Decoder(m, norm_dtype=7)
+
+
 @pytest.mark.parametrize("case", ["tied_pairs", "nan_row0", "nan_winner"])
 def test_decode_greedy_epilogue_ties_and_nan(oracle, case):
     """The TILED LM head picks the greedy token in its epilogue (one 64-bit key per row: the
