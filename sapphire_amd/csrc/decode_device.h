@@ -81,17 +81,35 @@ struct LaneBlock {
     float s;
 };
 
+// p as a pointer into device memory: loads and stores through it compile to global_*
+// instructions. A pointer the compiler cannot trace to a kernel argument (one read from LDS,
+// as the persistent step's layer descriptors are) is otherwise generic, and flat instructions
+// count in the LDS counter as well, so every later wait for an LDS result or a barrier would
+// also wait for them to come back from memory.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *as_global(const T *p) {
+    return (const __attribute__((address_space(1))) T *)p;
+}
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *as_global(T *p) {
+    return (__attribute__((address_space(1))) T *)p;
+}
+
 template <int DT>
 __device__ __forceinline__ void load_lane_block(const QMat &w, int row, int blk, int nb, bool on, LaneBlock<DT> &b) {
     const bool ok = on && row < w.M;
     const size_t bi = ok ? (size_t)row * nb + blk : 0;
-    const u32x4 *qp = reinterpret_cast<const u32x4 *>(w.q + bi * QB<DT>::BYTES);
+    const auto qp = as_global(reinterpret_cast<const u32x4 *>(w.q + bi * QB<DT>::BYTES));
 #pragma unroll
     for (int i = 0; i < QB<DT>::WORDS / 4; ++i) {
         const u32x4 t = qp[i];
         b.q[4 * i + 0] = t.x; b.q[4 * i + 1] = t.y; b.q[4 * i + 2] = t.z; b.q[4 * i + 3] = t.w;
     }
-    b.s = ok ? w.s[bi] : 0.f;
+    // loaded in every lane (block 0 stands in when !ok) and selected afterwards: a load that
+    // only some lanes issue into a register the others then write makes the compiler wait
+    // for every load in flight
+    const float sv = as_global(w.s)[bi];
+    b.s = ok ? sv : 0.f;
 }
 
 template <int DT>

@@ -102,6 +102,7 @@ struct PersistArgs {
     const float *norm_final = nullptr;
     int H = 0, nh = 0, nkv = 0, hd = 0, ffn = 0, max_ctx = 0;
     int rope_stride = 0;              // floats between consecutive positions' rows of cos_t / sin_t
+    int window = 0;                   // the local layers' sliding window (PLayer::window of a local layer)
     float scale = 1.f, eps = 1e-6f;
     const int *state = nullptr;       // [0] token, [1] position
     const uint32_t *seq = nullptr;    // step counter that makes the epochs unique

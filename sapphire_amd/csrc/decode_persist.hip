@@ -68,6 +68,58 @@ __device__ __forceinline__ void row_to_lds(const float *src_row, float *lds_row)
     }
 }
 
+// The layer-invariant geometry of one GEMV stage for this workgroup (the same for every layer:
+// all layers share their shapes), computed once per launch so that the stages do no integer
+// division: rows in wave-steps of 64 / lpr rows, contiguous ranges of ceil(S / G) wave-steps
+// per workgroup, wave w taking every fourth step; lane slot -> (step offset k, block round j).
+struct StageGeom {
+    int M, nb, bpl, s0, s1;
+    int k[kSlots], j[kSlots];
+};
+
+__device__ __forceinline__ void stage_geom(StageGeom &g, int M, int K, int lpr) {
+    const int rpw = kWave / lpr;
+    g.M = M;
+    g.nb = K / kBlock;
+    g.bpl = (g.nb + lpr - 1) / lpr;
+    const int S = (M + rpw - 1) / rpw, per = (S + (int)gridDim.x - 1) / (int)gridDim.x;
+    g.s0 = min(S, (int)blockIdx.x * per);
+    g.s1 = min(S, g.s0 + per);
+    for (int slot = 0; slot < kSlots; ++slot) {
+        g.k[slot] = slot / g.bpl;
+        g.j[slot] = slot - g.k[slot] * g.bpl;
+    }
+}
+
+struct CombGeom {
+    int e0, e1, E, hb;     // elements [e0, e1), nominal E, first element of the range's second head
+};
+
+__device__ __forceinline__ void comb_geom(CombGeom &c, uint32_t *off, int nh, int hd) {
+    const int nq = nh * hd, G = gridDim.x;
+    c.E = (nq + G - 1) / G;
+    c.e0 = min(nq, (int)blockIdx.x * c.E);
+    c.e1 = min(nq, c.e0 + c.E);
+    if (c.e0 >= c.e1) return;
+    const int h_lo = c.e0 / hd, h_hi = (c.e1 - 1) / hd;   // E <= hd: at most two heads
+    c.hb = (h_lo + 1) * hd;
+    const int per = c.E + 4;
+    for (int j = threadIdx.x; j < G * per; j += kThreads) {
+        const int b = j / per, k = j - b * per;
+        size_t o;
+        if (k < c.E) {
+            const int el = min(c.e0 + k, c.e1 - 1);
+            o = ((size_t)b * nh + el / hd) * (hd + 2) + el % hd;
+        } else {
+            const int hh = (k - c.E) < 2 ? h_lo : h_hi;
+            o = ((size_t)b * nh + hh) * (hd + 2) + hd + ((k - c.E) & 1);
+        }
+        off[j] = (uint32_t)o;
+    }
+}
+
+enum { kGeomQkv = 0, kGeomO = 1, kGeomGu = 2, kGeomDown = 3 };
+
 template <int NH, int DPL>
 struct alignas(16) PersistLds {
     float resid[kDecMaxK];                       // the residual stream
@@ -79,6 +131,10 @@ struct alignas(16) PersistLds {
     // the layer descriptors (PLayer), copied once per step: read from here, not with scalar
     // loads of global memory that a step's streaming has long evicted from every cache
     alignas(16) uint32_t layer_words[kPersistMaxLayers * sizeof(PLayer) / 4];
+    StageGeom geom[4];                           // kGeomQkv, kGeomO, kGeomGu, kGeomDown
+    int att_t[2][2];                             // attention slice [t0, t1) of local (0) / global (1) layers
+    CombGeom cg;                                 // the combine's element range
+    uint32_t comb_off[kCombMax];                 // the combine's gathered word offsets
     __device__ __forceinline__ const PLayer &layer(int l) const {
         return reinterpret_cast<const PLayer *>(layer_words)[l];
     }
@@ -161,16 +217,21 @@ struct Contig {
     __device__ const uint64_t *operator()(int j) const { return p + j; }
 };
 
-// Elements t + 256 e of a K-long weight vector in registers (loaded before a wait).
+// Elements t + 256 e of a K-long weight vector in registers (loaded before a wait). Every
+// lane loads (from element K - 1 past the end) and the value is selected where it is used:
+// a load into a register that other lanes of the wave then zero makes the compiler wait for
+// every load in flight at that point.
 template <int R>
 struct VecRegs {
     float v[R];
-    __device__ __forceinline__ void load(const float *__restrict__ p, int K) {
+    int K;
+    __device__ __forceinline__ void load(const float *__restrict__ p, int n) {
+        K = n;
 #pragma unroll
-        for (int e = 0; e < R; ++e) {
-            const int i = threadIdx.x + e * kThreads;
-            v[e] = i < K ? p[i] : 0.f;
-        }
+        for (int e = 0; e < R; ++e) v[e] = as_global(p)[min((int)threadIdx.x + e * kThreads, n - 1)];
+    }
+    __device__ __forceinline__ float operator[](int e) const {
+        return (int)threadIdx.x + e * kThreads < K ? v[e] : 0.f;
     }
 };
 
@@ -196,7 +257,7 @@ __device__ __forceinline__ void norm_to(float *xs, const float *resid, const Vec
 #pragma unroll
     for (int e = 0; e < R; ++e) {
         const int i = threadIdx.x + e * kThreads;
-        if (i < K) xs[i] = __fmul_rn(__fmul_rn(resid[i], r), __fadd_rn(1.0f, w.v[e]));
+        if (i < K) xs[i] = __fmul_rn(__fmul_rn(resid[i], r), __fadd_rn(1.0f, w[e]));
     }
     __syncthreads();
 }
@@ -219,7 +280,7 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
         const int i = threadIdx.x + e * kThreads;
         nv[e] = 0.f;
         if (i < K) {
-            nv[e] = __fadd_rn(resid[i], __fmul_rn(__fmul_rn(dl[i], r1), __fadd_rn(1.0f, wd.v[e])));
+            nv[e] = __fadd_rn(resid[i], __fmul_rn(__fmul_rn(dl[i], r1), __fadd_rn(1.0f, wd[e])));
             resid[i] = nv[e];
             acc = __builtin_fmaf(nv[e], nv[e], acc);
         }
@@ -231,7 +292,7 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
 #pragma unroll
     for (int e = 0; e < R; ++e) {
         const int i = threadIdx.x + e * kThreads;
-        if (i < K) xs[i] = __fmul_rn(__fmul_rn(nv[e], r2), __fadd_rn(1.0f, wn.v[e]));
+        if (i < K) xs[i] = __fmul_rn(__fmul_rn(nv[e], r2), __fadd_rn(1.0f, wn[e]));
     }
     __syncthreads();
 }
@@ -248,21 +309,17 @@ struct GemvStage {
     static_assert(LPR == 16 || LPR == 32, "rows of 16 or 32 lanes");
     static constexpr int RPW = kWave / LPR;   // rows per wave-step
     LaneBlock<DT> b0[SL], b1[GEGLU ? SL : 1];
-    int M, nb, bpl, q, rin, s0, s1;
+    const StageGeom *g;
 
-    __device__ __forceinline__ void load(const QMat &w0, const QMat &w1) {
-        M = w0.M;
-        nb = w0.K / kBlock;
-        bpl = (nb + LPR - 1) / LPR;
+    __device__ __forceinline__ void load(const QMat &w0, const QMat &w1, const StageGeom &geom) {
+        g = &geom;
+        const int M = g->M, nb = g->nb, s0 = g->s0, s1 = g->s1;
         const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-        q = lane & (LPR - 1);
-        rin = lane / LPR;
-        const int S = (M + RPW - 1) / RPW, per = (S + (int)gridDim.x - 1) / (int)gridDim.x;
-        s0 = min(S, (int)blockIdx.x * per);
-        s1 = min(S, s0 + per);
+        const int q = lane & (LPR - 1), rin = lane / LPR;
+        (void)M;
 #pragma unroll
         for (int slot = 0; slot < SL; ++slot) {
-            const int k = slot / bpl, j = slot - k * bpl;
+            const int k = g->k[slot], j = g->j[slot];
             const int st = s0 + wid + 4 * k;
             if (st < s1) {
                 const int blk = q + LPR * j;
@@ -275,11 +332,13 @@ struct GemvStage {
     // y[row] (tagged) = W0[row] . xs, or gelu(W0[row] . xs) * (W1[row] . xs) for the GeGLU form.
     // Ends with a workgroup barrier, after which xs may be overwritten.
     __device__ __forceinline__ void finish(const float *xs, uint64_t *y, uint32_t tag) {
-        const int wid = threadIdx.x / kWave;
+        const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+        const int q = lane & (LPR - 1), rin = lane / LPR;
+        const int M = g->M, nb = g->nb, bpl = g->bpl, s0 = g->s0, s1 = g->s1;
         float p0 = 0.f, p1 = 0.f;
 #pragma unroll
         for (int slot = 0; slot < SL; ++slot) {
-            const int k = slot / bpl, j = slot - k * bpl;
+            const int k = g->k[slot], j = g->j[slot];
             const int st = s0 + wid + 4 * k;
             if (st < s1) {
                 const int blk = q + LPR * j;
@@ -359,14 +418,21 @@ struct AttnStage {
         }
     }
 
-    __device__ __forceinline__ void prefetch(const PersistArgs &a, const PLayer &L, int pos, PersistLds<NH, DPL> &s) {
-        const int hd = a.hd;
+    // this workgroup's slice [t0, t1) of the positions a layer with sliding window `window`
+    // (0: global) attends to at pos (attention.c:122-127); computed once per launch
+    __device__ static void slice(int pos, int window, int &t0, int &t1) {
         const int seq = pos + 1;
-        const int start = (L.window > 0 && seq > L.window) ? seq - L.window : 0;
+        const int start = (window > 0 && seq > window) ? seq - window : 0;
         const int len = seq - start, G = gridDim.x;
         const int chunk = (len + G - 1) / G;
         t0 = min(seq, start + (int)blockIdx.x * chunk);
         t1 = min(seq, t0 + chunk);
+    }
+
+    __device__ __forceinline__ void prefetch(const PersistArgs &a, const PLayer &L, int pos, PersistLds<NH, DPL> &s) {
+        const int hd = a.hd;
+        t0 = s.att_t[L.window > 0 ? 0 : 1][0];
+        t1 = s.att_t[L.window > 0 ? 0 : 1][1];
         const int lane = threadIdx.x & (kWave - 1), d0 = lane * DPL;
         load_batch(L, hd, pos, t0, s);
         // gammas (one head_dim vector for every q head, one for k: attention.c:228-269) and the
@@ -374,10 +440,10 @@ struct AttnStage {
         const size_t ci = (size_t)pos * a.rope_stride + (size_t)(lane & (kWave / 2 - 1)) * DPL;
 #pragma unroll
         for (int i = 0; i < DPL; ++i) {
-            gq[i] = L.qn[d0 + i];
-            gk[i] = L.kn[d0 + i];
-            cs[i] = L.cos_t[ci + i];
-            sn[i] = L.sin_t[ci + i];
+            gq[i] = as_global(L.qn)[d0 + i];
+            gk[i] = as_global(L.kn)[d0 + i];
+            cs[i] = as_global(L.cos_t)[ci + i];
+            sn[i] = as_global(L.sin_t)[ci + i];
         }
     }
 
@@ -450,8 +516,8 @@ struct AttnStage {
             const size_t off = (size_t)pos * hd + d0;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) {
-                L.kc[off + i] = qk[HPW][i];
-                L.vc[off + i] = vnew[i];
+                as_global(L.kc)[off + i] = qk[HPW][i];
+                as_global(L.vc)[off + i] = vnew[i];
             }
         }
 
@@ -524,47 +590,42 @@ struct AttnStage {
 
 // Stage 3: attention elements [e0, e1) of this workgroup, E = ceil(NH*hd / G) each:
 // out = sum_b e_b o_b / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) over every workgroup's
-// partial b (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes.
+// partial b (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes. The
+// gathered words are E values, then (m, s) of the range's first and last head, of every
+// partial; their offsets (s.comb_off) and the range are computed once per launch.
 template <int NH, int DPL, class F>
 __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag_in, uint32_t tag_out,
                                               PersistLds<NH, DPL> &s, F on_arrival) {
-    const int hd = a.hd, nq = NH * hd, G = gridDim.x;
-    const int E = (nq + G - 1) / G;
-    const int e0 = min(nq, (int)blockIdx.x * E), e1 = min(nq, e0 + E);
-    if (e0 >= e1) {
+    const CombGeom c = s.cg;
+    if (c.e0 >= c.e1) {
         on_arrival();
         return true;
     }
-    const int h_lo = e0 / hd, h_hi = (e1 - 1) / hd;   // E <= hd: at most two heads
-    const int per = E + 4;                            // E values, then (m, s) of h_lo and h_hi
+    const int G = gridDim.x, per = c.E + 4;
+    constexpr int NE = kCombMax / kThreads;
+    uint32_t offs[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+        const int j = threadIdx.x + e * kThreads;
+        offs[e] = j < G * per ? s.comb_off[j] : 0u;
+    }
     const uint64_t *part = a.t_part;
-    auto src = [=](int j) -> const uint64_t * {
-        const int b = j / per, k = j - b * per;
-        size_t off;
-        if (k < E) {
-            const int el = min(e0 + k, e1 - 1);
-            off = ((size_t)b * NH + el / hd) * (hd + 2) + el % hd;
-        } else {
-            const int hh = (k - E) < 2 ? h_lo : h_hi;
-            off = ((size_t)b * NH + hh) * (hd + 2) + hd + ((k - E) & 1);
-        }
-        return part + off;
-    };
-    if (!gather<kCombMax / kThreads>(src, G * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag)) return false;
+    auto src = [&](int j) -> const uint64_t * { return part + offs[(j - (int)threadIdx.x) / kThreads]; };
+    if (!gather<NE>(src, G * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag)) return false;
     on_arrival();
     // 16-lane row r takes elements k = r, r + 16, ...; lane q of the row takes partials
     // b = q, q + 16, ...; max, weights and sums are reduced over the row by DPP
     const int q = threadIdx.x & 15;
-    for (int k = threadIdx.x / 16; k < e1 - e0; k += kThreads / 16) {
-        const int el = e0 + k, hk = el / hd == h_lo ? 0 : 2;
+    for (int k = threadIdx.x / 16; k < c.e1 - c.e0; k += kThreads / 16) {
+        const int el = c.e0 + k, hk = el < c.hb ? 0 : 2;
         float M = -INFINITY;
-        for (int b = q; b < G; b += 16) M = fmaxf(M, s.comb[b * per + E + hk]);
+        for (int b = q; b < G; b += 16) M = fmaxf(M, s.comb[b * per + c.E + hk]);
         M = row16_max(M);
         float S = 0.f, O = 0.f;
         for (int b = q; b < G; b += 16) {
-            const float mb = s.comb[b * per + E + hk];
+            const float mb = s.comb[b * per + c.E + hk];
             const float e = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
-            S = __builtin_fmaf(s.comb[b * per + E + hk + 1], e, S);
+            S = __builtin_fmaf(s.comb[b * per + c.E + hk + 1], e, S);
             O = __builtin_fmaf(s.comb[b * per + k], e, O);
         }
         S = row16_sum(S);
@@ -600,6 +661,18 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         uint32_t *dst = s.layer_words;
         const int nw = a.n_layers * (int)(sizeof(PLayer) / 4);
         for (int i = threadIdx.x; i < nw; i += kThreads) dst[i] = src[i];
+        // the stages' layer-invariant geometry
+        CombGeom cg;
+        comb_geom(cg, s.comb_off, NH, a.hd);
+        if (threadIdx.x == 0) {
+            stage_geom(s.geom[kGeomQkv], (NH + 2) * a.hd, H, kLpr);
+            stage_geom(s.geom[kGeomO], H, nq, 32);
+            stage_geom(s.geom[kGeomGu], a.ffn, H, kLpr);
+            stage_geom(s.geom[kGeomDown], H, a.ffn, 32);
+            AttnStage<DPL, NH>::slice(pos, a.window, s.att_t[0][0], s.att_t[0][1]);
+            AttnStage<DPL, NH>::slice(pos, 0, s.att_t[1][0], s.att_t[1][1]);
+            s.cg = cg;
+        }
     }
     __syncthreads();
     // Every stage issues the next stage's weight loads as soon as its own input has arrived,
@@ -608,30 +681,29 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     // order) does not wait on them.
     GemvStage<DT, false, SL> gq;               // the layer's QKV
     VecRegs<HR> wn_attn, wd_prev;              // its pre-norm; the previous layer's post-FFN norm
-    gq.load(s.layer(0).qkv, s.layer(0).qkv);
+    AttnStage<DPL, NH> at;                     // its attention (K/V rows in LDS, gammas, RoPE)
+    gq.load(s.layer(0).qkv, s.layer(0).qkv, s.geom[kGeomQkv]);
     wn_attn.load(s.layer(0).n_attn, H);
+    at.prefetch(a, s.layer(0), pos, s);
     for (int l = 0; l < a.n_layers; ++l) {
         const PLayer &L = s.layer(l);
         const uint32_t ep = base + 8u * (uint32_t)l;
-        AttnStage<DPL, NH> at;
-        // 1: previous layer's finalize, pre-attention norm, QKV (the attention's loads go out first)
+        // 1: previous layer's finalize, pre-attention norm, QKV
         if (l > 0) {
             if (!gather<HR>(Contig{a.t_dn}, H, ep - 2, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
-            at.prefetch(a, L, pos, s);
             add_norm_delta_norm(s.resid, s.xs, s.dl, wd_prev, wn_attn, H, a.eps, s.sh);
         } else {
-            at.prefetch(a, L, pos, s);
             norm_to(s.xs, s.resid, wn_attn, H, a.eps, s.sh);
         }
         gq.finish(s.xs, a.t_qkv, ep + 1);
         // 2: attention (the o-proj's weights go out when q, k, v have arrived)
         GemvStage<DT, false, SL, 32> go;
-        if (!at.run(a, L, pos, ep + 1, ep + 2, s, [&] { go.load(L.o, L.o); })) return;
+        if (!at.run(a, L, pos, ep + 1, ep + 2, s, [&] { go.load(L.o, L.o, s.geom[kGeomO]); })) return;
         // 3: combine (the gate/up weights and the norm weights of stage 5 go out)
         GemvStage<DT, true, SL> gu;
         VecRegs<HR> wd_attn, wn_ffn;
         if (!combine_stage<NH, DPL>(a, ep + 2, ep + 3, s, [&] {
-                gu.load(L.gate, L.up);
+                gu.load(L.gate, L.up, s.geom[kGeomGu]);
                 wd_attn.load(L.n_attn_post, H);
                 wn_ffn.load(L.n_ffn, H);
             }))
@@ -643,14 +715,15 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         // projection's weights go out)
         GemvStage<DT, false, SL, 32> gd;
         if (!gather<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
-        gd.load(L.down, L.down);
+        gd.load(L.down, L.down, s.geom[kGeomDown]);
         add_norm_delta_norm(s.resid, s.xs, s.dl, wd_attn, wn_ffn, H, a.eps, s.sh);
         gu.finish(s.xs, a.t_g, ep + 5);
         // 6: down (the next layer's QKV and norm weights, or the final norm's, go out)
         if (!gather<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag)) return;
         if (l + 1 < a.n_layers) {
-            gq.load(s.layer(l + 1).qkv, s.layer(l + 1).qkv);
+            gq.load(s.layer(l + 1).qkv, s.layer(l + 1).qkv, s.geom[kGeomQkv]);
             wn_attn.load(s.layer(l + 1).n_attn, H);
+            at.prefetch(a, s.layer(l + 1), pos, s);   // this layer's attention is done with the LDS rows
         } else {
             wn_attn.load(a.norm_final, H);
         }

@@ -325,6 +325,7 @@ int enqueue_step(sapphire_decoder *d) {
         pa.ffn = c.ffn;
         pa.max_ctx = c.max_ctx;
         pa.rope_stride = 4 * hd;
+        pa.window = win;
         pa.scale = scale;
         pa.eps = c.eps;
         pa.state = d->state;
