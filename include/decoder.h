@@ -117,6 +117,16 @@ int sapphire_decoder_set_epoch_count(sapphire_decoder_t *dec, uint32_t steps);
  * must be at most 2^21. NaN temperatures are rejected. 0 / -1. */
 int sapphire_decoder_set_sampling(sapphire_decoder_t *dec, float temperature, const float *draws, int n_draws);
 
+/* Stop tokens for the following generate calls (none by default; n = 0 clears them). The
+ * reference's generation loop ends when it samples 1 (<eos>) or 106 (<end_of_turn>)
+ * (inference.c:298-301); a host that mirrors it sets {1, 106}. On the device, the step that
+ * picks a stop token logs it to tokens_out and marks its sequence done; every later step of
+ * that sequence logs -1, leaves its position and its KV cache unchanged and, for a
+ * one-sequence decoder, returns at once from its layers and its greedy LM head (the
+ * multi-launch step and a batch whose other sequences go on still run their kernels). The
+ * logits of such steps are unspecified. At most 8 tokens, each in [0, vocab). 0 / -1. */
+int sapphire_decoder_set_stop_tokens(sapphire_decoder_t *dec, const int *ids, int n);
+
 /* ---- batched decode ----
  * `batch` (2..16) independent sequences decoded in lock step, each with its own KV cache,
  * position and token: one step runs every projection as one matrix-core GEMM over

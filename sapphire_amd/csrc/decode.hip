@@ -165,6 +165,7 @@ __global__ __launch_bounds__(NT) void dec_attn_part_kernel(AttnArgs a) {
         a.kc += b * a.kv_stride;
         a.vc += b * a.kv_stride;
         a.d_pos += b;
+        if (a.d_done) a.d_done += b;
         a.part += b * (size_t)gridDim.x * NH * (a.hd + 2);
     }
     __shared__ float raw[kAttnMaxQ + 2 * kAttnMaxKV];   // q | k | v as projected
@@ -251,7 +252,8 @@ __global__ __launch_bounds__(NT) void dec_attn_part_kernel(AttnArgs a) {
     }
     __syncthreads();
     const float *vnew = raw + (NH + nkv) * hd;
-    if (blockIdx.x == 0 && !a.kv_written)   // kv_cache_write_token: [head][pos][dim]
+    // kv_cache_write_token: [head][pos][dim] (a stopped sequence writes none)
+    if (blockIdx.x == 0 && !a.kv_written && !(a.d_done && *a.d_done))
         for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) {
             const int h = i / hd, d = i - h * hd;
             const size_t off = ((size_t)h * a.max_ctx + pos) * hd + d;
@@ -379,6 +381,217 @@ __global__ __launch_bounds__(NT) void dec_attn_part_kernel(AttnArgs a) {
     }
 }
 
+// The batch form with the K/V rows in LDS. A slice's rows go into LDS by DMA as soon as the
+// position is known, before this token's q/k/v are used, so the whole slice (up to PB
+// positions, 144 KiB) is in flight at once without holding it in registers; one workgroup per
+// CU. Wave w takes positions rb + w + 8j of a round [rb, rb + PB) and loads exactly those rows,
+// so it waits for its own DMA only; a slice longer than PB takes further rounds in the same
+// slots. Arithmetic and order are those of dec_attn_part_kernel.
+template <int DPL, int NH, int NKV>
+struct AttnLdsShape {
+    static constexpr int NT = kAttnThreadsBatch, NW = NT / kWave, HD = kWave * DPL;
+    // raw q|k|v, the normed q and k, and (within 2 KiB) the small merge arrays
+    static constexpr int kFixed = (2 * NH + 3 * NKV) * HD * 4 + 2048;
+    static constexpr int kRoom = (160 * 1024 - kFixed) / (2 * NKV * HD * 4) / NW * NW;
+    static constexpr int PB = kRoom < 72 ? kRoom : 72;   // positions per round
+    static_assert(PB >= NW, "at least one row per wave and round");
+    static_assert(NW * NH <= 2 * PB * NKV, "the wave merge fits in the row space");
+};
+
+template <int DPL, int NH, int NKV>
+__global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArgs a) {
+    using S = AttnLdsShape<DPL, NH, NKV>;
+    constexpr int NT = S::NT, NW = S::NW, HD = S::HD, PB = S::PB, PW = PB / NW;
+    {   // sequence blockIdx.y of a batch
+        const size_t b = blockIdx.y;
+        a.qkv += b * a.qkv_stride;
+        a.kc += b * a.kv_stride;
+        a.vc += b * a.kv_stride;
+        a.d_pos += b;
+        if (a.d_done) a.d_done += b;
+        a.part += b * (size_t)gridDim.x * NH * (HD + 2);
+    }
+    __shared__ __attribute__((aligned(16))) float kvr[2][PB * NKV][HD];   // K rows | V rows of a round
+    __shared__ float raw[(NH + 2 * NKV) * HD];                              // q | k | v as projected
+    __shared__ float qs[NH * HD];
+    __shared__ float ks[NKV * HD];
+    __shared__ float part8[8 * 16];
+    __shared__ float ss[16];
+    __shared__ float wm[NW][NH], wsum[NW][NH], wx[NW][NH];
+    __shared__ float wmax[NH], wtot[NH];
+    constexpr int half = HD / 2, group = NH / NKV;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int wu = __builtin_amdgcn_readfirstlane(wid);
+    // q | k | v and the QK-norm gammas wait for nothing (thread t takes pair i = t mod hd/2 of
+    // every head)
+    constexpr int nraw = (NH + 2 * NKV) * HD;
+    constexpr int kRawRegs = (nraw + NT - 1) / NT;
+    float rv[kRawRegs];
+#pragma unroll
+    for (int e = 0; e < kRawRegs; ++e) {
+        const int i = threadIdx.x + e * NT;
+        rv[e] = i < nraw ? a.qkv[i] : 0.f;
+    }
+    const int pi = threadIdx.x % half;
+    const float gq0 = a.qn[pi], gq1 = a.qn[pi + half], gk0 = a.kn[pi], gk1 = a.kn[pi + half];
+    const int pos = *a.d_pos, seq = pos + 1;
+    const float rc = a.cos_t[(size_t)pos * HD + pi], rs = a.sin_t[(size_t)pos * HD + pi];
+    const int start = (a.window > 0 && seq > a.window) ? seq - a.window : 0;
+    const int len = seq - start, nsplit = gridDim.x;
+    const int chunk = (len + nsplit - 1) / nsplit;
+    const int t0 = start + blockIdx.x * chunk, t1 = min(seq, t0 + chunk);
+    // this wave's rows of the round from rb into its own slots wu + NW j; the current
+    // position's row is this kernel's own k and v
+    auto issue = [&](int rb) {
+        const int re = min(t1, rb + PB);
+#pragma unroll
+        for (int j = 0; j < PW; ++j) {
+            const int t = rb + wu + NW * j;
+            if (t < re && t != pos)
+#pragma unroll
+                for (int hk = 0; hk < NKV; ++hk) {
+                    const size_t off = ((size_t)hk * a.max_ctx + t) * HD;
+                    row_to_lds<DPL>(a.kc + off, kvr[0][(wu + NW * j) * NKV + hk]);
+                    row_to_lds<DPL>(a.vc + off, kvr[1][(wu + NW * j) * NKV + hk]);
+                }
+        }
+    };
+    issue(t0);
+
+#pragma unroll
+    for (int e = 0; e < kRawRegs; ++e) {
+        const int i = threadIdx.x + e * NT;
+        if (i < nraw) raw[i] = rv[e];
+    }
+    __syncthreads();
+    // QK-norm and RoPE of the query heads and the K heads in one pass (norm_rope_heads'
+    // arithmetic)
+    vectors_sum_sq(raw, NH + NKV, HD, part8, ss);
+    if (threadIdx.x < NH + NKV) ss[threadIdx.x] = rms_inv_of(ss[threadIdx.x], HD, a.eps);
+    __syncthreads();
+    for (int v = threadIdx.x / half; v < NH + NKV; v += NT / half) {
+        const bool isq = v < NH;
+        const float r = ss[v], g0 = isq ? gq0 : gk0, g1 = isq ? gq1 : gk1;
+        const float *p = raw + (size_t)v * HD;
+        const float x0 = __fmul_rn(__fmul_rn(p[pi], r), __fadd_rn(1.0f, g0));
+        const float x1 = __fmul_rn(__fmul_rn(p[pi + half], r), __fadd_rn(1.0f, g1));
+        float *dst = isq ? qs + v * HD : ks + (v - NH) * HD;
+        dst[pi] = __builtin_fmaf(x0, rc, -__fmul_rn(x1, rs));
+        dst[pi + half] = __builtin_fmaf(x1, rc, __fmul_rn(x0, rs));
+    }
+    __syncthreads();
+    const float *vnew = raw + (NH + NKV) * HD;
+    // kv_cache_write_token: [head][pos][dim] (a stopped sequence writes none)
+    if (blockIdx.x == 0 && !a.kv_written && !(a.d_done && *a.d_done))
+        for (int i = threadIdx.x; i < NKV * HD; i += NT) {
+            const int h = i / HD, d = i - h * HD;
+            const size_t off = ((size_t)h * a.max_ctx + pos) * HD + d;
+            a.kc[off] = ks[i];
+            a.vc[off] = vnew[i];
+        }
+
+    const float sl2 = __fmul_rn(a.scale, 1.44269504088896341f);
+    float m[NH], s[NH], o[NH][DPL], qr[NH][DPL];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        m[h] = -INFINITY;
+        s[h] = 0.f;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) {
+            o[h][d] = 0.f;
+            qr[h][d] = qs[h * HD + lane * DPL + d];
+        }
+    }
+    constexpr int SB = 32 / NH < PW ? 32 / NH : PW;
+    for (int rb = t0; rb < t1; rb += PB) {
+        if (rb != t0) issue(rb);                       // the slots' previous rows are all read
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const int re = min(t1, rb + PB);
+        const int nj = min(PW, max(0, (re - rb - wu + NW - 1) / NW));   // this wave's positions
+#pragma unroll
+        for (int j0 = 0; j0 < PW; j0 += SB) {
+            if (j0 >= nj) break;
+            float sc[SB][NH];
+#pragma unroll
+            for (int jj = 0; jj < SB; ++jj) {
+                const int j = j0 + jj < PW ? j0 + jj : PW - 1;
+                const bool cur = rb + wu + NW * j == pos;
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    const int hk = h / group;
+                    const float *kp = cur ? ks + hk * HD : kvr[0][(wu + NW * j) * NKV + hk];
+                    float dp = 0.f;
+#pragma unroll
+                    for (int d = 0; d < DPL; ++d) dp = __builtin_fmaf(qr[h][d], kp[lane * DPL + d], dp);
+                    sc[jj][h] = j0 + jj < nj ? __fmul_rn(wave_sum_uniform(dp), sl2) : -INFINITY;
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const int hk = h / group;
+                float mb = sc[0][h];
+#pragma unroll
+                for (int jj = 1; jj < SB; ++jj) mb = fmaxf(mb, sc[jj][h]);
+                const float mn = fmaxf(m[h], mb);
+                const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
+                s[h] = __fmul_rn(s[h], c);
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) o[h][d] = __fmul_rn(o[h][d], c);
+#pragma unroll
+                for (int jj = 0; jj < SB; ++jj)
+                    if (j0 + jj < nj) {
+                        const int j = j0 + jj;
+                        const bool cur = rb + wu + NW * j == pos;
+                        const float *vp = cur ? vnew + hk * HD : kvr[1][(wu + NW * j) * NKV + hk];
+                        const float p = __builtin_amdgcn_exp2f(sc[jj][h] - mn);
+                        s[h] = __fadd_rn(s[h], p);
+#pragma unroll
+                        for (int d = 0; d < DPL; ++d) o[h][d] = __builtin_fmaf(p, vp[lane * DPL + d], o[h][d]);
+                    }
+                m[h] = mn;
+            }
+        }
+    }
+    // merge the waves (their rows are no longer read: the merge takes their space)
+    __syncthreads();
+    float *wo = &kvr[0][0][0];                         // [NW][NH][HD]
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        if (lane == 0) {
+            wm[wid][h] = m[h];
+            wsum[wid][h] = s[h];
+        }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) wo[(wid * NH + h) * HD + lane * DPL + d] = o[h][d];
+    }
+    __syncthreads();
+    if (threadIdx.x < NH) {
+        const int h = threadIdx.x;
+        float M = -INFINITY;
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w][h]);
+        float Ssum = 0.f;
+        for (int w = 0; w < NW; ++w) {
+            const float e = wm[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][h] - M);
+            wx[w][h] = e;
+            Ssum = __builtin_fmaf(wsum[w][h], e, Ssum);
+        }
+        wmax[h] = M;
+        wtot[h] = Ssum;
+    }
+    __syncthreads();
+    float *out = a.part + (size_t)blockIdx.x * NH * (HD + 2);
+    for (int idx = threadIdx.x; idx < NH * HD; idx += NT) {
+        const int h = idx / HD, d = idx - h * HD;
+        float O = 0.f;
+        for (int w = 0; w < NW; ++w) O = __builtin_fmaf(wo[(w * NH + h) * HD + d], wx[w][h], O);
+        out[h * (HD + 2) + d] = O;
+        if (d == 0) {
+            out[h * (HD + 2) + HD] = wmax[h];
+            out[h * (HD + 2) + HD + 1] = wtot[h];
+        }
+    }
+}
+
 // out[h*hd + d] = sum_b e_b o_b[d] / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) (the
 // partials' maxima are in log2 units): the softmax-weighted sum of values of
 // attention.c:140-158 over all slices. One workgroup per head, one thread per dim. Every load
@@ -421,13 +634,15 @@ __global__ void dec_embed_kernel(const uint16_t *__restrict__ embed, int hidden,
 }
 
 __global__ void dec_advance_kernel(const int *__restrict__ tok, int *__restrict__ pos, int *__restrict__ step,
-                                   int *__restrict__ log, uint32_t *__restrict__ seq) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        const int s = *step;
-        log[s] = *tok;
+                                   int *__restrict__ log, uint32_t *__restrict__ seq, int *__restrict__ done,
+                                   StopSet stop) {
+    if (threadIdx.x == 0 && blockIdx.x == 0 && !(done && *done)) {
+        const int s = *step, t = *tok;
+        log[s] = t;
         *step = s + 1;
         *pos = *pos + 1;
         if (seq) *seq = *seq + 1u;
+        if (done && stop.has(t)) *done = 1;   // inference.c:298-301
     }
 }
 
@@ -502,11 +717,14 @@ __global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int npa
 }
 
 __global__ void dec_advance_batch_kernel(const int *__restrict__ tok, int *__restrict__ pos, int *__restrict__ step,
-                                         int batch, int *__restrict__ log) {
+                                         int batch, int *__restrict__ log, int *__restrict__ done, StopSet stop) {
     const int s = *step;
     for (int b = threadIdx.x; b < batch; b += blockDim.x) {
-        log[(size_t)s * batch + b] = tok[b];
+        if (done && done[b]) continue;       // a stopped sequence: its entry keeps the fill
+        const int t = tok[b];
+        log[(size_t)s * batch + b] = t;
         pos[b] = pos[b] + 1;
+        if (done && stop.has(t)) done[b] = 1;   // inference.c:298-301
     }
     __syncthreads();
     if (threadIdx.x == 0) *step = s + 1;
@@ -579,7 +797,7 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
 #define SPH_ATTN(DPLV, NHV, NKVV)                                                                              \
     if (dpl == DPLV && a.nh == NHV && a.nkv == NKVV) {                                                         \
         if (wide)                                                                                              \
-            hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV, NKVV, kAttnThreadsBatch>), dim3(ns, a.batch),    \
+            hipLaunchKernelGGL((dec_attn_lds_kernel<DPLV, NHV, NKVV>), dim3(ns, a.batch),                          \
                                dim3(kAttnThreadsBatch), 0, s, a);                                               \
         else                                                                                                   \
             hipLaunchKernelGGL((dec_attn_part_kernel<DPLV, NHV, NKVV, kThreads>), dim3(ns, a.batch),             \
@@ -617,8 +835,9 @@ int dec_embed(const uint16_t *embed, int hidden, int vocab, float es, const int 
     return hip_ok(hipGetLastError(), "embed launch") ? 0 : -1;
 }
 
-int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, uint32_t *d_seq, hipStream_t s) {
-    hipLaunchKernelGGL(dec_advance_kernel, dim3(1), dim3(64), 0, s, d_token, d_pos, d_step, log, d_seq);
+int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, uint32_t *d_seq, int *d_done,
+                const StopSet &stop, hipStream_t s) {
+    hipLaunchKernelGGL(dec_advance_kernel, dim3(1), dim3(64), 0, s, d_token, d_pos, d_step, log, d_seq, d_done, stop);
     return hip_ok(hipGetLastError(), "advance launch") ? 0 : -1;
 }
 
@@ -642,8 +861,10 @@ int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_
     return hip_ok(hipGetLastError(), "argmax finish launch") ? 0 : -1;
 }
 
-int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, hipStream_t s) {
-    hipLaunchKernelGGL(dec_advance_batch_kernel, dim3(1), dim3(kWave), 0, s, d_tokens, d_pos, d_step, batch, log);
+int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, int *d_done,
+                      const StopSet &stop, hipStream_t s) {
+    hipLaunchKernelGGL(dec_advance_batch_kernel, dim3(1), dim3(kWave), 0, s, d_tokens, d_pos, d_step, batch, log,
+                       d_done, stop);
     return hip_ok(hipGetLastError(), "batched advance launch") ? 0 : -1;
 }
 

@@ -37,6 +37,24 @@ __device__ __forceinline__ float wave_sum_uniform(float v) {
     return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// One hd-long fp32 row (hd = 64 DPL) from global memory into LDS by DMA (no VGPRs): the
+// wave's lanes load 16 B each (DPL 4) or 4 B per 64-dim chunk; the data lands in natural
+// dim order at lds_row, which must be the same for the whole wave. Completion is counted by
+// vmcnt like any other load.
+template <int DPL>
+__device__ __forceinline__ void row_to_lds(const float *src_row, float *lds_row) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if constexpr (DPL == 4) {
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src_row + lane * 4),
+                                         (__attribute__((address_space(3))) void *)lds_row, 16, 0, 0);
+    } else {
+#pragma unroll
+        for (int c = 0; c < DPL; ++c)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src_row + c * kWave + lane),
+                                             (__attribute__((address_space(3))) void *)(lds_row + c * kWave), 4, 0, 0);
+    }
+}
+
 // Sum of squares of v[0..n) (LDS) in the reference order of sum_sq_avx2
 // (normalization.c:12-32): eight sequential FMA lanes over elements l, l+8, ..., then
 // ((s0+s4)+(s1+s5)) + ((s2+s6)+(s3+s7)) and a sequential fused tail. Threads 0..7 run the

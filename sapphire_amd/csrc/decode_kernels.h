@@ -47,12 +47,13 @@ struct AttnArgs {
     const float *cos_t = nullptr, *sin_t = nullptr;   // [max_ctx][hd] RoPE tables of the layer
     float *kc = nullptr, *vc = nullptr;          // this layer's caches [nkv][max_ctx][hd]
     const int *d_pos = nullptr;      // position of the token (device)
+    const int *d_done = nullptr;     // the sequence's done flag (device, may be NULL): set, no K/V row is written
     float *part = nullptr;           // [kAttnSplit][nh][hd + 2] partial (o, max, sum)
     int nh = 0, nkv = 0, hd = 0, max_ctx = 0;
     int window = 0;                  // sliding window of a local layer, 0 for a global one
     float scale = 1.f, eps = 1e-6f;
     // a batch of independent sequences: sequence b uses qkv + b*qkv_stride, the caches at
-    // + b*kv_stride, d_pos[b], and its own partials; out + b*out_stride
+    // + b*kv_stride, d_pos[b], d_done[b], and its own partials; out + b*out_stride
     int batch = 1;
     size_t qkv_stride = 0, kv_stride = 0, out_stride = 0;
     // the K/V rows of every position already hold this batch's tokens (dec_kv_write ran):
@@ -77,8 +78,10 @@ int dec_kv_write(const AttnArgs &a, hipStream_t s);
 // reads row 0
 int dec_embed(const uint16_t *embed, int hidden, int vocab, float es, const int *d_token, float *resid,
               hipStream_t s);
-// log[*d_step] = *d_token; ++*d_step; ++*d_pos; ++*d_seq when d_seq is set
-int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, uint32_t *d_seq, hipStream_t s);
+// Unless *d_done is set: log[*d_step] = *d_token; ++*d_step; ++*d_pos; ++*d_seq when d_seq is
+// set; *d_done = 1 when the token is in `stop`
+int dec_advance(const int *d_token, int *d_pos, int *d_step, int *log, uint32_t *d_seq, int *d_done,
+                const StopSet &stop, hipStream_t s);
 
 // ---- the layers of a step as one persistent kernel (decode_persist.hip) ----
 
@@ -105,6 +108,7 @@ struct PersistArgs {
     int window = 0;                   // the local layers' sliding window (PLayer::window of a local layer)
     float scale = 1.f, eps = 1e-6f;
     const int *state = nullptr;       // [0] token, [1] position
+    const int *done = nullptr;        // the sequence's done flag: set, the kernel returns at once
     const uint32_t *seq = nullptr;    // step counter that makes the epochs unique
     uint64_t *t_qkv = nullptr, *t_part = nullptr, *t_attn = nullptr, *t_o = nullptr, *t_g = nullptr,
              *t_dn = nullptr;
@@ -133,7 +137,9 @@ int dec_embed_batch(const uint16_t *embed, int hidden, int vocab, float es, cons
 // argmax_batch_part_floats(n, batch) floats
 size_t argmax_batch_part_floats(int n, int batch);
 int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_tokens, hipStream_t s);
-// log[*d_step][b] = tokens[b]; ++pos[b]; ++*d_step
-int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, hipStream_t s);
+// For every b with done[b] clear: log[*d_step][b] = tokens[b]; ++pos[b]; done[b] = 1 when the
+// token is in `stop`. Then ++*d_step.
+int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, int *d_done,
+                      const StopSet &stop, hipStream_t s);
 
 }  // namespace sapphire

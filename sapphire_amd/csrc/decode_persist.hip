@@ -50,24 +50,6 @@ __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t tag) { return (uint3
 
 constexpr int kAttnRows = 12;                     // K/V rows of one attention batch
 
-// One hd-long fp32 row (hd = 64 DPL) from global memory into LDS by DMA (no VGPRs): the
-// wave's lanes load 16 B each (DPL 4) or 4 B per 64-dim chunk; the data lands in natural
-// dim order at lds_row, which must be the same for the whole wave. Completion is counted by
-// vmcnt like any other load.
-template <int DPL>
-__device__ __forceinline__ void row_to_lds(const float *src_row, float *lds_row) {
-    const int lane = threadIdx.x & (kWave - 1);
-    if constexpr (DPL == 4) {
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src_row + lane * 4),
-                                         (__attribute__((address_space(3))) void *)lds_row, 16, 0, 0);
-    } else {
-#pragma unroll
-        for (int c = 0; c < DPL; ++c)
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src_row + c * kWave + lane),
-                                             (__attribute__((address_space(3))) void *)(lds_row + c * kWave), 4, 0, 0);
-    }
-}
-
 // The layer-invariant geometry of one GEMV stage for this workgroup (the same for every layer:
 // all layers share their shapes), computed once per launch so that the stages do no integer
 // division: rows in wave-steps of 64 / lpr rows, contiguous ranges of ceil(S / G) wave-steps
@@ -646,6 +628,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     // a wait of an earlier step of this generate call timed out: its results are void, and
     // every later step ends at once instead of timing out again
     if (*a.err != 0) return;
+    if (a.done && *a.done) return;                 // the sequence has stopped
     if (threadIdx.x == 0) s.flag = 0;
     const int H = a.H, nq = NH * a.hd;
     const int tok = a.state[0], pos = a.state[1];

@@ -68,7 +68,8 @@ struct sapphire_decoder {
     // between steps): the LM head that picks the token also advances the state
     unsigned long long *gkeys = nullptr;
     unsigned *gcount = nullptr;
-    int *state = nullptr;   // [0] token, [1] position, [2] step; batched: tokens[B], pos[B], step
+    // [0] token, [1] position, [2] step, [4] done; batched: tokens[B], pos[B], step, -, done[B]
+    int *state = nullptr;
     int *log = nullptr;     // [max_ctx] tokens of the steps; batched: [max_ctx][B]
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -103,6 +104,8 @@ struct sapphire_decoder {
     // temperature sampling (temperature > 0): the draws of a generate call [max_ctx][B], the
     // sampler's weights [B][vocab] and workspace
     float temperature = 0.0f;
+    // stop tokens (none by default): a sequence that logs one stops (done flag in the state)
+    StopSet stop;
     float *draws = nullptr;
     int n_draws = 0;
     float *smp_w = nullptr;
@@ -256,6 +259,9 @@ bool tiled_shapes_ok(const sapphire_decoder_config_t &c) {
 // A persistent-step wait longer than this many polls (about a second) is a failure.
 constexpr int kPersistSpinLimit = 1 << 19;
 
+// Per sequence 1 once it has logged a stop token (the state's last B words).
+int *done_flags(sapphire_decoder *d) { return d->state + 2 * d->batch + 2; }
+
 // The sampled tokens of the step's logits into tokens[B] (perform_inference's draw,
 // inference.c:262-266 and 297), the step's draws at d->draws[step * B].
 int enqueue_sample(sapphire_decoder *d, const int *d_step, hipStream_t s) {
@@ -289,6 +295,8 @@ int enqueue_lm_head(sapphire_decoder *d) {
             gs.step = d->state + 2;
             gs.log = d->log;
             gs.seq = d->groups > 0 ? d->seq : nullptr;
+            gs.done = done_flags(d);
+            gs.stop = d->stop;
             return launch_gemv_tiled_greedy_step(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, gs, s);
         }
         if (launch_gemv_tiled(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, s) != 0) return -1;
@@ -299,7 +307,8 @@ int enqueue_lm_head(sapphire_decoder *d) {
             return -1;
     }
     if (!greedy && enqueue_sample(d, d->state + 2, s) != 0) return -1;
-    return dec_advance(d->state, d->state + 1, d->state + 2, d->log, d->groups > 0 ? d->seq : nullptr, s);
+    return dec_advance(d->state, d->state + 1, d->state + 2, d->log, d->groups > 0 ? d->seq : nullptr, done_flags(d),
+                       d->stop, s);
 }
 
 // One decode step, enqueued on d->stream (recorded into the graph).
@@ -329,6 +338,7 @@ int enqueue_step(sapphire_decoder *d) {
         pa.scale = scale;
         pa.eps = c.eps;
         pa.state = d->state;
+        pa.done = done_flags(d);
         pa.seq = d->seq;
         const size_t nqkv = (size_t)(c.n_heads + 2 * c.n_kv_heads) * hd;
         pa.t_qkv = d->tbuf;
@@ -369,6 +379,7 @@ int enqueue_step(sapphire_decoder *d) {
         at.kc = d->kc + (size_t)l * layer_kv;
         at.vc = d->vc + (size_t)l * layer_kv;
         at.d_pos = d->state + 1;
+        at.d_done = done_flags(d);
         at.part = d->attn_part;
         at.nh = c.n_heads;
         at.nkv = c.n_kv_heads;
@@ -414,6 +425,7 @@ int enqueue_step(sapphire_decoder *d) {
 struct BatchRun {
     int B = 0;
     const int *d_tokens = nullptr, *d_pos = nullptr;
+    const int *d_done = nullptr;          // per sequence: set, its K/V rows are not written
     float *kc = nullptr, *vc = nullptr;   // layer 0 of the first sequence's caches
     size_t kv_stride = 0;                 // between sequences (0: one shared cache)
     bool prefill = false;
@@ -468,6 +480,7 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         at.kc = r.kc + (size_t)l * layer_kv;
         at.vc = r.vc + (size_t)l * layer_kv;
         at.d_pos = r.d_pos;
+        at.d_done = r.d_done;
         at.part = r.part;
         at.nh = c.n_heads;
         at.nkv = c.n_kv_heads;
@@ -532,6 +545,7 @@ int enqueue_step_batch(sapphire_decoder *d) {
     r.B = B;
     r.d_tokens = d->state;
     r.d_pos = d->state + B;
+    r.d_done = done_flags(d);
     r.kc = d->kc;
     r.vc = d->vc;
     r.kv_stride = (size_t)c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim;
@@ -562,7 +576,7 @@ int enqueue_step_batch(sapphire_decoder *d) {
         if ((d->temperature > 0.0f ? enqueue_sample(d, d->state + 2 * B, s)
                                    : dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s)) != 0)
             return -1;
-        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
+        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, s);
     }
     GemmIn li;
     li.x = d->resid[cur];
@@ -579,7 +593,7 @@ int enqueue_step_batch(sapphire_decoder *d) {
         // greedy tokens straight from the LM-head GEMM: no logits written or read again
         lo.tokens = d->state;
         if (launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s) != 0) return -1;
-        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
+        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, s);
     }
     lo.y = d->logits;
     lo.ldy = c.vocab;
@@ -587,7 +601,7 @@ int enqueue_step_batch(sapphire_decoder *d) {
     if ((d->temperature > 0.0f ? enqueue_sample(d, d->state + 2 * B, s)
                                : dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s)) != 0)
         return -1;
-    return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, s);
+    return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, s);
 }
 
 bool valid_config(const sapphire_decoder_config_t &c) {
@@ -847,7 +861,7 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
         !dev_alloc_t(d, &d->ffn_out, H, "ffn_out") || !dev_alloc_t(d, &d->xfin, b * H, "xfin") ||
         !dev_alloc_t(d, &d->logits, b * c.vocab, "logits") ||
         !dev_alloc_t(d, &d->attn_part, b * attn_part_floats(c.n_heads, hd), "attn partials") ||
-        !dev_alloc_t(d, &d->state, 2 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log") ||
+        !dev_alloc_t(d, &d->state, 3 * b + 2, "state") || !dev_alloc_t(d, &d->log, (size_t)c.max_ctx * b, "token log") ||
         !dev_alloc_t(d, &d->gkeys, tiled_greedy_key_slots(c.vocab), "greedy keys") ||
         !dev_alloc_t(d, &d->gcount, 1 + kGreedyGroups, "greedy counters") ||
         !hip_ok(hipMemset(d->gcount, 0, (1 + kGreedyGroups) * sizeof(unsigned)), "greedy counters zero") ||
@@ -1035,8 +1049,9 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         d->graph = g;
         SPH_CHECK(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
     }
-    // state: token, position, step (one sequence) or tokens[B], positions[B], step
-    std::vector<int> st((size_t)2 * B + 2, 0);
+    // state: token, position, step (one sequence) or tokens[B], positions[B], step; every done
+    // flag clear
+    std::vector<int> st((size_t)3 * B + 2, 0);
     if (B == 1) {
         st[0] = tokens[0];
         st[1] = pos[0];
@@ -1047,6 +1062,8 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         }
     }
     SPH_CHECK(hipMemcpy(d->state, st.data(), sizeof(int) * st.size(), hipMemcpyHostToDevice));
+    // with stop tokens, the steps after a sequence's stop log nothing: their entries read -1
+    if (d->stop.n > 0) SPH_CHECK(hipMemsetAsync(d->log, 0xFF, sizeof(int) * (size_t)steps * B, d->stream));
     if (d->groups > 0) {
         // epochs must stay below 2^32: start them over (and clear every tag) before they would wrap
         const uint64_t per = persist_epochs_per_step(c.n_layers);
@@ -1172,6 +1189,31 @@ int sapphire_decoder_set_sampling(sapphire_decoder_t *d, float temperature, cons
         d->graph = nullptr;
         d->temperature = t;
     }
+    return 0;
+}
+
+int sapphire_decoder_set_stop_tokens(sapphire_decoder_t *d, const int *ids, int n) {
+    if (!d || n < 0 || n > kMaxStop || (n > 0 && !ids)) {
+        set_error("sapphire_decoder_set_stop_tokens: bad arguments (at most %d tokens)", kMaxStop);
+        return -1;
+    }
+    StopSet st;
+    st.n = n;
+    for (int i = 0; i < n; ++i) {
+        if (ids[i] < 0 || ids[i] >= d->cfg.vocab) {
+            set_error("sapphire_decoder_set_stop_tokens: token %d outside the vocabulary", ids[i]);
+            return -1;
+        }
+        st.id[i] = ids[i];
+    }
+    SPH_CHECK(hipSetDevice(d->device));
+    SPH_CHECK(hipStreamSynchronize(d->stream));
+    // the set is an argument of the step's advance: capture again
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    d->exec = nullptr;
+    d->graph = nullptr;
+    d->stop = st;
     return 0;
 }
 

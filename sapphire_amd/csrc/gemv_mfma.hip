@@ -292,6 +292,10 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
     TileRegs<NG> RA;
     int t = wave;
     if (t < ntiles) tile_issue<DT, NG>(RA, rq, rs, t, lane);
+    // a stopped sequence: the whole launch returns (every workgroup reads the same flag, so no
+    // key slot or counter is touched); the check waits behind the first tile's loads
+    if constexpr (EP == kEpGreedyStep)
+        if (gs.done && *gs.done) return;
 
     float p[NG];
     long bop[NG];
@@ -380,6 +384,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
                 *gs.step = s + 1;
                 *gs.pos = *gs.pos + 1;
                 if (gs.seq) *gs.seq = *gs.seq + 1u;
+                if (gs.done && gs.stop.has(tok)) *gs.done = 1;   // inference.c:298-301
             }
         }
     }

@@ -58,16 +58,32 @@ int launch_gemv_tiled_softmax(int dt, const void *w, int M, int K, const float *
 // workgroup (tiled_greedy_key_slots); count: 1 + kGreedyGroups counters that are 0 before the
 // first launch and that every launch leaves at 0.
 constexpr int kGreedyGroups = 8;
+// Tokens that end a sequence (inference.c:298-301 stops on 1 and 106): the advance that logs
+// one sets the sequence's done flag; later steps log nothing, advance nothing and skip their
+// work (their log entries keep the caller's fill).
+constexpr int kMaxStop = 8;
+struct StopSet {
+    int n = 0;
+    int id[kMaxStop] = {};
+    __host__ __device__ bool has(int t) const {
+        bool r = false;
+        for (int i = 0; i < kMaxStop; ++i) r |= i < n && id[i] == t;
+        return r;
+    }
+};
 struct GreedyStep {
     unsigned long long *keys = nullptr;  // each workgroup's best greedy key
     unsigned *count = nullptr;           // [0] groups done, [1 + g] workgroups of group g done
     int *tok = nullptr, *pos = nullptr, *step = nullptr, *log = nullptr;
     uint32_t *seq = nullptr;             // the persistent step's counter (may be NULL)
+    int *done = nullptr;                 // the sequence's done flag (may be NULL): set, the launch does nothing
+    StopSet stop;
 };
 size_t tiled_greedy_key_slots(int M);
 // TILED GEMV whose epilogue writes the logits, picks the greedy token (sample_greedy's
-// order) into *tok and log[*step], and advances *pos, *step and *seq: one launch for the LM
-// head, the argmax and the advance. Launches that share the state must be ordered.
+// order) into *tok and log[*step], and advances *pos, *step and *seq (and sets *done when
+// the token is in gs.stop): one launch for the LM head, the argmax and the advance. With
+// *done set it returns at once. Launches that share the state must be ordered.
 int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const float *x, float *logits,
                                   const GreedyStep &gs, hipStream_t s);
 // Batched GEMM on the TILED layout (gemm_mfma.hip): Y[b][r] = W[r] . X[b] for b < batch, 16

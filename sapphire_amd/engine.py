@@ -63,6 +63,8 @@ def _protos(L):
     L.sapphire_decoder_set_epoch_count.argtypes = [C.c_void_p, C.c_uint32]
     L.sapphire_decoder_set_sampling.restype = C.c_int
     L.sapphire_decoder_set_sampling.argtypes = [C.c_void_p, C.c_float, C.c_void_p, C.c_int]
+    L.sapphire_decoder_set_stop_tokens.restype = C.c_int
+    L.sapphire_decoder_set_stop_tokens.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     L.sapphire_decoder_prefill.restype = C.c_int
     L.sapphire_decoder_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]
     L.sapphire_decoder_generate_batch.restype = C.c_int
@@ -158,6 +160,13 @@ class Decoder:
         self._check(self.lib.sapphire_decoder_set_sampling(self.ptr, float(temperature),
                                                            d.ctypes.data if d.size else None, int(d.size)),
                     "set_sampling")
+
+    def set_stop_tokens(self, ids) -> None:
+        """Later generate calls stop a sequence at the first of these tokens (logged; every later
+        step logs -1), as the reference's loop stops on 1 and 106 (inference.c:298-301)."""
+        t = np.ascontiguousarray(list(ids), np.int32)
+        self._check(self.lib.sapphire_decoder_set_stop_tokens(self.ptr, t.ctypes.data if t.size else None,
+                                                               int(t.size)), "set_stop_tokens")
 
     def generate_batch(self, tokens, pos, steps: int, keep_logits: bool = False):
         """(tokens[steps, batch], logits[steps, batch, vocab] or None, device milliseconds)."""
