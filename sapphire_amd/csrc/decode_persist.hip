@@ -17,8 +17,8 @@
 //
 // Stages of layer l, epoch e = seq * 8 * (n_layers + 1) + 8 * l + stage (seq counts steps):
 //   1 QKV GEMV       input: previous layer's down output (post-FFN norm + residual), pre-norm
-//   2 attention      input: q, k, v; QK-norm, RoPE, KV write; partial over a slice of positions
-//   3 combine        input: every workgroup's partial for this workgroup's attention elements
+//   2 attention      input: q, k, v; QK-norm, RoPE, KV write; partial of one head over a slice
+//   3 combine        input: the slices' partials for this workgroup's attention elements
 //   4 o-proj GEMV    input: attention output
 //   5 gate/up GEMV   input: o (post-attention norm + residual, pre-FFN norm); epilogue gelu*up
 //   6 down GEMV      input: g
@@ -48,7 +48,7 @@ __device__ __forceinline__ uint64_t get_tagged(const uint64_t *p) {
 }
 __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 
-constexpr int kAttnRows = 12;                     // K/V rows of one attention batch
+constexpr int kAttnRows = 36;                     // K/V rows of one attention batch (9 per wave)
 
 // The layer-invariant geometry of one GEMV stage for this workgroup (the same for every layer:
 // all layers share their shapes), computed once per launch so that the stages do no integer
@@ -78,7 +78,7 @@ struct CombGeom {
 };
 
 __device__ __forceinline__ void comb_geom(CombGeom &c, uint32_t *off, int nh, int hd) {
-    const int nq = nh * hd, G = gridDim.x;
+    const int nq = nh * hd, G = gridDim.x, S = G / nh;   // S slices: partial (b, h) of slice b
     c.E = (nq + G - 1) / G;
     c.e0 = min(nq, (int)blockIdx.x * c.E);
     c.e1 = min(nq, c.e0 + c.E);
@@ -86,7 +86,7 @@ __device__ __forceinline__ void comb_geom(CombGeom &c, uint32_t *off, int nh, in
     const int h_lo = c.e0 / hd, h_hi = (c.e1 - 1) / hd;   // E <= hd: at most two heads
     c.hb = (h_lo + 1) * hd;
     const int per = c.E + 4;
-    for (int j = threadIdx.x; j < G * per; j += kThreads) {
+    for (int j = threadIdx.x; j < S * per; j += kThreads) {
         const int b = j / per, k = j - b * per;
         size_t o;
         if (k < c.E) {
@@ -366,36 +366,36 @@ struct GemvStage {
 };
 
 // Stage 2: QK-norm, RoPE and the KV write of the token, then this workgroup's partial
-// (o, max in log2 units, sum per head) over its slice of the layer's positions
-// (attention.c:140-158 over the slice; dec_attn_part_kernel with one slice per workgroup).
-// Wave w owns query heads w, w + 4, ...: it gathers those heads and the K and V vectors of
-// the token into registers (lane l holds dims l*DPL .. l*DPL+DPL-1 of each), normalises them
-// by DPP sums, rotates them with the partner dims in lane l ^ 32, and walks every position of
-// the slice for its heads. No LDS and no workgroup barrier: each wave stores its heads'
-// partials as soon as its own inputs have arrived. prefetch() loads the slice's first K/V
-// rows, the gammas and the RoPE row entries; the kernel calls it a stage ahead, before the
-// QKV GEMV, so that the loads have returned when run() polls for q, k and v.
+// (o, max in log2 units, sum) of one query head over one slice of the layer's positions
+// (attention.c:140-158 over the slice). Workgroup b takes head b % NH and slice b / NH of
+// G / NH slices, so the combine merges G / NH partials per element instead of one per
+// workgroup. Its four waves take the slice's positions in turn (wave w: positions t0 + w +
+// 4j, K/V rows that the wave itself brought into LDS by DMA), each with the head's q and the
+// token's k and v in registers (lane l holds dims l*DPL .. l*DPL+DPL-1), normalised by DPP
+// sums and rotated with the partner dims in lane l ^ 32; the four running (max, sum, o) are
+// merged through LDS. prefetch() loads the slice's first K/V rows, the gammas and the RoPE row
+// entries; the kernel calls it a stage ahead, so the loads have returned when run() polls for
+// q, k and v.
 template <int DPL, int NH>
 struct AttnStage {
     static constexpr int NW = kThreads / kWave;
-    static_assert(NH % NW == 0, "query heads in whole heads per wave");
-    static constexpr int HPW = NH / NW;                // query heads per wave
-    // K/V rows of positions t0 .. t0 + PF - 1 (one K/V head: rows [max_ctx][hd]); a slice of
-    // up to PF positions (a 1536-position range over 128 workgroups) is one batch
+    // K/V rows of positions t0 .. t0 + PF - 1 (one K/V head: rows [max_ctx][hd]); wave w
+    // holds rows w, w + NW, ...
     static constexpr int PF = kAttnRows;
+    static_assert(PF % NW == 0, "whole rows per wave");
     float gq[DPL], gk[DPL], cs[DPL], sn[DPL];
     int t0, t1;
 
-    // DMA of the batch's K and V rows into LDS, rows spread over the waves (row pos is
-    // written by this step and taken from registers instead)
+    // DMA of this wave's K and V rows of the batch from tb into LDS (row pos is written by
+    // this step and taken from registers instead)
     __device__ __forceinline__ void load_batch(const PLayer &L, int hd, int pos, int tb, PersistLds<NH, DPL> &s) {
-        const int wid = threadIdx.x / kWave;
+        const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const int t = tb + j;
-            if (j % NW == wid && t < t1 && t != pos) {   // wave-uniform
-                row_to_lds<DPL>(L.kc + (size_t)t * hd, s.kvk[j]);
-                row_to_lds<DPL>(L.vc + (size_t)t * hd, s.kvv[j]);
+        for (int j = 0; j < PF / NW; ++j) {
+            const int r = wid + NW * j, t = tb + r;
+            if (t < t1 && t != pos) {   // wave-uniform
+                row_to_lds<DPL>(L.kc + (size_t)t * hd, s.kvk[r]);
+                row_to_lds<DPL>(L.vc + (size_t)t * hd, s.kvv[r]);
             }
         }
     }
@@ -405,9 +405,9 @@ struct AttnStage {
     __device__ static void slice(int pos, int window, int &t0, int &t1) {
         const int seq = pos + 1;
         const int start = (window > 0 && seq > window) ? seq - window : 0;
-        const int len = seq - start, G = gridDim.x;
-        const int chunk = (len + G - 1) / G;
-        t0 = min(seq, start + (int)blockIdx.x * chunk);
+        const int len = seq - start, S = (int)gridDim.x / NH;
+        const int chunk = (len + S - 1) / S;
+        t0 = min(seq, start + (int)(blockIdx.x / NH) * chunk);
         t1 = min(seq, t0 + chunk);
     }
 
@@ -436,13 +436,15 @@ struct AttnStage {
                                         uint32_t tag_out, PersistLds<NH, DPL> &s, F on_arrival) {
         const int hd = a.hd;
         const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+        const int wu = __builtin_amdgcn_readfirstlane(wid);
+        const int head = (int)blockIdx.x % NH;
         const int d0 = lane * DPL;                     // this lane's first dim
-        // the wave's words: q of its heads, then k, then v (t_qkv holds q | k | v)
-        constexpr int NWD = (HPW + 2) * DPL;
+        // the wave's words: q of the head, then k, then v (t_qkv holds q | k | v)
+        constexpr int NWD = 3 * DPL;
         uint64_t w[NWD];
         auto src = [&](int e) -> const uint64_t * {
             const int v = e / DPL, i = e - v * DPL;
-            const int vec = v < HPW ? wid + NW * v : NH + (v - HPW);   // q head, k (NH) or v (NH + 1)
+            const int vec = v == 0 ? head : NH + (v - 1);   // q head, k (NH) or v (NH + 1)
             return a.t_qkv + (size_t)vec * hd + d0 + i;
         };
 #pragma unroll
@@ -462,117 +464,127 @@ struct AttnStage {
             for (int e = 0; e < NWD; ++e)
                 if (!tag_is(w[e], tag_in)) w[e] = get_tagged(src(e));
         }
-        // every wave's K/V DMA (issued before its polls) has landed; then the rows are shared
+        // this wave's K/V DMA (issued before its polls) has landed
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         on_arrival();
         if (s.flag) return true;
-        float xv[HPW + 2][DPL];
+        float xv[3][DPL];
 #pragma unroll
-        for (int v = 0; v < HPW + 2; ++v)
+        for (int v = 0; v < 3; ++v)
 #pragma unroll
             for (int i = 0; i < DPL; ++i) xv[v][i] = __uint_as_float((uint32_t)w[v * DPL + i]);
 
-        // rmsnorm_delta of each q head and of k over its hd dims (wave sums of the lanes'
+        // rmsnorm_delta of the q head and of k over their hd dims (wave sums of the lanes'
         // squares), then the half-split rotation: dim d < half pairs with d + half in lane l ^ 32
         // (rope.c:113-115: x[i] = x0 c - x1 s, x[i + half] = x1 c + x0 s)
         const bool upper = lane >= kWave / 2;
-        float qk[HPW + 1][DPL];
+        float qk[2][DPL];
 #pragma unroll
-        for (int v = 0; v < HPW + 1; ++v) {
+        for (int v = 0; v < 2; ++v) {
             float acc = 0.f;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) acc = __builtin_fmaf(xv[v][i], xv[v][i], acc);
             const float r = rms_inv_of(wave_sum_uniform(acc), hd, a.eps);
 #pragma unroll
             for (int i = 0; i < DPL; ++i) {
-                const float g = v < HPW ? gq[i] : gk[i];
+                const float g = v == 0 ? gq[i] : gk[i];
                 const float xn = __fmul_rn(__fmul_rn(xv[v][i], r), __fadd_rn(1.0f, g));
                 const float xp = __shfl_xor(xn, kWave / 2, kWave);
                 qk[v][i] = upper ? __builtin_fmaf(xn, cs[i], __fmul_rn(xp, sn[i]))
                                  : __builtin_fmaf(xn, cs[i], -__fmul_rn(xp, sn[i]));
             }
         }
-        const float *vnew = xv[HPW + 1];
-        if (wid == 0 && t0 <= pos && pos < t1) {   // kv_cache_write_token: [head][pos][dim]
+        const float *vnew = xv[2];
+        // kv_cache_write_token: [head][pos][dim], once (head 0's workgroup of pos's slice)
+        if (head == 0 && wid == 0 && t0 <= pos && pos < t1) {
             const size_t off = (size_t)pos * hd + d0;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) {
-                as_global(L.kc)[off + i] = qk[HPW][i];
+                as_global(L.kc)[off + i] = qk[1][i];
                 as_global(L.vc)[off + i] = vnew[i];
             }
         }
 
         // scores in log2 units, so that every softmax weight is one exp2 (v_exp_f32)
         const float sl2 = __fmul_rn(a.scale, 1.44269504088896341f);
-        float m[HPW], sm[HPW], o[HPW][DPL];
+        float m = -INFINITY, sm = 0.f, o[DPL];
 #pragma unroll
-        for (int h = 0; h < HPW; ++h) {
-            m[h] = -INFINITY;
-            sm[h] = 0.f;
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) o[h][i] = 0.f;
-        }
+        for (int i = 0; i < DPL; ++i) o[i] = 0.f;
         for (int tb = t0; tb < t1; tb += PF) {
-            if (tb != t0) {   // a further batch: every wave is done with the rows in LDS
-                __syncthreads();
+            if (tb != t0) {   // a further batch into this wave's own rows (all read by now)
                 load_batch(L, hd, pos, tb, s);
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
             }
 #pragma unroll
-            for (int j = 0; j < PF; ++j) {
-                const int t = tb + j;
+            for (int j = 0; j < PF / NW; ++j) {
+                const int r = wu + NW * j, t = tb + r;
                 if (t >= t1) break;
                 float kr[DPL], vr[DPL];
                 if (t == pos) {
 #pragma unroll
                     for (int i = 0; i < DPL; ++i) {
-                        kr[i] = qk[HPW][i];
+                        kr[i] = qk[1][i];
                         vr[i] = vnew[i];
                     }
                 } else {
 #pragma unroll
                     for (int i = 0; i < DPL; ++i) {
-                        kr[i] = s.kvk[j][d0 + i];
-                        vr[i] = s.kvv[j][d0 + i];
+                        kr[i] = s.kvk[r][d0 + i];
+                        vr[i] = s.kvv[r][d0 + i];
                     }
                 }
+                float dp = 0.f;
 #pragma unroll
-                for (int h = 0; h < HPW; ++h) {
-                    float dp = 0.f;
+                for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qk[0][i], kr[i], dp);
+                const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
+                const float mn = fmaxf(m, score);
+                const float c = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+                const float p = __builtin_amdgcn_exp2f(score - mn);
+                sm = __builtin_fmaf(sm, c, p);
 #pragma unroll
-                    for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qk[h][i], kr[i], dp);
-                    const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
-                    const float mn = fmaxf(m[h], score);
-                    const float c = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
-                    const float p = __builtin_amdgcn_exp2f(score - mn);
-                    sm[h] = __builtin_fmaf(sm[h], c, p);
-#pragma unroll
-                    for (int i = 0; i < DPL; ++i) o[h][i] = __builtin_fmaf(o[h][i], c, p * vr[i]);
-                    m[h] = mn;
-                }
+                for (int i = 0; i < DPL; ++i) o[i] = __builtin_fmaf(o[i], c, p * vr[i]);
+                m = mn;
             }
         }
-        // this wave's heads' partials of the slice
-        uint64_t *out = a.t_part + (size_t)blockIdx.x * NH * (hd + 2);
+        // the waves' running partials merged through LDS (s.dl is free until the o-proj's
+        // residual stage): weights exp2(m_w - M), then one partial of the workgroup
+        float *mo = s.dl;                              // [NW][hd] o, then (m, sum) per wave
 #pragma unroll
-        for (int h = 0; h < HPW; ++h) {
-            uint64_t *oh = out + (size_t)(wid + NW * h) * (hd + 2);
+        for (int i = 0; i < DPL; ++i) mo[wid * hd + d0 + i] = o[i];
+        if (lane == 0) {
+            mo[NW * hd + 2 * wid] = m;
+            mo[NW * hd + 2 * wid + 1] = sm;
+        }
+        __syncthreads();
+        float M = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) put_tagged(oh + d0 + i, o[h][i], tag_out);
-            if (lane == 0) {
-                put_tagged(oh + hd, m[h], tag_out);
-                put_tagged(oh + hd + 1, sm[h], tag_out);
-            }
+        for (int v = 0; v < NW; ++v) M = fmaxf(M, mo[NW * hd + 2 * v]);
+        float ew[NW], S = 0.f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {
+            const float mv = mo[NW * hd + 2 * v];
+            ew[v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
+            S = __builtin_fmaf(mo[NW * hd + 2 * v + 1], ew[v], S);
+        }
+        uint64_t *out = a.t_part + (size_t)blockIdx.x * (hd + 2);
+        for (int d = threadIdx.x; d < hd; d += kThreads) {
+            float O = 0.f;
+#pragma unroll
+            for (int v = 0; v < NW; ++v) O = __builtin_fmaf(mo[v * hd + d], ew[v], O);
+            put_tagged(out + d, O, tag_out);
+        }
+        if (threadIdx.x == 0) {
+            put_tagged(out + hd, M, tag_out);
+            put_tagged(out + hd + 1, S, tag_out);
         }
         return true;
     }
 };
 
 // Stage 3: attention elements [e0, e1) of this workgroup, E = ceil(NH*hd / G) each:
-// out = sum_b e_b o_b / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) over every workgroup's
-// partial b (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes. The
+// out = sum_b e_b o_b / sum_b e_b s_b with e_b = exp2(m_b - max_b m_b) over the partials b of
+// the G / NH slices (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes. The
 // gathered words are E values, then (m, s) of the range's first and last head, of every
 // partial; their offsets (s.comb_off) and the range are computed once per launch.
 template <int NH, int DPL, class F>
@@ -583,17 +595,17 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag
         on_arrival();
         return true;
     }
-    const int G = gridDim.x, per = c.E + 4;
+    const int S = (int)gridDim.x / NH, per = c.E + 4;   // partials per head: one per slice
     constexpr int NE = kCombMax / kThreads;
     uint32_t offs[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
         const int j = threadIdx.x + e * kThreads;
-        offs[e] = j < G * per ? s.comb_off[j] : 0u;
+        offs[e] = j < S * per ? s.comb_off[j] : 0u;
     }
     const uint64_t *part = a.t_part;
     auto src = [&](int j) -> const uint64_t * { return part + offs[(j - (int)threadIdx.x) / kThreads]; };
-    if (!gather<NE>(src, G * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag)) return false;
+    if (!gather<NE>(src, S * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag)) return false;
     on_arrival();
     // 16-lane row r takes elements k = r, r + 16, ...; lane q of the row takes partials
     // b = q, q + 16, ...; max, weights and sums are reduced over the row by DPP
@@ -601,18 +613,18 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag
     for (int k = threadIdx.x / 16; k < c.e1 - c.e0; k += kThreads / 16) {
         const int el = c.e0 + k, hk = el < c.hb ? 0 : 2;
         float M = -INFINITY;
-        for (int b = q; b < G; b += 16) M = fmaxf(M, s.comb[b * per + c.E + hk]);
+        for (int b = q; b < S; b += 16) M = fmaxf(M, s.comb[b * per + c.E + hk]);
         M = row16_max(M);
-        float S = 0.f, O = 0.f;
-        for (int b = q; b < G; b += 16) {
+        float Sw = 0.f, O = 0.f;
+        for (int b = q; b < S; b += 16) {
             const float mb = s.comb[b * per + c.E + hk];
             const float e = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
-            S = __builtin_fmaf(s.comb[b * per + c.E + hk + 1], e, S);
+            Sw = __builtin_fmaf(s.comb[b * per + c.E + hk + 1], e, Sw);
             O = __builtin_fmaf(s.comb[b * per + k], e, O);
         }
-        S = row16_sum(S);
+        Sw = row16_sum(Sw);
         O = row16_sum(O);
-        if (q == 0) put_tagged(a.t_attn + el, O * (1.0f / S), tag_out);
+        if (q == 0) put_tagged(a.t_attn + el, O * (1.0f / Sw), tag_out);
     }
     __syncthreads();
     return true;
@@ -779,8 +791,9 @@ bool persist_supported(int dt, int groups, int n_layers, int H, int nh, int nkv,
         set_error("persistent decode: %d layers (at most %d)", n_layers, kPersistMaxLayers);
         return false;
     }
-    if (groups < nh || groups > kPersistMaxGroups) {
-        set_error("persistent decode: %d workgroups (needs %d..%d)", groups, nh, kPersistMaxGroups);
+    if (groups < nh || groups > kPersistMaxGroups || groups % nh) {
+        set_error("persistent decode: %d workgroups (a multiple of the %d heads, at most %d)", groups, nh,
+                  kPersistMaxGroups);
         return false;
     }
     if (H % kBlock || nq % kBlock || ffn % kBlock || H > kDecMaxK || nq > kDecMaxK || ffn > kDecMaxK) {
@@ -789,7 +802,7 @@ bool persist_supported(int dt, int groups, int n_layers, int H, int nh, int nkv,
     }
     const int worst = light_slots(groups, H, nh, nkv, hd, ffn);
     const int E = (nq + groups - 1) / groups;
-    if (worst > kSlots || groups * (E + 4) > kCombMax) {
+    if (worst > kSlots || groups / nh * (E + 4) > kCombMax) {
         set_error("persistent decode: %d workgroups are too few for these shapes", groups);
         return false;
     }
