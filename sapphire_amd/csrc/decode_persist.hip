@@ -194,6 +194,17 @@ __device__ __forceinline__ bool gather(Src src, int n, uint32_t tag, float *dst,
     return g.end(src, n, tag, dst, spin_limit, err, flag, sq);
 }
 
+// gather() with during() run between the first loads of the words and their first check:
+// loads it issues go out behind the polls, so the first check does not wait for them.
+template <int MAXE, class Src, class F>
+__device__ __forceinline__ bool gather_during(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
+                                              int *flag, float *sq, F during) {
+    Gather<MAXE, Src> g;
+    g.begin(src, n, tag);
+    during();
+    return g.end(src, n, tag, dst, spin_limit, err, flag, sq);
+}
+
 struct Contig {
     const uint64_t *p;
     __device__ const uint64_t *operator()(int j) const { return p + j; }
@@ -367,9 +378,9 @@ struct GemvStage {
 
 // Stage 2: QK-norm, RoPE and the KV write of the token, then this workgroup's partial
 // (o, max in log2 units, sum) of one query head over one slice of the layer's positions
-// (attention.c:140-158 over the slice). Workgroup b takes head b % NH and slice b / NH of
-// G / NH slices, so the combine merges G / NH partials per element instead of one per
-// workgroup. Its four waves take the slice's positions in turn (wave w: positions t0 + w +
+// (attention.c:140-158 over the slice). Workgroup b takes slice b % S and head b / S of
+// S = G / NH slices, so the combine merges S partials per element instead of one per
+// workgroup, and the NH workgroups of a slice read the same K/V rows on one XCD (b mod 8). Its four waves take the slice's positions in turn (wave w: positions t0 + w +
 // 4j, K/V rows that the wave itself brought into LDS by DMA), each with the head's q and the
 // token's k and v in registers (lane l holds dims l*DPL .. l*DPL+DPL-1), normalised by DPP
 // sums and rotated with the partner dims in lane l ^ 32; the four running (max, sum, o) are
@@ -407,16 +418,40 @@ struct AttnStage {
         const int start = (window > 0 && seq > window) ? seq - window : 0;
         const int len = seq - start, S = (int)gridDim.x / NH;
         const int chunk = (len + S - 1) / S;
-        t0 = min(seq, start + (int)(blockIdx.x / NH) * chunk);
+        t0 = min(seq, start + (int)(blockIdx.x % S) * chunk);
         t1 = min(seq, t0 + chunk);
     }
 
-    __device__ __forceinline__ void prefetch(const PersistArgs &a, const PLayer &L, int pos, PersistLds<NH, DPL> &s) {
-        const int hd = a.hd;
+    // the slice of layer L's kind (local or global)
+    __device__ __forceinline__ void set_slice(const PLayer &L, const PersistLds<NH, DPL> &s) {
         t0 = s.att_t[L.window > 0 ? 0 : 1][0];
         t1 = s.att_t[L.window > 0 ? 0 : 1][1];
+    }
+
+    // rows j0 <= j < j1 of this wave's part of the first batch (a third of it per stage of the
+    // previous layer, so that no stage stalls long on issuing them)
+    __device__ __forceinline__ void load_rows(const PLayer &L, int hd, int pos, int j0, int j1,
+                                              PersistLds<NH, DPL> &s) {
+        const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+#pragma unroll
+        for (int j = 0; j < PF / NW; ++j) {
+            const int r = wid + NW * j, t = t0 + r;
+            if (j >= j0 && j < j1 && t < t1 && t != pos) {   // wave-uniform
+                row_to_lds<DPL>(L.kc + (size_t)t * hd, s.kvk[r]);
+                row_to_lds<DPL>(L.vc + (size_t)t * hd, s.kvv[r]);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void prefetch(const PersistArgs &a, const PLayer &L, int pos, PersistLds<NH, DPL> &s) {
+        set_slice(L, s);
+        load_batch(L, a.hd, pos, t0, s);
+        prefetch_regs(a, L, pos);
+    }
+
+    // the gammas and the RoPE row entries of layer L (its rows are loaded already)
+    __device__ __forceinline__ void prefetch_regs(const PersistArgs &a, const PLayer &L, int pos) {
         const int lane = threadIdx.x & (kWave - 1), d0 = lane * DPL;
-        load_batch(L, hd, pos, t0, s);
         // gammas (one head_dim vector for every q head, one for k: attention.c:228-269) and the
         // RoPE row of pos at (dim mod half) (rope.c:99-117)
         const size_t ci = (size_t)pos * a.rope_stride + (size_t)(lane & (kWave / 2 - 1)) * DPL;
@@ -437,7 +472,7 @@ struct AttnStage {
         const int hd = a.hd;
         const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
         const int wu = __builtin_amdgcn_readfirstlane(wid);
-        const int head = (int)blockIdx.x % NH;
+        const int head = (int)blockIdx.x / ((int)gridDim.x / NH);
         const int d0 = lane * DPL;                     // this lane's first dim
         // the wave's words: q of the head, then k, then v (t_qkv holds q | k | v)
         constexpr int NWD = 3 * DPL;
@@ -519,32 +554,33 @@ struct AttnStage {
 #pragma unroll
             for (int j = 0; j < PF / NW; ++j) {
                 const int r = wu + NW * j, t = tb + r;
-                if (t >= t1) break;
-                float kr[DPL], vr[DPL];
-                if (t == pos) {
+                if (t < t1) {
+                    float kr[DPL], vr[DPL];
+                    if (t == pos) {   // the token's own row is in registers
 #pragma unroll
-                    for (int i = 0; i < DPL; ++i) {
-                        kr[i] = qk[1][i];
-                        vr[i] = vnew[i];
-                    }
-                } else {
+                        for (int i = 0; i < DPL; ++i) {
+                            kr[i] = qk[1][i];
+                            vr[i] = vnew[i];
+                        }
+                    } else {
 #pragma unroll
-                    for (int i = 0; i < DPL; ++i) {
-                        kr[i] = s.kvk[r][d0 + i];
-                        vr[i] = s.kvv[r][d0 + i];
+                        for (int i = 0; i < DPL; ++i) {
+                            kr[i] = s.kvk[r][d0 + i];
+                            vr[i] = s.kvv[r][d0 + i];
+                        }
                     }
+                    float dp = 0.f;
+#pragma unroll
+                    for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qk[0][i], kr[i], dp);
+                    const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
+                    const float mn = fmaxf(m, score);
+                    const float c = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+                    const float p = __builtin_amdgcn_exp2f(score - mn);
+                    sm = __builtin_fmaf(sm, c, p);
+#pragma unroll
+                    for (int i = 0; i < DPL; ++i) o[i] = __builtin_fmaf(o[i], c, p * vr[i]);
+                    m = mn;
                 }
-                float dp = 0.f;
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qk[0][i], kr[i], dp);
-                const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
-                const float mn = fmaxf(m, score);
-                const float c = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
-                const float p = __builtin_amdgcn_exp2f(score - mn);
-                sm = __builtin_fmaf(sm, c, p);
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) o[i] = __builtin_fmaf(o[i], c, p * vr[i]);
-                m = mn;
             }
         }
         // the waves' running partials merged through LDS (s.dl is free until the o-proj's
@@ -567,7 +603,9 @@ struct AttnStage {
             ew[v] = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
             S = __builtin_fmaf(mo[NW * hd + 2 * v + 1], ew[v], S);
         }
-        uint64_t *out = a.t_part + (size_t)blockIdx.x * (hd + 2);
+        // partial (slice, head) at (slice * NH + head) * (hd + 2)
+        const int nsl = (int)gridDim.x / NH;
+        uint64_t *out = a.t_part + ((size_t)(blockIdx.x % nsl) * NH + head) * (hd + 2);
         for (int d = threadIdx.x; d < hd; d += kThreads) {
             float O = 0.f;
 #pragma unroll
@@ -587,11 +625,12 @@ struct AttnStage {
 // the G / NH slices (attention.c:140-158; the maxima are in log2 units), reduced over 16 lanes. The
 // gathered words are E values, then (m, s) of the range's first and last head, of every
 // partial; their offsets (s.comb_off) and the range are computed once per launch.
-template <int NH, int DPL, class F>
+template <int NH, int DPL, class D, class F>
 __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag_in, uint32_t tag_out,
-                                              PersistLds<NH, DPL> &s, F on_arrival) {
+                                              PersistLds<NH, DPL> &s, D during, F on_arrival) {
     const CombGeom c = s.cg;
     if (c.e0 >= c.e1) {
+        during();
         on_arrival();
         return true;
     }
@@ -605,7 +644,7 @@ __device__ __forceinline__ bool combine_stage(const PersistArgs &a, uint32_t tag
     }
     const uint64_t *part = a.t_part;
     auto src = [&](int j) -> const uint64_t * { return part + offs[(j - (int)threadIdx.x) / kThreads]; };
-    if (!gather<NE>(src, S * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag)) return false;
+    if (!gather_during<NE>(src, S * per, tag_in, s.comb, a.spin_limit, a.err, &s.flag, nullptr, during)) return false;
     on_arrival();
     // 16-lane row r takes elements k = r, r + 16, ...; lane q of the row takes partials
     // b = q, q + 16, ...; max, weights and sums are reduced over the row by DPP
@@ -694,22 +733,34 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         // 2: attention (the o-proj's weights go out when q, k, v have arrived)
         GemvStage<DT, false, SL, 32> go;
         if (!at.run(a, L, pos, ep + 1, ep + 2, s, [&] { go.load(L.o, L.o, s.geom[kGeomO]); })) return;
+        // The next layer's K/V rows go into LDS (this layer's attention is done with them) a
+        // third at a time during the waits of stages 3, 4 and 5, behind each wait's first polls.
+        const bool nx = l + 1 < a.n_layers;
+        const PLayer &Ln = s.layer(nx ? l + 1 : l);
+        if (nx) at.set_slice(Ln, s);
+        constexpr int RPW = AttnStage<DPL, NH>::PF / (kThreads / kWave);   // rows per wave
         // 3: combine (the gate/up weights and the norm weights of stage 5 go out)
         GemvStage<DT, true, SL> gu;
         VecRegs<HR> wd_attn, wn_ffn;
-        if (!combine_stage<NH, DPL>(a, ep + 2, ep + 3, s, [&] {
-                gu.load(L.gate, L.up, s.geom[kGeomGu]);
-                wd_attn.load(L.n_attn_post, H);
-                wn_ffn.load(L.n_ffn, H);
-            }))
+        if (!combine_stage<NH, DPL>(
+                a, ep + 2, ep + 3, s, [&] { if (nx) at.load_rows(Ln, a.hd, pos, 0, RPW / 3, s); },
+                [&] {
+                    gu.load(L.gate, L.up, s.geom[kGeomGu]);
+                    wd_attn.load(L.n_attn_post, H);
+                    wn_ffn.load(L.n_ffn, H);
+                }))
             return;
         // 4: o-proj
-        if (!gather<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag)) return;
+        if (!gather_during<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag, nullptr,
+                                [&] { if (nx) at.load_rows(Ln, a.hd, pos, RPW / 3, 2 * RPW / 3, s); }))
+            return;
         go.finish(s.xs, a.t_o, ep + 4);
         // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU (the down
         // projection's weights go out)
         GemvStage<DT, false, SL, 32> gd;
-        if (!gather<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
+        if (!gather_during<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh,
+                               [&] { if (nx) at.load_rows(Ln, a.hd, pos, 2 * RPW / 3, RPW, s); }))
+            return;
         gd.load(L.down, L.down, s.geom[kGeomDown]);
         add_norm_delta_norm(s.resid, s.xs, s.dl, wd_attn, wn_ffn, H, a.eps, s.sh);
         gu.finish(s.xs, a.t_g, ep + 5);
@@ -718,7 +769,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         if (l + 1 < a.n_layers) {
             gq.load(s.layer(l + 1).qkv, s.layer(l + 1).qkv, s.geom[kGeomQkv]);
             wn_attn.load(s.layer(l + 1).n_attn, H);
-            at.prefetch(a, s.layer(l + 1), pos, s);   // this layer's attention is done with the LDS rows
+            at.prefetch_regs(a, s.layer(l + 1), pos);
         } else {
             wn_attn.load(a.norm_final, H);
         }
