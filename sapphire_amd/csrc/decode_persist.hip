@@ -743,12 +743,14 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         GemvStage<DT, true, SL> gu;
         VecRegs<HR> wd_attn, wn_ffn;
         if (!combine_stage<NH, DPL>(
-                a, ep + 2, ep + 3, s, [&] { if (nx) at.load_rows(Ln, a.hd, pos, 0, RPW / 3, s); },
+                a, ep + 2, ep + 3, s,
                 [&] {
                     gu.load(L.gate, L.up, s.geom[kGeomGu]);
                     wd_attn.load(L.n_attn_post, H);
                     wn_ffn.load(L.n_ffn, H);
-                }))
+                    if (nx) at.load_rows(Ln, a.hd, pos, 0, RPW / 3, s);
+                },
+                [] {}))
             return;
         // 4: o-proj
         if (!gather_during<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag, nullptr,
@@ -758,22 +760,25 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         // 5: post-attention norm + residual, pre-FFN norm, gate/up with the GeGLU (the down
         // projection's weights go out)
         GemvStage<DT, false, SL, 32> gd;
-        if (!gather_during<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh,
-                               [&] { if (nx) at.load_rows(Ln, a.hd, pos, 2 * RPW / 3, RPW, s); }))
+        if (!gather_during<HR>(Contig{a.t_o}, H, ep + 4, s.dl, a.spin_limit, a.err, &s.flag, s.sh, [&] {
+                gd.load(L.down, L.down, s.geom[kGeomDown]);
+                if (nx) at.load_rows(Ln, a.hd, pos, 2 * RPW / 3, RPW, s);
+            }))
             return;
-        gd.load(L.down, L.down, s.geom[kGeomDown]);
         add_norm_delta_norm(s.resid, s.xs, s.dl, wd_attn, wn_ffn, H, a.eps, s.sh);
         gu.finish(s.xs, a.t_g, ep + 5);
         // 6: down (the next layer's QKV and norm weights, or the final norm's, go out)
-        if (!gather<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag)) return;
-        if (l + 1 < a.n_layers) {
-            gq.load(s.layer(l + 1).qkv, s.layer(l + 1).qkv, s.geom[kGeomQkv]);
-            wn_attn.load(s.layer(l + 1).n_attn, H);
-            at.prefetch_regs(a, s.layer(l + 1), pos);
-        } else {
-            wn_attn.load(a.norm_final, H);
-        }
-        wd_prev.load(L.n_ffn_post, H);
+        if (!gather_during<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag, nullptr, [&] {
+                if (nx) {
+                    gq.load(Ln.qkv, Ln.qkv, s.geom[kGeomQkv]);
+                    wn_attn.load(Ln.n_attn, H);
+                    at.prefetch_regs(a, Ln, pos);
+                } else {
+                    wn_attn.load(a.norm_final, H);
+                }
+                wd_prev.load(L.n_ffn_post, H);
+            }))
+            return;
         gd.finish(s.xs, a.t_dn, ep + 6);
     }
     // last finalize + final norm (transformer.c:400-406)
