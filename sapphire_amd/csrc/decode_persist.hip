@@ -464,11 +464,11 @@ struct AttnStage {
         }
     }
 
-    // on_arrival() runs once the workgroup's q, k, v have arrived (it issues the next stage's
-    // loads).
+    // during() runs between the first loads of q, k, v and their first check (it issues the
+    // next stage's loads, which then go out behind the polls).
     template <class F>
     __device__ __forceinline__ bool run(const PersistArgs &a, const PLayer &L, int pos, uint32_t tag_in,
-                                        uint32_t tag_out, PersistLds<NH, DPL> &s, F on_arrival) {
+                                        uint32_t tag_out, PersistLds<NH, DPL> &s, F during) {
         const int hd = a.hd;
         const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
         const int wu = __builtin_amdgcn_readfirstlane(wid);
@@ -484,6 +484,7 @@ struct AttnStage {
         };
 #pragma unroll
         for (int e = 0; e < NWD; ++e) w[e] = get_tagged(src(e));
+        during();
         for (int spins = 0;; ++spins) {
             bool ready = true;
 #pragma unroll
@@ -502,7 +503,6 @@ struct AttnStage {
         // this wave's K/V DMA (issued before its polls) has landed
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        on_arrival();
         if (s.flag) return true;
         float xv[3][DPL];
 #pragma unroll
@@ -730,7 +730,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             norm_to(s.xs, s.resid, wn_attn, H, a.eps, s.sh);
         }
         gq.finish(s.xs, a.t_qkv, ep + 1);
-        // 2: attention (the o-proj's weights go out when q, k, v have arrived)
+        // 2: attention (the o-proj's weights go out during its wait)
         GemvStage<DT, false, SL, 32> go;
         if (!at.run(a, L, pos, ep + 1, ep + 2, s, [&] { go.load(L.o, L.o, s.geom[kGeomO]); })) return;
         // The next layer's K/V rows go into LDS (this layer's attention is done with them) a
