@@ -474,41 +474,23 @@ struct AttnStage {
         const int wu = __builtin_amdgcn_readfirstlane(wid);
         const int head = (int)blockIdx.x / ((int)gridDim.x / NH);
         const int d0 = lane * DPL;                     // this lane's first dim
-        // the wave's words: q of the head, then k, then v (t_qkv holds q | k | v)
-        constexpr int NWD = 3 * DPL;
-        uint64_t w[NWD];
-        auto src = [&](int e) -> const uint64_t * {
-            const int v = e / DPL, i = e - v * DPL;
+        // q of the head, k and v (t_qkv holds q | k | v), 3 hd words, gathered once per
+        // workgroup into LDS (s.xs is free between the QKV and o-proj stages) and read back by
+        // every wave
+        constexpr int NQW = (3 * kWave * DPL + kThreads - 1) / kThreads;
+        auto src = [&](int j) -> const uint64_t * {
+            const int v = j / hd, d = j - v * hd;
             const int vec = v == 0 ? head : NH + (v - 1);   // q head, k (NH) or v (NH + 1)
-            return a.t_qkv + (size_t)vec * hd + d0 + i;
+            return a.t_qkv + (size_t)vec * hd + d;
         };
-#pragma unroll
-        for (int e = 0; e < NWD; ++e) w[e] = get_tagged(src(e));
-        during();
-        for (int spins = 0;; ++spins) {
-            bool ready = true;
-#pragma unroll
-            for (int e = 0; e < NWD; ++e) ready = ready && tag_is(w[e], tag_in);
-            if (__all(ready)) break;
-            if (spins >= a.spin_limit) {
-                // no partial is stored: the combine of every workgroup times out in turn
-                if (lane == 0) s.flag = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-            for (int e = 0; e < NWD; ++e)
-                if (!tag_is(w[e], tag_in)) w[e] = get_tagged(src(e));
-        }
-        // this wave's K/V DMA (issued before its polls) has landed
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (s.flag) return true;
+        // this wave's K/V DMA was issued before the polls, so it has landed once they have
+        if (!gather_during<NQW>(src, 3 * hd, tag_in, s.xs, a.spin_limit, a.err, &s.flag, nullptr, during))
+            return false;
         float xv[3][DPL];
 #pragma unroll
         for (int v = 0; v < 3; ++v)
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) xv[v][i] = __uint_as_float((uint32_t)w[v * DPL + i]);
+            for (int i = 0; i < DPL; ++i) xv[v][i] = s.xs[v * hd + d0 + i];
 
         // rmsnorm_delta of the q head and of k over their hd dims (wave sums of the lanes'
         // squares), then the half-split rotation: dim d < half pairs with d + half in lane l ^ 32
