@@ -100,12 +100,14 @@ int sapphire_decoder_prefill(sapphire_decoder_t *dec, int seq, const int *tokens
 int sapphire_decoder_set_workgroups(sapphire_decoder_t *dec, int groups);
 /* The current form: workgroups of the persistent step, 0 for the multi-launch step. */
 int sapphire_decoder_workgroups(const sapphire_decoder_t *dec);
-/* No counterpart in the reference; for tests of the persistent step. Its stages tag exchanged
- * values with epochs (steps since the last reset x 8 x (n_layers + 1) + stage) that must stay
- * below 2^32, so generate starts them over (clearing every exchange word) before a call would
- * pass that. This sets the count of steps since the last reset, on the device and the host, as
- * if that many steps had run: a test can start just below the reset and decode across it.
- * No effect on the multi-launch step. 0 / -1 (count past the range). */
+/* No counterpart in the reference; for tests of the persistent step and the batched step. The
+ * persistent step's stages tag exchanged values with epochs (steps since the last reset x 8 x
+ * (n_layers + 1) + stage) that must stay below 2^32; the batched step's fused QKV + attention
+ * launch tags its q | k | v words with (steps since the last reset + 1) x 64 + layer + 1, whose
+ * step count must stay below 2^26 - 1. generate starts them over (clearing every tagged word)
+ * before a call would pass that. This sets the count of steps since the last reset, on the
+ * device and the host, as if that many steps had run: a test can start just below the reset
+ * and decode across it. No effect on the multi-launch step. 0 / -1 (count past the range). */
 int sapphire_decoder_set_epoch_count(sapphire_decoder_t *dec, uint32_t steps);
 
 /* How the following generate calls pick tokens (inference.c:262-266 and 297). temperature <= 0
@@ -133,7 +135,11 @@ int sapphire_decoder_set_stop_tokens(sapphire_decoder_t *dec, const int *ids, in
  * the batch (the reference decodes one sequence per inference_forward call). Shapes:
  * hidden, n_heads*head_dim and ffn multiples of 128, hidden <= 1152. Weights as for
  * sapphire_decoder_create. A decoder made by sapphire_decoder_create has batch 1; the
- * functions below accept it too. */
+ * functions below accept it too. For Q4_0 projections, 4..16 sequences and the head shapes
+ * of the Gemma-3 family, each layer's QKV GEMM and attention run as one launch (its
+ * attention workgroups stream their K/V rows while the GEMM's workgroups run, then take
+ * q | k | v from tagged words); the environment variable SAPPHIRE_FUSED_QKV_ATTN=0 at create
+ * time keeps them two launches. Both forms compute the same step. */
 sapphire_decoder_t *sapphire_decoder_create_batch(const sapphire_decoder_config_t *cfg,
                                                   const sapphire_decoder_weights_t *w, int batch);
 int sapphire_decoder_batch(const sapphire_decoder_t *dec);

@@ -16,6 +16,7 @@
 // Row sums are wave-wide shuffle reductions. These GEMVs are small (<= 2 MiB of weights):
 // their cost is latency, hence the fusion of the vector work around them.
 #include "decode_device.h"
+#include "gemm_body.h"
 
 namespace sapphire {
 
@@ -387,38 +388,64 @@ __global__ __launch_bounds__(NT) void dec_attn_part_kernel(AttnArgs a) {
 // CU. Wave w takes positions rb + w + 8j of a round [rb, rb + PB) and loads exactly those rows,
 // so it waits for its own DMA only; a slice longer than PB takes further rounds in the same
 // slots. Arithmetic and order are those of dec_attn_part_kernel.
-template <int DPL, int NH, int NKV>
+// PBMAX caps the positions per round (the LDS of a workgroup that shares its CU).
+template <int DPL, int NH, int NKV, int PBMAX = 72>
 struct AttnLdsShape {
     static constexpr int NT = kAttnThreadsBatch, NW = NT / kWave, HD = kWave * DPL;
     // raw q|k|v, the normed q and k, and (within 2 KiB) the small merge arrays
     static constexpr int kFixed = (2 * NH + 3 * NKV) * HD * 4 + 2048;
     static constexpr int kRoom = (160 * 1024 - kFixed) / (2 * NKV * HD * 4) / NW * NW;
-    static constexpr int PB = kRoom < 72 ? kRoom : 72;   // positions per round
+    static constexpr int PB = kRoom < PBMAX ? kRoom : PBMAX;   // positions per round
     static_assert(PB >= NW, "at least one row per wave and round");
     static_assert(NW * NH <= 2 * PB * NKV, "the wave merge fits in the row space");
 };
 
-template <int DPL, int NH, int NKV>
-__global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArgs a) {
-    using S = AttnLdsShape<DPL, NH, NKV>;
+template <int DPL, int NH, int NKV, int PBMAX = 72>
+struct AttnLds {
+    using S = AttnLdsShape<DPL, NH, NKV, PBMAX>;
+    alignas(16) float kvr[2][S::PB * NKV][S::HD];   // K rows | V rows of a round
+    float raw[(NH + 2 * NKV) * S::HD];              // q | k | v as projected
+    float qs[NH * S::HD];
+    float ks[NKV * S::HD];
+    float part8[8 * 16];
+    float ss[16];
+    float wm[S::NW][NH], wsum[S::NW][NH], wx[S::NW][NH];
+    float wmax[NH], wtot[NH];
+};
+
+// Where a batch attention workgroup takes q | k | v from: a.qkv (written by an earlier
+// launch), or epoch-tagged words that a GEMM in the same launch writes (words of sequence b at
+// w + b * stride, polled until their tag equals `tag`; a wait longer than spin_limit polls
+// counts in *err and goes on with what it has).
+struct QkvTagged {
+    const uint64_t *w = nullptr;
+    size_t stride = 0;
+    uint32_t tag = 0;
+    int spin_limit = 0;
+    int *err = nullptr;
+};
+
+// Slice bx of sequence by (gdx slices per sequence), with its LDS in L.
+template <int DPL, int NH, int NKV, int PBMAX>
+__device__ __forceinline__ void attn_lds_body(AttnLds<DPL, NH, NKV, PBMAX> &L, int bx, int by, int gdx, AttnArgs a,
+                                              const QkvTagged &tq) {
+    using S = AttnLdsShape<DPL, NH, NKV, PBMAX>;
     constexpr int NT = S::NT, NW = S::NW, HD = S::HD, PB = S::PB, PW = PB / NW;
-    {   // sequence blockIdx.y of a batch
-        const size_t b = blockIdx.y;
+    {   // sequence by of a batch
+        const size_t b = by;
         a.qkv += b * a.qkv_stride;
         a.kc += b * a.kv_stride;
         a.vc += b * a.kv_stride;
         a.d_pos += b;
         if (a.d_done) a.d_done += b;
-        a.part += b * (size_t)gridDim.x * NH * (HD + 2);
+        a.part += b * (size_t)gdx * NH * (HD + 2);
     }
-    __shared__ __attribute__((aligned(16))) float kvr[2][PB * NKV][HD];   // K rows | V rows of a round
-    __shared__ float raw[(NH + 2 * NKV) * HD];                              // q | k | v as projected
-    __shared__ float qs[NH * HD];
-    __shared__ float ks[NKV * HD];
-    __shared__ float part8[8 * 16];
-    __shared__ float ss[16];
-    __shared__ float wm[NW][NH], wsum[NW][NH], wx[NW][NH];
-    __shared__ float wmax[NH], wtot[NH];
+    auto &kvr = L.kvr;
+    float *raw = L.raw, *qs = L.qs, *ks = L.ks, *part8 = L.part8, *ss = L.ss;
+    auto &wm = L.wm;
+    auto &wsum = L.wsum;
+    auto &wx = L.wx;
+    float *wmax = L.wmax, *wtot = L.wtot;
     constexpr int half = HD / 2, group = NH / NKV;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int wu = __builtin_amdgcn_readfirstlane(wid);
@@ -427,19 +454,20 @@ __global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArg
     constexpr int nraw = (NH + 2 * NKV) * HD;
     constexpr int kRawRegs = (nraw + NT - 1) / NT;
     float rv[kRawRegs];
+    if (!tq.w)
 #pragma unroll
-    for (int e = 0; e < kRawRegs; ++e) {
-        const int i = threadIdx.x + e * NT;
-        rv[e] = i < nraw ? a.qkv[i] : 0.f;
-    }
+        for (int e = 0; e < kRawRegs; ++e) {
+            const int i = threadIdx.x + e * NT;
+            rv[e] = i < nraw ? a.qkv[i] : 0.f;
+        }
     const int pi = threadIdx.x % half;
     const float gq0 = a.qn[pi], gq1 = a.qn[pi + half], gk0 = a.kn[pi], gk1 = a.kn[pi + half];
     const int pos = *a.d_pos, seq = pos + 1;
     const float rc = a.cos_t[(size_t)pos * HD + pi], rs = a.sin_t[(size_t)pos * HD + pi];
     const int start = (a.window > 0 && seq > a.window) ? seq - a.window : 0;
-    const int len = seq - start, nsplit = gridDim.x;
+    const int len = seq - start, nsplit = gdx;
     const int chunk = (len + nsplit - 1) / nsplit;
-    const int t0 = start + blockIdx.x * chunk, t1 = min(seq, t0 + chunk);
+    const int t0 = start + bx * chunk, t1 = min(seq, t0 + chunk);
     // this wave's rows of the round from rb into its own slots wu + NW j; the current
     // position's row is this kernel's own k and v
     auto issue = [&](int rb) {
@@ -457,6 +485,46 @@ __global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArg
         }
     };
     issue(t0);
+    if (tq.w) {
+        // the GEMM's words, polled behind the rows' DMA (whose loads the GEMM's run outlasts).
+        // Until one word of this wave's share carries the tag, only one lane per wave polls
+        // (the GEMM's workgroups share the CUs); then every thread loads its words.
+        const uint64_t *src = tq.w + (size_t)by * tq.stride;
+        if (lane == 0) {
+            const uint64_t *sw = src + wu * (nraw / NW);
+            for (int spins = 0; spins < tq.spin_limit; ++spins) {
+                if ((uint32_t)(__hip_atomic_load(sw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) == tq.tag)
+                    break;
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        uint64_t w[kRawRegs];
+#pragma unroll
+        for (int e = 0; e < kRawRegs; ++e) {
+            const int i = threadIdx.x + e * NT;
+            w[e] = i < nraw ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : (uint64_t)tq.tag << 32;
+        }
+        for (int spins = 0;; ++spins) {
+            bool ready = true;
+#pragma unroll
+            for (int e = 0; e < kRawRegs; ++e) ready = ready && (uint32_t)(w[e] >> 32) == tq.tag;
+            if (ready) break;
+            if (spins >= tq.spin_limit) {
+                atomicAdd(tq.err, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+            for (int e = 0; e < kRawRegs; ++e) {
+                const int i = threadIdx.x + e * NT;
+                if (i < nraw && (uint32_t)(w[e] >> 32) != tq.tag)
+                    w[e] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < kRawRegs; ++e) rv[e] = __uint_as_float((uint32_t)w[e]);
+    }
 
 #pragma unroll
     for (int e = 0; e < kRawRegs; ++e) {
@@ -482,7 +550,7 @@ __global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArg
     __syncthreads();
     const float *vnew = raw + (NH + NKV) * HD;
     // kv_cache_write_token: [head][pos][dim] (a stopped sequence writes none)
-    if (blockIdx.x == 0 && !a.kv_written && !(a.d_done && *a.d_done))
+    if (bx == 0 && !a.kv_written && !(a.d_done && *a.d_done))
         for (int i = threadIdx.x; i < NKV * HD; i += NT) {
             const int h = i / HD, d = i - h * HD;
             const size_t off = ((size_t)h * a.max_ctx + pos) * HD + d;
@@ -579,7 +647,7 @@ __global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArg
         wtot[h] = Ssum;
     }
     __syncthreads();
-    float *out = a.part + (size_t)blockIdx.x * NH * (HD + 2);
+    float *out = a.part + (size_t)bx * NH * (HD + 2);
     for (int idx = threadIdx.x; idx < NH * HD; idx += NT) {
         const int h = idx / HD, d = idx - h * HD;
         float O = 0.f;
@@ -589,6 +657,63 @@ __global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArg
             out[h * (HD + 2) + HD] = wmax[h];
             out[h * (HD + 2) + HD + 1] = wtot[h];
         }
+    }
+}
+
+template <int DPL, int NH, int NKV>
+__global__ __launch_bounds__(kAttnThreadsBatch) void dec_attn_lds_kernel(AttnArgs a) {
+    __shared__ AttnLds<DPL, NH, NKV> L;
+    attn_lds_body<DPL, NH, NKV, 72>(L, blockIdx.x, blockIdx.y, gridDim.x, a, QkvTagged{});
+}
+
+// ---- the QKV GEMM and the attention partials of a batched step in one launch ----
+
+constexpr int kQkvAttnRows = 32;   // K/V positions per round of a fused attention workgroup (~75 KiB LDS)
+
+struct QkvAttnArgs {
+    GemmPlan P;                  // the QKV GEMM (prepared input, one K chunk, 8-wave workgroups)
+    GemmIn in;
+    GemmOut out;                 // rows as tagged words: out.tagged, out.ldy
+    AttnArgs at;
+    int ns = 0;                  // attention slices per sequence
+    const uint32_t *epoch = nullptr;   // the batched step counter that makes the tags unique
+    int layer = 0;
+    int spin_limit = 0;
+    int *err = nullptr;
+};
+
+// Workgroups [0, P.gx) run the QKV GEMM (its rows stored as words tagged with this step and
+// layer), the rest the attention partials of (slice, sequence), which bring their K/V rows
+// into LDS while the GEMM runs and then poll for their sequence's q | k | v words. The GEMM's
+// workgroups come first in dispatch order and wait for nothing, so the launch completes even
+// when not every workgroup is resident; the union keeps both roles at two workgroups per CU.
+template <int DT, int DPL, int NH, int NKV>
+__global__ __launch_bounds__(kAttnThreadsBatch) __attribute__((amdgpu_waves_per_eu(4))) void dec_qkv_attn_kernel(
+    QkvAttnArgs q) {
+    __shared__ union Lds {
+        gemmb::GemmLds<gemmb::kWaves> g;
+        AttnLds<DPL, NH, NKV, kQkvAttnRows> a;
+    } L;
+    // the step counter by a vector load: a scalar one would share lgkmcnt with the LDS
+    // accesses of the staging, whose every wait would then wait for it too
+    const uint32_t tag = (__hip_atomic_load(q.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << 6) +
+                         (uint32_t)q.layer + 1u;
+    const int ng = q.P.gx;
+    if ((int)blockIdx.x < ng) {
+        GemmOut o = q.out;
+        o.tag = tag;
+        gemmb::gemm_body<DT, gemmb::kStagePrepared, gemmb::kWaves, false>(
+            L.g, blockIdx.x, 0, ng, 1, q.P.wq, q.P.q_bytes, q.P.wsc, q.P.s_bytes, q.in, q.P.batch, q.P.M, q.P.K,
+            q.P.cb, o, q.P.Yp, static_cast<const gemmb::PrepChunk *>(q.P.prep), q.P.ks);
+    } else {
+        const int w = (int)blockIdx.x - ng;
+        QkvTagged t;
+        t.w = q.out.tagged;
+        t.stride = (size_t)q.out.ldy;
+        t.tag = tag;
+        t.spin_limit = q.spin_limit;
+        t.err = q.err;
+        attn_lds_body<DPL, NH, NKV, kQkvAttnRows>(L.a, w % q.ns, w / q.ns, q.ns, q.at, t);
     }
 }
 
@@ -717,7 +842,8 @@ __global__ void dec_argmax_finish_kernel(const float *__restrict__ part, int npa
 }
 
 __global__ void dec_advance_batch_kernel(const int *__restrict__ tok, int *__restrict__ pos, int *__restrict__ step,
-                                         int batch, int *__restrict__ log, int *__restrict__ done, StopSet stop) {
+                                         int batch, int *__restrict__ log, int *__restrict__ done, StopSet stop,
+                                         uint32_t *__restrict__ epoch) {
     const int s = *step;
     for (int b = threadIdx.x; b < batch; b += blockDim.x) {
         if (done && done[b]) continue;       // a stopped sequence: its entry keeps the fill
@@ -727,7 +853,10 @@ __global__ void dec_advance_batch_kernel(const int *__restrict__ tok, int *__res
         if (done && stop.has(t)) done[b] = 1;   // inference.c:298-301
     }
     __syncthreads();
-    if (threadIdx.x == 0) *step = s + 1;
+    if (threadIdx.x == 0) {
+        *step = s + 1;
+        if (epoch) *epoch = *epoch + 1u;
+    }
 }
 
 template <int DT, bool GEGLU>
@@ -819,6 +948,60 @@ int dec_attention(const AttnArgs &a, float *out, hipStream_t s) {
     return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
 }
 
+// The fused form is instantiated where both roles fit two workgroups per CU (LDS <= 80 KiB,
+// <= 128 VGPRs, no scratch): Q4_0 weights, head_dim 64 or 128 with 4 or 8 query heads and 1 or
+// 2 K/V heads, or head_dim 256 with 4 query heads and one K/V head (the Gemma-3 shapes). Q8_0's
+// larger weight units and the larger attention shapes spill; they keep two launches.
+bool qkv_attention_fusable(int dt, int K, const AttnArgs &a) {
+    const int dpl = a.hd / kWave;
+    const bool shape = a.hd % kWave == 0 && (((dpl == 1 || dpl == 2) && (a.nh == 4 || a.nh == 8) &&
+                                              (a.nkv == 1 || a.nkv == 2)) ||
+                                             (dpl == 4 && a.nh == 4 && a.nkv == 1));
+    return dt == DT_Q4_0 && shape && a.batch >= 4 && a.batch <= kGemmSeqs && a.nh % a.nkv == 0 && !a.kv_written &&
+           a.out_blocked && gemm_splits(K) == 1;
+}
+
+int dec_qkv_attention(int dt, const void *w, int M, int K, const GemmIn &in, void *ws, uint64_t *tagged,
+                      const AttnArgs &a, const uint32_t *epoch, int layer, int spin_limit, int *err, float *out,
+                      hipStream_t s) {
+    if (!qkv_attention_fusable(dt, K, a) || !tagged || !epoch || !err || layer < 0 || layer > 62) {
+        set_error("fused QKV + attention: unsupported shape");
+        return -1;
+    }
+    QkvAttnArgs q;
+    if (plan_gemm_tiled(dt, w, M, K, a.batch, in, ws, s, &q.P) != 0) return -1;
+    if (q.P.nw != kAttnThreadsBatch / kWave || q.P.mode != 1 || q.P.nsplit != 1) {
+        set_error("fused QKV + attention: the QKV GEMM's launch form does not fit");
+        return -1;
+    }
+    q.in = in;
+    q.out.tagged = tagged;
+    q.out.ldy = M;
+    q.at = a;
+    q.ns = kAttnSplitBatch;
+    q.epoch = epoch;
+    q.layer = layer;
+    q.spin_limit = spin_limit;
+    q.err = err;
+    const dim3 grid((unsigned)(q.P.gx + q.ns * a.batch));
+    const int dpl = a.hd / kWave;
+#define SPH_QA(DTV, DPLV, NHV, NKVV)                                                                         \
+    if (dt == DTV && dpl == DPLV && a.nh == NHV && a.nkv == NKVV)                                          \
+        hipLaunchKernelGGL((dec_qkv_attn_kernel<DTV, DPLV, NHV, NKVV>), grid, dim3(kAttnThreadsBatch), 0, s, q); \
+    else
+    SPH_QA(DT_Q4_0, 1, 4, 1) SPH_QA(DT_Q4_0, 2, 4, 1) SPH_QA(DT_Q4_0, 4, 4, 1) SPH_QA(DT_Q4_0, 1, 8, 1)
+    SPH_QA(DT_Q4_0, 2, 8, 1) SPH_QA(DT_Q4_0, 1, 4, 2) SPH_QA(DT_Q4_0, 2, 4, 2) SPH_QA(DT_Q4_0, 1, 8, 2)
+    SPH_QA(DT_Q4_0, 2, 8, 2) {
+        set_error("fused QKV + attention: shape not instantiated");
+        return -1;
+    }
+#undef SPH_QA
+    if (!hip_ok(hipGetLastError(), "fused QKV + attention launch")) return -1;
+    hipLaunchKernelGGL(dec_attn_combine_kernel<kAttnSplitBatch>, dim3(a.nh, a.batch), dim3(kThreads), 0, s, a.part,
+                       a.nh, a.hd, out, a.out_stride, a.out_blocked);
+    return hip_ok(hipGetLastError(), "attention combine launch") ? 0 : -1;
+}
+
 int dec_kv_write(const AttnArgs &a, hipStream_t s) {
     if (a.nkv * a.hd > kAttnMaxKV || a.batch <= 0) {
         set_error("KV write: %d K/V heads of dim %d", a.nkv, a.hd);
@@ -862,9 +1045,9 @@ int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_
 }
 
 int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, int *d_done,
-                      const StopSet &stop, hipStream_t s) {
+                      const StopSet &stop, uint32_t *d_epoch, hipStream_t s) {
     hipLaunchKernelGGL(dec_advance_batch_kernel, dim3(1), dim3(kWave), 0, s, d_tokens, d_pos, d_step, batch, log,
-                       d_done, stop);
+                       d_done, stop, d_epoch);
     return hip_ok(hipGetLastError(), "batched advance launch") ? 0 : -1;
 }
 

@@ -69,6 +69,15 @@ struct AttnArgs {
 // attn_part_floats(nh, hd) floats per sequence.
 size_t attn_part_floats(int nh, int hd);
 int dec_attention(const AttnArgs &a, float *out, hipStream_t s);
+// A batched step's QKV GEMM (W [M][K] TILED, input `in` with norms or parts, as
+// launch_gemm_tiled_ex) and its attention partials as one launch, then the combine into out:
+// the GEMM's rows go to `tagged` ([batch][M] words, tagged with the step counter *epoch and
+// `layer`), and the attention workgroups poll them while their K/V rows arrive. A poll longer
+// than spin_limit counts in *err. qkv_attention_fusable tells whether the shapes allow it.
+bool qkv_attention_fusable(int dt, int K, const AttnArgs &a);
+int dec_qkv_attention(int dt, const void *w, int M, int K, const GemmIn &in, void *ws, uint64_t *tagged,
+                      const AttnArgs &a, const uint32_t *epoch, int layer, int spin_limit, int *err, float *out,
+                      hipStream_t s);
 // The K/V rows of the batch only: K = rope(rmsnorm_delta(k, kn)) and V as projected, at
 // d_pos[b] (attention.c:292-309 writes every row of a batch before its attention runs).
 // Bit-identical to the rows dec_attention writes.
@@ -138,8 +147,8 @@ int dec_embed_batch(const uint16_t *embed, int hidden, int vocab, float es, cons
 size_t argmax_batch_part_floats(int n, int batch);
 int dec_argmax_batch(const float *logits, int n, int batch, float *part, int *d_tokens, hipStream_t s);
 // For every b with done[b] clear: log[*d_step][b] = tokens[b]; ++pos[b]; done[b] = 1 when the
-// token is in `stop`. Then ++*d_step.
+// token is in `stop`. Then ++*d_step, and ++*d_epoch when d_epoch is set.
 int dec_advance_batch(const int *d_tokens, int *d_pos, int *d_step, int batch, int *log, int *d_done,
-                      const StopSet &stop, hipStream_t s);
+                      const StopSet &stop, uint32_t *d_epoch, hipStream_t s);
 
 }  // namespace sapphire

@@ -92,6 +92,13 @@ struct sapphire_decoder {
     uint32_t *seq = nullptr;
     int *perr = nullptr;
     uint64_t persist_steps = 0;
+    // batched step: the QKV GEMM and the attention in one launch (SAPPHIRE_FUSED_QKV_ATTN=0 turns
+    // it off at create time), exchanging q | k | v as words tagged with the step counter bepoch
+    // (starts at 1, advanced every step; the host restarts it before a tag would wrap)
+    bool fuse_qkv_attn = true;
+    uint64_t *tqkv = nullptr;
+    uint32_t *bepoch = nullptr;
+    uint64_t bepoch_steps = 0;
     // prefill (chunks of up to kPrefillChunk tokens of one sequence through the batched
     // GEMMs); pf_ok is false when the shapes do not fit the TILED GEMM
     bool pf_ok = false;
@@ -258,6 +265,9 @@ bool tiled_shapes_ok(const sapphire_decoder_config_t &c) {
 
 // A persistent-step wait longer than this many polls (about a second) is a failure.
 constexpr int kPersistSpinLimit = 1 << 19;
+// the batched step counter's range (tags are counter << 6 | layer + 1 in 32 bits)
+constexpr uint64_t kBatchEpochLimit = uint64_t(1) << 26;
+int batch_qkv_width(const sapphire_decoder_config_t &c) { return (c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
 
 // Per sequence 1 once it has logged a stop token (the state's last B words).
 int *done_flags(sapphire_decoder *d) { return d->state + 2 * d->batch + 2; }
@@ -433,6 +443,10 @@ struct BatchRun {
     float *qkv = nullptr, *attn = nullptr, *o = nullptr, *g = nullptr, *dparts = nullptr, *dout = nullptr;
     float *part = nullptr;
     void *gws = nullptr;
+    // the fused QKV + attention launch of a decode step (not set for a prefill chunk)
+    uint64_t *tqkv = nullptr;
+    const uint32_t *epoch = nullptr;
+    int *err = nullptr;
 };
 
 int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
@@ -467,10 +481,6 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
             qi.ldr = H;
             cur = 1 - cur;
         }
-        GemmOut qo;
-        qo.y = r.qkv;
-        qo.ldy = nqkv;
-        if (launch_gemm_tiled_ex(c.wdtype, L.t_qkv, nqkv, H, B, qi, qo, r.gws, s) != 0) return -1;
         AttnArgs at;
         at.qkv = r.qkv;
         at.qn = L.qn;
@@ -495,10 +505,21 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         at.out_stride = (size_t)nq;
         at.out_blocked = true;          // the o projection stages it with contiguous loads
         if (r.prefill) {
+            if (launch_gemm_tiled_ex(c.wdtype, L.t_qkv, nqkv, H, B, qi, GemmOut{r.qkv, nqkv}, r.gws, s) != 0)
+                return -1;
             if (dec_kv_write(at, s) != 0) return -1;
             at.kv_written = true;
+            if (dec_attention(at, r.attn, s) != 0) return -1;
+        } else if (d->fuse_qkv_attn && r.tqkv && qkv_attention_fusable(c.wdtype, H, at)) {
+            // one launch: the attention workgroups stream their K/V rows while the GEMM runs
+            if (dec_qkv_attention(c.wdtype, L.t_qkv, nqkv, H, qi, r.gws, r.tqkv, at, r.epoch, l, kPersistSpinLimit,
+                                  r.err, r.attn, s) != 0)
+                return -1;
+        } else {
+            if (launch_gemm_tiled_ex(c.wdtype, L.t_qkv, nqkv, H, B, qi, GemmOut{r.qkv, nqkv}, r.gws, s) != 0)
+                return -1;
+            if (dec_attention(at, r.attn, s) != 0) return -1;
         }
-        if (dec_attention(at, r.attn, s) != 0) return -1;
         GemmIn oi;
         oi.x = r.attn;
         oi.x_blocked = true;
@@ -559,6 +580,9 @@ int enqueue_step_batch(sapphire_decoder *d) {
     r.dout = d->dout;
     r.part = d->attn_part;
     r.gws = d->gws;
+    r.tqkv = d->tqkv;
+    r.epoch = d->bepoch;
+    r.err = d->perr;
     const int cur = enqueue_layers_batch(d, r);
     if (cur < 0) return -1;
     // last finalize + final norm (transformer.c:400-406), LM head, greedy tokens
@@ -576,7 +600,8 @@ int enqueue_step_batch(sapphire_decoder *d) {
         if ((d->temperature > 0.0f ? enqueue_sample(d, d->state + 2 * B, s)
                                    : dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s)) != 0)
             return -1;
-        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, s);
+        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, d->bepoch,
+                             s);
     }
     GemmIn li;
     li.x = d->resid[cur];
@@ -593,7 +618,8 @@ int enqueue_step_batch(sapphire_decoder *d) {
         // greedy tokens straight from the LM-head GEMM: no logits written or read again
         lo.tokens = d->state;
         if (launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s) != 0) return -1;
-        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, s);
+        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, d->bepoch,
+                             s);
     }
     lo.y = d->logits;
     lo.ldy = c.vocab;
@@ -601,7 +627,8 @@ int enqueue_step_batch(sapphire_decoder *d) {
     if ((d->temperature > 0.0f ? enqueue_sample(d, d->state + 2 * B, s)
                                : dec_argmax_batch(d->logits, c.vocab, B, d->amax_part, d->state, s)) != 0)
         return -1;
-    return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, s);
+    return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, d->bepoch,
+                             s);
 }
 
 bool valid_config(const sapphire_decoder_config_t &c) {
@@ -877,6 +904,16 @@ sapphire_decoder_t *create_decoder(const sapphire_decoder_config_t *cfg, const s
             !dev_alloc_t(d, &d->dout, b * H, "down output") ||
             !dev_alloc_t(d, &d->amax_part, argmax_batch_part_floats(c.vocab, B), "argmax partials"))
             return fail();
+        const uint32_t one = 1;
+        if (const char *e = getenv("SAPPHIRE_FUSED_QKV_ATTN")) d->fuse_qkv_attn = atoi(e) != 0;
+        if (!dev_alloc_t(d, &d->tqkv, b * (nq + 2 * nk), "tagged qkv") ||
+            !hip_ok(hipMemset(d->tqkv, 0, b * (nq + 2 * nk) * sizeof(uint64_t)), "tagged qkv zero") ||
+            !dev_alloc_t(d, &d->bepoch, 1, "step counter") ||
+            !hip_ok(hipMemcpy(d->bepoch, &one, sizeof(uint32_t), hipMemcpyHostToDevice), "step counter") ||
+            (!d->perr && (!dev_alloc_t(d, &d->perr, 1, "timeout counter") ||
+                          !hip_ok(hipMemset(d->perr, 0, sizeof(int)), "timeout zero"))) ||
+            !hip_ok(hipDeviceSynchronize(), "batched state zero"))
+            return fail();
     }
     if (d->pf_ok) {
         const size_t p = kPrefillChunk;
@@ -1075,6 +1112,17 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         SPH_CHECK(hipMemsetAsync(d->perr, 0, sizeof(int), d->stream));
         d->persist_steps += (uint64_t)steps;
     }
+    if (B > 1) {
+        // the fused QKV + attention launch tags its words with (step counter << 6) + layer + 1:
+        // the counter starts over at 1 (and every word is cleared) before it would pass 2^26
+        if (d->bepoch_steps + (uint64_t)steps + 1 >= kBatchEpochLimit) {
+            SPH_CHECK(hipMemsetAsync(d->tqkv, 0, (size_t)B * batch_qkv_width(c) * sizeof(uint64_t), d->stream));
+            SPH_CHECK(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(d->bepoch), 1, 1, d->stream));
+            d->bepoch_steps = 0;
+        }
+        SPH_CHECK(hipMemsetAsync(d->perr, 0, sizeof(int), d->stream));
+        d->bepoch_steps += (uint64_t)steps;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (elapsed_ms) {
         SPH_CHECK(hipEventCreate(&e0));
@@ -1095,7 +1143,7 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         (void)hipEventDestroy(e0);
         (void)hipEventDestroy(e1);
     }
-    if (d->groups > 0) {
+    if (d->groups > 0 || B > 1) {
         int timeouts = 0;
         SPH_CHECK(hipMemcpy(&timeouts, d->perr, sizeof(int), hipMemcpyDeviceToHost));
         if (timeouts) {
@@ -1137,6 +1185,19 @@ int sapphire_decoder_set_epoch_count(sapphire_decoder_t *d, uint32_t steps) {
     if (!d) {
         set_error("sapphire_decoder_set_epoch_count: bad arguments");
         return -1;
+    }
+    if (d->batch > 1) {
+        if ((uint64_t)steps + 1 >= kBatchEpochLimit) {
+            set_error("sapphire_decoder_set_epoch_count: %u steps are past the step counter's range", steps);
+            return -1;
+        }
+        SPH_CHECK(hipSetDevice(d->device));
+        SPH_CHECK(hipStreamSynchronize(d->stream));
+        const uint32_t e = steps + 1u;
+        SPH_CHECK(hipMemset(d->tqkv, 0, (size_t)d->batch * batch_qkv_width(d->cfg) * sizeof(uint64_t)));
+        SPH_CHECK(hipMemcpy(d->bepoch, &e, sizeof(uint32_t), hipMemcpyHostToDevice));
+        d->bepoch_steps = steps;
+        return 0;
     }
     if (d->groups <= 0) return 0;
     if ((uint64_t)(steps + 1ull) * persist_epochs_per_step(d->cfg.n_layers) > 0xFFFFFFFFull) {

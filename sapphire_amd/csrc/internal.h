@@ -134,6 +134,11 @@ struct GemmIn {
 struct GemmOut {
     float *y = nullptr;
     int ldy = 0;
+    // rows as epoch-tagged words for a consumer in the same launch (gemm_body.h):
+    // tagged[b * ldy + r] = tag << 32 | bits(y[b][r]), stored with agent-scope atomics. One K
+    // chunk, rows form only.
+    uint64_t *tagged = nullptr;
+    uint32_t tag = 0;
     float *parts = nullptr;
     bool geglu = false;
     // y in block order (block_order_index over the M or M / 2 outputs; ldy unused): one K
@@ -147,6 +152,24 @@ struct GemmOut {
 };
 int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
                          void *ws, hipStream_t s);
+// The launch parameters of one batched GEMM pass (gemm_mfma.hip), for a kernel that runs the
+// GEMM's workgroups beside other work (gemm_body.h): weights, K chunking (cb blocks per chunk,
+// nsplit chunks), waves per tile ks, workgroups gx of nw waves, staging mode (0 full, 1
+// prepared, 2 plain), the prepared operands and the partial-sum workspace.
+struct GemmPlan {
+    const uint8_t *wq = nullptr;
+    uint32_t q_bytes = 0;
+    const uint8_t *wsc = nullptr;
+    uint32_t s_bytes = 0;
+    int M = 0, K = 0, batch = 0, cb = 0, nsplit = 1, ks = 1, gx = 0, nw = 0, mode = 0;
+    const void *prep = nullptr;
+    float *Yp = nullptr;
+};
+// For an input with norms or parts and one K chunk: launches the input pass (gemm_prep_kernel)
+// on s and returns the plan of the GEMM that consumes it (mode 1). ws as for
+// launch_gemm_tiled_ex. 0 / -1.
+int plan_gemm_tiled(int dt, const void *w, int M, int K, int batch, const GemmIn &in, void *ws, hipStream_t s,
+                    GemmPlan *P);
 int launch_gemv_f(int dt, const void *w, int M, int K, const float *x, float *y, hipStream_t s);
 // BF16 W [M][K] times up to any number of fp32 vectors X[b][ldx] -> Y[b][ldy] on the matrix
 // cores (gemm_bf16.hip); supported: K % 8 == 0, W 16-byte aligned, below 4 GiB

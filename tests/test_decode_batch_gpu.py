@@ -114,3 +114,63 @@ def test_decode_batch_repeatable_and_rejects(oracle):
     dec.close()
     with pytest.raises(RuntimeError):
         Decoder(m, batch=17)
+
+
+def test_decode_batch_fused_qkv_attention_matches_unfused(oracle, monkeypatch):
+    """The batched step's QKV GEMM and attention run as one launch (the attention workgroups
+    poll q | k | v words that the GEMM's workgroups store tagged with the step and layer), or,
+    with SAPPHIRE_FUSED_QKV_ATTN=0 at create time, as two. Both forms decode the oracle's
+    tokens, and their logits agree to rounding (the fused launch's attention takes its K/V
+    rows in rounds of 32 positions instead of 72)."""
+    from sapphire_amd.engine import Decoder
+    cfg, seed, batch, steps = GQA2, 58, 5, 10
+    prefills = [40, 12, 30, 55, 3]
+    m = smodel.synthetic_model(cfg, seed)
+    toks0 = synth.rng(seed, 4242).integers(0, cfg.vocab, size=batch).astype(np.int32)
+    kvs = [m.kv_prefill(prefills[b], seed_offset=100 + b) for b in range(batch)]
+    out = {}
+    for fused in ("1", "0"):
+        monkeypatch.setenv("SAPPHIRE_FUSED_QKV_ATTN", fused)
+        dec = Decoder(m, batch=batch)
+        try:
+            for b in range(batch):
+                dec.set_kv_seq(b, *kvs[b])
+            out[fused] = dec.generate_batch(toks0, np.asarray(prefills, np.int32), steps, keep_logits=True)[:2]
+        finally:
+            dec.close()
+    (tf, lf), (tu, lu) = out["1"], out["0"]
+    assert np.array_equal(tf, tu)
+    d = np.abs(lf - lu).max() / np.abs(lu).max()
+    print(f"fused vs unfused logits: {d:.2e}", flush=True)
+    assert d <= 1e-4
+    for b in (0, 4):
+        ref_toks, _ = oracle_decode(oracle, m, *kvs[b], int(toks0[b]), prefills[b], steps, nthreads=4)
+        assert np.array_equal(tf[:, b], ref_toks), f"sequence {b}"
+
+
+def test_decode_batch_step_counter_across_the_restart(oracle):
+    """The fused launch's tags are (step counter << 6) + layer + 1 in 32 bits: generate starts
+    the counter over at 1, clearing every tagged word, before a call would take it to 2^26.
+    A first call runs the counter's last values, the second starts over, the third goes on;
+    each decodes the oracle's tokens from the same state."""
+    from sapphire_amd.engine import Decoder
+    cfg, seed, batch, steps = smodel.TINY, 59, 4, 6
+    prefills = [30, 9, 41, 22]
+    m = smodel.synthetic_model(cfg, seed)
+    toks0 = synth.rng(seed, 4242).integers(0, cfg.vocab, size=batch).astype(np.int32)
+    kvs = [m.kv_prefill(prefills[b], seed_offset=100 + b) for b in range(batch)]
+    refs = [oracle_decode(oracle, m, kvs[b][0].copy(), kvs[b][1].copy(), int(toks0[b]), prefills[b], steps,
+                          nthreads=4)[0] for b in range(batch)]
+    last = (1 << 26) - 2                 # the largest count set_epoch_count takes
+    dec = Decoder(m, batch=batch)
+    try:
+        assert dec.lib.sapphire_decoder_set_epoch_count(dec.ptr, last - steps - 1) == 0
+        for _ in range(3):
+            for b in range(batch):
+                dec.set_kv_seq(b, *kvs[b])
+            got, _, _ = dec.generate_batch(toks0, np.asarray(prefills, np.int32), steps)
+            for b in range(batch):
+                assert np.array_equal(got[:, b], refs[b]), f"sequence {b}"
+        assert dec.lib.sapphire_decoder_set_epoch_count(dec.ptr, last + 1) == -1
+    finally:
+        dec.close()
