@@ -117,8 +117,14 @@ struct PersistArgs {
     int window = 0;                   // the local layers' sliding window (PLayer::window of a local layer)
     float scale = 1.f, eps = 1e-6f;
     const int *state = nullptr;       // [0] token, [1] position
-    const int *done = nullptr;        // the sequence's done flag: set, the kernel returns at once
+    int *done = nullptr;              // the sequence's done flag: set, the kernel returns at once
     const uint32_t *seq = nullptr;    // step counter that makes the epochs unique
+    // set: the token, position and epoch counter come from the previous step's LM head through
+    // these slots instead of state and seq (the first step of a run takes tok0 and pos0); the
+    // kernel logs that token in log and sets done on a token in stop
+    TokenSlots *slots = nullptr;
+    int *log = nullptr;
+    StopSet stop;
     uint64_t *t_qkv = nullptr, *t_part = nullptr, *t_attn = nullptr, *t_o = nullptr, *t_g = nullptr,
              *t_dn = nullptr;
     float *xfin = nullptr;            // [H] final-norm output (the LM-head input)

@@ -664,8 +664,38 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     if (a.done && *a.done) return;                 // the sequence has stopped
     if (threadIdx.x == 0) s.flag = 0;
     const int H = a.H, nq = NH * a.hd;
-    const int tok = a.state[0], pos = a.state[1];
-    const uint32_t base = *a.seq * persist_epochs_per_step(a.n_layers);
+    int tok, pos;
+    uint32_t seq;
+    if (a.slots) {
+        // the previous step's LM head left its greedy key in the slots (none before a run's
+        // first step): every workgroup decodes the same token; workgroup 0 logs it
+        // (inference.c:297) and, on a stop token (inference.c:298-301), marks the sequence done,
+        // and every workgroup returns
+        TokenSlots &ts = *a.slots;
+        const uint32_t st = ts.a;
+        tok = ts.tok0;
+        pos = ts.pos0 + (int)st;
+        seq = ts.seq0 + st;
+        if (st > 0) {
+            if (!slot_token(ts.key, st, a.vocab, tok)) {
+                if (threadIdx.x == 0) atomicAdd(a.err, 1);
+                return;
+            }
+            const bool stop = a.stop.has(tok);
+            if (blockIdx.x == 0 && threadIdx.x == 0) {
+                a.log[ts.logbase + (int)st - 1] = tok;
+                if (stop) *a.done = 1;
+            }
+            if (stop) return;
+        }
+        // nothing in this launch reads b; the LM head after it tags its keys with it
+        if (blockIdx.x == 0 && threadIdx.x == 0) ts.b = st + 1u;
+    } else {
+        tok = a.state[0];
+        pos = a.state[1];
+        seq = *a.seq;
+    }
+    const uint32_t base = seq * persist_epochs_per_step(a.n_layers);
     {   // sapphire_embed_lookup (transformer.c:347-365)
         const size_t row = embed_row(tok, a.vocab, H);
         for (int i = threadIdx.x; i < H; i += kThreads) {
@@ -857,6 +887,11 @@ bool persist_supported(int dt, int groups, int n_layers, int H, int nh, int nkv,
 }
 
 int dec_persist(int dt, const PersistArgs &a, int groups, hipStream_t s) {
+    if (a.slots && (!a.log || !a.done || a.vocab > kSlotMaxVocab)) {
+        set_error("persistent decode: token slots need the log, the done flag and a vocabulary of at most %d",
+                  kSlotMaxVocab);
+        return -1;
+    }
     const PersistKernel k = kernel_for(dt, a.nh, a.hd, a.H, light_slots(groups, a.H, a.nh, a.nkv, a.hd, a.ffn));
     if (!k) {
         set_error("persistent decode: shape not instantiated");

@@ -68,6 +68,11 @@ struct sapphire_decoder {
     // between steps): the LM head that picks the token also advances the state
     unsigned long long *gkeys = nullptr;
     unsigned *gcount = nullptr;
+    // the persistent step's greedy token hand-over (TokenSlots); graph_slots: the captured step
+    // uses it
+    TokenSlots *tslots = nullptr;
+    bool graph_slots = false;
+    int slot_run = kSlotRunSteps;   // steps per run (SAPPHIRE_TOKEN_SLOT_RUN at create time, for tests)
     // [0] token, [1] position, [2] step, [4] done; batched: tokens[B], pos[B], step, -, done[B]
     int *state = nullptr;
     int *log = nullptr;     // [max_ctx] tokens of the steps; batched: [max_ctx][B]
@@ -280,13 +285,24 @@ int enqueue_sample(sapphire_decoder *d, const int *d_step, hipStream_t s) {
                          d->state, d->smp_ws, s);
 }
 
+// Whether the persistent step hands its greedy token to the next step through d->tslots: a
+// greedy TILED LM head over a vocabulary the slot keys can index.
+bool use_token_slots(const sapphire_decoder *d) {
+    return d->groups > 0 && d->batch == 1 && d->tslots && !(d->temperature > 0.0f) && d->cfg.lm_dtype != DT_BF16 &&
+           d->lm_layout == LAYOUT_TILED && d->cfg.vocab <= kSlotMaxVocab;
+}
+
 // LM head on d->xfin with the greedy (or sampled) token into d->state[0], then the advance
-// (for a greedy TILED head both happen in the LM head's own epilogue).
+// (for a greedy TILED head both happen in the LM head's own epilogue, or, with token slots, in
+// the next step's layers kernel).
 int enqueue_lm_head(sapphire_decoder *d) {
     const auto &c = d->cfg;
     hipStream_t s = d->stream;
     const int H = c.hidden;
     const bool greedy = !(d->temperature > 0.0f);
+    if (use_token_slots(d))
+        return launch_gemv_tiled_greedy_slots(c.lm_dtype, d->lm, c.vocab, H, d->xfin, d->logits, d->tslots,
+                                              done_flags(d), s);
     if (c.lm_dtype == DT_BF16) {
         // weight tying: the logits are the embedding table times the final norm
         // (transformer.c:393-408 projects through embedding_weight)
@@ -360,6 +376,11 @@ int enqueue_step(sapphire_decoder *d) {
         pa.xfin = d->xfin;
         pa.err = d->perr;
         pa.spin_limit = kPersistSpinLimit;
+        if (use_token_slots(d)) {
+            pa.slots = d->tslots;
+            pa.log = d->log;
+            pa.stop = d->stop;
+        }
         if (dec_persist(c.wdtype, pa, d->groups, s) != 0) return -1;
         return enqueue_lm_head(d);
     }
@@ -971,8 +992,11 @@ bool setup_persistent(sapphire_decoder *d) {
         !dev_alloc_t(d, &d->tbuf, d->tbuf_words, "exchange buffers") ||
         !hip_ok(hipMemset(d->tbuf, 0, d->tbuf_words * sizeof(uint64_t)), "exchange zero") ||
         !dev_alloc_t(d, &d->seq, 1, "epoch counter") || !hip_ok(hipMemset(d->seq, 0, sizeof(uint32_t)), "epoch zero") ||
+        !dev_alloc_t(d, &d->tslots, 1, "token slots") ||
+        !hip_ok(hipMemset(d->tslots, 0, sizeof(TokenSlots)), "token slots zero") ||
         !dev_alloc_t(d, &d->perr, 1, "timeout counter") || !hip_ok(hipMemset(d->perr, 0, sizeof(int)), "timeout zero"))
         return false;
+    if (const char *e = getenv("SAPPHIRE_TOKEN_SLOT_RUN")) d->slot_run = std::min(std::max(atoi(e), 1), kSlotRunSteps);
     int g = kDefaultGroups;
     if (const char *e = getenv("SAPPHIRE_DECODE_WORKGROUPS")) g = atoi(e);
     d->groups = g > 0 && persist_supported(c.wdtype, g, c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, hd, c.ffn) ? g : 0;
@@ -1075,6 +1099,7 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
     }
     if (!d->exec) {
         d->graph_logits = want_logits;
+        d->graph_slots = B == 1 && use_token_slots(d);
         SPH_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
         const int rc = B == 1 ? enqueue_step(d) : enqueue_step_batch(d);
         hipGraph_t g = nullptr;
@@ -1106,8 +1131,19 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         const uint64_t per = persist_epochs_per_step(c.n_layers);
         if ((d->persist_steps + (uint64_t)steps + 1) * per > 0xFFFFFFFFull) {
             SPH_CHECK(hipMemsetAsync(d->tbuf, 0, d->tbuf_words * sizeof(uint64_t), d->stream));
-            SPH_CHECK(hipMemsetAsync(d->seq, 0, sizeof(uint32_t), d->stream));
             d->persist_steps = 0;
+        }
+        // the call's steps take the epoch counter from here on (one per step, whichever form
+        // advances it)
+        const uint32_t seq0 = (uint32_t)d->persist_steps;
+        SPH_CHECK(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(d->seq), (int)seq0, 1, d->stream));
+        if (d->graph_slots) {
+            TokenSlots ts{};
+            ts.tok0 = tokens[0];
+            ts.pos0 = pos[0];
+            ts.seq0 = seq0;
+            SPH_CHECK(hipMemcpyAsync(d->tslots, &ts, sizeof(ts), hipMemcpyHostToDevice, d->stream));
+            SPH_CHECK(hipStreamSynchronize(d->stream));   // ts is a local
         }
         SPH_CHECK(hipMemsetAsync(d->perr, 0, sizeof(int), d->stream));
         d->persist_steps += (uint64_t)steps;
@@ -1135,6 +1171,10 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         if (logits_out)
             SPH_CHECK(hipMemcpyAsync(logits_out + (size_t)s * lstep, d->logits, sizeof(float) * lstep,
                                      hipMemcpyDeviceToHost, d->stream));
+        // token slots: a run's last token is logged after its last step
+        if (d->graph_slots && ((s + 1) % d->slot_run == 0 || s + 1 == steps) &&
+            launch_token_slots_settle(d->tslots, c.vocab, d->log, done_flags(d), d->stop, d->perr, d->stream) != 0)
+            return -1;
     }
     if (elapsed_ms) SPH_CHECK(hipEventRecord(e1, d->stream));
     SPH_CHECK(hipStreamSynchronize(d->stream));
@@ -1147,7 +1187,8 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         int timeouts = 0;
         SPH_CHECK(hipMemcpy(&timeouts, d->perr, sizeof(int), hipMemcpyDeviceToHost));
         if (timeouts) {
-            set_error("sapphire_decoder_generate: %d persistent-step waits timed out; results are invalid", timeouts);
+            set_error("sapphire_decoder_generate: %d persistent-step waits timed out (or a step found no token); "
+                      "results are invalid", timeouts);
             return -1;
         }
     }

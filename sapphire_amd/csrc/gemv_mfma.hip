@@ -246,7 +246,7 @@ struct NfCtx {
 
 // Epilogues of the TILED GEMV: the logits only; the logits and each workgroup's softmax /
 // argmax partial; the logits and the greedy token with the decode step's advance.
-constexpr int kEpNone = 0, kEpSoftmax = 1, kEpGreedyStep = 2;
+constexpr int kEpNone = 0, kEpSoftmax = 1, kEpGreedyStep = 2, kEpGreedySlots = 3;
 static_assert(kGreedyGroups == 8, "one counter per XCD-interleaved group of workgroups");
 
 // The 16 columns of each row summed across the row group; lane 16m + 4r stores row
@@ -261,7 +261,7 @@ __device__ __forceinline__ void tile_store(const float (&acc)[4], float *__restr
         if (nc.nf) v += nonfinite::fold<DT, LAYOUT_TILED>(nc.wq, nc.wsc, nc.nb, row, nc.x);
         y[row] = v;
         if constexpr (EP == kEpSoftmax) soft_push(sp, v, row);
-        if constexpr (EP == kEpGreedyStep) {
+        if constexpr (EP == kEpGreedyStep || EP == kEpGreedySlots) {
             const unsigned long long k = greedy_key(v, row);
             key = k > key ? k : key;
         }
@@ -275,7 +275,10 @@ __device__ __forceinline__ void tile_store(const float (&acc)[4], float *__restr
 // partial of its rows in part[blockIdx.x] (folded by softmax_finish_parts). With
 // kEpGreedyStep every workgroup leaves the greedy key of its rows in its slot of gs.keys and
 // counts itself done; the last one takes the maximum key, decodes the token and advances the
-// decode state (dec_advance_kernel's work), so the step needs no further launch.
+// decode state (dec_advance_kernel's work), so the step needs no further launch. With
+// kEpGreedySlots every workgroup folds its key into its group's slot of gs.slots, tagged with
+// the step (gs.slots->b), and workgroup 0 writes gs.slots->a = b: the next step's layers
+// kernel picks the token.
 template <int DT, int NG, int EP>
 __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq, uint32_t q_bytes,
                                                  const uint8_t *__restrict__ wsc, uint32_t s_bytes,
@@ -294,8 +297,10 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
     if (t < ntiles) tile_issue<DT, NG>(RA, rq, rs, t, lane);
     // a stopped sequence: the whole launch returns (every workgroup reads the same flag, so no
     // key slot or counter is touched); the check waits behind the first tile's loads
-    if constexpr (EP == kEpGreedyStep)
+    if constexpr (EP == kEpGreedyStep || EP == kEpGreedySlots)
         if (gs.done && *gs.done) return;
+    uint32_t tag = 0;
+    if constexpr (EP == kEpGreedySlots) tag = gs.slots->b;
 
     float p[NG];
     long bop[NG];
@@ -386,6 +391,22 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
                 if (gs.seq) *gs.seq = *gs.seq + 1u;
                 if (gs.done && gs.stop.has(tok)) *gs.done = 1;   // inference.c:298-301
             }
+        }
+    }
+    if constexpr (EP == kEpGreedySlots) {
+#pragma unroll
+        for (int mask = 1; mask < kWave; mask <<= 1) key = key_max_shfl(key, mask);
+        __shared__ unsigned long long wkeys[4];
+        const int wid = threadIdx.x / kWave;
+        if (lane == 0) wkeys[wid] = key;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long b = wkeys[0];
+            for (int w = 1; w < nw_blk; ++w) b = wkeys[w] > b ? wkeys[w] : b;
+            // no return value: the launch's end waits for it, nothing in the launch does
+            __hip_atomic_fetch_max(gs.slots->key + blockIdx.x % kGreedyGroups, slot_key(b, tag), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            if (blockIdx.x == 0) gs.slots->a = tag;
         }
     }
     if constexpr (EP == kEpSoftmax) {
@@ -570,7 +591,10 @@ int launch_mfma_typed(const uint8_t *w, int M, int K, const float *x, float *y, 
     const size_t sbytes = q_tiled_bytes(DT, M, K) - so;
     const unsigned blocks = tiled_blocks(DT, M);
     const GreedyStep g = gs ? *gs : GreedyStep{};
-    if (gs)
+    if (gs && gs->slots)
+        hipLaunchKernelGGL((gemv_mfma<DT, NG, kEpGreedySlots>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so,
+                           w + so, (uint32_t)sbytes, x, y, M, ntiles, part, g);
+    else if (gs)
         hipLaunchKernelGGL((gemv_mfma<DT, NG, kEpGreedyStep>), dim3(blocks), dim3(256), 0, st, w, (uint32_t)so,
                            w + so, (uint32_t)sbytes, x, y, M, ntiles, part, g);
     else if (part)
@@ -678,6 +702,46 @@ int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const flo
         return -1;
     }
     return launch_tiled(dt, w, M, K, x, logits, nullptr, st, &gs);
+}
+
+int launch_gemv_tiled_greedy_slots(int dt, const void *w, int M, int K, const float *x, float *logits,
+                                   TokenSlots *slots, const int *done, hipStream_t st) {
+    if (!slots || M > kSlotMaxVocab) {
+        set_error("greedy LM head: token slots need a vocabulary of at most %d", kSlotMaxVocab);
+        return -1;
+    }
+    GreedyStep gs;
+    gs.slots = slots;
+    gs.done = const_cast<int *>(done);
+    return launch_tiled(dt, w, M, K, x, logits, nullptr, st, &gs);
+}
+
+namespace {
+__global__ void token_slots_settle_kernel(TokenSlots *ts, int vocab, int *log, int *done, StopSet stop, int *err) {
+    if (threadIdx.x != 0 || (done && *done)) return;
+    const uint32_t a = ts->a;
+    if (a == 0) return;
+    int tok = 0;
+    if (!slot_token(ts->key, a, vocab, tok)) {
+        atomicAdd(err, 1);
+        return;
+    }
+    log[ts->logbase + (int)a - 1] = tok;
+    if (done && stop.has(tok)) *done = 1;   // inference.c:298-301
+    ts->tok0 = tok;
+    ts->pos0 += (int)a;
+    ts->seq0 += a;
+    ts->logbase += (int)a;
+    ts->a = 0;
+    ts->b = 0;
+    for (int i = 0; i < kGreedyGroups; ++i) ts->key[i] = 0;
+}
+}  // namespace
+
+int launch_token_slots_settle(TokenSlots *slots, int vocab, int *log, int *done, const StopSet &stop, int *err,
+                              hipStream_t st) {
+    hipLaunchKernelGGL(token_slots_settle_kernel, dim3(1), dim3(64), 0, st, slots, vocab, log, done, stop, err);
+    return hip_ok(hipGetLastError(), "token slots settle launch") ? 0 : -1;
 }
 
 }  // namespace sapphire

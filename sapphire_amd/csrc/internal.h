@@ -71,6 +71,7 @@ struct StopSet {
         return r;
     }
 };
+struct TokenSlots;
 struct GreedyStep {
     unsigned long long *keys = nullptr;  // each workgroup's best greedy key
     unsigned *count = nullptr;           // [0] groups done, [1 + g] workgroups of group g done
@@ -78,6 +79,7 @@ struct GreedyStep {
     uint32_t *seq = nullptr;             // the persistent step's counter (may be NULL)
     int *done = nullptr;                 // the sequence's done flag (may be NULL): set, the launch does nothing
     StopSet stop;
+    TokenSlots *slots = nullptr;         // set: the token goes through these (launch_gemv_tiled_greedy_slots)
 };
 size_t tiled_greedy_key_slots(int M);
 // TILED GEMV whose epilogue writes the logits, picks the greedy token (sample_greedy's
@@ -86,6 +88,53 @@ size_t tiled_greedy_key_slots(int M);
 // *done set it returns at once. Launches that share the state must be ordered.
 int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const float *x, float *logits,
                                   const GreedyStep &gs, hipStream_t s);
+
+// The greedy token handed from a step's LM head to the next step's layers kernel without a
+// reduction inside the LM head. Its workgroups fold the greedy key of their rows into eight
+// slots by atomic maxima (one slot per XCD-interleaved group), each key tagged with the step,
+// so that the slots need no clearing between steps; the next step's layers kernel takes the
+// largest, decodes the token, logs it and stops the sequence on a stop token. Two step words
+// alternate, so that no launch writes a word its own workgroups read: the layers kernel reads
+// `a` (steps of this run whose LM head has run) and writes b = a + 1; the LM head reads b, its
+// tag, and writes a = b. A run covers at most kSlotRunSteps steps; token_slots_settle logs a
+// run's last token and starts the next run from it.
+constexpr int kSlotIndexBits = 18, kSlotTagBits = 64 - 32 - kSlotIndexBits;
+constexpr int kSlotMaxVocab = 1 << kSlotIndexBits;
+constexpr int kSlotRunSteps = (1 << kSlotTagBits) - 1;
+struct TokenSlots {
+    unsigned long long key[kGreedyGroups];   // tag << 50 | ordered value << 18 | (2^18 - 1 - index)
+    uint32_t a, b;
+    int tok0, pos0;                          // the run's first token and position
+    uint32_t seq0;                           // the persistent step's epoch counter at the run's start
+    int logbase;                             // log index of the run's first step
+};
+// A slot key from greedy_key's (ordered value << 32 | ~index) for rows below kSlotMaxVocab.
+__host__ __device__ inline unsigned long long slot_key(unsigned long long gk, uint32_t tag) {
+    constexpr unsigned long long lo = (1ull << (64 - kSlotTagBits)) - 1;
+    const unsigned long long body = gk ? ((gk >> 32) << kSlotIndexBits) | (gk & (kSlotMaxVocab - 1)) : 0ull;
+    return ((unsigned long long)tag << (64 - kSlotTagBits)) | (body & lo);
+}
+// The token of the slots tagged `tag` (0 when no row had a key, as sample_greedy starts at
+// index 0); false when the largest slot carries another tag.
+__host__ __device__ inline bool slot_token(const unsigned long long (&key)[kGreedyGroups], uint32_t tag, int vocab,
+                                           int &tok) {
+    unsigned long long k = key[0];
+    for (int i = 1; i < kGreedyGroups; ++i) k = key[i] > k ? key[i] : k;
+    constexpr unsigned long long lo = (1ull << (64 - kSlotTagBits)) - 1;
+    const int r = (kSlotMaxVocab - 1) - (int)(k & (kSlotMaxVocab - 1));
+    tok = (k & lo) != 0 && r < vocab ? r : 0;
+    return (uint32_t)(k >> (64 - kSlotTagBits)) == tag;
+}
+// The TILED LM head of a persistent step whose token goes through `slots` (gs.done, if set,
+// makes it return at once; gs.keys, count, tok, pos, step and log are not used).
+int launch_gemv_tiled_greedy_slots(int dt, const void *w, int M, int K, const float *x, float *logits,
+                                   TokenSlots *slots, const int *done, hipStream_t s);
+// After a run's last step: logs its last token (log[logbase + a - 1]; done set on a stop token)
+// and makes it the next run's first (tok0, pos0 + a, seq0 + a, logbase + a, a = b = 0, slots
+// cleared). Does nothing once done is set; counts *err when the slots do not carry the run's
+// last tag.
+int launch_token_slots_settle(TokenSlots *slots, int vocab, int *log, int *done, const StopSet &stop, int *err,
+                              hipStream_t s);
 // Batched GEMM on the TILED layout (gemm_mfma.hip): Y[b][r] = W[r] . X[b] for b < batch, 16
 // sequences per pass. ws: gemm_workspace_bytes(M, K) bytes of 256-byte aligned device memory
 // (the K-split partial sums). Calls sharing a workspace must be ordered.

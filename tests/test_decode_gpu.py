@@ -313,6 +313,48 @@ def test_decode_persistent_epochs_across_the_reset(oracle):
         dec.close()
 
 
+@pytest.mark.parametrize("run,stop_at", [(4, None), (3, 7), (5, 4)], ids=["run4", "run3_stop7", "run5_stop4"])
+def test_decode_token_slots_across_runs(oracle, monkeypatch, run, stop_at):
+    """The persistent step's greedy token goes from the LM head to the next step's layers
+    kernel through tagged slots, in runs of at most 2^14 - 1 steps, each ending with a settle
+    launch that logs its last token and starts the next run from it. With runs of 3-5 steps
+    (SAPPHIRE_TOKEN_SLOT_RUN) a 14-step call crosses several runs: the tokens, logits and K/V
+    rows are the oracle's; with a stop token first seen at step stop_at, the call ends there
+    (stop at the end of a run, and inside one)."""
+    from sapphire_amd.engine import Decoder
+    cfg, seed, prefill, steps = smodel.TINY, 39, 30, 14
+    monkeypatch.setenv("SAPPHIRE_TOKEN_SLOT_RUN", str(run))
+    m = smodel.synthetic_model(cfg, seed)
+    k0, v0 = m.kv_prefill(prefill)
+    tok = smodel.start_token(cfg, seed)
+    k, v = k0.copy(), v0.copy()
+    ref_toks, ref_logits = oracle_decode(oracle, m, k, v, tok, prefill, steps, nthreads=4, keep_logits=True)
+    stops = []
+    if stop_at is not None:
+        # a token that first appears at stop_at (the seed is chosen so that one does)
+        assert ref_toks[stop_at] not in ref_toks[:stop_at], ref_toks
+        stops = [int(ref_toks[stop_at])]
+    dec = Decoder(m)
+    try:
+        assert dec.workgroups > 0
+        dec.set_stop_tokens(stops)
+        for _ in range(2):                  # the second call starts its runs over
+            dec.set_kv(k0, v0)
+            got_toks, got_logits, _ = dec.generate(tok, prefill, steps, keep_logits=True)
+            n = steps if stop_at is None else stop_at + 1
+            print(f"run {run}: tokens {got_toks.tolist()}", flush=True)
+            assert _compare(ref_toks[:n], ref_logits[:n], got_toks[:n], got_logits[:n], f"run {run}") == n
+            assert np.all(got_toks[n:] == -1)
+            gk, gv = dec.get_kv()
+            sl = slice(prefill, prefill + n)
+            for name, g, r in (("K", gk, k), ("V", gv, v)):
+                d = np.abs(g[:, :, sl] - r[:, :, sl]).max() / np.abs(r[:, :, sl]).max()
+                assert d <= REL, f"{name} cache rows differ: {d:.2e}"
+            assert np.array_equal(gk[:, :, prefill + n:], k0[:, :, prefill + n:])
+    finally:
+        dec.close()
+
+
 def test_decode_repeatable(oracle):
     """Two generate calls on one decoder (the captured graph is replayed, the state reset)."""
     from sapphire_amd.engine import Decoder
