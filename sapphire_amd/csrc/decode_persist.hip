@@ -677,7 +677,17 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         pos = ts.pos0 + (int)st;
         seq = ts.seq0 + st;
         if (st > 0) {
-            if (!slot_token(ts.key, st, a.vocab, tok)) {
+            // lane l reads slot l; the wave's maximum by 64-bit shuffles (no LDS, no barrier)
+            static_assert(kSlotCount == kWave, "one slot per lane");
+            const int lane = threadIdx.x & (kWave - 1);
+            unsigned long long k = ts.key[lane];
+#pragma unroll
+            for (int mask = 1; mask < kWave; mask <<= 1) {
+                const uint32_t lo = __shfl_xor((uint32_t)k, mask, kWave), hi = __shfl_xor((uint32_t)(k >> 32), mask, kWave);
+                const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+                k = o > k ? o : k;
+            }
+            if (!slot_token(k, st, a.vocab, tok)) {
                 if (threadIdx.x == 0) atomicAdd(a.err, 1);
                 return;
             }

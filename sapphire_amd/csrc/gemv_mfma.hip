@@ -404,7 +404,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
             unsigned long long b = wkeys[0];
             for (int w = 1; w < nw_blk; ++w) b = wkeys[w] > b ? wkeys[w] : b;
             // no return value: the launch's end waits for it, nothing in the launch does
-            __hip_atomic_fetch_max(gs.slots->key + blockIdx.x % kGreedyGroups, slot_key(b, tag), __ATOMIC_RELAXED,
+            __hip_atomic_fetch_max(gs.slots->key + blockIdx.x % kSlotCount, slot_key(b, tag), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             if (blockIdx.x == 0) gs.slots->a = tag;
         }
@@ -721,8 +721,10 @@ __global__ void token_slots_settle_kernel(TokenSlots *ts, int vocab, int *log, i
     if (threadIdx.x != 0 || (done && *done)) return;
     const uint32_t a = ts->a;
     if (a == 0) return;
+    unsigned long long k = 0;
+    for (int i = 0; i < kSlotCount; ++i) k = ts->key[i] > k ? ts->key[i] : k;
     int tok = 0;
-    if (!slot_token(ts->key, a, vocab, tok)) {
+    if (!slot_token(k, a, vocab, tok)) {
         atomicAdd(err, 1);
         return;
     }
@@ -734,7 +736,7 @@ __global__ void token_slots_settle_kernel(TokenSlots *ts, int vocab, int *log, i
     ts->logbase += (int)a;
     ts->a = 0;
     ts->b = 0;
-    for (int i = 0; i < kGreedyGroups; ++i) ts->key[i] = 0;
+    for (int i = 0; i < kSlotCount; ++i) ts->key[i] = 0;
 }
 }  // namespace
 

@@ -90,8 +90,9 @@ int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const flo
                                   const GreedyStep &gs, hipStream_t s);
 
 // The greedy token handed from a step's LM head to the next step's layers kernel without a
-// reduction inside the LM head. Its workgroups fold the greedy key of their rows into eight
-// slots by atomic maxima (one slot per XCD-interleaved group), each key tagged with the step,
+// reduction inside the LM head. Its workgroups fold the greedy key of their rows into 64
+// slots by atomic maxima (workgroup b into slot b mod 64, so that no address takes more than a
+// few of them: atomics on one address from every XCD serialize), each key tagged with the step,
 // so that the slots need no clearing between steps; the next step's layers kernel takes the
 // largest, decodes the token, logs it and stops the sequence on a stop token. Two step words
 // alternate, so that no launch writes a word its own workgroups read: the layers kernel reads
@@ -101,8 +102,9 @@ int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const flo
 constexpr int kSlotIndexBits = 18, kSlotTagBits = 64 - 32 - kSlotIndexBits;
 constexpr int kSlotMaxVocab = 1 << kSlotIndexBits;
 constexpr int kSlotRunSteps = (1 << kSlotTagBits) - 1;
+constexpr int kSlotCount = 64;               // one per lane of a wave, which reads them all at once
 struct TokenSlots {
-    unsigned long long key[kGreedyGroups];   // tag << 50 | ordered value << 18 | (2^18 - 1 - index)
+    unsigned long long key[kSlotCount];      // tag << 50 | ordered value << 18 | (2^18 - 1 - index)
     uint32_t a, b;
     int tok0, pos0;                          // the run's first token and position
     uint32_t seq0;                           // the persistent step's epoch counter at the run's start
@@ -114,12 +116,9 @@ __host__ __device__ inline unsigned long long slot_key(unsigned long long gk, ui
     const unsigned long long body = gk ? ((gk >> 32) << kSlotIndexBits) | (gk & (kSlotMaxVocab - 1)) : 0ull;
     return ((unsigned long long)tag << (64 - kSlotTagBits)) | (body & lo);
 }
-// The token of the slots tagged `tag` (0 when no row had a key, as sample_greedy starts at
-// index 0); false when the largest slot carries another tag.
-__host__ __device__ inline bool slot_token(const unsigned long long (&key)[kGreedyGroups], uint32_t tag, int vocab,
-                                           int &tok) {
-    unsigned long long k = key[0];
-    for (int i = 1; i < kGreedyGroups; ++i) k = key[i] > k ? key[i] : k;
+// The token of the largest slot key k, which must carry `tag` (0 when no row had a key, as
+// sample_greedy starts at index 0); false when it carries another tag.
+__host__ __device__ inline bool slot_token(unsigned long long k, uint32_t tag, int vocab, int &tok) {
     constexpr unsigned long long lo = (1ull << (64 - kSlotTagBits)) - 1;
     const int r = (kSlotMaxVocab - 1) - (int)(k & (kSlotMaxVocab - 1));
     tok = (k & lo) != 0 && r < vocab ? r : 0;
