@@ -13,7 +13,7 @@ import pytest
 from oracle.oracle import oracle_decode
 from sapphire_amd import model as smodel
 from sapphire_amd import synth
-from tests.test_decode_gpu import GQA2, MID, _compare
+from tests.test_decode_gpu import GQA2, MID, NH8, NH8_KV2, _compare
 
 pytestmark = pytest.mark.gpu
 
@@ -64,7 +64,9 @@ TINY_TIED = smodel.DecodeConfig(**{**smodel.TINY.__dict__, "lm_dtype": synth.BF1
     (MID, 54, 5, [40, 44, 20, 47, 1], 16),                   # head_dim 128, 48-position window
     (TINY_TIED, 56, 6, [12, 33, 4, 50, 27, 9], 10),         # tied BF16 LM head on the matrix cores
     (GQA2, 57, 4, [40, 12, 30, 55], 10),                     # two K/V heads
-], ids=["tiny_b4", "tiny_q8_b3", "tiny_b16", "mid_b5", "tiny_tied_bf16_b6", "gqa2_b4"])
+    (NH8, 61, 7, [40, 12, 30, 55, 3, 24, 60], 10),           # eight query heads over one K/V head
+    (NH8_KV2, 62, 4, [40, 12, 30, 55], 10),                  # eight query heads over two K/V heads of 128
+], ids=["tiny_b4", "tiny_q8_b3", "tiny_b16", "mid_b5", "tiny_tied_bf16_b6", "gqa2_b4", "nh8_b7", "nh8_kv2_b4"])
 def test_decode_batch_matches_oracle(oracle, cfg, seed, batch, prefills, steps):
     print(f"batched decode cfg={cfg.n_layers}x{cfg.hidden} batch={batch} steps={steps}", flush=True)
     _run(oracle, cfg, seed, batch, prefills, steps)

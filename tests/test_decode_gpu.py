@@ -63,6 +63,13 @@ H1280 = smodel.DecodeConfig(n_layers=2, hidden=1280, n_heads=4, n_kv_heads=1, he
                             max_ctx=96, sliding_window=24, global_layers=(1,))
 
 
+# eight query heads: over one K/V head of 64 dims, and over two of 128 (four per K/V head)
+NH8 = smodel.DecodeConfig(n_layers=2, hidden=256, n_heads=8, n_kv_heads=1, head_dim=64, ffn=512, vocab=4096,
+                          max_ctx=96, sliding_window=24, global_layers=(1,))
+NH8_KV2 = smodel.DecodeConfig(n_layers=2, hidden=256, n_heads=8, n_kv_heads=2, head_dim=128, ffn=512, vocab=4096,
+                              max_ctx=96, sliding_window=24, global_layers=(1,))
+
+
 # groups: workgroups of the persistent step (None: the decoder's default), 0: the multi-launch step
 @pytest.mark.parametrize("cfg,seed,prefill,steps,groups", [
     (smodel.TINY, 31, 40, 16, None),      # window 24 < positions: local layers slide
@@ -81,9 +88,12 @@ H1280 = smodel.DecodeConfig(n_layers=2, hidden=1280, n_heads=4, n_kv_heads=1, he
     (WIDE, 42, 40, 16, 0),
     (H1280, 44, 40, 12, None),            # hidden 1280 (eight vector elements per thread)
     (H1280, 44, 40, 12, 0),
+    (NH8, 45, 40, 12, None),              # eight query heads (16 slices per head)
+    (NH8, 45, 40, 12, 0),
+    (NH8_KV2, 46, 40, 12, 0),             # eight query heads over two K/V heads (multi-launch step only)
 ], ids=["tiny", "tiny_graph", "tiny_g16", "tiny_g256", "tiny_q8", "tiny_q8_graph", "mid_window", "mid_window_graph",
         "mid_window_g96", "tiny_tied_bf16", "tiny_tied_bf16_graph", "gqa2_graph", "wide", "wide_graph", "h1280",
-        "h1280_graph"])
+        "h1280_graph", "nh8", "nh8_graph", "nh8_kv2_graph"])
 def test_decode_matches_oracle(oracle, cfg, seed, prefill, steps, groups):
     from sapphire_amd.engine import Decoder
     print(f"decode cfg={cfg.n_layers}x{cfg.hidden} seed={seed} prefill={prefill} steps={steps} groups={groups}",
