@@ -102,10 +102,17 @@ __device__ __forceinline__ void comb_geom(CombGeom &c, uint32_t *off, int nh, in
 
 enum { kGeomQkv = 0, kGeomO = 1, kGeomGu = 2, kGeomDown = 3 };
 
+// The GEMV input in LDS: each 32-element block padded to 36 floats. The 16 (or 32) lanes of a
+// row read 16 different blocks at once; at a 128-byte stride every second lane fell on the same
+// four of the 64 four-byte banks (an 8-way conflict on every ds_read_b128), at 144 bytes the 16
+// lanes of a row take 16 different bank quads.
+constexpr int kXBlock = kBlock + 4;
+__device__ __forceinline__ int xpad(int i) { return i + (i >> 5) * (kXBlock - kBlock); }
+
 template <int NH, int DPL>
 struct alignas(16) PersistLds {
     float resid[kDecMaxK];                       // the residual stream
-    float xs[kDecMaxK];                          // input of the current GEMV
+    float xs[kDecMaxK / kBlock * kXBlock];       // input of the current GEMV (padded blocks, xpad)
     float dl[kDecMaxK];                          // gathered delta vector
     float comb[kCombMax];
     // K / V rows of the attention slice's current batch (natural dim order), filled by DMA
@@ -147,6 +154,7 @@ struct Gather {
         }
     }
 
+    template <bool PAD = false>
     __device__ __forceinline__ bool end(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
                                         int *flag, float *sq = nullptr) {
         for (int spins = 0;; ++spins) {
@@ -171,7 +179,7 @@ struct Gather {
             const int j = threadIdx.x + e * kThreads;
             if (j < n) {
                 const float v = __uint_as_float((uint32_t)w[e]);
-                dst[j] = v;
+                dst[PAD ? xpad(j) : j] = v;
                 acc = __builtin_fmaf(v, v, acc);
             }
         }
@@ -195,14 +203,15 @@ __device__ __forceinline__ bool gather(Src src, int n, uint32_t tag, float *dst,
 }
 
 // gather() with during() run between the first loads of the words and their first check:
-// loads it issues go out behind the polls, so the first check does not wait for them.
-template <int MAXE, class Src, class F>
+// loads it issues go out behind the polls, so the first check does not wait for them. PAD:
+// dst is a GEMV input (element j at xpad(j)).
+template <int MAXE, bool PAD = false, class Src, class F>
 __device__ __forceinline__ bool gather_during(Src src, int n, uint32_t tag, float *dst, int spin_limit, int *err,
                                               int *flag, float *sq, F during) {
     Gather<MAXE, Src> g;
     g.begin(src, n, tag);
     during();
-    return g.end(src, n, tag, dst, spin_limit, err, flag, sq);
+    return g.template end<PAD>(src, n, tag, dst, spin_limit, err, flag, sq);
 }
 
 struct Contig {
@@ -242,7 +251,7 @@ __device__ __forceinline__ float par_sum_sq(const float *v, int K, float *sh) {
     return (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
-// xs = rmsnorm_delta(resid, w) (normalization.c:104-117)
+// xs = rmsnorm_delta(resid, w) (normalization.c:104-117), xs a GEMV input (xpad)
 template <int R>
 __device__ __forceinline__ void norm_to(float *xs, const float *resid, const VecRegs<R> &w, int K, float eps,
                                         float *sh) {
@@ -250,7 +259,7 @@ __device__ __forceinline__ void norm_to(float *xs, const float *resid, const Vec
 #pragma unroll
     for (int e = 0; e < R; ++e) {
         const int i = threadIdx.x + e * kThreads;
-        if (i < K) xs[i] = __fmul_rn(__fmul_rn(resid[i], r), __fadd_rn(1.0f, w[e]));
+        if (i < K) xs[xpad(i)] = __fmul_rn(__fmul_rn(resid[i], r), __fadd_rn(1.0f, w[e]));
     }
     __syncthreads();
 }
@@ -285,7 +294,7 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
 #pragma unroll
     for (int e = 0; e < R; ++e) {
         const int i = threadIdx.x + e * kThreads;
-        if (i < K) xs[i] = __fmul_rn(__fmul_rn(nv[e], r2), __fadd_rn(1.0f, wn[e]));
+        if (i < K) xs[xpad(i)] = __fmul_rn(__fmul_rn(nv[e], r2), __fadd_rn(1.0f, wn[e]));
     }
     __syncthreads();
 }
@@ -337,7 +346,7 @@ struct GemvStage {
                 const int blk = q + LPR * j;
                 const bool on = blk < nb;
                 float xv[32];
-                const float4 *xp = reinterpret_cast<const float4 *>(xs + blk * kBlock);
+                const float4 *xp = reinterpret_cast<const float4 *>(xs + blk * kXBlock);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const float4 v = on ? xp[i] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -775,7 +784,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
                 [] {}))
             return;
         // 4: o-proj
-        if (!gather_during<NQR>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag, nullptr,
+        if (!gather_during<NQR, true>(Contig{a.t_attn}, nq, ep + 3, s.xs, a.spin_limit, a.err, &s.flag, nullptr,
                                 [&] { if (nx) at.load_rows(Ln, a.hd, pos, RPW / 3, 2 * RPW / 3, s); }))
             return;
         go.finish(s.xs, a.t_o, ep + 4);
@@ -790,7 +799,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
         add_norm_delta_norm(s.resid, s.xs, s.dl, wd_attn, wn_ffn, H, a.eps, s.sh);
         gu.finish(s.xs, a.t_g, ep + 5);
         // 6: down (the next layer's QKV and norm weights, or the final norm's, go out)
-        if (!gather_during<kVecRegs>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag, nullptr, [&] {
+        if (!gather_during<kVecRegs, true>(Contig{a.t_g}, a.ffn, ep + 5, s.xs, a.spin_limit, a.err, &s.flag, nullptr, [&] {
                 if (nx) {
                     gq.load(Ln.qkv, Ln.qkv, s.geom[kGeomQkv]);
                     wn_attn.load(Ln.n_attn, H);
@@ -808,7 +817,7 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     if (!gather<HR>(Contig{a.t_dn}, H, ep_last, s.dl, a.spin_limit, a.err, &s.flag, s.sh)) return;
     add_norm_delta_norm(s.resid, s.xs, s.dl, wd_prev, wn_attn, H, a.eps, s.sh);
     if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i < H; i += kThreads) a.xfin[i] = s.xs[i];
+        for (int i = threadIdx.x; i < H; i += kThreads) a.xfin[i] = s.xs[xpad(i)];
 }
 
 using PersistKernel = void (*)(PersistArgs);
