@@ -97,8 +97,8 @@ int launch_gemv_tiled_greedy_step(int dt, const void *w, int M, int K, const flo
 // largest, decodes the token, logs it and stops the sequence on a stop token. Two step words
 // alternate, so that no launch writes a word its own workgroups read: the layers kernel reads
 // `a` (steps of this run whose LM head has run) and writes b = a + 1; the LM head reads b, its
-// tag, and writes a = b. A run covers at most kSlotRunSteps steps; token_slots_settle logs a
-// run's last token and starts the next run from it.
+// tag, and writes a = b. A run covers at most kSlotRunSteps steps; launch_token_slots_settle
+// logs a run's last token and starts the next run from it.
 constexpr int kSlotIndexBits = 18, kSlotTagBits = 64 - 32 - kSlotIndexBits;
 constexpr int kSlotMaxVocab = 1 << kSlotIndexBits;
 constexpr int kSlotRunSteps = (1 << kSlotTagBits) - 1;
