@@ -667,53 +667,64 @@ template <int DT, int DPL, int NH, int HR, int SL>
 __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
     constexpr int NQR = (NH * kWave * DPL + kThreads - 1) / kThreads;
     __shared__ PersistLds<NH, DPL> s;
-    // a wait of an earlier step of this generate call timed out: its results are void, and
-    // every later step ends at once instead of timing out again
-    if (*a.err != 0) return;
-    if (a.done && *a.done) return;                 // the sequence has stopped
-    if (threadIdx.x == 0) s.flag = 0;
-    const int H = a.H, nq = NH * a.hd;
+    // Every load the start needs goes out at once: each check below that returns would
+    // otherwise hold the next load back by a memory round trip.
+    const int lane0 = threadIdx.x & (kWave - 1);
+    const int err0 = *a.err;
+    const int done0 = a.done ? *a.done : 0;
     int tok, pos;
-    uint32_t seq;
+    uint32_t seq, st = 0;
+    unsigned long long key = 0;
     if (a.slots) {
-        // the previous step's LM head left its greedy key in the slots (none before a run's
-        // first step): every workgroup decodes the same token; workgroup 0 logs it
-        // (inference.c:297) and, on a stop token (inference.c:298-301), marks the sequence done,
-        // and every workgroup returns
-        TokenSlots &ts = *a.slots;
-        const uint32_t st = ts.a;
+        const TokenSlots &ts = *a.slots;
+        st = ts.a;
+        static_assert(kSlotCount == kWave, "one slot per lane");
+        key = ts.key[lane0];                       // lane l reads slot l
         tok = ts.tok0;
         pos = ts.pos0 + (int)st;
         seq = ts.seq0 + st;
-        if (st > 0) {
-            // lane l reads slot l; the wave's maximum by 64-bit shuffles (no LDS, no barrier)
-            static_assert(kSlotCount == kWave, "one slot per lane");
-            const int lane = threadIdx.x & (kWave - 1);
-            unsigned long long k = ts.key[lane];
-#pragma unroll
-            for (int mask = 1; mask < kWave; mask <<= 1) {
-                const uint32_t lo = __shfl_xor((uint32_t)k, mask, kWave), hi = __shfl_xor((uint32_t)(k >> 32), mask, kWave);
-                const unsigned long long o = ((unsigned long long)hi << 32) | lo;
-                k = o > k ? o : k;
-            }
-            if (!slot_token(k, st, a.vocab, tok)) {
-                if (threadIdx.x == 0) atomicAdd(a.err, 1);
-                return;
-            }
-            const bool stop = a.stop.has(tok);
-            if (blockIdx.x == 0 && threadIdx.x == 0) {
-                a.log[ts.logbase + (int)st - 1] = tok;
-                if (stop) *a.done = 1;
-            }
-            if (stop) return;
-        }
-        // nothing in this launch reads b; the LM head after it tags its keys with it
-        if (blockIdx.x == 0 && threadIdx.x == 0) ts.b = st + 1u;
     } else {
         tok = a.state[0];
         pos = a.state[1];
         seq = *a.seq;
     }
+    {   // the layer descriptors into LDS (they do not depend on the token)
+        static_assert(sizeof(PLayer) % 4 == 0, "descriptors copied as words");
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.layers);
+        uint32_t *dst = s.layer_words;
+        const int nw = a.n_layers * (int)(sizeof(PLayer) / 4);
+        for (int i = threadIdx.x; i < nw; i += kThreads) dst[i] = src[i];
+    }
+    // a wait of an earlier step of this generate call timed out: its results are void, and
+    // every later step ends at once instead of timing out again
+    if (err0 != 0) return;
+    if (done0) return;                             // the sequence has stopped
+    if (threadIdx.x == 0) s.flag = 0;
+    const int H = a.H, nq = NH * a.hd;
+    if (a.slots && st > 0) {
+        // the previous step's LM head left its greedy key in the slots (none before a run's
+        // first step): every workgroup decodes the same token (the wave's maximum by 64-bit
+        // shuffles, no LDS, no barrier); workgroup 0 logs it (inference.c:297) and, on a stop
+        // token (inference.c:298-301), marks the sequence done, and every workgroup returns
+#pragma unroll
+        for (int mask = 1; mask < kWave; mask <<= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)key, mask, kWave), hi = __shfl_xor((uint32_t)(key >> 32), mask, kWave);
+            const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+            key = o > key ? o : key;
+        }
+        if (!slot_token(key, st, a.vocab, tok)) {
+            if (threadIdx.x == 0) atomicAdd(a.err, 1);
+            return;
+        }
+        const bool stop = a.stop.has(tok);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            a.log[a.slots->logbase + (int)st - 1] = tok;
+            if (stop) *a.done = 1;
+        }
+        if (stop) return;
+    }
+    // nothing in this launch reads b; the LM head after it tags its keys with it
+    if (a.slots && blockIdx.x == 0 && threadIdx.x == 0) a.slots->b = st + 1u;
     const uint32_t base = seq * persist_epochs_per_step(a.n_layers);
     {   // sapphire_embed_lookup (transformer.c:347-365)
         const size_t row = embed_row(tok, a.vocab, H);
@@ -721,11 +732,6 @@ __global__ __launch_bounds__(kThreads) void dec_persist_kernel(PersistArgs a) {
             const float v = __uint_as_float((uint32_t)a.embed[row + i] << 16);
             s.resid[i] = a.es != 1.0f ? __fmul_rn(v, a.es) : v;
         }
-        static_assert(sizeof(PLayer) % 4 == 0, "descriptors copied as words");
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.layers);
-        uint32_t *dst = s.layer_words;
-        const int nw = a.n_layers * (int)(sizeof(PLayer) / 4);
-        for (int i = threadIdx.x; i < nw; i += kThreads) dst[i] = src[i];
         // the stages' layer-invariant geometry
         CombGeom cg;
         comb_geom(cg, s.comb_off, NH, a.hd);
