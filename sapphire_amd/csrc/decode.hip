@@ -964,13 +964,14 @@ bool qkv_attention_fusable(int dt, int K, const AttnArgs &a) {
 int dec_qkv_attention(int dt, const void *w, int M, int K, const GemmIn &in, void *ws, uint64_t *tagged,
                       const AttnArgs &a, const uint32_t *epoch, int layer, int spin_limit, int *err, float *out,
                       hipStream_t s) {
+    // the tags are (step counter << 6) + layer + 1, so at most 63 layers
     if (!qkv_attention_fusable(dt, K, a) || !tagged || !epoch || !err || layer < 0 || layer > 62) {
         set_error("fused QKV + attention: unsupported shape");
         return -1;
     }
     QkvAttnArgs q;
     if (plan_gemm_tiled(dt, w, M, K, a.batch, in, ws, s, &q.P) != 0) return -1;
-    if (q.P.nw != kAttnThreadsBatch / kWave || q.P.mode != 1 || q.P.nsplit != 1) {
+    if (q.P.nw != kAttnThreadsBatch / kWave || q.P.mode != gemmb::kStagePrepared || q.P.nsplit != 1) {
         set_error("fused QKV + attention: the QKV GEMM's launch form does not fit");
         return -1;
     }

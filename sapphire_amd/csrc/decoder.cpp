@@ -531,7 +531,7 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
             if (dec_kv_write(at, s) != 0) return -1;
             at.kv_written = true;
             if (dec_attention(at, r.attn, s) != 0) return -1;
-        } else if (d->fuse_qkv_attn && r.tqkv && qkv_attention_fusable(c.wdtype, H, at)) {
+        } else if (d->fuse_qkv_attn && r.tqkv && l <= 62 && qkv_attention_fusable(c.wdtype, H, at)) {
             // one launch: the attention workgroups stream their K/V rows while the GEMM runs
             if (dec_qkv_attention(c.wdtype, L.t_qkv, nqkv, H, qi, r.gws, r.tqkv, at, r.epoch, l, kPersistSpinLimit,
                                   r.err, r.attn, s) != 0)
