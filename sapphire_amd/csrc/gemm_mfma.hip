@@ -39,6 +39,7 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
     __shared__ float npart[kBatchMax][8];
     __shared__ float rinv[kBatchMax];
     __shared__ float wmx[kPrepThreads / kWave];
+    __shared__ float wsq[kPrepThreads / kWave];
     __shared__ int wflag[kPrepThreads / kWave];
     const int seq = blockIdx.x, chunk = blockIdx.y, p = threadIdx.x;
     const int lane = p & (kWave - 1), wid = p / kWave;
@@ -90,13 +91,22 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
         dst[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
     if (in.w_norm) {
-        __syncthreads();                               // raw may still be read by the delta norm
+        // The pre-norm's sum of squares as a tree over every thread's eight values: one wave
+        // sum each (lane 0's), then the waves in a fixed order, with no staging through LDS and
+        // no K/8-long chain. Its last bits differ from the reference's eight-lane order, inside
+        // the decode tolerance; the residual above keeps that order and stays bit-identical.
+        float sq = 0.f;
         if (on)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) raw[p * 8 + e] = v[e];
+            for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(v[e], v[e], sq);
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
+        if (lane == 0) wsq[wid] = sq;
         __syncthreads();
-        rows_rms_inv<36>(raw, kRawLd, K, 1, in.eps, npart, rinv);
-        const float r = rinv[0];
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < kPrepThreads / kWave; ++w) tot += wsq[w];
+        const float r = devmath::rms_inv_of(tot, K, in.eps);
         if (on)
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, wn[e]));
