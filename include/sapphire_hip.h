@@ -122,6 +122,9 @@ int sapphire_gemm_q_greedy_dev(int dtype, const void *w_tiled, int M, int K, con
  *   input = rmsnorm_delta(h, w_norm) when w_norm is set, else h
  * (the residual of attention.c:356-366 / transformer.c:231-239 and the pre-norms of
  * attention.c:316-325 / transformer.c:119-121; rmsnorm_delta of normalization.c:104-117).
+ * The residual's norm sums its squares in the reference's order (sum_sq_avx2,
+ * normalization.c:12-32), so resid_out is the reference's bit for bit; the pre-norm's sum is a
+ * tree over the row, whose last bits may differ from that order.
  * The norms need whole rows: K <= 1152 when w_delta or w_norm is set. Output: with
  * out.parts set, the K chunks' partial sums are left in parts[c][b][M] (c < the number
  * sapphire_gemm_splits(K) returns) for the next call's input; else y[b * ldy + r]. With

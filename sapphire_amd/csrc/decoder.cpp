@@ -490,6 +490,7 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         qi.ldx = H;
         qi.w_norm = L.n_attn;
         qi.eps = c.eps;
+        qi.tree_norms = true;           // both norms as trees (the decode tolerance)
         if (l > 0) {
             // the previous down projection's K-chunk partial sums, added in chunk order by the
             // GEMM's input pass
@@ -561,6 +562,7 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
         fi.ldr = H;
         fi.w_norm = L.n_ffn;
         fi.eps = c.eps;
+        fi.tree_norms = true;           // both norms as trees (the decode tolerance)
         cur = 1 - cur;
         GemmOut fo;
         fo.y = r.g;
@@ -634,6 +636,7 @@ int enqueue_step_batch(sapphire_decoder *d) {
     li.w_delta = d->layers[c.n_layers - 1].n_ffn_post;
     li.w_norm = d->norm_final;
     li.eps = c.eps;
+    li.tree_norms = true;
     GemmOut lo;
     if (d->temperature <= 0.0f && !d->graph_logits && gemm_splits(H) == 1) {
         // greedy tokens straight from the LM-head GEMM: no logits written or read again

@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
     __shared__ float npart[kBatchMax][8];
     __shared__ float rinv[kBatchMax];
     __shared__ float wmx[kPrepThreads / kWave];
-    __shared__ float wsq[kPrepThreads / kWave];
+    __shared__ float wsq[2][kPrepThreads / kWave];
     __shared__ int wflag[kPrepThreads / kWave];
     const int seq = blockIdx.x, chunk = blockIdx.y, p = threadIdx.x;
     const int lane = p & (kWave - 1), wid = p / kWave;
@@ -47,6 +47,23 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
     const int pairs = (b1 - b0) * 4, kb = b0 * kBlock;
     const bool on = p < pairs;
     PrepChunk &pc = prep[chunk];
+    // 1 / rms of this sequence's K values, summed as a tree: each thread's eight squares, one
+    // wave sum each (lane 0's), then the waves in a fixed order (slot: which of the two norms,
+    // so that the second does not overwrite sums the first may still be reading)
+    auto tree_rms_inv = [&](const float (&x)[8], int slot) {
+        float sq = 0.f;
+        if (p < pairs)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(x[e], x[e], sq);
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
+        if (lane == 0) wsq[slot][wid] = sq;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < kPrepThreads / kWave; ++w) tot += wsq[slot][w];
+        return devmath::rms_inv_of(tot, K, in.eps);
+    };
     float v[8], xv[8], wd[8], wn[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = xv[e] = wd[e] = wn[e] = 0.f;
@@ -71,12 +88,17 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
                     for (int e = 0; e < 8; ++e) v[e] = __fadd_rn(v[e], t[c][e]);
         }
         if (in.w_delta) {
-            if (on)
+            float r;
+            if (in.tree_norms) {
+                r = tree_rms_inv(v, 0);
+            } else {
+                if (on)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) raw[p * 8 + e] = v[e];
-            __syncthreads();
-            rows_rms_inv<36>(raw, kRawLd, K, 1, in.eps, npart, rinv);
-            const float r = rinv[0];
+                    for (int e = 0; e < 8; ++e) raw[p * 8 + e] = v[e];
+                __syncthreads();
+                rows_rms_inv<36>(raw, kRawLd, K, 1, in.eps, npart, rinv);
+                r = rinv[0];
+            }
             if (on)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, wd[e]));
@@ -91,22 +113,11 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
         dst[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
     if (in.w_norm) {
-        // The pre-norm's sum of squares as a tree over every thread's eight values: one wave
-        // sum each (lane 0's), then the waves in a fixed order, with no staging through LDS and
-        // no K/8-long chain. Its last bits differ from the reference's eight-lane order, inside
-        // the decode tolerance; the residual above keeps that order and stays bit-identical.
-        float sq = 0.f;
-        if (on)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(v[e], v[e], sq);
-#pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
-        if (lane == 0) wsq[wid] = sq;
-        __syncthreads();
-        float tot = 0.f;
-#pragma unroll
-        for (int w = 0; w < kPrepThreads / kWave; ++w) tot += wsq[w];
-        const float r = devmath::rms_inv_of(tot, K, in.eps);
+        // The pre-norm's sum of squares as a tree (tree_rms_inv: no staging through LDS and no
+        // K/8-long chain). Its last bits differ from the reference's eight-lane order, inside
+        // the decode tolerance; the residual above keeps that order (unless tree_norms is set)
+        // and stays bit-identical.
+        const float r = tree_rms_inv(v, 1);
         if (on)
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], r), __fadd_rn(1.0f, wn[e]));

@@ -174,6 +174,10 @@ struct GemmIn {
     // x in block order (block_order_index; ldx unused): only with neither parts, norms nor
     // resid_out
     bool x_blocked = false;
+    // the delta norm's sum of squares as a tree over all threads too, not in the reference's
+    // eight-lane order (resid_out then differs from it in the last bits, inside the decode
+    // tolerance); the decoder's own steps set it
+    bool tree_norms = false;
 };
 // Output of a batched GEMM. parts set: the K chunks' partial sums go to parts[c][b][M] (an
 // input of the next GEMM's GemmIn), nothing else is written. geglu: the weight rows are
