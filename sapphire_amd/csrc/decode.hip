@@ -74,9 +74,9 @@ __global__ __launch_bounds__(kThreads) void dec_gemv_kernel(QMat w0, QMat w1, Ge
     float p1 = 0.f;
     if constexpr (GEGLU) p1 = block_value<DT>(b1, xv, xsum);
     for (int r = 0; r < rps; ++r) {
-        const float t0 = wave_sum(r_in == r ? p0 : 0.f);
+        const float t0 = xor_sum(r_in == r ? p0 : 0.f);
         float v = t0;
-        if constexpr (GEGLU) v = __fmul_rn(gelu_ref(t0), wave_sum(r_in == r ? p1 : 0.f));
+        if constexpr (GEGLU) v = __fmul_rn(gelu_ref(t0), xor_sum(r_in == r ? p1 : 0.f));
         const int orow = st * rps + r;
         if (lane == r && orow < M) y[orow] = v;
     }
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(NT) void dec_attn_part_kernel(AttnArgs a) {
                     float dp = 0.f;
 #pragma unroll
                     for (int d = 0; d < DPL; ++d) dp = __builtin_fmaf(qr[h][d], kr[j0 + jj][hk][d], dp);
-                    sc[jj][h] = j0 + jj < nj ? __fmul_rn(wave_sum_uniform(dp), sl2) : -INFINITY;
+                    sc[jj][h] = j0 + jj < nj ? __fmul_rn(lanes::wave_sum(dp), sl2) : -INFINITY;
                 }
 #pragma unroll
             for (int h = 0; h < NH; ++h) {
@@ -591,7 +591,7 @@ __device__ __forceinline__ void attn_lds_body(AttnLds<DPL, NH, NKV, PBMAX> &L, i
                     float dp = 0.f;
 #pragma unroll
                     for (int d = 0; d < DPL; ++d) dp = __builtin_fmaf(qr[h][d], kp[lane * DPL + d], dp);
-                    sc[jj][h] = j0 + jj < nj ? __fmul_rn(wave_sum_uniform(dp), sl2) : -INFINITY;
+                    sc[jj][h] = j0 + jj < nj ? __fmul_rn(lanes::wave_sum(dp), sl2) : -INFINITY;
                 }
             }
 #pragma unroll
@@ -738,11 +738,9 @@ __global__ __launch_bounds__(kThreads) void dec_attn_combine_kernel(const float 
     const int d = t;                                     // head_dim <= 256 = one dim per thread
 #pragma unroll
     for (int b = 0; b < NS; ++b) o[b] = d < hd ? ph[b * hs + d] : 0.f;
-    float M = mb;
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
+    const float M = lanes::wave_max(mb);
     const float e = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
-    const float inv = 1.0f / wave_sum(e * sb);
+    const float inv = 1.0f / lanes::wave_sum(e * sb);
     float O = 0.f;
 #pragma unroll
     for (int b = 0; b < NS; ++b) O = __builtin_fmaf(o[b], lane_value(e, b), O);

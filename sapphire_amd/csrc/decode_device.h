@@ -20,7 +20,8 @@ constexpr int kWave = 64;
 constexpr int kThreads = 256;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_sum(float v) {
+// Sum over the 64 lanes of a wave by an xor butterfly (the multi-launch GEMV's row sums).
+__device__ __forceinline__ float xor_sum(float v) {
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
     return v;
@@ -28,13 +29,6 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float lane_value(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
-// Sum over the 64 lanes of a wave as a wave-uniform value: row sums by DPP, then the four
-// rows added in a fixed order.
-__device__ __forceinline__ float wave_sum_uniform(float v) {
-    v = row16_sum(v);
-    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 // One hd-long fp32 row (hd = 64 DPL) from global memory into LDS by DMA (no VGPRs): the

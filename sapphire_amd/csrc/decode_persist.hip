@@ -184,7 +184,7 @@ struct Gather {
             }
         }
         if (sq) {
-            acc = wave_sum_uniform(acc);
+            acc = lanes::wave_sum(acc);
             if ((threadIdx.x & (kWave - 1)) == 0) sq[threadIdx.x / kWave] = acc;
         }
         __syncthreads();
@@ -245,7 +245,7 @@ struct VecRegs {
 __device__ __forceinline__ float par_sum_sq(const float *v, int K, float *sh) {
     float acc = 0.f;
     for (int i = threadIdx.x; i < K; i += kThreads) acc = __builtin_fmaf(v[i], v[i], acc);
-    acc = wave_sum_uniform(acc);
+    acc = lanes::wave_sum(acc);
     if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = acc;
     __syncthreads();
     return (sh[0] + sh[1]) + (sh[2] + sh[3]);
@@ -287,7 +287,7 @@ __device__ __forceinline__ void add_norm_delta_norm(float *resid, float *xs, con
             acc = __builtin_fmaf(nv[e], nv[e], acc);
         }
     }
-    acc = wave_sum_uniform(acc);
+    acc = lanes::wave_sum(acc);
     if ((threadIdx.x & (kWave - 1)) == 0) sh[4 + threadIdx.x / kWave] = acc;
     __syncthreads();
     const float r2 = rms_inv_of((sh[4] + sh[5]) + (sh[6] + sh[7]), K, eps);
@@ -511,7 +511,7 @@ struct AttnStage {
             float acc = 0.f;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) acc = __builtin_fmaf(xv[v][i], xv[v][i], acc);
-            const float r = rms_inv_of(wave_sum_uniform(acc), hd, a.eps);
+            const float r = rms_inv_of(lanes::wave_sum(acc), hd, a.eps);
 #pragma unroll
             for (int i = 0; i < DPL; ++i) {
                 const float g = v == 0 ? gq[i] : gk[i];
@@ -563,7 +563,7 @@ struct AttnStage {
                     float dp = 0.f;
 #pragma unroll
                     for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qk[0][i], kr[i], dp);
-                    const float score = __fmul_rn(wave_sum_uniform(dp), sl2);
+                    const float score = __fmul_rn(lanes::wave_sum(dp), sl2);
                     const float mn = fmaxf(m, score);
                     const float c = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
                     const float p = __builtin_amdgcn_exp2f(score - mn);

@@ -55,8 +55,7 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
         if (p < pairs)
 #pragma unroll
             for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(x[e], x[e], sq);
-#pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
+        sq = lanes::wave_sum(sq);
         if (lane == 0) wsq[slot][wid] = sq;
         __syncthreads();
         float tot = 0.f;
@@ -135,8 +134,7 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
         v[e] = nonfinite::is_nf(t) ? 0.f : t;
         mx = fmaxf(mx, fabsf(v[e]));
     }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    mx = lanes::wave_max(mx);
     const bool wnan = __any(nan) != 0, wnf = __any(nan || pinf != 0 || ninf != 0) != 0;
     if (lane == 0) {
         wmx[wid] = mx;
@@ -145,10 +143,8 @@ __global__ __launch_bounds__(kPrepThreads) void gemm_prep_kernel(GemmIn in, int 
     // the four pairs of a block sit in threads 4 bl .. 4 bl + 3
     pinf <<= 8 * (p & 3);
     ninf <<= 8 * (p & 3);
-    pinf |= __shfl_xor(pinf, 1, kWave);
-    ninf |= __shfl_xor(ninf, 1, kWave);
-    pinf |= __shfl_xor(pinf, 2, kWave);
-    ninf |= __shfl_xor(ninf, 2, kWave);
+    pinf = lanes::quad_or(pinf);
+    ninf = lanes::quad_or(ninf);
     if (on && (p & 3) == 0) {
         pc.inf[seq][0][p >> 2] = pinf;
         pc.inf[seq][1][p >> 2] = ninf;

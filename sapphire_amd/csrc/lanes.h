@@ -1,5 +1,5 @@
-// lanes.h - cross-lane sums and maxima over rows of 16 lanes by DPP (shared by the GEMV and
-// decode kernels; not installed).
+// lanes.h - cross-lane sums and maxima by DPP over rows of 16 lanes and whole waves (shared by
+// the GEMV, GEMM and decode kernels; not installed).
 #pragma once
 
 namespace sapphire {
@@ -28,6 +28,37 @@ __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, dpp_mov<0x4E>(v));
     v = fmaxf(v, dpp_mov<0x141>(v));
     v = fmaxf(v, dpp_mov<0x140>(v));
+    return v;
+}
+
+// Sum over the 64 lanes of a wave, the same bits in every lane: row16_sum, then the four
+// rows' sums (read from lanes 0, 16, 32, 48) added as a pair of pairs.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Maximum over the 64 lanes of a wave, in every lane (as wave_sum).
+__device__ __forceinline__ float wave_max(float v) {
+    v = row16_max(v);
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Bitwise OR over each quad of lanes (4 q .. 4 q + 3), left in every lane of the quad:
+// quad_perm [1,0,3,2], then [2,3,0,1].
+__device__ __forceinline__ uint32_t quad_or(uint32_t v) {
+    v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
     return v;
 }
 
