@@ -78,6 +78,9 @@ struct sapphire_decoder {
     int *log = nullptr;     // [max_ctx] tokens of the steps; batched: [max_ctx][B]
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // kMultiSteps steps captured back to back (calls that take no logits), and their form
+    hipGraph_t graph_multi = nullptr;
+    hipGraphExec_t exec_multi = nullptr;
     // whether the captured step writes the logits: a greedy batched step that returns no
     // logits picks its tokens inside the LM-head GEMM instead
     bool graph_logits = true;
@@ -272,6 +275,9 @@ bool tiled_shapes_ok(const sapphire_decoder_config_t &c) {
 constexpr int kPersistSpinLimit = 1 << 19;
 // the batched step counter's range (tags are counter << 6 | layer + 1 in 32 bits)
 constexpr uint64_t kBatchEpochLimit = uint64_t(1) << 26;
+// steps per launch of the persistent step's multi-step graph (each graph launch costs the GPU a
+// gap of its own: 0.384 -> 0.380 ms per token)
+constexpr int kMultiSteps = 8;
 int batch_qkv_width(const sapphire_decoder_config_t &c) { return (c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
 
 // Per sequence 1 once it has logged a stop token (the state's last B words).
@@ -680,6 +686,17 @@ bool valid_config(const sapphire_decoder_config_t &c) {
     return true;
 }
 
+// Drops the captured step graphs (one step and kMultiSteps steps): the next generate captures
+// them again with the decoder's current form, sampling and stop set.
+void drop_step_graphs(sapphire_decoder *d) {
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    if (d->exec_multi) (void)hipGraphExecDestroy(d->exec_multi);
+    if (d->graph_multi) (void)hipGraphDestroy(d->graph_multi);
+    d->exec = d->exec_multi = nullptr;
+    d->graph = d->graph_multi = nullptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -688,8 +705,7 @@ void sapphire_decoder_destroy(sapphire_decoder_t *d) {
     if (!d) return;
     (void)hipSetDevice(d->device);
     if (d->stream) (void)hipStreamSynchronize(d->stream);
-    if (d->exec) (void)hipGraphExecDestroy(d->exec);
-    if (d->graph) (void)hipGraphDestroy(d->graph);
+    drop_step_graphs(d);
     for (hipGraphExec_t e : d->pf_exec)
         if (e) (void)hipGraphExecDestroy(e);
     for (hipGraph_t g : d->pf_graph)
@@ -1093,27 +1109,31 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
     }
     SPH_CHECK(hipSetDevice(d->device));
     const bool want_logits = logits_out != nullptr || B == 1;
-    if (d->exec && d->graph_logits != want_logits) {
-        // the step's LM head changes form: capture again
-        (void)hipGraphExecDestroy(d->exec);
-        (void)hipGraphDestroy(d->graph);
-        d->exec = nullptr;
-        d->graph = nullptr;
-    }
-    if (!d->exec) {
-        d->graph_logits = want_logits;
-        d->graph_slots = B == 1 && use_token_slots(d);
+    if (d->exec && d->graph_logits != want_logits) drop_step_graphs(d);   // the LM head changes form
+    // n steps back to back as one graph (every step's state lives on the device)
+    auto capture = [&](int n, hipGraph_t *graph, hipGraphExec_t *exec) -> int {
         SPH_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = B == 1 ? enqueue_step(d) : enqueue_step_batch(d);
+        int rc = 0;
+        for (int i = 0; i < n && rc == 0; ++i) rc = B == 1 ? enqueue_step(d) : enqueue_step_batch(d);
         hipGraph_t g = nullptr;
         const hipError_t e = hipStreamEndCapture(d->stream, &g);
         if (rc != 0 || !hip_ok(e, "hipStreamEndCapture")) {
             if (g) (void)hipGraphDestroy(g);
             return -1;
         }
-        d->graph = g;
-        SPH_CHECK(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
+        *graph = g;
+        SPH_CHECK(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
+        return 0;
+    };
+    if (!d->exec) {
+        d->graph_logits = want_logits;
+        d->graph_slots = B == 1 && use_token_slots(d);
+        if (capture(1, &d->graph, &d->exec) != 0) return -1;
     }
+    // a persistent-form call that takes no logits runs its steps kMultiSteps to a launch where
+    // it can (a batched step's graph of ~190 kernels measured slower captured eight times over)
+    const bool multi = logits_out == nullptr && B == 1 && d->groups > 0 && steps >= kMultiSteps;
+    if (multi && !d->exec_multi && capture(kMultiSteps, &d->graph_multi, &d->exec_multi) != 0) return -1;
     // state: token, position, step (one sequence) or tokens[B], positions[B], step; every done
     // flag clear
     std::vector<int> st((size_t)3 * B + 2, 0);
@@ -1169,13 +1189,17 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         SPH_CHECK(hipEventRecord(e0, d->stream));
     }
     const size_t lstep = (size_t)B * c.vocab;
-    for (int s = 0; s < steps; ++s) {
-        SPH_CHECK(hipGraphLaunch(d->exec, d->stream));
+    for (int s = 0; s < steps;) {
+        // kMultiSteps at once where they fit in the call and (token slots) inside one run
+        const bool many = multi && s + kMultiSteps <= steps &&
+                          (!d->graph_slots || s % d->slot_run + kMultiSteps <= d->slot_run);
+        SPH_CHECK(hipGraphLaunch(many ? d->exec_multi : d->exec, d->stream));
         if (logits_out)
             SPH_CHECK(hipMemcpyAsync(logits_out + (size_t)s * lstep, d->logits, sizeof(float) * lstep,
                                      hipMemcpyDeviceToHost, d->stream));
+        s += many ? kMultiSteps : 1;
         // token slots: a run's last token is logged after its last step
-        if (d->graph_slots && ((s + 1) % d->slot_run == 0 || s + 1 == steps) &&
+        if (d->graph_slots && (s % d->slot_run == 0 || s == steps) &&
             launch_token_slots_settle(d->tslots, c.vocab, d->log, done_flags(d), d->stop, d->perr, d->stream) != 0)
             return -1;
     }
@@ -1215,10 +1239,7 @@ int sapphire_decoder_set_workgroups(sapphire_decoder_t *d, int groups) {
     }
     if (groups == d->groups) return 0;
     SPH_CHECK(hipStreamSynchronize(d->stream));
-    if (d->exec) (void)hipGraphExecDestroy(d->exec);
-    if (d->graph) (void)hipGraphDestroy(d->graph);
-    d->exec = nullptr;
-    d->graph = nullptr;
+    drop_step_graphs(d);
     d->groups = groups;
     return 0;
 }
@@ -1288,10 +1309,7 @@ int sapphire_decoder_set_sampling(sapphire_decoder_t *d, float temperature, cons
     d->n_draws = t > 0.0f ? n_draws : 0;
     if (t != d->temperature) {
         // the step's kernels (and the temperature in their arguments) change: capture again
-        if (d->exec) (void)hipGraphExecDestroy(d->exec);
-        if (d->graph) (void)hipGraphDestroy(d->graph);
-        d->exec = nullptr;
-        d->graph = nullptr;
+        drop_step_graphs(d);
         d->temperature = t;
     }
     return 0;
@@ -1314,10 +1332,7 @@ int sapphire_decoder_set_stop_tokens(sapphire_decoder_t *d, const int *ids, int 
     SPH_CHECK(hipSetDevice(d->device));
     SPH_CHECK(hipStreamSynchronize(d->stream));
     // the set is an argument of the step's advance: capture again
-    if (d->exec) (void)hipGraphExecDestroy(d->exec);
-    if (d->graph) (void)hipGraphDestroy(d->graph);
-    d->exec = nullptr;
-    d->graph = nullptr;
+    drop_step_graphs(d);
     d->stop = st;
     return 0;
 }

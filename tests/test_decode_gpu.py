@@ -365,6 +365,48 @@ def test_decode_token_slots_across_runs(oracle, monkeypatch, run, stop_at):
         dec.close()
 
 
+@pytest.mark.parametrize("run,stop_at", [(None, None), (None, 5), (10, None), (10, 12)],
+                         ids=["default_run", "stop5", "run10", "run10_stop12"])
+def test_decode_multi_step_graph(oracle, monkeypatch, run, stop_at):
+    """A persistent-form call that takes no logits launches its steps eight to a graph, where
+    the eight fit in the call and inside one token-slot run, and the others one at a time. A
+    21-step call (8 + 8 + 5 single steps; with runs of 10 steps, 8 + 1 + 1 per run) decodes the
+    oracle's tokens and K/V rows, also with a stop token inside an eight-step launch."""
+    from sapphire_amd.engine import Decoder
+    cfg, seed, prefill, steps = smodel.TINY, 39, 30, 21
+    if run is not None:
+        monkeypatch.setenv("SAPPHIRE_TOKEN_SLOT_RUN", str(run))
+    m = smodel.synthetic_model(cfg, seed)
+    k0, v0 = m.kv_prefill(prefill)
+    tok = smodel.start_token(cfg, seed)
+    k, v = k0.copy(), v0.copy()
+    ref_toks, _ = oracle_decode(oracle, m, k, v, tok, prefill, steps, nthreads=4)
+    stops = []
+    if stop_at is not None:
+        # a token that first appears at stop_at (every token of this seed's 21 differs)
+        assert ref_toks[stop_at] not in ref_toks[:stop_at], ref_toks
+        stops = [int(ref_toks[stop_at])]
+    n = steps if stop_at is None else stop_at + 1
+    dec = Decoder(m)
+    try:
+        assert dec.workgroups > 0
+        dec.set_stop_tokens(stops)
+        for _ in range(2):                  # the second call replays the captured graphs
+            dec.set_kv(k0, v0)
+            got, _, _ = dec.generate(tok, prefill, steps)
+            print(f"run {run}, stop {stop_at}: tokens {got.tolist()}", flush=True)
+            assert list(got[:n]) == list(ref_toks[:n])
+            assert np.all(got[n:] == -1)
+            gk, gv = dec.get_kv()
+            sl = slice(prefill, prefill + n)
+            for name, g, r in (("K", gk, k), ("V", gv, v)):
+                d = np.abs(g[:, :, sl] - r[:, :, sl]).max() / np.abs(r[:, :, sl]).max()
+                assert d <= REL, f"{name} cache rows differ: {d:.2e}"
+            assert np.array_equal(gk[:, :, prefill + n:], k0[:, :, prefill + n:])
+    finally:
+        dec.close()
+
+
 def test_decode_repeatable(oracle):
     """Two generate calls on one decoder (the captured graph is replayed, the state reset)."""
     from sapphire_amd.engine import Decoder
