@@ -84,6 +84,9 @@ struct sapphire_decoder {
     // whether the captured step writes the logits: a greedy batched step that returns no
     // logits picks its tokens inside the LM-head GEMM instead
     bool graph_logits = true;
+    // batched: the captured step ends by looking up the next step's input rows (and does not
+    // look up its own)
+    bool graph_embeds_next = false;
     // batched decoder
     int batch = 1;
     float *dparts = nullptr;     // the down projection's K-chunk partial sums [splits][B][hidden]
@@ -474,6 +477,7 @@ struct BatchRun {
     uint64_t *tqkv = nullptr;
     const uint32_t *epoch = nullptr;
     int *err = nullptr;
+    bool embedded = false;                // resid[0] already holds the tokens' embeddings
 };
 
 int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
@@ -486,7 +490,7 @@ int enqueue_layers_batch(sapphire_decoder *d, const BatchRun &r) {
     const int win = c.sliding_window > 0 ? c.sliding_window : 1024;
     const size_t layer_kv = (size_t)c.n_kv_heads * c.max_ctx * hd;
     const int nsd = gemm_splits(c.ffn);
-    if (dec_embed_batch(d->embed, H, c.vocab, es, r.d_tokens, B, r.resid[0], s) != 0) return -1;
+    if (!r.embedded && dec_embed_batch(d->embed, H, c.vocab, es, r.d_tokens, B, r.resid[0], s) != 0) return -1;
     int cur = 0;
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer &L = d->layers[l];
@@ -612,6 +616,12 @@ int enqueue_step_batch(sapphire_decoder *d) {
     r.tqkv = d->tqkv;
     r.epoch = d->bepoch;
     r.err = d->perr;
+    // the greedy GEMM form's finish looks up the next step's input rows: the step starts
+    // from them (generate looks up the first step's before the first launch)
+    const bool greedy_gemm =
+        c.lm_dtype != DT_BF16 && d->temperature <= 0.0f && !d->graph_logits && gemm_splits(H) == 1;
+    r.embedded = greedy_gemm;
+    d->graph_embeds_next = greedy_gemm;
     const int cur = enqueue_layers_batch(d, r);
     if (cur < 0) return -1;
     // last finalize + final norm (transformer.c:400-406), LM head, greedy tokens
@@ -644,12 +654,23 @@ int enqueue_step_batch(sapphire_decoder *d) {
     li.eps = c.eps;
     li.tree_norms = true;
     GemmOut lo;
-    if (d->temperature <= 0.0f && !d->graph_logits && gemm_splits(H) == 1) {
-        // greedy tokens straight from the LM-head GEMM: no logits written or read again
+    if (greedy_gemm) {
+        // greedy tokens straight from the LM-head GEMM: no logits written or read again; its
+        // finish launch also advances the step and looks up the next step's input rows
+        BatchAdvance adv;
+        adv.pos = d->state + B;
+        adv.step = d->state + 2 * B;
+        adv.log = d->log;
+        adv.done = done_flags(d);
+        adv.epoch = d->bepoch;
+        adv.stop = d->stop;
+        adv.embed = d->embed;
+        adv.hidden = H;
+        adv.es = sqrtf((float)H);
+        adv.resid = d->resid[0];
         lo.tokens = d->state;
-        if (launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s) != 0) return -1;
-        return dec_advance_batch(d->state, d->state + B, d->state + 2 * B, B, d->log, done_flags(d), d->stop, d->bepoch,
-                             s);
+        lo.advance = &adv;
+        return launch_gemm_tiled_ex(c.lm_dtype, d->lm, c.vocab, H, B, li, lo, d->gws, s);
     }
     lo.y = d->logits;
     lo.ldy = c.vocab;
@@ -1188,6 +1209,10 @@ int sapphire_decoder_generate_batch(sapphire_decoder_t *d, const int *tokens, co
         SPH_CHECK(hipEventCreate(&e1));
         SPH_CHECK(hipEventRecord(e0, d->stream));
     }
+    // a batched step that ends by looking up the next step's input rows needs the first's
+    if (B > 1 && d->graph_embeds_next &&
+        dec_embed_batch(d->embed, c.hidden, c.vocab, sqrtf((float)c.hidden), d->state, B, d->resid[0], d->stream) != 0)
+        return -1;
     const size_t lstep = (size_t)B * c.vocab;
     for (int s = 0; s < steps;) {
         // kMultiSteps at once where they fit in the call and (token slots) inside one run

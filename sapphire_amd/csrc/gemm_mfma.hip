@@ -218,6 +218,60 @@ __global__ void gemm_greedy_finish_kernel(const float *__restrict__ part, int np
     if (threadIdx.x == 0) tokens[blockIdx.x] = bi >= 0 && bi < n ? bi : 0;
 }
 
+// grid 1, one wave per sequence: wave b picks sequence b's token from its nparts workgroup
+// partials (as gemm_greedy_finish_kernel), then the step ends as BatchAdvance describes. Every
+// wave reads the step counter before the barrier, and thread 0 advances it after.
+__global__ __launch_bounds__(kBatchMax *kWave) void gemm_greedy_finish_advance_kernel(
+    const float *__restrict__ part, int nparts, int n, int *__restrict__ tokens, int batch, BatchAdvance a) {
+    const int b = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    const int s = *a.step;
+    const float *p = part + (size_t)b * nparts * 2;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int j = lane; j < nparts; j += kWave) {
+        const float v = p[2 * j];
+        const int i = __float_as_int(p[2 * j + 1]);
+        if (devmath::greedy_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    // rows of 16 lanes by DPP, then the four rows' bests in row order (a total order: every
+    // order of the comparisons picks the same pair)
+    lanes::row16_best(bv, bi, devmath::greedy_better);
+    float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 0));
+    int i = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+    for (int r = 16; r < kWave; r += 16) {
+        const float ov = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), r));
+        const int oi = __builtin_amdgcn_readlane(bi, r);
+        if (devmath::greedy_better(ov, oi, v, i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+    const int t = i >= 0 && i < n ? i : 0;
+    if (lane == 0) {
+        tokens[b] = t;
+        if (!(a.done && a.done[b])) {               // a stopped sequence: its entry keeps the fill
+            a.log[(size_t)s * batch + b] = t;
+            a.pos[b] = a.pos[b] + 1;
+            if (a.done && a.stop.has(t)) a.done[b] = 1;   // inference.c:298-301
+        }
+    }
+    const uint16_t *row = a.embed + (size_t)t * a.hidden;
+    float *out = a.resid + (size_t)b * a.hidden;
+    for (int k = lane; k < a.hidden; k += kWave) {
+        const float x = __uint_as_float((uint32_t)row[k] << 16);
+        out[k] = a.es != 1.0f ? __fmul_rn(x, a.es) : x;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        *a.step = s + 1;
+        if (a.epoch) *a.epoch = *a.epoch + 1u;
+    }
+}
+
 // y[b * ldy + r] = sum over c of parts[c * stride + b * M + r], in chunk order.
 __global__ void sum_parts_kernel(const float *__restrict__ parts, int nparts, size_t stride, int batch, int M,
                                  float *__restrict__ y, int ldy) {
@@ -339,10 +393,12 @@ int gemm_pass(int dt, const void *w, int M, int K, int batch, const GemmIn &in, 
     hipLaunchKernelGGL(kern, dim3((unsigned)gx, (unsigned)nsplit), dim3(P.nw * kWave), 0, st, P.wq, P.q_bytes, P.wsc,
                        P.s_bytes, in, batch, M, K, P.cb, o, P.Yp, (const PrepChunk *)P.prep, P.ks);
     if (!hip_ok(hipGetLastError(), "gemm_mfma launch")) return -1;
-    if (o.tokens) {
+    if (o.tokens && o.advance)
+        hipLaunchKernelGGL(gemm_greedy_finish_advance_kernel, dim3(1), dim3(batch * kWave), 0, st, o.amax, gx, M,
+                           o.tokens, batch, *o.advance);
+    else if (o.tokens)
         hipLaunchKernelGGL(gemm_greedy_finish_kernel, dim3(batch), dim3(kWave), 0, st, o.amax, gx, M, o.tokens);
-        return hip_ok(hipGetLastError(), "greedy finish launch") ? 0 : -1;
-    }
+    if (o.tokens) return hip_ok(hipGetLastError(), "greedy finish launch") ? 0 : -1;
     if (nsplit > 1 && !out.parts) return launch_sum_parts(P.Yp, nsplit, (size_t)batch * M, batch, M, out.y, out.ldy, st);
     return 0;
 }
@@ -386,7 +442,9 @@ int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const G
                     (!out.geglu || (nsplit == 1 && M % 16 == 0 && !out.parts)) &&
                     (out.parts || nsplit == 1 || ((reinterpret_cast<uintptr_t>(ws) & 255u) == 0 && ws)) &&
                     (!in.x_blocked || (in.x && !in.parts && !norms && !in.resid_out)) &&
-                    (!out.y_blocked || (nsplit == 1 && !out.parts && out.y));
+                    (!out.y_blocked || (nsplit == 1 && !out.parts && out.y)) &&
+                    (!out.advance || (out.tokens && out.advance->pos && out.advance->step && out.advance->log &&
+                                      out.advance->embed && out.advance->resid && out.advance->hidden > 0));
     if (!ok) {
         set_error("batched GEMM: unsupported arguments (batch=%d M=%d K=%d nsplit=%d)", batch, M, K, nsplit);
         return -1;

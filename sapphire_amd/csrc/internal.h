@@ -183,6 +183,21 @@ struct GemmIn {
 // input of the next GEMM's GemmIn), nothing else is written. geglu: the weight rows are
 // interleaved by eight (gate rows 8i..8i+7, then the matching up rows) and
 // y[b * ldy + j] = gelu(gate_j) * up_j for j < M / 2 (transformer.c:141-157).
+// The batched step's end, done by the greedy LM head's finish launch (GemmOut.advance): for
+// every sequence b that has not stopped, log[step * batch + b] = tokens[b], pos[b] + 1 and
+// done[b] on a stop token, then step + 1 and epoch + 1 (dec_advance_batch's work); and for every
+// b, resid[b] = the bf16 embedding row of tokens[b] times es, the next step's input
+// (dec_embed_batch's work).
+struct BatchAdvance {
+    int *pos = nullptr, *step = nullptr, *log = nullptr, *done = nullptr;
+    uint32_t *epoch = nullptr;
+    StopSet stop{};
+    const uint16_t *embed = nullptr;
+    int hidden = 0;
+    float es = 1.0f;
+    float *resid = nullptr;
+};
+
 struct GemmOut {
     float *y = nullptr;
     int ldy = 0;
@@ -201,6 +216,9 @@ struct GemmOut {
     // workgroups' partials go to the workspace, which is then required.
     int *tokens = nullptr;
     float *amax = nullptr;   // set by the launch: the partials in the workspace
+    // greedy form: the step's advance and next input in the finish launch (host pointer, read
+    // by the launcher only; batch <= 16)
+    const BatchAdvance *advance = nullptr;
 };
 int launch_gemm_tiled_ex(int dt, const void *w, int M, int K, int batch, const GemmIn &in, const GemmOut &out,
                          void *ws, hipStream_t s);
