@@ -34,6 +34,7 @@
 #include <algorithm>
 
 #include "internal.h"
+#include "lanes.h"
 #include "nonfinite.h"
 
 namespace sapphire {
@@ -212,8 +213,30 @@ __device__ __forceinline__ SoftPart soft_merge(SoftPart a, SoftPart b) {
     return r;
 }
 
-__device__ __forceinline__ SoftPart soft_shfl_xor(SoftPart p, int mask) {
-    return SoftPart{__shfl_xor(p.m, mask, kWave), __shfl_xor(p.s, mask, kWave), __shfl_xor(p.i, mask, kWave)};
+template <int CTRL>
+__device__ __forceinline__ SoftPart soft_dpp(const SoftPart &p) {
+    return SoftPart{lanes::dpp_mov<CTRL>(p.m), lanes::dpp_mov<CTRL>(p.s),
+                    __float_as_int(lanes::dpp_mov<CTRL>(__int_as_float(p.i)))};
+}
+
+__device__ __forceinline__ SoftPart soft_lane(const SoftPart &p, int l) {
+    return SoftPart{__int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.m), l)),
+                    __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.s), l)), __builtin_amdgcn_readlane(p.i, l)};
+}
+
+// The merge of the wave's 64 partials, the same in every lane: rows of 16 lanes by DPP
+// (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror; each lane merges with a
+// partner that holds the same set, and soft_merge is commutative, so a row's lanes agree), then
+// the four rows' merges in row order.
+__device__ __forceinline__ SoftPart soft_wave_fold(SoftPart p) {
+    p = soft_merge(p, soft_dpp<0xB1>(p));
+    p = soft_merge(p, soft_dpp<0x4E>(p));
+    p = soft_merge(p, soft_dpp<0x141>(p));
+    p = soft_merge(p, soft_dpp<0x140>(p));
+    SoftPart r = soft_lane(p, 0);
+    r = soft_merge(r, soft_lane(p, 16));
+    r = soft_merge(r, soft_lane(p, 32));
+    return soft_merge(r, soft_lane(p, 48));
 }
 
 // sample_greedy's order (utils.c:145-156: best = 0, then every later strictly greater value)
@@ -229,10 +252,28 @@ __device__ __forceinline__ unsigned long long greedy_key(float v, int row) {
     return ((unsigned long long)u << 32) | (0xFFFFFFFFu - (uint32_t)row);
 }
 
-__device__ __forceinline__ unsigned long long key_max_shfl(unsigned long long k, int mask) {
-    const uint32_t lo = __shfl_xor((uint32_t)k, mask, kWave), hi = __shfl_xor((uint32_t)(k >> 32), mask, kWave);
-    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
-    return o > k ? o : k;
+template <int CTRL>
+__device__ __forceinline__ unsigned long long key_dpp(unsigned long long k) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ unsigned long long key_lane(unsigned long long k, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// The largest key of the wave, in every lane: rows of 16 lanes by DPP (as soft_wave_fold),
+// then the four rows' maxima.
+__device__ __forceinline__ unsigned long long key_wave_max(unsigned long long k) {
+    auto mx = [](unsigned long long a, unsigned long long b) { return a > b ? a : b; };
+    k = mx(k, key_dpp<0xB1>(k));
+    k = mx(k, key_dpp<0x4E>(k));
+    k = mx(k, key_dpp<0x141>(k));
+    k = mx(k, key_dpp<0x140>(k));
+    return mx(mx(key_lane(k, 0), key_lane(k, 16)), mx(key_lane(k, 32), key_lane(k, 48)));
 }
 
 // What tile_store needs for activations with NaN / inf elements (nf, wave-uniform): the
@@ -340,8 +381,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
         }
     }
     if constexpr (EP == kEpGreedyStep) {
-#pragma unroll
-        for (int mask = 1; mask < kWave; mask <<= 1) key = key_max_shfl(key, mask);
+        key = key_wave_max(key);
         __shared__ unsigned long long wkeys[4];
         __shared__ int last;
         const int wid = threadIdx.x / kWave;
@@ -373,8 +413,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
                 const unsigned long long k = __hip_atomic_load(gs.keys + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 b = k > b ? k : b;
             }
-#pragma unroll
-            for (int mask = 1; mask < kWave; mask <<= 1) b = key_max_shfl(b, mask);
+            b = key_wave_max(b);
             if (lane == 0) wkeys[wid] = b;
             __syncthreads();
             if (threadIdx.x == 0) {
@@ -394,8 +433,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
         }
     }
     if constexpr (EP == kEpGreedySlots) {
-#pragma unroll
-        for (int mask = 1; mask < kWave; mask <<= 1) key = key_max_shfl(key, mask);
+        key = key_wave_max(key);
         __shared__ unsigned long long wkeys[4];
         const int wid = threadIdx.x / kWave;
         if (lane == 0) wkeys[wid] = key;
@@ -410,11 +448,9 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
         }
     }
     if constexpr (EP == kEpSoftmax) {
-        // lanes 16m + 4r hold the wave's partials (the others are still empty)
-        sp = soft_merge(sp, soft_shfl_xor(sp, 4));
-        sp = soft_merge(sp, soft_shfl_xor(sp, 8));
-        sp = soft_merge(sp, soft_shfl_xor(sp, 16));
-        sp = soft_merge(sp, soft_shfl_xor(sp, 32));
+        // lanes 16m + 4r hold the wave's partials (the others are still empty, and merge as
+        // the identity)
+        sp = soft_wave_fold(sp);
         __shared__ SoftPart wparts[4];
         const int wid = threadIdx.x / kWave;
         if (lane == 0) wparts[wid] = sp;
@@ -458,8 +494,7 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
         const SoftPart p1 = i + (int)blockDim.x < nparts ? part[i + blockDim.x] : none;
         b = soft_merge(b, soft_merge(p0, p1));
     }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) b = soft_merge(b, soft_shfl_xor(b, off));
+    b = soft_wave_fold(b);
     if (lane == 0) wp[wid] = b;
     __syncthreads();
     if (threadIdx.x == 0) {
