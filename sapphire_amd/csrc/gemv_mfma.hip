@@ -473,9 +473,10 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
                                                             float *__restrict__ probs, int *__restrict__ argmax,
                                                             int aligned) {
     __shared__ SoftPart wp[4];
-    __shared__ SoftPart tot;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    // the first pass's logits are loaded before the partials are folded (independent loads)
+    // the first pass's logits (and logits[0] for the token) are loaded before the partials are
+    // folded (independent loads)
+    const float l0 = blockIdx.x == 0 && threadIdx.x == 0 && argmax ? logits[0] : 0.f;
     constexpr int U = kFinishVec;
     const int begin = blockIdx.x * chunk, end = min(n, begin + chunk);
     float4 v0[U];
@@ -485,29 +486,27 @@ __global__ __launch_bounds__(256) void softmax_finish_parts(const float *__restr
             const int i = begin + 4 * threadIdx.x + 4 * u * blockDim.x;
             v0[u] = i + 3 < end ? *reinterpret_cast<const float4 *>(logits + i) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    // two partials per thread and trip, both loads issued before either is merged (the fold's
+    // four partials per thread and trip, all four loads issued before any is merged (the fold's
     // order changes only the rounding of the sum: ties keep the lower index whatever the order)
     const SoftPart none{-INFINITY, 0.f, 0x7fffffff};
     SoftPart b = none;
-    for (int i = threadIdx.x; i < nparts; i += 2 * blockDim.x) {
-        const SoftPart p0 = part[i];
-        const SoftPart p1 = i + (int)blockDim.x < nparts ? part[i + blockDim.x] : none;
-        b = soft_merge(b, soft_merge(p0, p1));
+    for (int i = threadIdx.x; i < nparts; i += 4 * blockDim.x) {
+        SoftPart q[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = i + k * (int)blockDim.x < nparts ? part[i + k * blockDim.x] : none;
+        b = soft_merge(b, soft_merge(soft_merge(q[0], q[1]), soft_merge(q[2], q[3])));
     }
     b = soft_wave_fold(b);
     if (lane == 0) wp[wid] = b;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        SoftPart t = wp[0];
-        for (int w = 1; w < (int)(blockDim.x / kWave); ++w) t = soft_merge(t, wp[w]);
-        tot = t;
-        // sample_greedy (utils.c:145-156) starts at index 0 and only a greater logit replaces
-        // it: 0 when logits[0] is NaN or no logit is above -inf, else the first maximum
-        if (blockIdx.x == 0 && argmax) *argmax = (t.i >= 0 && t.i < n && !isnan(logits[0])) ? t.i : 0;
-    }
-    __syncthreads();
+    // every thread folds the waves' partials in the same order (the same result everywhere)
+    SoftPart t = wp[0];
+    for (int w = 1; w < (int)(blockDim.x / kWave); ++w) t = soft_merge(t, wp[w]);
+    // sample_greedy (utils.c:145-156) starts at index 0 and only a greater logit replaces it:
+    // 0 when logits[0] is NaN or no logit is above -inf, else the first maximum
+    if (blockIdx.x == 0 && threadIdx.x == 0 && argmax) *argmax = (t.i >= 0 && t.i < n && !isnan(l0)) ? t.i : 0;
     if (!probs) return;
-    const float m = tot.m, inv = 1.0f / tot.s;
+    const float m = t.m, inv = 1.0f / t.s;
     if (!aligned) {
         for (int i = begin + threadIdx.x; i < end; i += blockDim.x) probs[i] = expf(logits[i] - m) * inv;
         return;
