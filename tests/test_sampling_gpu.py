@@ -162,6 +162,30 @@ def test_decoder_sampling_matches_oracle(oracle, cfg, seed, prefill, steps, t, g
     assert greedy[0] == oracle_decode_forced(oracle, m, k.copy(), v.copy(), tok, prefill, nthreads=8)[0]
 
 
+def test_decoder_sampling_multi_step_graph():
+    """A sampled persistent-form call that takes no logits launches eight steps per graph; its
+    tokens are, draw for draw, those of the call that takes the logits (one step per launch,
+    checked against the oracle above). 19 steps: two eight-step launches and three single ones."""
+    from sapphire_amd.engine import Decoder
+    cfg, seed, prefill, steps = smodel.TINY, 66, 40, 19
+    m = smodel.synthetic_model(cfg, seed)
+    k, v = m.kv_prefill(prefill)
+    tok = smodel.start_token(cfg, seed)
+    draws = np.random.default_rng(seed).random(steps).astype(np.float32)
+    dec = Decoder(m)
+    try:
+        assert dec.workgroups > 0
+        dec.set_sampling(0.9, draws)
+        dec.set_kv(k, v)
+        with_logits, _, _ = dec.generate(tok, prefill, steps, keep_logits=True)
+        dec.set_kv(k, v)
+        without, _, _ = dec.generate(tok, prefill, steps)
+        print(f"sampled without logits {without.tolist()}", flush=True)
+        assert list(without) == list(with_logits)
+    finally:
+        dec.close()
+
+
 @pytest.mark.parametrize("cfg,seed,prefills,steps,t", [
     (smodel.TINY, 64, [40, 10, 23, 55], 10, 0.7),
     (G270M, 65, [1024, 300, 900], 6, 1.0),
