@@ -218,6 +218,8 @@ __global__ void gemm_greedy_finish_kernel(const float *__restrict__ part, int np
     if (threadIdx.x == 0) tokens[blockIdx.x] = bi >= 0 && bi < n ? bi : 0;
 }
 
+constexpr int kEmbedPasses = 4;   // 16-byte embedding loads per lane of the finish (hidden <= 2048)
+
 // grid 1, one wave per sequence: wave b picks sequence b's token from its nparts workgroup
 // partials (as gemm_greedy_finish_kernel), then the step ends as BatchAdvance describes. Every
 // wave reads the step counter before the barrier, and thread 0 advances it after.
@@ -261,9 +263,33 @@ __global__ __launch_bounds__(kBatchMax *kWave) void gemm_greedy_finish_advance_k
     }
     const uint16_t *row = a.embed + (size_t)t * a.hidden;
     float *out = a.resid + (size_t)b * a.hidden;
-    for (int k = lane; k < a.hidden; k += kWave) {
-        const float x = __uint_as_float((uint32_t)row[k] << 16);
-        out[k] = a.es != 1.0f ? __fmul_rn(x, a.es) : x;
+    auto widen = [&](uint32_t bits) {
+        const float x = __uint_as_float(bits << 16);
+        return a.es != 1.0f ? __fmul_rn(x, a.es) : x;
+    };
+    if (a.hidden % 8 == 0 && a.hidden <= kEmbedPasses * kWave * 8) {
+        // eight bf16 (16 bytes) per lane and pass, every pass's load issued before any store
+        // (rows are 16-byte aligned: the table and resid start so, and hidden % 8 == 0)
+        const int chunks = a.hidden / 8;
+        uint4 u[kEmbedPasses];
+#pragma unroll
+        for (int q = 0; q < kEmbedPasses; ++q) {
+            const int c = lane + q * kWave;
+            u[q] = c < chunks ? reinterpret_cast<const uint4 *>(row)[c] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < kEmbedPasses; ++q) {
+            const int c = lane + q * kWave;
+            if (c < chunks) {
+                float4 *dst = reinterpret_cast<float4 *>(out + 8 * c);
+                dst[0] = make_float4(widen(u[q].x & 0xFFFFu), widen(u[q].x >> 16), widen(u[q].y & 0xFFFFu),
+                                     widen(u[q].y >> 16));
+                dst[1] = make_float4(widen(u[q].z & 0xFFFFu), widen(u[q].z >> 16), widen(u[q].w & 0xFFFFu),
+                                     widen(u[q].w >> 16));
+            }
+        }
+    } else {
+        for (int k = lane; k < a.hidden; k += kWave) out[k] = widen(row[k]);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
