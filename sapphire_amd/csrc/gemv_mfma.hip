@@ -252,30 +252,6 @@ __device__ __forceinline__ unsigned long long greedy_key(float v, int row) {
     return ((unsigned long long)u << 32) | (0xFFFFFFFFu - (uint32_t)row);
 }
 
-template <int CTRL>
-__device__ __forceinline__ unsigned long long key_dpp(unsigned long long k) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
-__device__ __forceinline__ unsigned long long key_lane(unsigned long long k, int l) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), l);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
-// The largest key of the wave, in every lane: rows of 16 lanes by DPP (as soft_wave_fold),
-// then the four rows' maxima.
-__device__ __forceinline__ unsigned long long key_wave_max(unsigned long long k) {
-    auto mx = [](unsigned long long a, unsigned long long b) { return a > b ? a : b; };
-    k = mx(k, key_dpp<0xB1>(k));
-    k = mx(k, key_dpp<0x4E>(k));
-    k = mx(k, key_dpp<0x141>(k));
-    k = mx(k, key_dpp<0x140>(k));
-    return mx(mx(key_lane(k, 0), key_lane(k, 16)), mx(key_lane(k, 32), key_lane(k, 48)));
-}
-
 // What tile_store needs for activations with NaN / inf elements (nf, wave-uniform): the
 // weight planes, the blocks per row and x itself, for the fold of its non-finite elements.
 struct NfCtx {
@@ -381,7 +357,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
         }
     }
     if constexpr (EP == kEpGreedyStep) {
-        key = key_wave_max(key);
+        key = lanes::u64_wave_max(key);
         __shared__ unsigned long long wkeys[4];
         __shared__ int last;
         const int wid = threadIdx.x / kWave;
@@ -413,7 +389,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
                 const unsigned long long k = __hip_atomic_load(gs.keys + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 b = k > b ? k : b;
             }
-            b = key_wave_max(b);
+            b = lanes::u64_wave_max(b);
             if (lane == 0) wkeys[wid] = b;
             __syncthreads();
             if (threadIdx.x == 0) {
@@ -433,7 +409,7 @@ __global__ __launch_bounds__(256) void gemv_mfma(const uint8_t *__restrict__ wq,
         }
     }
     if constexpr (EP == kEpGreedySlots) {
-        key = key_wave_max(key);
+        key = lanes::u64_wave_max(key);
         __shared__ unsigned long long wkeys[4];
         const int wid = threadIdx.x / kWave;
         if (lane == 0) wkeys[wid] = key;

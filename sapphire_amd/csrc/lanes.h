@@ -62,6 +62,31 @@ __device__ __forceinline__ uint32_t quad_or(uint32_t v) {
     return v;
 }
 
+// The largest unsigned 64-bit value of the wave, in every lane: rows of 16 lanes by DPP on
+// both halves (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror), then the four
+// rows' maxima read from lanes 0, 16, 32 and 48.
+template <int CTRL>
+__device__ __forceinline__ unsigned long long u64_dpp(unsigned long long k) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ unsigned long long u64_lane(unsigned long long k, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ unsigned long long u64_wave_max(unsigned long long k) {
+    auto mx = [](unsigned long long a, unsigned long long b) { return a > b ? a : b; };
+    k = mx(k, u64_dpp<0xB1>(k));
+    k = mx(k, u64_dpp<0x4E>(k));
+    k = mx(k, u64_dpp<0x141>(k));
+    k = mx(k, u64_dpp<0x140>(k));
+    return mx(mx(u64_lane(k, 0), u64_lane(k, 16)), mx(u64_lane(k, 32), u64_lane(k, 48)));
+}
+
 // The greedy (value, index) best over each row of 16 lanes, left in every lane of the row: the
 // steps of row16_max, each pairing a lane with a partner that takes the same pair, under
 // `better` (a total order on (value, index) pairs, so every lane ends with the same pair).
