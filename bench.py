@@ -257,8 +257,8 @@ def main() -> int:
                          "calibration kernel of the FETCH_SIZE/WRITE_SIZE counters), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: the path has no multi-GPU mode in this build "
-              "(the one-GPU box runs --gpus 1).", file=sys.stderr)
+        print("bench.py measures one GPU: the path has no multi-GPU mode; run it with --gpus 1.",
+              file=sys.stderr)
         return 2
 
     from sapphire_amd import load, synth
