@@ -77,7 +77,7 @@ int sapphire_decoder_get_kv(sapphire_decoder_t *dec, float *k, float *v);
  * lowest index among equal maxima), or the sampled one (sapphire_decoder_set_sampling). logits_out, if not NULL, receives [steps][vocab] logits
  * (copied back after each step, which costs time). elapsed_ms, if not NULL, receives the
  * device time of the steps (HIP events on the decoder's stream). A call without logits_out on
- * the persistent step launches eight steps per captured graph where they fit. 0 / -1. */
+ * the persistent step launches sixteen steps per captured graph where they fit. 0 / -1. */
 int sapphire_decoder_generate(sapphire_decoder_t *dec, int token, int pos, int steps, int *tokens_out,
                               float *logits_out, float *elapsed_ms);
 

@@ -279,8 +279,9 @@ constexpr int kPersistSpinLimit = 1 << 19;
 // the batched step counter's range (tags are counter << 6 | layer + 1 in 32 bits)
 constexpr uint64_t kBatchEpochLimit = uint64_t(1) << 26;
 // steps per launch of the persistent step's multi-step graph (each graph launch costs the GPU a
-// gap of its own: 0.384 -> 0.380 ms per token)
-constexpr int kMultiSteps = 8;
+// gap of its own: 0.384 ms per token at one step per launch, 0.3829 at 8 and 0.3824 at 16 on
+// one box)
+constexpr int kMultiSteps = 16;
 int batch_qkv_width(const sapphire_decoder_config_t &c) { return (c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
 
 // Per sequence 1 once it has logged a stop token (the state's last B words).

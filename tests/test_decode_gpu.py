@@ -365,15 +365,16 @@ def test_decode_token_slots_across_runs(oracle, monkeypatch, run, stop_at):
         dec.close()
 
 
-@pytest.mark.parametrize("run,stop_at", [(None, None), (None, 5), (10, None), (10, 12)],
-                         ids=["default_run", "stop5", "run10", "run10_stop12"])
+@pytest.mark.parametrize("run,stop_at", [(None, None), (None, 5), (20, None), (20, 12)],
+                         ids=["default_run", "stop5", "run20", "run20_stop12"])
 def test_decode_multi_step_graph(oracle, monkeypatch, run, stop_at):
-    """A persistent-form call that takes no logits launches its steps eight to a graph, where
-    the eight fit in the call and inside one token-slot run, and the others one at a time. A
-    21-step call (8 + 8 + 5 single steps; with runs of 10 steps, 8 + 1 + 1 per run) decodes the
-    oracle's tokens and K/V rows, also with a stop token inside an eight-step launch."""
+    """A persistent-form call that takes no logits launches its steps sixteen to a graph,
+    where the sixteen fit in the call and inside one token-slot run, and the others one at a
+    time. A 45-step call (16 + 16 + 13 single steps; with runs of 20 steps, 16 + 4 single per
+    run and 5 single at the end) decodes the oracle's tokens and K/V rows, also with a stop token
+    inside a sixteen-step launch."""
     from sapphire_amd.engine import Decoder
-    cfg, seed, prefill, steps = smodel.TINY, 39, 30, 21
+    cfg, seed, prefill, steps = smodel.TINY, 39, 30, 45
     if run is not None:
         monkeypatch.setenv("SAPPHIRE_TOKEN_SLOT_RUN", str(run))
     m = smodel.synthetic_model(cfg, seed)
@@ -383,7 +384,7 @@ def test_decode_multi_step_graph(oracle, monkeypatch, run, stop_at):
     ref_toks, _ = oracle_decode(oracle, m, k, v, tok, prefill, steps, nthreads=4)
     stops = []
     if stop_at is not None:
-        # a token that first appears at stop_at (every token of this seed's 21 differs)
+        # a token that first appears at stop_at (the seed is chosen so that one does)
         assert ref_toks[stop_at] not in ref_toks[:stop_at], ref_toks
         stops = [int(ref_toks[stop_at])]
     n = steps if stop_at is None else stop_at + 1

@@ -163,11 +163,12 @@ def test_decoder_sampling_matches_oracle(oracle, cfg, seed, prefill, steps, t, g
 
 
 def test_decoder_sampling_multi_step_graph():
-    """A sampled persistent-form call that takes no logits launches eight steps per graph; its
-    tokens are, draw for draw, those of the call that takes the logits (one step per launch,
-    checked against the oracle above). 19 steps: two eight-step launches and three single ones."""
+    """A sampled persistent-form call that takes no logits launches sixteen steps per graph;
+    its tokens are, draw for draw, those of the call that takes the logits (one step per launch,
+    checked against the oracle above). 35 steps: two sixteen-step launches and three single
+    ones."""
     from sapphire_amd.engine import Decoder
-    cfg, seed, prefill, steps = smodel.TINY, 66, 40, 19
+    cfg, seed, prefill, steps = smodel.TINY, 66, 40, 35
     m = smodel.synthetic_model(cfg, seed)
     k, v = m.kv_prefill(prefill)
     tok = smodel.start_token(cfg, seed)
