@@ -368,12 +368,15 @@ struct GemvStage {
                 if (j == bpl - 1) {   // the step's last block: sum the row's lanes and store
                     p0 = row16_sum(p0);
                     if constexpr (GEGLU) p1 = row16_sum(p1);
-                    if constexpr (LPR == 32) {   // the row's two 16-lane halves
-                        p0 += __shfl_xor(p0, 16, kWave);
-                        if constexpr (GEGLU) p1 += __shfl_xor(p1, 16, kWave);
+                    if constexpr (LPR == 32) {   // the row's two 16-lane halves: the second's lanes
+                        // add the first's sum (DPP row_bcast:15 into rows 1 and 3)
+                        p0 += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p0), 0x142, 0xA, 0xF, false));
+                        if constexpr (GEGLU)
+                            p1 += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p1), 0x142, 0xA, 0xF, false));
                     }
                     const int row = st * RPW + rin;
-                    if (q == 0 && row < M) put_tagged(y + row, GEGLU ? __fmul_rn(gelu_ref(p0), p1) : p0, tag);
+                    if (q == (LPR == 32 ? 16 : 0) && row < M)
+                        put_tagged(y + row, GEGLU ? __fmul_rn(gelu_ref(p0), p1) : p0, tag);
                     p0 = 0.f;
                     p1 = 0.f;
                 }
